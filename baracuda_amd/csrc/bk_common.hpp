@@ -1,0 +1,98 @@
+// bk_common.hpp -- shared vocabulary of the gfx950 kernels behind the
+// baracuda_kernels_* C ABI: status codes, vector types and the exact scalar
+// codecs (bf16 RNE, OCP e4m3) the epilogues use.
+//
+// Status codes are the reference's (crates/baracuda-kernels-sys/src/lib.rs:19-27):
+//   0 ok, 1 misaligned, 2 invalid problem, 3 unsupported, 4 workspace, 5 launch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "baracuda_kernels.h"
+#include <cstddef>
+#include <cstdint>
+
+namespace bk {
+
+enum Status : int32_t {
+    kOk = 0,
+    kMisaligned = 1,
+    kInvalid = 2,
+    kUnsupported = 3,
+    kWorkspace = 4,
+    kLaunch = 5,
+};
+
+typedef int v2i __attribute__((ext_vector_type(2)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+inline int32_t launch_status() {
+    return hipPeekAtLastError() == hipSuccess ? kOk : kLaunch;
+}
+
+// f32 -> bf16 bits, round to nearest even; NaN keeps its top half with the
+// quiet bit set (crates/baracuda-kernelgen/src/oracle.rs:397-404).
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float x) {
+    uint32_t bits = __float_as_uint(x);
+    if ((bits & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((bits >> 16) | 0x0040u);
+    uint32_t bias = 0x7fffu + ((bits >> 16) & 1u);
+    return (uint16_t)((bits + bias) >> 16);
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+    return __uint_as_float((uint32_t)b << 16);
+}
+
+// f32 -> f16 bits, round to nearest even, overflow to inf, NaN quiet.
+__device__ __forceinline__ uint16_t f32_to_f16_rne(float x) {
+    _Float16 h = (_Float16)x;   // v_cvt_f16_f32 rounds to nearest even
+    return __builtin_bit_cast(uint16_t, h);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t b) {
+    return (float)__builtin_bit_cast(_Float16, b);
+}
+
+// OCP E4M3 (e4m3fn) saturating encode with round-to-nearest-even, written
+// from the format definition: bias 7, max finite 448 (S.1111.110), NaN
+// S.1111.111, subnormals m * 2^-9.  |x| > 448 (and +-inf) clamps to +-448.
+__device__ __forceinline__ uint8_t f32_to_e4m3_satfinite(float x) {
+    uint32_t bits = __float_as_uint(x);
+    uint8_t sign = (uint8_t)((bits >> 24) & 0x80u);
+    uint32_t abs = bits & 0x7fffffffu;
+    if (abs > 0x7f800000u) return (uint8_t)(sign | 0x7f);
+    if (abs >= 0x43e00000u) return (uint8_t)(sign | 0x7e);   // >= 448 (incl. inf)
+    if (abs < 0x3c800000u) {                                  // < 2^-6: subnormal grid
+        float q = __builtin_rintf(__uint_as_float(abs) * 512.0f);
+        return (uint8_t)(sign | (uint8_t)q);                  // q == 8 -> min normal
+    }
+    // Normal: keep 3 mantissa bits with RNE on the f32 bit pattern.
+    uint32_t lsb = (abs >> 20) & 1u;
+    uint32_t r = abs + 0x7ffffu + lsb;
+    uint32_t e = (r >> 23) - 127 + 7;
+    uint32_t m = (r >> 20) & 7u;
+    if (e > 15 || (e == 15 && m == 7)) return (uint8_t)(sign | 0x7e);
+    return (uint8_t)(sign | (uint8_t)(e << 3) | (uint8_t)m);
+}
+
+__device__ __forceinline__ float e4m3_to_f32(uint8_t b) {
+    uint32_t s = (uint32_t)(b & 0x80u) << 24;
+    uint32_t e = (b >> 3) & 0xfu, m = b & 7u;
+    if (e == 15 && m == 7) return __uint_as_float(s | 0x7fc00000u);
+    if (e == 0) {
+        float v = (float)m * (1.0f / 512.0f);
+        return __uint_as_float(__float_as_uint(v) | s);
+    }
+    return __uint_as_float(s | ((e - 7 + 127) << 23) | (m << 20));
+}
+
+__device__ __forceinline__ int8_t sat_cast_s8(float x) {
+    float r = __builtin_rintf(x);   // round half to even
+    r = r < -128.0f ? -128.0f : r;
+    r = r > 127.0f ? 127.0f : r;
+    return (int8_t)(int)r;
+}
+
+}  // namespace bk

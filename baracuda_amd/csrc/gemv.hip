@@ -1,0 +1,272 @@
+// gemv.hip -- capture-safe m=1 decode GEMVs for gfx950 (HBM-bound, no MFMA).
+//
+// 1. gemv_s8w_m1_bf16_gfx950 (new SKU): int8 weight-only decode GEMV
+//      out[n] = bf16_rne( scale[n] * sum_k x[k] * w[n, k] ),  f32 accumulate
+//    W is [N, K] int8 row-major (ldw), x bf16 [K], scale f32 [N], out bf16 [N].
+//    One wave64 owns ROWS consecutive output rows; lane l reads the 16-byte
+//    unit l of every 1 KiB K-chunk of each row (global_load_dwordx4, fully
+//    coalesced 1 KiB per wave per row), keeps the matching 16 x values in
+//    registers, and the 64 partial sums are folded with a fixed butterfly.
+//    Per-lane order and butterfly order are fixed, so every launch is
+//    bit-identical (graph replay safe) and independent of the grid.
+//
+// 2. gemv_dense_m1_{f32,f16,bf16} (reference ABI,
+//    crates/baracuda-kernels-sys/kernels/gemm/gemv_dense.cu:101-342):
+//      D[g, j] = alpha * sum_k A[g, k] * B[g, k, j] + beta * D[g, j]   (RRR)
+//    Workgroup of 1024 threads owns 64 columns; its 16 waves split K into
+//    16 contiguous slices (lane = column, coalesced 64-wide row reads), and
+//    the 16 partials are summed in LDS in slice order.  Fixed order => the
+//    result does not depend on grid shape and replays bit-identically.
+//    beta == 0 never reads D (write-only, gemv_dense.cu:163-169).
+#include "bk_common.hpp"
+
+namespace bk {
+namespace {
+
+// ---------------------------------------------------------------------------
+// int8 weight-only GEMV
+// ---------------------------------------------------------------------------
+constexpr int kGemvWaves = 4;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ float dot16_s8_bf16(const v4i w, const v4i xlo, const v4i xhi, float acc) {
+    // w: 16 int8; x: 16 bf16 as 8 dwords (xlo = k 0..7, xhi = k 8..15).
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t wq = (uint32_t)w[q];
+        const uint32_t x01 = (uint32_t)(q < 2 ? xlo[q * 2] : xhi[(q - 2) * 2]);
+        const uint32_t x23 = (uint32_t)(q < 2 ? xlo[q * 2 + 1] : xhi[(q - 2) * 2 + 1]);
+        const float x0 = __uint_as_float(x01 << 16), x1 = __uint_as_float(x01 & 0xffff0000u);
+        const float x2 = __uint_as_float(x23 << 16), x3 = __uint_as_float(x23 & 0xffff0000u);
+        acc = __builtin_fmaf((float)(int8_t)(wq & 0xff), x0, acc);
+        acc = __builtin_fmaf((float)(int8_t)((wq >> 8) & 0xff), x1, acc);
+        acc = __builtin_fmaf((float)(int8_t)((wq >> 16) & 0xff), x2, acc);
+        acc = __builtin_fmaf((float)(int8_t)(wq >> 24), x3, acc);
+    }
+    return acc;
+}
+
+// Fast path: K % 1024 == 0, 16-byte aligned rows.
+template <int ROWS>
+__global__ __launch_bounds__(64 * kGemvWaves) void gemv_s8w_m1_kernel(
+    int N, int K, const uint16_t *__restrict__ x, const int8_t *__restrict__ w, int64_t ldw,
+    const float *__restrict__ scale, uint16_t *__restrict__ d) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int row0 = (blockIdx.x * kGemvWaves + wave) * ROWS;
+    if (row0 >= N) return;
+    const int chunks = K >> 10;
+    const int8_t *wr[ROWS];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) wr[r] = w + (int64_t)min(row0 + r, N - 1) * ldw + lane * 16;
+    const v4i *xv = reinterpret_cast<const v4i *>(x) + lane * 2;
+    float acc[ROWS];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) acc[r] = 0.0f;
+#pragma unroll 4
+    for (int c = 0; c < chunks; ++c) {
+        v4i wv[ROWS];
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r)
+            wv[r] = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(wr[r] + (int64_t)c * 1024));
+        const v4i xlo = xv[c * 128], xhi = xv[c * 128 + 1];
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) acc[r] = dot16_s8_bf16(wv[r], xlo, xhi, acc[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+        const float s = wave_sum(acc[r]);
+        if (lane == 0 && row0 + r < N) d[row0 + r] = f32_to_bf16_rne(s * scale[row0 + r]);
+    }
+}
+
+// General path: any K, any alignment; lane l takes k = l, l+64, ... (bytes).
+__global__ __launch_bounds__(64 * kGemvWaves) void gemv_s8w_m1_generic_kernel(
+    int N, int K, const uint16_t *__restrict__ x, const int8_t *__restrict__ w, int64_t ldw,
+    const float *__restrict__ scale, uint16_t *__restrict__ d) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * kGemvWaves + (threadIdx.x >> 6);
+    if (row >= N) return;
+    const int8_t *wr = w + (int64_t)row * ldw;
+    float acc = 0.0f;
+    for (int k = lane; k < K; k += 64) acc = __builtin_fmaf((float)wr[k], bf16_to_f32(x[k]), acc);
+    const float s = wave_sum(acc);
+    if (lane == 0) d[row] = f32_to_bf16_rne(s * scale[row]);
+}
+
+constexpr int kGemvRows = 2;
+
+int32_t gemv_s8w_check(int32_t n, int32_t k, int64_t ldw) {
+    if (n < 0 || k < 0) return kInvalid;
+    if (ldw < (k > 0 ? k : 1)) return kInvalid;
+    return kOk;
+}
+
+// ---------------------------------------------------------------------------
+// float gemv_dense_m1 (reference ABI)
+// ---------------------------------------------------------------------------
+constexpr int kDenseCols = 64;
+constexpr int kDenseSlices = 16;
+
+struct F16Tag { typedef uint16_t S; };
+struct Bf16Tag { typedef uint16_t S; };
+
+template <typename Tag> struct Codec;
+template <> struct Codec<float> {
+    typedef float S;
+    __device__ static float ld(S v) { return v; }
+    __device__ static S st(float v) { return v; }
+};
+template <> struct Codec<F16Tag> {
+    typedef uint16_t S;
+    __device__ static float ld(S v) { return f16_to_f32(v); }
+    __device__ static S st(float v) { return f32_to_f16_rne(v); }
+};
+template <> struct Codec<Bf16Tag> {
+    typedef uint16_t S;
+    __device__ static float ld(S v) { return bf16_to_f32(v); }
+    __device__ static S st(float v) { return f32_to_bf16_rne(v); }
+};
+
+template <typename Tag>
+__global__ __launch_bounds__(kDenseCols * kDenseSlices) void gemv_dense_m1_kernel(
+    int n, int k, float alpha, float beta, const typename Codec<Tag>::S *__restrict__ a,
+    int64_t stride_a, const typename Codec<Tag>::S *__restrict__ b, int64_t ldb, int64_t stride_b,
+    typename Codec<Tag>::S *__restrict__ d, int64_t stride_d) {
+    typedef Codec<Tag> C;
+    __shared__ float part[kDenseSlices][kDenseCols];
+    const int slot = blockIdx.y;
+    const int lane = threadIdx.x & 63;
+    const int slice = threadIdx.x >> 6;
+    const int j = blockIdx.x * kDenseCols + lane;
+    const typename C::S *arow = a + (int64_t)slot * stride_a;
+    const typename C::S *bmat = b + (int64_t)slot * stride_b;
+    const int per = (k + kDenseSlices - 1) / kDenseSlices;
+    const int k0 = slice * per;
+    const int k1 = min(k, k0 + per);
+    float acc = 0.0f;
+    if (j < n) {
+        for (int kk = k0; kk < k1; ++kk)
+            acc = __builtin_fmaf(C::ld(arow[kk]), C::ld(bmat[(int64_t)kk * ldb + j]), acc);
+    }
+    part[slice][lane] = acc;
+    __syncthreads();
+    if (slice == 0 && j < n) {
+        float s = 0.0f;
+#pragma unroll
+        for (int q = 0; q < kDenseSlices; ++q) s += part[q][lane];
+        typename C::S *drow = d + (int64_t)slot * stride_d;
+        float out = alpha * s;
+        if (beta != 0.0f) out += beta * C::ld(drow[j]);
+        drow[j] = C::st(out);
+    }
+}
+
+// gemv_dense.cu:101-122 gemv_validate, restated.
+int32_t gemv_validate(int32_t m, int32_t n, int32_t k, int32_t batch, int32_t layout, int64_t lda,
+                      int64_t ldb, int64_t ldd, int64_t stride_d) {
+    if (m < 0 || n < 0 || k < 0 || batch < 0) return kInvalid;
+    if (m > 1) return kInvalid;
+    if (layout != 0) return kInvalid;
+    const int64_t min_lda = k > 0 ? k : 1;
+    const int64_t min_ld_n = n > 0 ? n : 1;
+    if (lda < min_lda || ldb < min_ld_n || ldd < min_ld_n) return kInvalid;
+    if (batch > 1 && stride_d == 0) return kInvalid;
+    return kOk;
+}
+
+template <typename Tag>
+int32_t launch_dense(int32_t m, int32_t n, int32_t k, int32_t batch, int32_t layout, float alpha,
+                     float beta, const void *a, int64_t lda, int64_t stride_a, const void *b,
+                     int64_t ldb, int64_t stride_b, void *d, int64_t ldd, int64_t stride_d,
+                     hipStream_t stream) {
+    const int32_t st = gemv_validate(m, n, k, batch, layout, lda, ldb, ldd, stride_d);
+    if (st != kOk) return st;
+    if (m == 0 || n == 0 || batch == 0) return kOk;
+    if (!a || !b || !d) return kInvalid;
+    typedef typename Codec<Tag>::S S;
+    dim3 grid((n + kDenseCols - 1) / kDenseCols, batch);
+    hipLaunchKernelGGL((gemv_dense_m1_kernel<Tag>), grid, dim3(kDenseCols * kDenseSlices), 0, stream,
+                       n, k, alpha, beta, (const S *)a, stride_a, (const S *)b, ldb, stride_b,
+                       (S *)d, stride_d);
+    return launch_status();
+}
+
+}  // namespace
+}  // namespace bk
+
+using namespace bk;
+
+extern "C" {
+
+// ---- int8 weight-only m=1 GEMV (new SKU) ------------------------------------
+int32_t baracuda_kernels_gemv_s8w_m1_bf16_gfx950_can_implement(int32_t n, int32_t k, int64_t ldw) {
+    return gemv_s8w_check(n, k, ldw);
+}
+
+size_t baracuda_kernels_gemv_s8w_m1_bf16_gfx950_workspace_size(int32_t n, int32_t k) {
+    (void)n; (void)k;
+    return 0;
+}
+
+int32_t baracuda_kernels_gemv_s8w_m1_bf16_gfx950_run(int32_t n, int32_t k, const void *x,
+                                                     const void *w, int64_t ldw, const void *scale,
+                                                     void *d, void *workspace,
+                                                     size_t workspace_bytes, void *stream_ptr) {
+    (void)workspace; (void)workspace_bytes;
+    int32_t st = gemv_s8w_check(n, k, ldw);
+    if (st != kOk) return st;
+    if (n == 0) return kOk;
+    if (!x || !w || !scale || !d) return kInvalid;
+    hipStream_t stream = (hipStream_t)stream_ptr;
+    const bool fast = k > 0 && k % 1024 == 0 && ldw % 16 == 0 &&
+                      (reinterpret_cast<uintptr_t>(w) & 15u) == 0 &&
+                      (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+    if (fast) {
+        const int waves = (n + kGemvRows - 1) / kGemvRows;
+        hipLaunchKernelGGL((gemv_s8w_m1_kernel<kGemvRows>), dim3((waves + kGemvWaves - 1) / kGemvWaves),
+                           dim3(64 * kGemvWaves), 0, stream, n, k, (const uint16_t *)x,
+                           (const int8_t *)w, ldw, (const float *)scale, (uint16_t *)d);
+    } else {
+        hipLaunchKernelGGL(gemv_s8w_m1_generic_kernel, dim3((n + kGemvWaves - 1) / kGemvWaves),
+                           dim3(64 * kGemvWaves), 0, stream, n, k, (const uint16_t *)x,
+                           (const int8_t *)w, ldw, (const float *)scale, (uint16_t *)d);
+    }
+    return launch_status();
+}
+
+// ---- gemv_dense_m1_{f32,f16,bf16} (gemv_dense.cu:235-342 ABI) -----------------
+#define BK_GEMV_DENSE(TAG, TY)                                                                    \
+    int32_t baracuda_kernels_gemv_dense_m1_##TAG##_run(                                           \
+        int32_t m, int32_t n, int32_t k, int32_t batch, int32_t layout, float alpha, float beta,  \
+        const void *a, int64_t lda, int64_t stride_a, const void *b, int64_t ldb,                 \
+        int64_t stride_b, void *d, int64_t ldd, int64_t stride_d, void *workspace,                \
+        size_t workspace_bytes, void *stream) {                                                   \
+        (void)workspace; (void)workspace_bytes;                                                   \
+        return launch_dense<TY>(m, n, k, batch, layout, alpha, beta, a, lda, stride_a, b, ldb,    \
+                                stride_b, d, ldd, stride_d, (hipStream_t)stream);                 \
+    }                                                                                             \
+    int32_t baracuda_kernels_gemv_dense_m1_##TAG##_can_implement(                                 \
+        int32_t m, int32_t n, int32_t k, int32_t batch, int32_t layout, int64_t lda, int64_t ldb, \
+        int64_t ldd, int64_t stride_a, int64_t stride_b, int64_t stride_d) {                      \
+        (void)stride_a; (void)stride_b;                                                           \
+        return gemv_validate(m, n, k, batch, layout, lda, ldb, ldd, stride_d);                    \
+    }                                                                                             \
+    size_t baracuda_kernels_gemv_dense_m1_##TAG##_workspace_size(int32_t m, int32_t n, int32_t k, \
+                                                                 int32_t batch, int32_t layout) { \
+        (void)m; (void)n; (void)k; (void)batch; (void)layout;                                     \
+        return 0;                                                                                 \
+    }
+
+BK_GEMV_DENSE(f32, float)
+BK_GEMV_DENSE(f16, F16Tag)
+BK_GEMV_DENSE(bf16, Bf16Tag)
+
+#undef BK_GEMV_DENSE
+
+}  // extern "C"

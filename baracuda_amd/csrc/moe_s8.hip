@@ -1,0 +1,172 @@
+// moe_s8.hip -- grouped int8 MoE expert GEMM for gfx950, one GEMM launch
+// over all experts, W8A8 dequant epilogue to bf16.
+//
+// Routing contract of the reference MoE path
+// (crates/baracuda-kernels-sys/kernels/moe/moe_wmma.cu:121-175,
+//  crates/baracuda-kernels-sys/kernels/include/baracuda_moe.cuh:827-944,1121-1162):
+//   sorted_token_ids[size_m]  pair ids (token*topk + slot) grouped by expert
+//   expert_ids[size_m]        expert of each sorted position
+//   expert_counts[E], expert_offsets[E+1]   caller-provided, filled here
+//   input row of pair p       = sorted_token_ids[p] / topk   (topk_weights == NULL)
+//                             = sorted_token_ids[p]          (topk_weights != NULL)
+//   output row of pair p      = sorted_token_ids[p]
+//   out[row, n] = bf16( ((sa[in_row] * sw[e*N + n]) * acc) [* topk_weights[row]] )
+//
+// Differences by design: expert offsets are computed by one workgroup with
+// LDS counters (no global atomics, no memset: graph-capturable), and the GEMM
+// is one launch whose workgroups walk the ragged per-expert tile list.
+#include "gemm_mfma.hpp"
+
+namespace bk {
+namespace {
+
+using namespace mfma;
+
+constexpr int kMaxExperts = 1024;
+
+// expert_counts / expert_offsets from expert_ids (one workgroup, 1024 threads).
+__global__ __launch_bounds__(1024) void moe_offsets_kernel(const int32_t *__restrict__ expert_ids,
+                                                           int32_t size_m, int32_t num_experts,
+                                                           int32_t *__restrict__ counts,
+                                                           int32_t *__restrict__ offsets) {
+    __shared__ int32_t cnt[kMaxExperts];
+    for (int e = threadIdx.x; e < num_experts; e += blockDim.x) cnt[e] = 0;
+    __syncthreads();
+    for (int i = threadIdx.x; i < size_m; i += blockDim.x) {
+        const int e = expert_ids[i];
+        if (e >= 0 && e < num_experts) atomicAdd(&cnt[e], 1);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int run = 0;
+        offsets[0] = 0;
+        for (int e = 0; e < num_experts; ++e) {
+            counts[e] = cnt[e];
+            run += cnt[e];
+            offsets[e + 1] = run;
+        }
+    }
+}
+
+struct MoeArgs {
+    const int8_t *x;            // [tokens, K]
+    const int8_t *w;            // [E, N, K]
+    const int32_t *sorted_ids;  // [size_m]
+    const int32_t *offsets;     // [E+1]
+    const float *topk_w;        // [size_m] or nullptr
+    const float *sa;            // [tokens]
+    const float *sw;            // [E, N]
+    uint16_t *out;              // [size_m, N] bf16
+    int E, topk, size_m, N, K;
+};
+
+template <bool Checked>
+__global__ __launch_bounds__(NT, 1) void moe_s8_grouped_kernel(MoeArgs p) {
+    __shared__ __attribute__((aligned(16))) int8_t lds[4 * LDS_TILE];
+    __shared__ int32_t s_rows_tok[BM];
+
+    // Ragged tile list: slot -> (expert, m-tile).  Workgroup-uniform walk.
+    int slot = blockIdx.x;
+    int e = 0, seg0 = 0, seg_rows = 0;
+    for (; e < p.E; ++e) {
+        const int o0 = p.offsets[e], o1 = min(p.offsets[e + 1], p.size_m);
+        const int rows = o1 > o0 ? o1 - o0 : 0;
+        const int tiles = (rows + BM - 1) / BM;
+        if (slot < tiles) { seg0 = o0 + slot * BM; seg_rows = min(BM, rows - slot * BM); break; }
+        slot -= tiles;
+    }
+    if (e >= p.E) return;   // past the last real tile: whole workgroup exits
+    const int n_base = blockIdx.y * BN;
+
+    const int tid = threadIdx.x;
+    for (int r = tid; r < BM; r += NT) s_rows_tok[r] = p.sorted_ids[seg0 + min(r, seg_rows - 1)];
+    __syncthreads();
+
+    const int in_div = p.topk_w ? 1 : p.topk;
+    const int8_t *we = p.w + (int64_t)e * p.N * p.K;
+    RowSet as, bs;
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+        const int r = i * LOAD_ROWS + (tid >> 3);
+        as.ptr[i] = p.x + (int64_t)(s_rows_tok[r] / in_div) * p.K;
+        bs.ptr[i] = we + (int64_t)min(n_base + r, p.N - 1) * p.K;
+    }
+    v4i acc[TM][TN];
+    mainloop<Elem::S8, Checked>(lds, as, bs, p.K, acc);
+
+    const float *swe = p.sw + (int64_t)e * p.N;
+    for_each_fragment(acc, [&](int ml, int nl, const v4i &v) {
+        const int n0 = n_base + nl;
+        if (ml >= seg_rows || n0 >= p.N) return;
+        const int tok = s_rows_tok[ml];
+        const float sam = p.sa[tok / in_div];
+        const int count = p.N - n0 < 4 ? p.N - n0 : 4;
+        float y[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) y[r] = r < count ? (sam * swe[n0 + r]) * (float)v[r] : 0.0f;
+        if (p.topk_w) {
+            const float tw = p.topk_w[tok];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) y[r] = y[r] * tw;
+        }
+        store4_bf16(p.out + (int64_t)tok * p.N + n0, y, count == 4 && (p.N % 4 == 0), count);
+    });
+}
+
+}  // namespace
+}  // namespace bk
+
+using namespace bk;
+
+extern "C" {
+
+int32_t baracuda_kernels_moe_s8_grouped_bf16_gfx950_can_implement(
+    int32_t num_experts, int32_t topk, int32_t size_m, int32_t size_n, int32_t size_k) {
+    if (num_experts <= 0 || topk <= 0) return kInvalid;
+    if (size_m <= 0 || size_n <= 0 || size_k <= 0) return kInvalid;
+    if (topk > num_experts) return kInvalid;
+    if (num_experts > kMaxExperts) return kUnsupported;
+    return kOk;
+}
+
+size_t baracuda_kernels_moe_s8_grouped_bf16_gfx950_workspace_size(
+    int32_t num_experts, int32_t topk, int32_t size_m, int32_t size_n, int32_t size_k) {
+    (void)num_experts; (void)topk; (void)size_m; (void)size_n; (void)size_k;
+    return 0;
+}
+
+// Argument order follows baracuda_kernels_moe_wmma_bf16_run (moe_wmma.cu:154-175)
+// with the two W8A8 scale vectors inserted before the workspace.
+int32_t baracuda_kernels_moe_s8_grouped_bf16_gfx950_run(
+    const void *input, const void *weights, const int32_t *sorted_token_ids,
+    const int32_t *expert_ids, const float *topk_weights, void *output,
+    int32_t *expert_counts, int32_t *expert_offsets, int32_t num_experts, int32_t topk,
+    int32_t size_m, int32_t size_n, int32_t size_k, const float *scale_a, const float *scale_w,
+    void *workspace, size_t workspace_bytes, void *stream_ptr) {
+    (void)workspace; (void)workspace_bytes;
+    if (!input || !weights || !sorted_token_ids || !expert_ids || !output || !expert_counts ||
+        !expert_offsets || !scale_a || !scale_w)
+        return kInvalid;
+    int32_t st = baracuda_kernels_moe_s8_grouped_bf16_gfx950_can_implement(num_experts, topk, size_m,
+                                                                           size_n, size_k);
+    if (st != kOk) return st;
+    hipStream_t stream = (hipStream_t)stream_ptr;
+    hipLaunchKernelGGL(moe_offsets_kernel, dim3(1), dim3(1024), 0, stream, expert_ids, size_m,
+                       num_experts, expert_counts, expert_offsets);
+    if (hipPeekAtLastError() != hipSuccess) return kLaunch;
+
+    MoeArgs p{(const int8_t *)input, (const int8_t *)weights, sorted_token_ids, expert_offsets,
+              topk_weights, scale_a, scale_w, (uint16_t *)output, num_experts, topk, size_m,
+              size_n, size_k};
+    // Upper bound on ragged m-tiles: sum_e ceil(cnt_e / BM) <= ceil(size_m / BM) + E.
+    const int slots = (size_m + BM - 1) / BM + num_experts;
+    dim3 grid(slots, (size_n + BN - 1) / BN);
+    const bool fast_k = size_k % BK == 0 && mfma::aligned16(input) && mfma::aligned16(weights);
+    if (fast_k)
+        hipLaunchKernelGGL((moe_s8_grouped_kernel<false>), grid, dim3(NT), 0, stream, p);
+    else
+        hipLaunchKernelGGL((moe_s8_grouped_kernel<true>), grid, dim3(NT), 0, stream, p);
+    return launch_status();
+}
+
+}  // extern "C"

@@ -1,0 +1,399 @@
+"""Host-side mirror of baracuda's Plan surface for this path, over the C ABI.
+
+Mirrors (names, argument meaning, error behaviour):
+  IntGemmPlan   crates/baracuda-kernels/src/gemm/int_gemm.rs:48-654
+  Fp8GemmPlan   crates/baracuda-kernels/src/gemm/fp8_gemm.rs:36-767
+  GemvDensePlan crates/baracuda-kernels/src/gemm/gemv_dense.rs:55-412
+  GemmSku / PrecisionGuarantee  crates/baracuda-cutlass/src/types.rs:271-370
+  ArchSku       crates/baracuda-kernel-vocab/src/layout.rs:43-52 (+ Gfx950)
+gather_rows has no Plan in the reference (callers use the FFI directly,
+crates/baracuda-kernels/tests/capture_replay_gather_gemv.rs:73-79); it is
+exposed here as a function.  Every plan's ``run`` issues exactly one C-ABI
+call on the given stream (torch's current stream by default), never
+allocates and never synchronises.
+
+Device buffers are torch tensors (plumbing only: the arithmetic is the HIP
+library's).  Shapes are validated against the descriptor before the call.
+"""
+from __future__ import annotations
+
+import enum
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from .ffi import lib
+
+
+# ---- vocabulary ------------------------------------------------------------
+class ArchSku(enum.Enum):
+    Sm80 = "sm80"
+    Sm89 = "sm89"
+    Sm90a = "sm90a"
+    Gfx950 = "gfx950"
+
+
+class LayoutSku(enum.Enum):
+    Rrr = "rrr"
+    Rcr = "rcr"
+
+
+class EpilogueKind(enum.Enum):
+    Identity = "identity"
+    Bias = "bias"
+    BiasRelu = "bias_relu"
+    BiasGelu = "bias_gelu"
+    BiasSilu = "bias_silu"
+
+
+class ElementKind(enum.Enum):
+    S8 = "s8"
+    I32 = "i32"
+    F32 = "f32"
+    F16 = "f16"
+    Bf16 = "bf16"
+    Fp8E4M3 = "fp8_e4m3"
+    U32 = "u32"
+
+
+class BackendKind(enum.Enum):
+    Bespoke = "bespoke"
+
+
+class MathPrecision(enum.Enum):
+    Int8 = "int8"
+    Fp8E4M3 = "fp8_e4m3"
+    F32 = "f32"
+    F16 = "f16"
+    Bf16 = "bf16"
+
+
+@dataclass(frozen=True)
+class PrecisionGuarantee:
+    math_precision: MathPrecision
+    accumulator: ElementKind
+    bit_stable_on_same_hardware: bool
+    deterministic: bool
+
+
+@dataclass(frozen=True)
+class GemmSku:
+    arch: ArchSku
+    layout: LayoutSku
+    epilogue: EpilogueKind
+    element: ElementKind
+    output: ElementKind
+    bias_element: Optional[ElementKind] = None
+
+    def precision_guarantee(self) -> PrecisionGuarantee:
+        # types.rs:296-369: int8 accumulates in i32 and is bit-stable; the
+        # gfx950 FP8 MFMA path is deterministic (fixed per-tile K order, no
+        # atomics) and therefore also bit-stable on the same hardware.
+        if self.element == ElementKind.S8:
+            return PrecisionGuarantee(MathPrecision.Int8, ElementKind.I32, True, True)
+        return PrecisionGuarantee(MathPrecision.Fp8E4M3, ElementKind.F32, True, True)
+
+
+# ---- errors (status codes, crates/baracuda-kernels-sys/src/lib.rs:19-27) ----
+class KernelError(RuntimeError):
+    status = -1
+
+
+class Misaligned(KernelError):
+    status = 1
+
+
+class InvalidProblem(KernelError):
+    status = 2
+
+
+class Unsupported(KernelError):
+    status = 3
+
+
+class WorkspaceTooSmall(KernelError):
+    status = 4
+
+
+class LaunchFailed(KernelError):
+    status = 5
+
+
+_STATUS = {1: Misaligned, 2: InvalidProblem, 3: Unsupported, 4: WorkspaceTooSmall, 5: LaunchFailed}
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        raise _STATUS.get(status, KernelError)(f"{what}: status {status}")
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(stream) -> int:
+    if stream is None:
+        return torch.cuda.current_stream().cuda_stream
+    return stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream)
+
+
+def _need(cond: bool, msg: str) -> None:
+    if not cond:
+        raise InvalidProblem(msg)
+
+
+def _ld(t: torch.Tensor) -> int:
+    _need(t.dim() == 2 and t.stride(1) == 1, "operand must be a 2-D row-major view")
+    return t.stride(0)
+
+
+# ---- int8 GEMM -------------------------------------------------------------
+@dataclass(frozen=True)
+class IntGemmDescriptor:
+    m: int
+    n: int
+    k: int
+    layout: LayoutSku = LayoutSku.Rcr
+    epilogue: EpilogueKind = EpilogueKind.Identity
+    output: ElementKind = ElementKind.S8     # S8 (reference), I32 or Bf16 (W8A8)
+
+
+class IntGemmPlan:
+    """int_gemm.rs IntGemmPlan: select / can_implement / workspace_size / sku / run.
+
+    RCR only on gfx950; outputs: S8 (sat(alpha*acc+beta*C)), I32 (raw acc),
+    Bf16 (W8A8 per-token x per-channel dequant, needs scale_a / scale_b)."""
+
+    def __init__(self, desc: IntGemmDescriptor, sku: GemmSku):
+        self.desc, self._sku = desc, sku
+
+    @classmethod
+    def select(cls, desc: IntGemmDescriptor) -> "IntGemmPlan":
+        if desc.m <= 0 or desc.n <= 0 or desc.k <= 0:
+            raise InvalidProblem("int GEMM problem must have positive M, N, K")
+        if desc.layout != LayoutSku.Rcr:
+            raise Unsupported("gfx950 int8 GEMM implements the RCR layout")
+        if desc.epilogue != EpilogueKind.Identity:
+            raise Unsupported("gfx950 int8 GEMM implements the Identity epilogue")
+        if desc.output not in (ElementKind.S8, ElementKind.I32, ElementKind.Bf16):
+            raise Unsupported(f"int8 GEMM output {desc.output}")
+        return cls(desc, GemmSku(ArchSku.Gfx950, desc.layout, desc.epilogue, ElementKind.S8, desc.output))
+
+    def sku(self) -> GemmSku:
+        return self._sku
+
+    def precision_guarantee(self) -> PrecisionGuarantee:
+        return self._sku.precision_guarantee()
+
+    def workspace_size(self) -> int:
+        d, L = self.desc, lib()
+        f = {ElementKind.S8: L.gemm_s8_rcr_gfx950_workspace_size,
+             ElementKind.I32: L.gemm_s8_rcr_gfx950_i32_workspace_size,
+             ElementKind.Bf16: L.gemm_w8a8_rcr_gfx950_bf16_workspace_size}[d.output]
+        return f(d.m, d.n, d.k)
+
+    def can_implement(self, a, b, d, c=None) -> None:
+        desc = self.desc
+        _need(tuple(a.shape) == (desc.m, desc.k), "A shape mismatch with descriptor (M, K)")
+        _need(tuple(b.shape) == (desc.n, desc.k), "B shape mismatch with descriptor ([N, K] = col-major [K, N])")
+        _need(tuple(d.shape) == (desc.m, desc.n), "D shape mismatch with descriptor (M, N)")
+        want = {ElementKind.S8: torch.int8, ElementKind.I32: torch.int32, ElementKind.Bf16: torch.bfloat16}[desc.output]
+        _need(a.dtype == torch.int8 and b.dtype == torch.int8 and d.dtype == want, "dtype mismatch")
+        if c is not None:
+            _need(tuple(c.shape) == (desc.m, desc.n) and c.dtype == torch.int8, "C shape mismatch")
+
+    def run(self, a, b, d, c=None, alpha=1.0, beta=0.0, scale_a=None, scale_b=None,
+            workspace=None, stream=None) -> None:
+        self.can_implement(a, b, d, c)
+        desc, L, s = self.desc, lib(), _stream(stream)
+        if desc.output == ElementKind.S8:
+            if c is None:
+                beta = 0.0
+            st = L.gemm_s8_rcr_gfx950_run(desc.m, desc.n, desc.k, _ptr(a), _ld(a), _ptr(b), _ld(b),
+                                          _ptr(c), _ld(c) if c is not None else 0, _ptr(d), _ld(d),
+                                          alpha, beta, _ptr(workspace), 0, s)
+        elif desc.output == ElementKind.I32:
+            st = L.gemm_s8_rcr_gfx950_i32_run(desc.m, desc.n, desc.k, _ptr(a), _ld(a), _ptr(b), _ld(b),
+                                              _ptr(d), _ld(d), _ptr(workspace), 0, s)
+        else:
+            _need(scale_a is not None and scale_b is not None, "W8A8 needs scale_a and scale_b")
+            _need(scale_a.numel() == desc.m and scale_b.numel() == desc.n and
+                  scale_a.dtype == torch.float32 and scale_b.dtype == torch.float32, "scale shape/dtype")
+            st = L.gemm_w8a8_rcr_gfx950_bf16_run(desc.m, desc.n, desc.k, _ptr(a), _ld(a), _ptr(b), _ld(b),
+                                                 _ptr(scale_a), _ptr(scale_b), _ptr(d), _ld(d),
+                                                 _ptr(workspace), 0, s)
+        check(st, "IntGemmPlan::run")
+
+
+# ---- FP8 GEMM --------------------------------------------------------------
+@dataclass(frozen=True)
+class Fp8GemmDescriptor:
+    m: int
+    n: int
+    k: int
+    layout: LayoutSku = LayoutSku.Rcr
+    epilogue: EpilogueKind = EpilogueKind.Identity
+    output: ElementKind = ElementKind.Fp8E4M3   # Fp8E4M3 (reference), Bf16, F32
+
+
+class Fp8GemmPlan:
+    """fp8_gemm.rs Fp8GemmPlan for E4M3 RCR on gfx950."""
+
+    def __init__(self, desc: Fp8GemmDescriptor, sku: GemmSku):
+        self.desc, self._sku = desc, sku
+
+    @classmethod
+    def select(cls, desc: Fp8GemmDescriptor) -> "Fp8GemmPlan":
+        if desc.m <= 0 or desc.n <= 0 or desc.k <= 0:
+            raise InvalidProblem("FP8 GEMM problem must have positive M, N, K")
+        if desc.layout != LayoutSku.Rcr:
+            raise Unsupported("gfx950 FP8 GEMM implements the RCR layout")
+        if desc.epilogue != EpilogueKind.Identity:
+            raise Unsupported("gfx950 FP8 GEMM implements the Identity epilogue")
+        if desc.output not in (ElementKind.Fp8E4M3, ElementKind.Bf16, ElementKind.F32):
+            raise Unsupported(f"FP8 GEMM output {desc.output}")
+        return cls(desc, GemmSku(ArchSku.Gfx950, desc.layout, desc.epilogue, ElementKind.Fp8E4M3, desc.output))
+
+    def sku(self) -> GemmSku:
+        return self._sku
+
+    def precision_guarantee(self) -> PrecisionGuarantee:
+        return self._sku.precision_guarantee()
+
+    def workspace_size(self) -> int:
+        return 0
+
+    def run(self, a, b, d, c=None, alpha=1.0, beta=0.0, scale_a=1.0, scale_b=1.0,
+            workspace=None, stream=None) -> None:
+        desc, L, s = self.desc, lib(), _stream(stream)
+        _need(tuple(a.shape) == (desc.m, desc.k) and tuple(b.shape) == (desc.n, desc.k)
+              and tuple(d.shape) == (desc.m, desc.n), "shape mismatch with descriptor")
+        _need(a.element_size() == 1 and b.element_size() == 1, "FP8 operands are 1-byte")
+        if desc.output == ElementKind.Fp8E4M3:
+            if c is None:
+                beta = 0.0
+            st = L.gemm_fp8_e4m3_rcr_gfx950_run(desc.m, desc.n, desc.k, _ptr(a), _ld(a), _ptr(b), _ld(b),
+                                                _ptr(c), _ld(c) if c is not None else 0, _ptr(d), _ld(d),
+                                                alpha, beta, _ptr(workspace), 0, s)
+        elif desc.output == ElementKind.Bf16:
+            _need(d.dtype == torch.bfloat16, "D must be bf16")
+            st = L.gemm_fp8_e4m3_rcr_gfx950_bf16_run(desc.m, desc.n, desc.k, _ptr(a), _ld(a), _ptr(b), _ld(b),
+                                                     scale_a, scale_b, _ptr(d), _ld(d), _ptr(workspace), 0, s)
+        else:
+            _need(d.dtype == torch.float32, "D must be f32")
+            st = L.gemm_fp8_e4m3_rcr_gfx950_f32_run(desc.m, desc.n, desc.k, _ptr(a), _ld(a), _ptr(b), _ld(b),
+                                                    alpha, _ptr(d), _ld(d), _ptr(workspace), 0, s)
+        check(st, "Fp8GemmPlan::run")
+
+
+# ---- GEMV m = 1 ------------------------------------------------------------
+_GEMV_TAG = {torch.float32: "f32", torch.float16: "f16", torch.bfloat16: "bf16"}
+
+
+@dataclass(frozen=True)
+class GemvDenseDescriptor:
+    n: int
+    k: int
+    batch: int = 1
+    m: int = 1
+    layout: int = 0   # RRR
+
+
+class GemvDensePlan:
+    """gemv_dense.rs GemvDensePlan<T> (RRR, strided batch, stride_b == 0 broadcast)."""
+
+    def __init__(self, desc: GemvDenseDescriptor, dtype: torch.dtype):
+        self.desc, self.dtype = desc, dtype
+
+    @classmethod
+    def select(cls, desc: GemvDenseDescriptor, dtype: torch.dtype) -> "GemvDensePlan":
+        if dtype not in _GEMV_TAG:
+            raise Unsupported(f"gemv_dense_m1 dtype {dtype}")
+        if desc.m < 0 or desc.n < 0 or desc.k < 0 or desc.batch < 0 or desc.m > 1 or desc.layout != 0:
+            raise InvalidProblem("gemv_dense_m1 descriptor")
+        return cls(desc, dtype)
+
+    def _fn(self, suffix):
+        return getattr(lib(), f"gemv_dense_m1_{_GEMV_TAG[self.dtype]}_{suffix}")
+
+    def workspace_size(self) -> int:
+        d = self.desc
+        return self._fn("workspace_size")(d.m, d.n, d.k, d.batch, d.layout)
+
+    def can_implement(self, lda, ldb, ldd, stride_a, stride_b, stride_d) -> None:
+        d = self.desc
+        check(self._fn("can_implement")(d.m, d.n, d.k, d.batch, d.layout, lda, ldb, ldd,
+                                        stride_a, stride_b, stride_d), "GemvDensePlan::can_implement")
+
+    def run(self, a, b, d, *, lda, stride_a, ldb, stride_b, ldd, stride_d, alpha=1.0, beta=0.0,
+            workspace=None, stream=None) -> None:
+        desc = self.desc
+        for t in (a, b, d):
+            _need(t.dtype == self.dtype, "dtype mismatch")
+        st = self._fn("run")(desc.m, desc.n, desc.k, desc.batch, desc.layout, alpha, beta,
+                             _ptr(a), lda, stride_a, _ptr(b), ldb, stride_b, _ptr(d), ldd, stride_d,
+                             _ptr(workspace), 0, _stream(stream))
+        check(st, "GemvDensePlan::run")
+
+
+class GemvS8wPlan:
+    """New SKU of the gemv_dense_m1 family: int8 weight-only m=1 decode GEMV."""
+
+    def __init__(self, n: int, k: int):
+        self.n, self.k = n, k
+
+    @classmethod
+    def select(cls, n: int, k: int) -> "GemvS8wPlan":
+        if n < 0 or k < 0:
+            raise InvalidProblem("gemv_s8w_m1 extents")
+        return cls(n, k)
+
+    def run(self, x, w, scale, d, stream=None) -> None:
+        _need(w.dtype == torch.int8 and tuple(w.shape) == (self.n, self.k), "W must be int8 [N, K]")
+        _need(x.dtype == torch.bfloat16 and x.numel() == self.k, "x must be bf16 [K]")
+        _need(scale.dtype == torch.float32 and scale.numel() == self.n, "scale must be f32 [N]")
+        _need(d.dtype == torch.bfloat16 and d.numel() == self.n, "d must be bf16 [N]")
+        st = lib().gemv_s8w_m1_bf16_gfx950_run(self.n, self.k, _ptr(x), _ptr(w), _ld(w), _ptr(scale),
+                                               _ptr(d), None, 0, _stream(stream))
+        check(st, "GemvS8wPlan::run")
+
+
+# ---- gather_rows (direct FFI in the reference) ------------------------------
+_GATHER_TAG = {torch.float32: "f32", torch.float16: "f16", torch.bfloat16: "bf16"}
+
+
+def gather_rows(dest: torch.Tensor, table: torch.Tensor, idx: torch.Tensor, stream=None) -> None:
+    """dest[r,:] = table[idx[r],:] (idx uint32, out-of-range -> zeros)."""
+    _need(table.dim() == 2 and table.is_contiguous() and dest.is_contiguous(), "contiguous 2-D table/dest")
+    _need(idx.dtype == torch.uint32 and idx.is_contiguous(), "idx must be contiguous uint32")
+    V, H = table.shape
+    n = idx.numel()
+    _need(dest.numel() == n * H and dest.dtype == table.dtype, "dest must be [n, H] of table.dtype")
+    fn = getattr(lib(), f"gather_rows_{_GATHER_TAG[table.dtype]}_run")
+    check(fn(_ptr(dest), _ptr(table), _ptr(idx), V, H, n, _stream(stream)), "gather_rows")
+
+
+# ---- grouped MoE int8 -------------------------------------------------------
+class MoeS8GroupedPlan:
+    """Grouped int8 expert GEMM with the moe_wmma routing contract (new SKU)."""
+
+    def __init__(self, num_experts, topk, size_m, size_n, size_k):
+        self.E, self.topk, self.size_m, self.n, self.k = num_experts, topk, size_m, size_n, size_k
+
+    @classmethod
+    def select(cls, num_experts, topk, size_m, size_n, size_k) -> "MoeS8GroupedPlan":
+        check(lib().moe_s8_grouped_bf16_gfx950_can_implement(num_experts, topk, size_m, size_n, size_k),
+              "MoeS8GroupedPlan::select")
+        return cls(num_experts, topk, size_m, size_n, size_k)
+
+    def run(self, x, w, sorted_token_ids, expert_ids, out, expert_counts, expert_offsets,
+            scale_a, scale_w, topk_weights=None, stream=None) -> None:
+        _need(x.dtype == torch.int8 and w.dtype == torch.int8 and out.dtype == torch.bfloat16, "dtypes")
+        _need(w.numel() == self.E * self.n * self.k and x.shape[-1] == self.k, "shapes")
+        _need(out.numel() >= self.size_m * self.n, "out too small")
+        st = lib().moe_s8_grouped_bf16_gfx950_run(
+            _ptr(x), _ptr(w), _ptr(sorted_token_ids), _ptr(expert_ids), _ptr(topk_weights), _ptr(out),
+            _ptr(expert_counts), _ptr(expert_offsets), self.E, self.topk, self.size_m, self.n, self.k,
+            _ptr(scale_a), _ptr(scale_w), None, 0, _stream(stream))
+        check(st, "MoeS8GroupedPlan::run")

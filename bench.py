@@ -1,0 +1,220 @@
+"""Benchmark of the quantized-inference contraction path on one MI355X.
+
+Headline (BASELINE.json metric, config 2): W8A8 int8 GEMM, M=N=K=4096, RCR,
+per-token x per-channel dequant to bf16, TOPS and fraction of the int8 MFMA
+peak.  A "step" is one GEMM launch over the resident inputs.  The same JSON
+line carries the roofline of the dominant kernel, the CPU baseline (the
+oracle's restatement of the reference CPU path on a bounded row sample) and
+secondary figures (m=1 GEMV HBM GB/s, FP8 GEMM, grouped MoE, gather_rows).
+
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "int8/fp8 GEMM TOPS (% MFMA peak) at 4096³; m=1 GEMV HBM GB/s (% peak)"
+PEAK_INT8_TOPS = 5000.0     # MI355X dense int8 MFMA, TOP/s
+PEAK_FP8_TFLOPS = 5000.0    # MI355X dense fp8 MFMA, TFLOP/s
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E, GB/s
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def time_launches(fn, steps, warmup, stream):
+    """Average device time per launch (ms) from HIP events on `stream`."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        fn()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def cpu_cores():
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+def cpu_baseline_w8a8(a, w, sa, sw, budget_s=15.0):
+    """The oracle's W8A8 restatement on a bounded row sample, all host cores."""
+    from oracle import oracle as O
+    cores = cpu_cores()
+    t0 = time.perf_counter()
+    O.gemm_w8a8_bf16(a, w, sa, sw, rows=(0, cores), nthreads=cores)
+    dt = time.perf_counter() - t0
+    rows = int(max(cores, min(a.shape[0], cores * max(1, int(budget_s / max(dt, 1e-3))))))
+    t0 = time.perf_counter()
+    O.gemm_w8a8_bf16(a, w, sa, sw, rows=(0, rows), nthreads=cores)
+    dt = time.perf_counter() - t0
+    ops = 2.0 * rows * w.shape[0] * a.shape[1]
+    return {"value": round(ops / dt / 1e12, 6), "unit": "TOPS", "cores": cores, "kind": "port",
+            "sample": f"W8A8 4096^3 rows 0..{rows} of 4096 ({rows}x4096x4096, {dt:.1f} s), "
+                      "oracle/oracle.c bo_gemm_w8a8_rcr_bf16, OpenMP"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default="", help="run only: w8a8|gemv|fp8|moe|gather (profiling)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(see DESIGN.md for how the path would shard). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from baracuda_amd import plans as P
+    from oracle.inputs import w8a8
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    only = args.only
+    result = {}
+
+    # ---- headline: W8A8 4096^3 -------------------------------------------------
+    M = N = K = 4096
+    a, w, sa, sw = w8a8(M, N, K, seed=2)
+    da, dw = torch.from_numpy(a).to(dev), torch.from_numpy(w).to(dev)
+    dsa, dsw = torch.from_numpy(sa).to(dev), torch.from_numpy(sw).to(dev)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    plan = P.IntGemmPlan.select(P.IntGemmDescriptor(M, N, K, output=P.ElementKind.Bf16))
+    run = lambda: plan.run(da, dw, out, scale_a=dsa, scale_b=dsw, stream=stream)  # noqa: E731
+    ms = None
+    if only in ("", "w8a8"):
+        log("bench: w8a8 4096^3")
+        ms = time_launches(run, args.steps, args.warmup, stream)
+    ops = 2.0 * M * N * K
+    tops = ops / (ms * 1e-3) / 1e12 if ms else None
+
+    extra = {}
+    if not args.no_extra:
+        if only in ("", "gemv"):
+            log("bench: gemv_s8w m=1 14336x4096")
+            n, k = 14336, 4096
+            copies = 10   # 10 x 58.7 MB > 512 MB: defeats the 256 MB Infinity Cache
+            ws = [torch.randint(-127, 128, (n, k), dtype=torch.int8, device=dev) for _ in range(copies)]
+            scale = torch.rand(n, device=dev) * 0.009 + 0.001
+            x = torch.randn(k, device=dev).to(torch.bfloat16)
+            d = torch.empty(n, dtype=torch.bfloat16, device=dev)
+            gp = P.GemvS8wPlan.select(n, k)
+            it = [0]
+
+            def gemv():
+                gp.run(x, ws[it[0] % copies], scale, d, stream=stream)
+                it[0] += 1
+            gms = time_launches(gemv, 200, 20, stream)
+            nbytes = n * k + 2 * k + 4 * n + 2 * n
+            gbs = nbytes / (gms * 1e-3) / 1e9
+            extra["gemv_s8w_m1_14336x4096"] = {"us": round(gms * 1e3, 3), "GB_s": round(gbs, 1),
+                                               "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),
+                                               "bytes_per_call": nbytes, "weight_copies_rotated": copies}
+            del ws
+        if only in ("", "fp8"):
+            log("bench: fp8 2048x14336x4096")
+            m, n, k = 2048, 14336, 4096
+            fa = torch.randint(0, 256, (m, k), dtype=torch.uint8, device=dev)
+            fb = torch.randint(0, 256, (n, k), dtype=torch.uint8, device=dev)
+            fa[(fa & 0x7F) == 0x7F] = 0   # no NaN codes
+            fb[(fb & 0x7F) == 0x7F] = 0
+            fd = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+            fp = P.Fp8GemmPlan.select(P.Fp8GemmDescriptor(m, n, k, output=P.ElementKind.Bf16))
+            fms = time_launches(lambda: fp.run(fa, fb, fd, scale_a=0.01, scale_b=0.02, stream=stream),
+                                20, 5, stream)
+            tf = 2.0 * m * n * k / (fms * 1e-3) / 1e12
+            extra["fp8_e4m3_gemm_2048x14336x4096"] = {"us": round(fms * 1e3, 2), "TFLOPS": round(tf, 1),
+                                                      "frac_fp8_peak": round(tf / PEAK_FP8_TFLOPS, 4)}
+            del fa, fb, fd
+        if only in ("", "moe"):
+            log("bench: moe grouped int8")
+            from oracle.inputs import moe_routing
+            tokens, E, topk, n, k = 4096, 8, 2, 14336, 4096
+            sid, eid = moe_routing(tokens, E, topk, seed=5)
+            mx = torch.randint(-127, 128, (tokens, k), dtype=torch.int8, device=dev)
+            mw = torch.randint(-127, 128, (E, n, k), dtype=torch.int8, device=dev)
+            msa = torch.rand(tokens, device=dev) * 0.015 + 0.005
+            msw = torch.rand(E * n, device=dev) * 0.009 + 0.001
+            mo = torch.empty((tokens * topk, n), dtype=torch.bfloat16, device=dev)
+            cnt = torch.empty(E, dtype=torch.int32, device=dev)
+            off = torch.empty(E + 1, dtype=torch.int32, device=dev)
+            dsid, deid = torch.from_numpy(sid).to(dev), torch.from_numpy(eid).to(dev)
+            mp = P.MoeS8GroupedPlan.select(E, topk, tokens * topk, n, k)
+            mms = time_launches(lambda: mp.run(mx, mw, dsid, deid, mo, cnt, off, msa, msw, stream=stream),
+                                10, 3, stream)
+            mt = 2.0 * tokens * topk * n * k / (mms * 1e-3) / 1e12
+            extra["moe_s8_grouped_e8_top2_4096x14336x4096"] = {
+                "us": round(mms * 1e3, 1), "TOPS": round(mt, 1), "frac_int8_peak": round(mt / PEAK_INT8_TOPS, 4),
+                "expert_rows": np.bincount(eid, minlength=E).tolist()}
+            del mx, mw, mo
+        if only in ("", "gather"):
+            log("bench: gather_rows bf16")
+            V, H = 128256, 4096
+            table = torch.empty((V, H), dtype=torch.bfloat16, device=dev).normal_(0, 0.02)
+            g = {}
+            for nr in (1, 8, 64):
+                idx = torch.randint(0, V, (nr,), dtype=torch.int32, device=dev).view(torch.uint32)
+                dst = torch.empty((nr, H), dtype=torch.bfloat16, device=dev)
+                gms = time_launches(lambda: P.gather_rows(dst, table, idx, stream=stream), 200, 20, stream)
+                nb = 2 * nr * H * 2 + 4 * nr
+                g[f"n{nr}"] = {"us": round(gms * 1e3, 2), "GB_s": round(nb / (gms * 1e-3) / 1e9, 1)}
+            extra["gather_rows_bf16_128256x4096"] = g
+            del table
+
+    cpu = None
+    if not args.no_cpu and ms is not None:
+        log("bench: cpu baseline")
+        cpu = cpu_baseline_w8a8(a, w, sa, sw)
+
+    result = {
+        "metric": METRIC,
+        "value": round(tops, 2) if tops else None,
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5) if ms else None,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded PCG64 int8 U[-127,127], scales U per BASELINE config 2)",
+        "config": {"workload": "W8A8 int8 GEMM M=N=K=4096, RCR, per-token x per-channel f32 scales, "
+                               "int32 acc, bf16 out (BASELINE config 2)",
+                   "m": M, "n": N, "k": K, "layout": "rcr", "out": "bf16"},
+        "roofline": None if not ms else {
+            "bound": "mfma", "achieved": round(tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
+            "frac": round(tops / PEAK_INT8_TOPS, 4), "traffic": None,
+            "kernel": "gemm_s8_rcr_kernel<EPI_W8A8_BF16> (int8 tera-ops per second)"},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,187 @@
+/*
+ * baracuda_kernels.h -- C ABI of the MI355X (gfx950) quantized-inference
+ * contraction path: a drop-in for the corresponding baracuda-kernels-sys
+ * entry points.
+ *
+ * Conventions (crates/baracuda-kernels-sys/src/lib.rs:10-27, ARCHITECTURE.md:253-375
+ * of the reference):
+ *   - status: 0 ok, 1 misaligned, 2 invalid problem, 3 unsupported,
+ *             4 workspace too small, 5 launch failure;
+ *   - all pointers are device pointers owned by the caller; nothing here
+ *     allocates, frees, memsets or synchronises, so every _run can be
+ *     captured into a hipGraph;
+ *   - `stream` is a hipStream_t passed as void* (NULL = default stream);
+ *   - strides and leading dimensions are in elements;
+ *   - workspace is accepted for signature parity and is never required
+ *     (every _workspace_size returns 0).
+ *
+ * Each declaration cites the reference entry point it replaces
+ * (paths relative to the baracuda repository root).
+ */
+#ifndef BARACUDA_KERNELS_GFX950_H
+#define BARACUDA_KERNELS_GFX950_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ======================= int8 GEMM, RCR layout ===========================
+ * A row-major [M,K] (lda), B column-major [K,N] = row-major [N,K] (ldb),
+ * int32 accumulator (wraps mod 2^32; equals the reference's saturating
+ * accumulator whenever |acc| < 2^31, e.g. |a|,|b| <= 127 and K < 133143). */
+
+/* Replaces baracuda_kernels_gemm_s8_rcr_sm80_{run,workspace_size,can_implement}
+ * (crates/baracuda-kernels-sys/src/cutlass_reexport.rs:661-666,
+ *  crates/baracuda-cutlass-kernels-sys/kernels/gemm_s8_rcr_sm80.cu:169-198):
+ * D = sat_s8(rne(alpha*acc + beta*C)); C may be NULL when beta == 0. */
+int32_t baracuda_kernels_gemm_s8_rcr_gfx950_run(
+    int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,
+    const void *c, int64_t ldc, void *d, int64_t ldd, float alpha, float beta,
+    void *workspace, size_t workspace_bytes, void *stream);
+size_t baracuda_kernels_gemm_s8_rcr_gfx950_workspace_size(int32_t m, int32_t n, int32_t k);
+int32_t baracuda_kernels_gemm_s8_rcr_gfx950_can_implement(
+    int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,
+    const void *c, int64_t ldc, void *d, int64_t ldd);
+
+/* New SKU (same family): D = acc as int32 [M,N] (ldd).  The plain int8
+ * contraction of kernelgen's oracle (crates/baracuda-kernelgen/src/oracle.rs:1289-1372)
+ * evaluated on the device. */
+int32_t baracuda_kernels_gemm_s8_rcr_gfx950_i32_run(
+    int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,
+    void *d, int64_t ldd, void *workspace, size_t workspace_bytes, void *stream);
+size_t baracuda_kernels_gemm_s8_rcr_gfx950_i32_workspace_size(int32_t m, int32_t n, int32_t k);
+int32_t baracuda_kernels_gemm_s8_rcr_gfx950_i32_can_implement(
+    int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,
+    const void *d, int64_t ldd);
+
+/* New SKU: W8A8 per-token x per-channel dequant to bf16,
+ * D[m,n] = bf16_rne((scale_a[m] * scale_b[n]) * (float)acc), the
+ * quantized_linear_w8a8 epilogue order
+ * (crates/baracuda-kernels-sys/kernels/include/baracuda_quantize_compose.cuh:265-274). */
+int32_t baracuda_kernels_gemm_w8a8_rcr_gfx950_bf16_run(
+    int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,
+    const float *scale_a, const float *scale_b, void *d, int64_t ldd,
+    void *workspace, size_t workspace_bytes, void *stream);
+size_t baracuda_kernels_gemm_w8a8_rcr_gfx950_bf16_workspace_size(int32_t m, int32_t n, int32_t k);
+int32_t baracuda_kernels_gemm_w8a8_rcr_gfx950_bf16_can_implement(
+    int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,
+    const void *scale_a, const void *scale_b, const void *d, int64_t ldd);
+
+/* Replaces baracuda_kernels_quantized_linear_w8a8_f32_{run,can_implement}
+ * (baracuda_quantize_compose.cuh:340-370, crates/baracuda-kernels-sys/src/lib.rs:64915,64963):
+ * output[M,C_out] f32 = scale_a[m]*scale_w[c]*acc, weight [C_out,K], act [M,K]. */
+int32_t baracuda_kernels_quantized_linear_w8a8_f32_gfx950_run(
+    int32_t M, int32_t C_out, int32_t K, const void *weight_q, const void *act_q,
+    const void *scale_a, const void *scale_w, void *output,
+    void *workspace, size_t workspace_bytes, void *stream);
+int32_t baracuda_kernels_quantized_linear_w8a8_f32_gfx950_can_implement(
+    int32_t M, int32_t C_out, int32_t K, const void *weight_q, const void *act_q,
+    const void *scale_a, const void *scale_w, const void *output);
+
+/* ======================= FP8 e4m3 GEMM, RCR layout ======================
+ * OCP e4m3 (e4m3fn) operands, f32 accumulator. */
+
+/* Replaces baracuda_kernels_gemm_fp8_e4m3_rcr_sm89_{run,workspace_size,can_implement}
+ * (crates/baracuda-kernels-sys/kernels/gemm/gemm_fp8_e4m3_rcr_sm89.cu:31-67):
+ * D = sat_e4m3(rne(alpha*acc + beta*dequant(C))). */
+int32_t baracuda_kernels_gemm_fp8_e4m3_rcr_gfx950_run(
+    int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,
+    const void *c, int64_t ldc, void *d, int64_t ldd, float alpha, float beta,
+    void *workspace, size_t workspace_bytes, void *stream);
+size_t baracuda_kernels_gemm_fp8_e4m3_rcr_gfx950_workspace_size(int32_t m, int32_t n, int32_t k);
+int32_t baracuda_kernels_gemm_fp8_e4m3_rcr_gfx950_can_implement(
+    int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,
+    const void *c, int64_t ldc, const void *d, int64_t ldd);
+
+/* New SKU: per-tensor scales, bf16 out: D = bf16_rne((scale_a*scale_b) * acc). */
+int32_t baracuda_kernels_gemm_fp8_e4m3_rcr_gfx950_bf16_run(
+    int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,
+    float scale_a, float scale_b, void *d, int64_t ldd,
+    void *workspace, size_t workspace_bytes, void *stream);
+size_t baracuda_kernels_gemm_fp8_e4m3_rcr_gfx950_bf16_workspace_size(int32_t m, int32_t n, int32_t k);
+int32_t baracuda_kernels_gemm_fp8_e4m3_rcr_gfx950_bf16_can_implement(
+    int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,
+    const void *d, int64_t ldd);
+
+/* New SKU: f32 out, D = alpha * acc (exposes the f32 accumulator). */
+int32_t baracuda_kernels_gemm_fp8_e4m3_rcr_gfx950_f32_run(
+    int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,
+    float alpha, void *d, int64_t ldd, void *workspace, size_t workspace_bytes, void *stream);
+size_t baracuda_kernels_gemm_fp8_e4m3_rcr_gfx950_f32_workspace_size(int32_t m, int32_t n, int32_t k);
+int32_t baracuda_kernels_gemm_fp8_e4m3_rcr_gfx950_f32_can_implement(
+    int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,
+    const void *d, int64_t ldd);
+
+/* ======================= m = 1 decode GEMV ===============================*/
+
+/* Replaces baracuda_kernels_gemv_dense_m1_{f32,f16,bf16}_{run,can_implement,workspace_size}
+ * (crates/baracuda-kernels-sys/kernels/gemm/gemv_dense.cu:235-342), same ABI:
+ * D[g,0,:] = alpha*A[g,0,:]·B[g] + beta*D[g,0,:], RRR (layout 0), f32 accumulate,
+ * stride_b == 0 broadcasts B, beta == 0 never reads D. */
+#define BK_GEMV_DENSE_DECL(TAG)                                                                  \
+    int32_t baracuda_kernels_gemv_dense_m1_##TAG##_run(                                          \
+        int32_t m, int32_t n, int32_t k, int32_t batch, int32_t layout, float alpha, float beta, \
+        const void *a, int64_t lda, int64_t stride_a, const void *b, int64_t ldb,                \
+        int64_t stride_b, void *d, int64_t ldd, int64_t stride_d, void *workspace,               \
+        size_t workspace_bytes, void *stream);                                                   \
+    int32_t baracuda_kernels_gemv_dense_m1_##TAG##_can_implement(                                \
+        int32_t m, int32_t n, int32_t k, int32_t batch, int32_t layout, int64_t lda,             \
+        int64_t ldb, int64_t ldd, int64_t stride_a, int64_t stride_b, int64_t stride_d);        \
+    size_t baracuda_kernels_gemv_dense_m1_##TAG##_workspace_size(                                \
+        int32_t m, int32_t n, int32_t k, int32_t batch, int32_t layout);
+BK_GEMV_DENSE_DECL(f32)
+BK_GEMV_DENSE_DECL(f16)
+BK_GEMV_DENSE_DECL(bf16)
+#undef BK_GEMV_DENSE_DECL
+
+/* New SKU (gemv_dense_m1 family): int8 weight-only decode GEMV,
+ * d[n] = bf16_rne(scale[n] * sum_k x[k]*w[n,k]), w [N,K] int8 (ldw), x bf16 [K],
+ * scale f32 [N], f32 accumulate in a fixed order (bit-identical replays). */
+int32_t baracuda_kernels_gemv_s8w_m1_bf16_gfx950_run(
+    int32_t n, int32_t k, const void *x, const void *w, int64_t ldw, const void *scale, void *d,
+    void *workspace, size_t workspace_bytes, void *stream);
+size_t baracuda_kernels_gemv_s8w_m1_bf16_gfx950_workspace_size(int32_t n, int32_t k);
+int32_t baracuda_kernels_gemv_s8w_m1_bf16_gfx950_can_implement(int32_t n, int32_t k, int64_t ldw);
+
+/* ======================= gather_rows =====================================
+ * Replaces baracuda_kernels_gather_rows_{f16,bf16,f32}_{run,can_implement,workspace_size}
+ * (crates/baracuda-kernels-sys/kernels/indexing/gather_rows.cu:122-148), same ABI:
+ * dest[r,:] = table[idx[r],:], idx u32, idx >= V writes zeros. */
+#define BK_GATHER_DECL(TAG)                                                                      \
+    int32_t baracuda_kernels_gather_rows_##TAG##_run(void *dest, const void *table,              \
+                                                     const void *idx, int64_t V, int64_t H,      \
+                                                     int64_t n, void *stream);                   \
+    int32_t baracuda_kernels_gather_rows_##TAG##_can_implement(int64_t V, int64_t H, int64_t n); \
+    size_t baracuda_kernels_gather_rows_##TAG##_workspace_size(int64_t V, int64_t H, int64_t n);
+BK_GATHER_DECL(f16)
+BK_GATHER_DECL(bf16)
+BK_GATHER_DECL(f32)
+#undef BK_GATHER_DECL
+
+/* ======================= grouped MoE int8 GEMM ===========================
+ * New SKU in the moe_wmma family; argument order of
+ * baracuda_kernels_moe_wmma_bf16_run (crates/baracuda-kernels-sys/kernels/moe/moe_wmma.cu:154-175)
+ * plus scale_a [tokens] and scale_w [E*N].  Routing: pairs grouped by expert
+ * through sorted_token_ids / expert_ids; input row = id / topk (id when
+ * topk_weights != NULL); output row = id; expert_counts [E] and
+ * expert_offsets [E+1] are caller buffers filled by the call.
+ * out[id,n] = bf16_rne(((scale_a[in_row]*scale_w[e*N+n]) * acc) [* topk_weights[id]]). */
+int32_t baracuda_kernels_moe_s8_grouped_bf16_gfx950_run(
+    const void *input, const void *weights, const int32_t *sorted_token_ids,
+    const int32_t *expert_ids, const float *topk_weights, void *output,
+    int32_t *expert_counts, int32_t *expert_offsets, int32_t num_experts, int32_t topk,
+    int32_t size_m, int32_t size_n, int32_t size_k, const float *scale_a, const float *scale_w,
+    void *workspace, size_t workspace_bytes, void *stream);
+int32_t baracuda_kernels_moe_s8_grouped_bf16_gfx950_can_implement(
+    int32_t num_experts, int32_t topk, int32_t size_m, int32_t size_n, int32_t size_k);
+size_t baracuda_kernels_moe_s8_grouped_bf16_gfx950_workspace_size(
+    int32_t num_experts, int32_t topk, int32_t size_m, int32_t size_n, int32_t size_k);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BARACUDA_KERNELS_GFX950_H */

@@ -1,0 +1,121 @@
+/*
+ * oracle.h -- CPU restatement of baracuda's reference arithmetic for the
+ * quantized-inference contraction path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the parity checker: only
+ * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load
+ * it.  The product (baracuda_amd/, libbaracuda_kernels.so) never links or
+ * calls it.
+ *
+ * Every function cites the reference file:line whose behaviour it restates
+ * (paths relative to the baracuda repository root).  How each function is
+ * pinned (golden vectors, closed forms, library cross-checks) is recorded in
+ * tests/test_oracle.py next to the pin itself.
+ */
+#ifndef BARACUDA_ORACLE_H
+#define BARACUDA_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- scalar codecs ----------------------------------------------------- */
+uint16_t bo_f32_to_bf16_bits(float x);
+float    bo_bf16_bits_to_f32(uint16_t b);
+uint16_t bo_f32_to_f16_bits(float x);
+float    bo_f16_bits_to_f32(uint16_t h);
+float    bo_e4m3_to_f32(uint8_t b);
+uint8_t  bo_f32_to_e4m3_satfinite(float x);
+int32_t  bo_f64_to_i32_as(double f);     /* Rust `f as i32` (saturating, NaN->0) */
+int8_t   bo_sat_cast_s8(float x);        /* RNE + clamp to [-128,127]            */
+
+/* ---- contractions ------------------------------------------------------ */
+/* oracle.rs eval_contraction restated for int8 operands read as I32:
+ * out[m*ldo+n] = (i32)( sum_{k ascending} (f64)a[m*sa0+k*sa1] * (f64)b[k*sb0+n*sb1] ) */
+void bo_contraction_s8_i32(int64_t m, int64_t n, int64_t k,
+                           const int8_t *a, int64_t sa0, int64_t sa1,
+                           const int8_t *b, int64_t sb0, int64_t sb1,
+                           int32_t *out, int64_t ldo);
+/* Same over f64 operands (the oracle's own hand-computed test uses f32/f64). */
+void bo_contraction_f64(int64_t m, int64_t n, int64_t k,
+                        const double *a, int64_t sa0, int64_t sa1,
+                        const double *b, int64_t sb0, int64_t sb1,
+                        double *out, int64_t ldo);
+
+/* int32 RCR accumulator, exact integer arithmetic (int64 sum).  Rows
+ * [row0,row1) only, so a bounded sample can be timed. nthreads<=1 = serial. */
+void bo_gemm_s8_rcr_i32(int64_t m, int64_t n, int64_t k,
+                        const int8_t *a, int64_t lda,
+                        const int8_t *b, int64_t ldb,
+                        int32_t *d, int64_t ldd,
+                        int64_t row0, int64_t row1, int nthreads);
+
+/* int8 GEMM with the int8-out epilogue of cpu_int_gemm_rcr:
+ * z = alpha*(f32)acc + beta*(f32)C ; D = sat_cast_s8(z).  c may be NULL. */
+void bo_gemm_s8_rcr_s8(int64_t m, int64_t n, int64_t k,
+                       const int8_t *a, int64_t lda,
+                       const int8_t *b, int64_t ldb,
+                       const int8_t *c, int64_t ldc,
+                       int8_t *d, int64_t ldd,
+                       float alpha, float beta);
+
+/* W8A8: out = bf16( (sa[m]*sw[n]) * (f32)acc ) with f32 products. */
+void bo_gemm_w8a8_rcr_bf16(int64_t m, int64_t n, int64_t k,
+                           const int8_t *a, int64_t lda,
+                           const int8_t *w, int64_t ldw,
+                           const float *sa, const float *sw,
+                           uint16_t *d, int64_t ldd,
+                           int64_t row0, int64_t row1, int nthreads);
+
+/* FP8 e4m3 RCR: acc = sum_k dec(a)*dec(b) in f64 (exact reference value),
+ * written as f64; callers derive bf16 / e4m3 / f32 outputs from it. */
+void bo_gemm_fp8_e4m3_rcr_f64(int64_t m, int64_t n, int64_t k,
+                              const uint8_t *a, int64_t lda,
+                              const uint8_t *b, int64_t ldb,
+                              double *acc, int64_t ldacc,
+                              int64_t row0, int64_t row1, int nthreads);
+/* The reference smoke test's own f32 K-ascending accumulation. */
+void bo_gemm_fp8_e4m3_rcr_f32(int64_t m, int64_t n, int64_t k,
+                              const uint8_t *a, int64_t lda,
+                              const uint8_t *b, int64_t ldb,
+                              float *acc, int64_t ldacc);
+
+/* gemv_dense_m1 f64 reference (RRR):
+ * D[g,j] = alpha*sum_k A[g,k]*B[g,k,j] + beta*Dinit[g,j] */
+void bo_gemv_dense_m1_f64(int64_t n, int64_t k, int64_t batch,
+                          const double *a, int64_t stride_a,
+                          const double *b, int64_t ldb, int64_t stride_b,
+                          const double *d_init, double *d, int64_t stride_d,
+                          double alpha, double beta);
+
+/* int8 weight-only m=1 GEMV: acc[n] = sum_k x[k]*w[n,k] (f64), out in f64
+ * before scale; caller applies scale/bf16. x given as bf16 bits. */
+void bo_gemv_s8w_m1_f64(int64_t n, int64_t k,
+                        const uint16_t *x_bf16, const int8_t *w, int64_t ldw,
+                        double *acc, int nthreads);
+
+/* gather_rows: dest[r,:] = table[idx[r],:], zero when idx[r] >= V.
+ * elem_size in bytes (2 or 4). */
+void bo_gather_rows(void *dest, const void *table, const uint32_t *idx,
+                    int64_t V, int64_t H, int64_t n, int64_t elem_size);
+
+/* MoE routing helpers (baracuda_moe.cuh:1121-1162). */
+void bo_moe_expert_offsets(const int32_t *expert_ids, int64_t size_m,
+                           int32_t num_experts, int32_t *counts,
+                           int32_t *offsets);
+/* Grouped int8 expert GEMM, int32 accumulators, row = sorted pair:
+ *   for each segment e, pair p in it: tok = sorted_token_ids[p],
+ *   in_row = tok / topk ; acc[tok, n] = sum_k x[in_row,k]*w[e,n,k]. */
+void bo_moe_s8_grouped_i32(const int8_t *x, const int8_t *w,
+                           const int32_t *sorted_token_ids,
+                           const int32_t *offsets, int32_t num_experts,
+                           int32_t topk, int64_t size_m, int64_t n,
+                           int64_t k, int32_t *acc_out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,233 @@
+"""ctypes/numpy front end of the CPU parity oracle (liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, never by the product (baracuda_amd/).
+Each function forwards to the C restatement in oracle.c, which cites the
+reference file:line it follows.  ``build()`` compiles liboracle.so with gcc.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "liboracle.so"
+_lib = None
+
+
+def build() -> Path:
+    subprocess.run(["make", "-s", "-C", str(HERE), "-B", "liboracle.so"], check=True)
+    return LIB_PATH
+
+
+def _L():
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        _lib = C.CDLL(str(LIB_PATH))
+        vp, i64, f32, f64, i32 = C.c_void_p, C.c_int64, C.c_float, C.c_double, C.c_int
+        sig = {
+            "bo_f32_to_bf16_bits": (C.c_uint16, [f32]),
+            "bo_bf16_bits_to_f32": (f32, [C.c_uint16]),
+            "bo_f32_to_f16_bits": (C.c_uint16, [f32]),
+            "bo_f16_bits_to_f32": (f32, [C.c_uint16]),
+            "bo_e4m3_to_f32": (f32, [C.c_uint8]),
+            "bo_f32_to_e4m3_satfinite": (C.c_uint8, [f32]),
+            "bo_f64_to_i32_as": (C.c_int32, [f64]),
+            "bo_sat_cast_s8": (C.c_int8, [f32]),
+            "bo_contraction_s8_i32": (None, [i64, i64, i64, vp, i64, i64, vp, i64, i64, vp, i64]),
+            "bo_contraction_f64": (None, [i64, i64, i64, vp, i64, i64, vp, i64, i64, vp, i64]),
+            "bo_gemm_s8_rcr_i32": (None, [i64, i64, i64, vp, i64, vp, i64, vp, i64, i64, i64, i32]),
+            "bo_gemm_s8_rcr_s8": (None, [i64, i64, i64, vp, i64, vp, i64, vp, i64, vp, i64, f32, f32]),
+            "bo_gemm_w8a8_rcr_bf16": (None, [i64, i64, i64, vp, i64, vp, i64, vp, vp, vp, i64, i64, i64, i32]),
+            "bo_gemm_fp8_e4m3_rcr_f64": (None, [i64, i64, i64, vp, i64, vp, i64, vp, i64, i64, i64, i32]),
+            "bo_gemm_fp8_e4m3_rcr_f32": (None, [i64, i64, i64, vp, i64, vp, i64, vp, i64]),
+            "bo_gemv_dense_m1_f64": (None, [i64, i64, i64, vp, i64, vp, i64, i64, vp, vp, i64, f64, f64]),
+            "bo_gemv_s8w_m1_f64": (None, [i64, i64, vp, vp, i64, vp, i32]),
+            "bo_gather_rows": (None, [vp, vp, vp, i64, i64, i64, i64]),
+            "bo_moe_expert_offsets": (None, [vp, i64, C.c_int32, vp, vp]),
+            "bo_moe_s8_grouped_i32": (None, [vp, vp, vp, vp, C.c_int32, C.c_int32, i64, i64, i64, vp]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(_lib, name)
+            fn.restype, fn.argtypes = res, args
+    return _lib
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data
+
+
+# ---- scalar codecs, vectorised over numpy arrays ---------------------------
+def f32_to_bf16_bits(x) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    f = _L().bo_f32_to_bf16_bits
+    return np.array([f(float(v)) for v in x.ravel()], dtype=np.uint16).reshape(x.shape)
+
+
+def bf16_bits_to_f32(b) -> np.ndarray:
+    b = np.asarray(b, dtype=np.uint16)
+    return (b.astype(np.uint32) << 16).view(np.float32)
+
+
+def e4m3_table() -> np.ndarray:
+    f = _L().bo_e4m3_to_f32
+    return np.array([f(i) for i in range(256)], dtype=np.float32)
+
+
+def e4m3_to_f32(b) -> np.ndarray:
+    return e4m3_table()[np.asarray(b, dtype=np.uint8)]
+
+
+def f32_to_e4m3(x) -> np.ndarray:
+    x = np.asarray(x, dtype=np.float32)
+    f = _L().bo_f32_to_e4m3_satfinite
+    return np.array([f(float(v)) for v in x.ravel()], dtype=np.uint8).reshape(x.shape)
+
+
+def f32_to_bf16_bits_fast(x) -> np.ndarray:
+    """Vectorised restatement of the same RNE rule (checked against the C one)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+# ---- contractions -----------------------------------------------------------
+def contraction_s8_i32(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """oracle.rs eval_contraction: a [M,K] (any strides), b [K,N] (any strides)."""
+    a = np.asarray(a, dtype=np.int8)
+    b = np.asarray(b, dtype=np.int8)
+    m, k = a.shape
+    n = b.shape[1]
+    out = np.zeros((m, n), dtype=np.int32)
+    sa = [s // a.itemsize for s in a.strides]
+    sb = [s // b.itemsize for s in b.strides]
+    _L().bo_contraction_s8_i32(m, n, k, _p(a), sa[0], sa[1], _p(b), sb[0], sb[1], _p(out), n)
+    return out
+
+
+def contraction_f64(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    a = np.asarray(a, dtype=np.float64)
+    b = np.asarray(b, dtype=np.float64)
+    m, k = a.shape
+    n = b.shape[1]
+    out = np.zeros((m, n), dtype=np.float64)
+    _L().bo_contraction_f64(m, n, k, _p(a), a.strides[0] // 8, a.strides[1] // 8,
+                            _p(b), b.strides[0] // 8, b.strides[1] // 8, _p(out), n)
+    return out
+
+
+def gemm_s8_rcr_i32(a, b, rows=None, nthreads=1) -> np.ndarray:
+    """A [M,K] int8, B [N,K] int8 (col-major [K,N]); returns acc int32 [len(rows), N]."""
+    a = np.ascontiguousarray(a, dtype=np.int8)
+    b = np.ascontiguousarray(b, dtype=np.int8)
+    m, k = a.shape
+    n = b.shape[0]
+    r0, r1 = rows if rows is not None else (0, m)
+    out = np.zeros((m, n), dtype=np.int32)
+    _L().bo_gemm_s8_rcr_i32(m, n, k, _p(a), k, _p(b), k, _p(out), n, r0, r1, nthreads)
+    return out[r0:r1]
+
+
+def gemm_s8_rcr_s8(a, b, alpha, beta=0.0, c=None) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.int8)
+    b = np.ascontiguousarray(b, dtype=np.int8)
+    m, k = a.shape
+    n = b.shape[0]
+    d = np.zeros((m, n), dtype=np.int8)
+    cp = None if c is None else np.ascontiguousarray(c, dtype=np.int8)
+    _L().bo_gemm_s8_rcr_s8(m, n, k, _p(a), k, _p(b), k, None if cp is None else _p(cp), n,
+                           _p(d), n, alpha, beta)
+    return d
+
+
+def gemm_w8a8_bf16(a, w, sa, sw, rows=None, nthreads=1) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.int8)
+    w = np.ascontiguousarray(w, dtype=np.int8)
+    sa = np.ascontiguousarray(sa, dtype=np.float32)
+    sw = np.ascontiguousarray(sw, dtype=np.float32)
+    m, k = a.shape
+    n = w.shape[0]
+    r0, r1 = rows if rows is not None else (0, m)
+    d = np.zeros((m, n), dtype=np.uint16)
+    _L().bo_gemm_w8a8_rcr_bf16(m, n, k, _p(a), k, _p(w), k, _p(sa), _p(sw), _p(d), n, r0, r1, nthreads)
+    return d[r0:r1]
+
+
+def gemm_fp8_e4m3_f64(a_bits, b_bits, rows=None, nthreads=1) -> np.ndarray:
+    a = np.ascontiguousarray(a_bits, dtype=np.uint8)
+    b = np.ascontiguousarray(b_bits, dtype=np.uint8)
+    m, k = a.shape
+    n = b.shape[0]
+    r0, r1 = rows if rows is not None else (0, m)
+    acc = np.zeros((m, n), dtype=np.float64)
+    _L().bo_gemm_fp8_e4m3_rcr_f64(m, n, k, _p(a), k, _p(b), k, _p(acc), n, r0, r1, nthreads)
+    return acc[r0:r1]
+
+
+def gemm_fp8_e4m3_f32(a_bits, b_bits) -> np.ndarray:
+    a = np.ascontiguousarray(a_bits, dtype=np.uint8)
+    b = np.ascontiguousarray(b_bits, dtype=np.uint8)
+    m, k = a.shape
+    n = b.shape[0]
+    acc = np.zeros((m, n), dtype=np.float32)
+    _L().bo_gemm_fp8_e4m3_rcr_f32(m, n, k, _p(a), k, _p(b), k, _p(acc), n)
+    return acc
+
+
+def gemv_dense_m1_f64(a, b, d_init, n, k, batch, stride_a, ldb, stride_b, stride_d, alpha, beta):
+    a = np.ascontiguousarray(a, dtype=np.float64)
+    b = np.ascontiguousarray(b, dtype=np.float64)
+    d_init = np.ascontiguousarray(d_init, dtype=np.float64)
+    d = d_init.copy()
+    _L().bo_gemv_dense_m1_f64(n, k, batch, _p(a), stride_a, _p(b), ldb, stride_b, _p(d_init), _p(d),
+                              stride_d, alpha, beta)
+    return d
+
+
+def gemv_s8w_m1_f64(x_bf16_bits, w, nthreads=1) -> np.ndarray:
+    x = np.ascontiguousarray(x_bf16_bits, dtype=np.uint16)
+    w = np.ascontiguousarray(w, dtype=np.int8)
+    n, k = w.shape
+    acc = np.zeros(n, dtype=np.float64)
+    _L().bo_gemv_s8w_m1_f64(n, k, _p(x), _p(w), k, _p(acc), nthreads)
+    return acc
+
+
+def gather_rows(table: np.ndarray, idx: np.ndarray) -> np.ndarray:
+    table = np.ascontiguousarray(table)
+    idx = np.ascontiguousarray(idx, dtype=np.uint32)
+    V, H = table.shape
+    dest = np.full((idx.size, H), 0x5A, dtype=np.uint8).view(table.dtype).reshape(idx.size, H) \
+        if table.dtype.itemsize == 1 else np.empty((idx.size, H), dtype=table.dtype)
+    _L().bo_gather_rows(_p(dest), _p(table), _p(idx), V, H, idx.size, table.dtype.itemsize)
+    return dest
+
+
+def moe_expert_offsets(expert_ids: np.ndarray, num_experts: int):
+    e = np.ascontiguousarray(expert_ids, dtype=np.int32)
+    counts = np.zeros(num_experts, dtype=np.int32)
+    offs = np.zeros(num_experts + 1, dtype=np.int32)
+    _L().bo_moe_expert_offsets(_p(e), e.size, num_experts, _p(counts), _p(offs))
+    return counts, offs
+
+
+def moe_s8_grouped_i32(x, w, sorted_ids, offsets, topk, size_m) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.int8)
+    w = np.ascontiguousarray(w, dtype=np.int8)
+    s = np.ascontiguousarray(sorted_ids, dtype=np.int32)
+    o = np.ascontiguousarray(offsets, dtype=np.int32)
+    E, n, k = w.shape
+    acc = np.zeros((size_m, n), dtype=np.int32)
+    _L().bo_moe_s8_grouped_i32(_p(x), _p(w), _p(s), _p(o), E, topk, size_m, n, k, _p(acc))
+    return acc
+
+
+def scalar(name):
+    return getattr(_L(), name)

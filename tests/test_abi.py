@@ -1,0 +1,114 @@
+"""C-ABI boundary checks that need no GPU: every declared symbol is exported
+with the declared name, and the host-side validation (can_implement /
+workspace_size / empty problems / Plan.select) behaves like the reference."""
+import re
+from pathlib import Path
+
+import pytest
+
+from baracuda_amd import ffi
+from baracuda_amd import plans as P
+
+HDR = Path(__file__).resolve().parents[1] / "include" / "baracuda_kernels.h"
+
+
+def _declared():
+    text = re.sub(r"/\*.*?\*/", "", HDR.read_text(), flags=re.S)
+    names = set(re.findall(r"\b(baracuda_kernels_\w+)\s*\(", text))
+    for tag_macro, body in (("BK_GEMV_DENSE_DECL", "gemv_dense_m1"), ("BK_GATHER_DECL", "gather_rows")):
+        for tag in re.findall(tag_macro + r"\((\w+)\)", text):
+            for suf in ("run", "can_implement", "workspace_size"):
+                names.add(f"baracuda_kernels_{body}_{tag}_{suf}")
+    return {n for n in names if "_TAG_" not in n}
+
+
+def test_header_and_binding_agree():
+    assert _declared() == set(ffi.SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ffi.lib()
+    import ctypes
+    dll = ctypes.CDLL(str(lib.path))
+    for name in _declared():
+        assert hasattr(dll, name), name
+
+
+def test_gemv_can_implement_rejection_table():
+    # gemv_dense_smoke.rs:401-432, same argument tuples and expectations.
+    L = ffi.lib()
+    for tag in ("f32", "f16", "bf16"):
+        can = getattr(L, f"gemv_dense_m1_{tag}_can_implement")
+        assert can(1, 6, 4, 1, 0, 4, 6, 6, 0, 0, 0) == 0
+        assert can(2, 6, 4, 1, 0, 4, 6, 6, 0, 0, 0) == 2
+        assert can(1, 6, 4, 1, 1, 4, 6, 6, 0, 0, 0) == 2
+        assert can(1, 6, 4, 1, 0, 3, 6, 6, 0, 0, 0) == 2
+        assert can(1, 6, 4, 1, 0, 4, 5, 6, 0, 0, 0) == 2
+        assert can(1, 6, 4, 1, 0, 4, 6, 5, 0, 0, 0) == 2
+        assert can(1, 6, 4, 2, 0, 4, 6, 6, 0, 0, 0) == 2
+        assert can(1, 6, 4, 2, 0, 4, 6, 6, 4, 0, 6) == 0
+        assert can(1, -1, 4, 1, 0, 4, 6, 6, 0, 0, 0) == 2
+        assert getattr(L, f"gemv_dense_m1_{tag}_workspace_size")(1, 6, 4, 1, 0) == 0
+
+
+def test_gemv_empty_problem_returns_ok_without_launch():
+    # gemv_dense.cu:190: m == 0 / n == 0 / batch == 0 -> 0, no launch, null pointers allowed.
+    L = ffi.lib()
+    assert L.gemv_dense_m1_f32_run(0, 6, 4, 1, 0, 1.0, 0.0, None, 4, 0, None, 6, 0, None, 6, 0, None, 0, None) == 0
+    assert L.gemv_dense_m1_bf16_run(1, 0, 4, 1, 0, 1.0, 0.0, None, 4, 0, None, 1, 0, None, 1, 0, None, 0, None) == 0
+    assert L.gemv_s8w_m1_bf16_gfx950_run(0, 4096, None, None, 4096, None, None, None, 0, None) == 0
+
+
+def test_gather_can_implement_and_empty():
+    L = ffi.lib()
+    for tag in ("f32", "f16", "bf16"):
+        assert getattr(L, f"gather_rows_{tag}_can_implement")(3, 4, 1) == 0
+        assert getattr(L, f"gather_rows_{tag}_can_implement")(0, 4, 1) == 2
+        assert getattr(L, f"gather_rows_{tag}_can_implement")(3, 4, -1) == 2
+        assert getattr(L, f"gather_rows_{tag}_workspace_size")(3, 4, 1) == 0
+        # n == 0 is a valid no-op; null pointers with n > 0 are invalid
+        assert getattr(L, f"gather_rows_{tag}_run")(None, None, None, 3, 4, 0, None) == 0
+        assert getattr(L, f"gather_rows_{tag}_run")(None, None, None, 3, 4, 1, None) == 2
+
+
+def test_gemm_invalid_problems_rejected_before_launch():
+    L = ffi.lib()
+    # non-positive extents -> 2 (baracuda_int8_rrr_sm80.cuh:321)
+    assert L.gemm_s8_rcr_gfx950_can_implement(0, 4, 4, None, 4, None, 4, None, 0, None, 4) == 2
+    assert L.gemm_s8_rcr_gfx950_can_implement(4, 4, 4, None, 3, None, 4, None, 0, None, 4) == 2
+    assert L.gemm_s8_rcr_gfx950_can_implement(4, 4, 4, None, 4, None, 4, None, 0, None, 4) == 0
+    assert L.gemm_s8_rcr_gfx950_run(4, 4, 4, None, 4, None, 4, None, 0, None, 4, 1.0, 0.0, None, 0, None) == 2
+    assert L.gemm_s8_rcr_gfx950_i32_run(-1, 4, 4, None, 4, None, 4, None, 4, None, 0, None) == 2
+    assert L.gemm_w8a8_rcr_gfx950_bf16_can_implement(8, 8, 8, None, 8, None, 8, None, None, None, 7) == 2
+    assert L.gemm_fp8_e4m3_rcr_gfx950_can_implement(1, 1, 0, None, 1, None, 1, None, 0, None, 1) == 2
+    assert L.gemm_fp8_e4m3_rcr_gfx950_bf16_workspace_size(16, 16, 16) == 0
+    assert L.quantized_linear_w8a8_f32_gfx950_can_implement(-1, 2, 2, None, None, None, None, None) == 2
+    assert L.quantized_linear_w8a8_f32_gfx950_run(0, 2, 2, None, None, None, None, None, None, 0, None) == 0
+
+
+def test_moe_can_implement():
+    L = ffi.lib()
+    # moe_wmma.cu:177-187
+    assert L.moe_s8_grouped_bf16_gfx950_can_implement(8, 2, 8192, 14336, 4096) == 0
+    assert L.moe_s8_grouped_bf16_gfx950_can_implement(2, 3, 16, 16, 16) == 2
+    assert L.moe_s8_grouped_bf16_gfx950_can_implement(2048, 2, 16, 16, 16) == 3
+    assert L.moe_s8_grouped_bf16_gfx950_can_implement(8, 2, 0, 16, 16) == 2
+
+
+def test_plan_select_and_sku():
+    plan = P.IntGemmPlan.select(P.IntGemmDescriptor(4096, 4096, 4096, output=P.ElementKind.Bf16))
+    sku = plan.sku()
+    assert sku.arch == P.ArchSku.Gfx950 and sku.layout == P.LayoutSku.Rcr
+    pg = plan.precision_guarantee()
+    assert pg.accumulator == P.ElementKind.I32 and pg.bit_stable_on_same_hardware and pg.deterministic
+    assert plan.workspace_size() == 0
+    with pytest.raises(P.InvalidProblem):
+        P.IntGemmPlan.select(P.IntGemmDescriptor(0, 1, 1))
+    with pytest.raises(P.Unsupported):
+        P.IntGemmPlan.select(P.IntGemmDescriptor(8, 8, 8, layout=P.LayoutSku.Rrr))
+    f = P.Fp8GemmPlan.select(P.Fp8GemmDescriptor(2048, 14336, 4096, output=P.ElementKind.Bf16))
+    assert f.sku().element == P.ElementKind.Fp8E4M3 and f.workspace_size() == 0
+    with pytest.raises(P.InvalidProblem):
+        P.GemvDensePlan.select(P.GemvDenseDescriptor(n=4, k=4, m=2), __import__("torch").float32)
+    with pytest.raises(P.Unsupported):
+        P.MoeS8GroupedPlan.select(2048, 2, 16, 16, 16)

@@ -1,0 +1,172 @@
+"""GPU parity of the decode kernels: gemv_s8w_m1, gemv_dense_m1 and gather_rows,
+including hipGraph capture + replay (capture_replay_gather_gemv.rs)."""
+import numpy as np
+import pytest
+import torch
+
+from baracuda_amd import plans as P
+from baracuda_amd.ffi import lib
+from oracle import oracle as O
+from oracle.inputs import int8_uniform, rng
+from tests.gpu_util import bf16_ulp, dev, host_bits16, sync
+
+pytestmark = pytest.mark.gpu
+GOLD = __import__("pathlib").Path(__file__).resolve().parent / "golden"
+
+
+def _gemv_inputs(n, k, seed=4):
+    g = rng(seed)
+    w = int8_uniform(g, (n, k))
+    scale = g.uniform(0.001, 0.01, n).astype(np.float32)
+    xb = O.f32_to_bf16_bits_fast(g.standard_normal(k).astype(np.float32))
+    return w, scale, xb
+
+
+def _gemv_check(got_bits, w, scale, xb):
+    # <= 1 bf16 ulp of the exact value; absolute floor 1e-6 * scale * sum|x*w|
+    # for outputs whose sum cancels.
+    acc = O.gemv_s8w_m1_f64(xb, w, nthreads=8)
+    exact = acc * scale.astype(np.float64)
+    got = O.bf16_bits_to_f32(got_bits).astype(np.float64)
+    absum = np.abs(w.astype(np.float64)) @ np.abs(O.bf16_bits_to_f32(xb).astype(np.float64)) * scale
+    err = np.abs(got - exact)
+    assert np.all(err <= bf16_ulp(exact) + 1e-6 * absum), err.max()
+
+
+def _gemv_run(w, scale, xb):
+    n, k = w.shape
+    d = torch.empty(n, dtype=torch.bfloat16, device="cuda:0")
+    x = dev(xb).view(torch.bfloat16)
+    P.GemvS8wPlan.select(n, k).run(x, dev(w), dev(scale), d)
+    sync()
+    return host_bits16(d)
+
+
+@pytest.mark.parametrize("shape", [(14336, 4096), (4096, 14336), (1, 1024), (77, 3000), (1000, 17), (33, 0)])
+def test_gemv_s8w(gpu, shape):
+    print(f"case: gemv_s8w {shape}", flush=True)
+    w, scale, xb = _gemv_inputs(*shape)
+    _gemv_check(_gemv_run(w, scale, xb), w, scale, xb)
+
+
+def test_gemv_s8w_graph_replay_bit_identical(gpu):
+    n, k = 14336, 4096
+    w, scale, xb = _gemv_inputs(n, k)
+    wd, sd, x = dev(w), dev(scale), dev(xb).view(torch.bfloat16)
+    d = torch.zeros(n, dtype=torch.bfloat16, device="cuda:0")
+    plan = P.GemvS8wPlan.select(n, k)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        plan.run(x, wd, sd, d)
+    torch.cuda.synchronize()
+    warm = host_bits16(d).copy()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        plan.run(x, wd, sd, d)
+    for rep in range(4):
+        d.fill_(0)
+        graph.replay()
+        sync()
+        assert np.array_equal(host_bits16(d), warm), rep
+    _gemv_check(warm, w, scale, xb)
+
+
+_TORCH = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
+
+
+@pytest.mark.parametrize("tag", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("case", [(4096, 4096, 1, False, 0.0), (37, 19, 3, True, 0.25), (300, 1000, 4, False, 0.5)])
+def test_gemv_dense_m1(gpu, tag, case):
+    # gemv_dense_smoke.rs: f32 rel 1e-4, bf16 rel 1.6e-2 (f16 taken as 2e-3),
+    # GQA broadcast (stride_b = 0), strided batch, beta, inter-slot gaps untouched.
+    n, k, batch, bcast, beta = case
+    print(f"case: gemv_dense {tag} {case}", flush=True)
+    g = rng(n + k + batch)
+    dt = _TORCH[tag]
+    stride_a, stride_d, ldb = k + 3, n + 5, n
+    stride_b = 0 if bcast else k * ldb
+    a = torch.from_numpy(g.standard_normal(batch * stride_a).astype(np.float32)).to(dt)
+    b = torch.from_numpy(g.standard_normal(max(1, (1 if bcast else batch)) * k * ldb).astype(np.float32) / 8).to(dt)
+    d0 = torch.from_numpy(g.standard_normal(batch * stride_d).astype(np.float32)).to(dt)
+    d = d0.clone().cuda()
+    plan = P.GemvDensePlan.select(P.GemvDenseDescriptor(n=n, k=k, batch=batch), dt)
+    plan.can_implement(k, ldb, n, stride_a, stride_b, stride_d)
+    plan.run(a.cuda(), b.cuda(), d, lda=k, stride_a=stride_a, ldb=ldb, stride_b=stride_b, ldd=n,
+             stride_d=stride_d, alpha=0.75, beta=beta)
+    sync()
+    want = O.gemv_dense_m1_f64(a.double().numpy(), b.double().numpy(), d0.double().numpy(), n, k, batch,
+                               stride_a, ldb, stride_b, stride_d, 0.75, beta)
+    got = d.cpu().double().numpy()
+    rel = {"f32": 1e-4, "f16": 2e-3, "bf16": 1.6e-2}[tag]
+    for gi in range(batch):
+        sl = slice(gi * stride_d, gi * stride_d + n)
+        scale = np.abs(want[sl]).max()
+        assert np.allclose(got[sl], want[sl], rtol=rel, atol=rel * scale), gi
+        gap = slice(gi * stride_d + n, (gi + 1) * stride_d)
+        assert np.array_equal(got[gap], d0.double().numpy()[gap])
+
+
+def test_gemv_dense_beta0_never_reads_d(gpu):
+    n, k = 256, 64
+    a = torch.ones(k, device="cuda:0")
+    b = torch.ones(k * n, device="cuda:0")
+    d = torch.full((n,), float("nan"), device="cuda:0")
+    P.GemvDensePlan.select(P.GemvDenseDescriptor(n=n, k=k), torch.float32).run(
+        a, b, d, lda=k, stride_a=0, ldb=n, stride_b=0, ldd=n, stride_d=0, alpha=1.0, beta=0.0)
+    sync()
+    assert torch.all(d == k)
+
+
+# ---- gather_rows ---------------------------------------------------------------
+def test_gather_rows_capture_replay_golden(gpu):
+    # capture_replay_gather_gemv.rs:54-117: warm launch + 4 graph replays == [1,2,3,4].
+    z = np.load(GOLD / "wte_gather.npz")
+    table = dev(z["table"])
+    idx = dev(z["idx"].view(np.int32)).view(torch.uint32)
+    dest = torch.zeros((1, 4), dtype=torch.float32, device="cuda:0")
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        P.gather_rows(dest, table, idx)
+    torch.cuda.synchronize()
+    assert np.array_equal(dest.cpu().numpy(), z["expected"])
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        P.gather_rows(dest, table, idx)
+    for rep in range(4):
+        graph.replay()
+        sync()
+        assert np.array_equal(dest.cpu().numpy(), z["expected"]), rep
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16, torch.float32])
+def test_gather_rows_oob_and_ragged(gpu, dt):
+    g = rng(31)
+    V, H = 50, 36 if dt != torch.float32 else 37     # 72-byte / 148-byte rows: element path
+    table = torch.from_numpy(g.standard_normal((V, H)).astype(np.float32)).to(dt)
+    idx = np.array([3, 49, 50, 2 ** 32 - 1, 0, 3], np.uint32)
+    dest = torch.full((idx.size, H), 7, dtype=dt, device="cuda:0")
+    P.gather_rows(dest, table.cuda(), dev(idx.view(np.int32)).view(torch.uint32))
+    sync()
+    tb = table.view(torch.int16 if dt != torch.float32 else torch.int32).numpy()
+    want = O.gather_rows(tb, idx)
+    got = dest.cpu().view(torch.int16 if dt != torch.float32 else torch.int32).numpy()
+    assert np.array_equal(got, want)
+
+
+def test_gather_rows_config4_bf16_table(gpu):
+    # BASELINE config 4b: bf16 [128256, 4096] ~ N(0, 0.02), n in {1, 8, 64}.
+    V, H = 128256, 4096
+    gen = torch.Generator(device="cuda:0").manual_seed(4)
+    table = (torch.randn((V, H), generator=gen, device="cuda:0") * 0.02).to(torch.bfloat16)
+    g = rng(41)
+    for n in (1, 8, 64):
+        print(f"case: gather bf16 n={n}", flush=True)
+        idx = g.integers(0, V, n).astype(np.uint32)
+        idx[0] = V - 1
+        dest = torch.empty((n, H), dtype=torch.bfloat16, device="cuda:0")
+        P.gather_rows(dest, table, dev(idx.view(np.int32)).view(torch.uint32))
+        sync()
+        rows = table[torch.from_numpy(idx.astype(np.int64)).cuda()].cpu().view(torch.int16).numpy()
+        # oracle on the gathered rows only (remapped indices 0..n-1), bit-exact
+        want = O.gather_rows(rows, np.arange(n, dtype=np.uint32))
+        assert np.array_equal(dest.cpu().view(torch.int16).numpy(), want)

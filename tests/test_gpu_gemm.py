@@ -1,0 +1,217 @@
+"""GPU parity of the int8 / FP8 RCR GEMMs against the CPU oracle.
+
+Bars: int32 accumulators and int8 outputs bit-exact; W8A8 bf16 bit-exact
+(same f32 epilogue order as the oracle); FP8 f32 accumulator within 1e-3
+relative to the exact f64 sum, with an absolute floor of 1e-5 * sum|a*b| for
+sums that cancel; FP8 bf16 within 1 bf16 ulp of the exact value (same floor).
+"""
+import numpy as np
+import pytest
+import torch
+
+from baracuda_amd import plans as P
+from oracle import oracle as O
+from oracle.inputs import int8_uniform, rng, w8a8
+from tests.gpu_util import bf16_ulp, dev, host_bits16, sync
+
+pytestmark = pytest.mark.gpu
+
+GOLD = __import__("pathlib").Path(__file__).resolve().parent / "golden"
+REF_SHAPES = [(64, 64, 32), (128, 128, 128), (256, 128, 64), (100, 70, 50)]   # int8_rrr_smoke.rs / fp8 smokes
+
+
+def _i32(a, b):
+    m, k = a.shape
+    n = b.shape[0]
+    d = torch.full((m, n), -7, dtype=torch.int32, device="cuda:0")
+    P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, output=P.ElementKind.I32)).run(dev(a), dev(b), d)
+    sync()
+    return d.cpu().numpy()
+
+
+def test_config1_256_cubed_matches_golden_and_oracle(gpu):
+    z = np.load(GOLD / "config1_s8_rcr_256.npz")
+    print("case: config1 i32 256^3", flush=True)
+    got = _i32(z["a"], z["b"])
+    assert np.array_equal(got, z["c"])
+    assert np.array_equal(got, O.contraction_s8_i32(z["a"], z["b"].T))
+
+
+@pytest.mark.parametrize("shape", REF_SHAPES + [(1, 1, 1), (3, 300, 17), (257, 513, 129), (512, 256, 4096)])
+def test_i32_ragged_shapes(gpu, shape):
+    m, n, k = shape
+    print(f"case: i32 {shape}", flush=True)
+    g = rng(m * 7 + n * 3 + k)
+    a, b = int8_uniform(g, (m, k)), int8_uniform(g, (n, k))
+    assert np.array_equal(_i32(a, b), O.gemm_s8_rcr_i32(a, b, nthreads=8))
+
+
+def test_i32_extreme_values_no_overflow(gpu):
+    # |acc| = 127*127*K stays < 2^31 for K < 133143: all -127 (and -128) inputs.
+    m = n = 256
+    k = 8192
+    a = np.full((m, k), -128, np.int8)
+    b = np.full((n, k), -127, np.int8)
+    got = _i32(a, b)
+    assert np.all(got == 128 * 127 * k)
+
+
+def test_i32_strided_leading_dims(gpu):
+    g = rng(9)
+    m, n, k, lda, ldb, ldd = 200, 136, 96, 112, 128, 160
+    a = int8_uniform(g, (m, lda))
+    b = int8_uniform(g, (n, ldb))
+    d = torch.zeros((m, ldd), dtype=torch.int32, device="cuda:0")
+    P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, output=P.ElementKind.I32)).run(
+        dev(a)[:, :k], dev(b)[:, :k], d[:, :n])
+    sync()
+    out = d.cpu().numpy()
+    assert np.array_equal(out[:, :n], O.gemm_s8_rcr_i32(a[:, :k], b[:, :k]))
+    assert np.all(out[:, n:] == 0)   # untouched padding
+
+
+@pytest.mark.parametrize("shape", REF_SHAPES)
+def test_s8_sat_epilogue_reference_pattern(gpu, shape):
+    # int8_smoke.rs:159-172 patterns, alpha = 0.125; 0 mismatches (the reference allows +-1).
+    m, n, k = shape
+    print(f"case: s8 sat {shape}", flush=True)
+    a = ((np.arange(m * k) * 7) % 15 - 7).astype(np.int8).reshape(m, k)
+    b = ((np.arange(k * n) * 11) % 13 - 6).astype(np.int8).reshape(n, k)
+    d = torch.zeros((m, n), dtype=torch.int8, device="cuda:0")
+    P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k)).run(dev(a), dev(b), d, alpha=0.125)
+    sync()
+    assert np.array_equal(d.cpu().numpy(), O.gemm_s8_rcr_s8(a, b, 0.125))
+
+
+def test_s8_sat_with_beta_c(gpu):
+    g = rng(12)
+    m, n, k = 300, 260, 384
+    a, b = int8_uniform(g, (m, k)), int8_uniform(g, (n, k))
+    c = int8_uniform(g, (m, n))
+    d = torch.zeros((m, n), dtype=torch.int8, device="cuda:0")
+    P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k)).run(dev(a), dev(b), d, c=dev(c), alpha=0.002, beta=0.75)
+    sync()
+    assert np.array_equal(d.cpu().numpy(), O.gemm_s8_rcr_s8(a, b, 0.002, 0.75, c))
+
+
+def _w8a8(a, w, sa, sw):
+    m, k = a.shape
+    n = w.shape[0]
+    d = torch.empty((m, n), dtype=torch.bfloat16, device="cuda:0")
+    P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, output=P.ElementKind.Bf16)).run(
+        dev(a), dev(w), d, scale_a=dev(sa), scale_b=dev(sw))
+    sync()
+    return host_bits16(d)
+
+
+@pytest.mark.parametrize("shape", [(512, 512, 512), (100, 70, 50), (384, 1024, 256)])
+def test_w8a8_bf16_bit_exact(gpu, shape):
+    print(f"case: w8a8 {shape}", flush=True)
+    a, w, sa, sw = w8a8(*shape, seed=2)
+    assert np.array_equal(_w8a8(a, w, sa, sw), O.gemm_w8a8_bf16(a, w, sa, sw, nthreads=8))
+
+
+def test_w8a8_config2_full_size_sampled_rows(gpu):
+    # 4096^3; every row sampled below is compared bit-exact,
+    # plus size-independent checks on the whole output.
+    print("case: w8a8 4096^3", flush=True)
+    a, w, sa, sw = w8a8(4096, 4096, 4096, seed=2)
+    got = _w8a8(a, w, sa, sw)
+    rows = [0, 1, 255, 256, 1023, 2048, 3071, 4095] + list(rng(21).integers(0, 4096, 24))
+    for r in rows:
+        want = O.gemm_w8a8_bf16(a, w, sa, sw, rows=(int(r), int(r) + 1), nthreads=8)
+        assert np.array_equal(got[r], want[0]), r
+    # column-sum identity on the int32 accumulator: sum_m acc[m, n] = (sum_m a[m,:]) . w[n,:]
+    d = torch.empty((4096, 4096), dtype=torch.int32, device="cuda:0")
+    P.IntGemmPlan.select(P.IntGemmDescriptor(4096, 4096, 4096, output=P.ElementKind.I32)).run(dev(a), dev(w), d)
+    sync()
+    colsum = d.to(torch.int64).sum(0).cpu().numpy()
+    assert np.array_equal(colsum, w.astype(np.int64) @ a.astype(np.int64).sum(0))
+    rowsum = d.to(torch.int64).sum(1).cpu().numpy()
+    assert np.array_equal(rowsum, a.astype(np.int64) @ w.astype(np.int64).sum(0))
+
+
+def test_quantized_linear_w8a8_f32(gpu):
+    a, w, sa, sw = w8a8(130, 70, 200, seed=8)
+    out = torch.empty((130, 70), dtype=torch.float32, device="cuda:0")
+    from baracuda_amd.ffi import lib
+    st = lib().quantized_linear_w8a8_f32_gfx950_run(130, 70, 200, dev(w).data_ptr(), dev(a).data_ptr(),
+                                                    dev(sa).data_ptr(), dev(sw).data_ptr(), out.data_ptr(),
+                                                    None, 0, torch.cuda.current_stream().cuda_stream)
+    assert st == 0
+    sync()
+    acc = O.gemm_s8_rcr_i32(a, w).astype(np.float32)
+    want = (sa[:, None] * sw[None, :]).astype(np.float32) * acc
+    assert np.array_equal(out.cpu().numpy(), want)
+
+
+def test_int8_determinism_replays(gpu):
+    a, w, sa, sw = w8a8(1024, 768, 1024, seed=4)
+    outs = [_w8a8(a, w, sa, sw) for _ in range(3)]
+    assert all(np.array_equal(outs[0], o) for o in outs[1:])
+
+
+# ---- FP8 ---------------------------------------------------------------------
+def _fp8_inputs(m, n, k, seed=3):
+    # BASELINE config 3 recipe: N(0,1), scale absmax -> 448, cast to e4m3.
+    g = rng(seed)
+    xa = g.standard_normal((m, k)).astype(np.float32)
+    xb = g.standard_normal((n, k)).astype(np.float32)
+    sa = np.float32(np.abs(xa).max() / 448.0)
+    sb = np.float32(np.abs(xb).max() / 448.0)
+    ta = torch.from_numpy(xa / sa).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    tb = torch.from_numpy(xb / sb).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    return ta, tb, float(sa), float(sb)
+
+
+def _fp8_run(a, b, output, **kw):
+    m, k = a.shape
+    n = b.shape[0]
+    dt = {P.ElementKind.F32: torch.float32, P.ElementKind.Bf16: torch.bfloat16, P.ElementKind.Fp8E4M3: torch.uint8}[output]
+    d = torch.zeros((m, n), dtype=dt, device="cuda:0")
+    P.Fp8GemmPlan.select(P.Fp8GemmDescriptor(m, n, k, output=output)).run(dev(a), dev(b), d, **kw)
+    sync()
+    return d
+
+
+def _fp8_check_acc(got, a, b, alpha=1.0, rows=None):
+    exact = O.gemm_fp8_e4m3_f64(a, b, rows=rows, nthreads=8) * alpha
+    ta, tb = np.abs(O.e4m3_to_f32(a).astype(np.float64)), np.abs(O.e4m3_to_f32(b).astype(np.float64))
+    absum = (ta[rows[0]:rows[1]] if rows else ta) @ tb.T * abs(alpha)
+    err = np.abs(got.astype(np.float64) - exact)
+    assert np.all(err <= 1e-3 * np.abs(exact) + 1e-5 * absum), err.max()
+    return exact
+
+
+@pytest.mark.parametrize("shape", REF_SHAPES + [(512, 384, 1024)])
+def test_fp8_f32_accumulator(gpu, shape):
+    print(f"case: fp8 f32 {shape}", flush=True)
+    a, b, _, _ = _fp8_inputs(*shape)
+    got = _fp8_run(a, b, P.ElementKind.F32, alpha=1.0).cpu().numpy()
+    _fp8_check_acc(got, a, b)
+
+
+def test_fp8_e4m3_out_reference_pattern(gpu):
+    # fp8_e4m3_rcr_smoke.rs:113-126 patterns, alpha = 0.25; +-1 e4m3 grid step.
+    for (m, n, k) in REF_SHAPES:
+        a = O.f32_to_e4m3((((np.arange(m * k) * 5) % 13) - 6.0) * 0.125).reshape(m, k)
+        b = O.f32_to_e4m3((((np.arange(k * n) * 7) % 11) - 5.0) * 0.125).reshape(n, k)
+        got = O.e4m3_to_f32(_fp8_run(a, b, P.ElementKind.Fp8E4M3, alpha=0.25).cpu().numpy())
+        # the patterns are small dyadic rationals: the f32 sum is exact, so the
+        # e4m3 output must equal the oracle's encode of the exact value.
+        want = O.e4m3_to_f32(O.f32_to_e4m3((O.gemm_fp8_e4m3_f64(a, b) * 0.25).astype(np.float32)))
+        assert np.array_equal(got, want), (m, n, k)
+
+
+def test_fp8_bf16_config3_sampled(gpu):
+    print("case: fp8 bf16 2048x14336x4096", flush=True)
+    a, b, sa, sb = _fp8_inputs(2048, 14336, 4096)
+    d = _fp8_run(a, b, P.ElementKind.Bf16, scale_a=sa, scale_b=sb)
+    got = O.bf16_bits_to_f32(host_bits16(d))
+    alpha = float(np.float32(sa) * np.float32(sb))
+    for r in [0, 777, 2047]:
+        exact = O.gemm_fp8_e4m3_f64(a, b, rows=(r, r + 1), nthreads=8)[0] * alpha
+        err = np.abs(got[r].astype(np.float64) - exact)
+        ta = np.abs(O.e4m3_to_f32(a[r]).astype(np.float64))
+        absum = np.abs(O.e4m3_to_f32(b).astype(np.float64)) @ ta * alpha
+        assert np.all(err <= bf16_ulp(exact) + 1e-5 * absum), (r, err.max())

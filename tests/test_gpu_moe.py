@@ -1,0 +1,73 @@
+"""GPU parity of the grouped int8 MoE GEMM (routing contract of moe_wmma)."""
+import numpy as np
+import pytest
+import torch
+
+from baracuda_amd import plans as P
+from oracle import oracle as O
+from oracle.inputs import int8_uniform, moe_routing, rng
+from tests.gpu_util import dev, host_bits16, sync
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(tokens, E, topk, n, k, seed, topk_w=False, pairs_check=None):
+    sorted_ids, expert_ids = moe_routing(tokens, E, topk, seed=seed)
+    size_m = tokens * topk
+    g = rng(seed + 100)
+    x, w = int8_uniform(g, (tokens, k)), int8_uniform(g, (E, n, k))
+    sa = g.uniform(0.005, 0.02, tokens).astype(np.float32)
+    sw = g.uniform(0.001, 0.01, E * n).astype(np.float32)
+    tw = g.uniform(0.1, 1.0, size_m).astype(np.float32) if topk_w else None
+    xin = x if not topk_w else np.repeat(x, topk, axis=0)   # topk_weights form reads row = pair id
+    out = torch.zeros((size_m, n), dtype=torch.bfloat16, device="cuda:0")
+    counts = torch.zeros(E, dtype=torch.int32, device="cuda:0")
+    offs = torch.zeros(E + 1, dtype=torch.int32, device="cuda:0")
+    plan = P.MoeS8GroupedPlan.select(E, topk, size_m, n, k)
+    plan.run(dev(xin), dev(w), dev(sorted_ids), dev(expert_ids), out, counts, offs, dev(sa), dev(sw),
+             topk_weights=dev(tw) if tw is not None else None)
+    sync()
+    c_ref, o_ref = O.moe_expert_offsets(expert_ids, E)
+    assert np.array_equal(counts.cpu().numpy(), c_ref)
+    assert np.array_equal(offs.cpu().numpy(), o_ref)
+    got = host_bits16(out)
+    pairs = range(size_m) if pairs_check is None else pairs_check
+    pair_e = np.empty(size_m, np.int32)
+    pair_e[sorted_ids] = expert_ids
+    for p in pairs:
+        e, t = pair_e[p], p // topk
+        acc = (w[e].astype(np.int64) @ x[t].astype(np.int64)).astype(np.float32)
+        y = (sa[t] * sw[e * n:(e + 1) * n]).astype(np.float32) * acc
+        if tw is not None:
+            y = (y * tw[p]).astype(np.float32)
+        assert np.array_equal(got[p], O.f32_to_bf16_bits_fast(y)), p
+    return got
+
+
+def test_moe_small_all_pairs(gpu):
+    print("case: moe small", flush=True)
+    _run(tokens=300, E=8, topk=2, n=272, k=384, seed=5)
+
+
+def test_moe_ragged_k_and_topk_weights(gpu):
+    print("case: moe ragged k, topk weights", flush=True)
+    _run(tokens=100, E=5, topk=3, n=100, k=200, seed=6, topk_w=True)
+
+
+def test_moe_oracle_grouped_agrees(gpu):
+    # the oracle's grouped restatement and the bf16 check above agree on i32 accumulators
+    sorted_ids, expert_ids = moe_routing(64, 4, 2, seed=7)
+    _, offs = O.moe_expert_offsets(expert_ids, 4)
+    g = rng(8)
+    x, w = int8_uniform(g, (64, 128)), int8_uniform(g, (4, 64, 128))
+    acc = O.moe_s8_grouped_i32(x, w, sorted_ids, offs, 2, 128)
+    pair_e = np.empty(128, np.int32)
+    pair_e[sorted_ids] = expert_ids
+    assert np.array_equal(acc[5], w[pair_e[5]].astype(np.int64) @ x[2].astype(np.int64))
+
+
+def test_moe_config5_full_size_sampled(gpu):
+    # 8 experts, hidden 4096, ffn 14336, 4096 tokens top-2 Zipf(1.1).
+    print("case: moe config5", flush=True)
+    pairs = [0, 1, 2, 8191, 4095] + list(rng(51).integers(0, 8192, 27))
+    _run(tokens=4096, E=8, topk=2, n=14336, k=4096, seed=5, pairs_check=pairs)

@@ -1,0 +1,220 @@
+"""Pins the CPU oracle (oracle/) before it is trusted as the parity checker.
+
+Every oracle function is checked against something it was not written from:
+the reference's own hand-computed vectors, a library routine (torch / numpy
+casts and int64 matmul), closed forms, or brute force on tiny inputs.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from oracle.inputs import int8_uniform, moe_routing, rng
+from tests.golden import __file__ as _g  # noqa: F401  (package marker)
+
+GOLD = __import__("pathlib").Path(__file__).resolve().parent / "golden"
+
+
+# ---- scalar codecs -----------------------------------------------------------
+def _specials():
+    vals = [0.0, -0.0, 1.0, -1.0, 1.00390625, 1.01171875, 3.4e38, -3.4e38, 1e-40, -1e-45,
+            float("inf"), float("-inf"), 65504.0, 65520.0, 448.0, 464.0, 2 ** -6, 2 ** -9, 2 ** -10]
+    g = rng(11)
+    rnd = np.concatenate([g.standard_normal(4000) * 10 ** g.uniform(-8, 8, 4000),
+                          g.uniform(-500, 500, 4000)]).astype(np.float32)
+    return np.concatenate([np.array(vals, np.float32), rnd])
+
+
+def test_bf16_rne_matches_torch_cast():
+    # oracle.rs:397-404 vs torch's f32->bf16 (round to nearest even).
+    x = _specials()
+    got = O.f32_to_bf16_bits(x)
+    want = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, want)
+    assert np.array_equal(O.f32_to_bf16_bits_fast(x), got)
+
+
+def test_bf16_nan_stays_quiet_nan():
+    nan = np.array([np.float32("nan"), np.uint32(0x7f800001).view(np.float32)], np.float32)
+    b = O.f32_to_bf16_bits(nan)
+    assert all(math.isnan(v) for v in O.bf16_bits_to_f32(b))
+    assert all((v & 0x0040) for v in b)
+
+
+def test_bf16_ties_to_even_closed_form():
+    # 1 + 2^-8 is exactly half an ulp above 1.0 -> stays 1.0 (even); 1 + 3*2^-8 -> rounds up.
+    assert O.scalar("bo_f32_to_bf16_bits")(1.0 + 2 ** -8) == 0x3F80
+    assert O.scalar("bo_f32_to_bf16_bits")(1.0 + 3 * 2 ** -8) == 0x3F82
+
+
+def test_f16_matches_numpy_cast():
+    x = _specials()
+    x = x[np.isfinite(x)]
+    got = np.array([O.scalar("bo_f32_to_f16_bits")(float(v)) for v in x], np.uint16)
+    want = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
+    back = np.array([O.scalar("bo_f16_bits_to_f32")(int(v)) for v in want], np.float32)
+    assert np.array_equal(back, want.view(np.float16).astype(np.float32))
+
+
+def test_e4m3_decode_table_matches_torch_float8_e4m3fn():
+    # OCP E4M3 spec decode vs torch.float8_e4m3fn, all 256 codes.
+    got = O.e4m3_table()
+    want = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float().numpy()
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan], want[~nan])
+    assert nan.sum() == 2 and np.nanmax(got) == 448.0
+
+
+def test_e4m3_encode_matches_torch_in_range_and_saturates():
+    x = _specials()
+    x = x[np.isfinite(x)]
+    inr = np.abs(x) <= 448.0
+    got = O.f32_to_e4m3(x[inr])
+    want = torch.from_numpy(x[inr]).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(got, want)
+    over = O.f32_to_e4m3(np.array([449.0, 1e6, -1e30, np.inf, -np.inf], np.float32))
+    assert list(over) == [0x7E, 0x7E, 0xFE, 0x7E, 0xFE]
+    # brute force: every code round-trips through decode -> encode
+    tab = O.e4m3_table()
+    codes = [c for c in range(256) if not math.isnan(tab[c])]
+    back = O.f32_to_e4m3(tab[codes])
+    for c, b in zip(codes, back):
+        assert b == c or (tab[c] == 0.0 and tab[b] == 0.0)
+
+
+def test_rust_as_i32_semantics():
+    f = O.scalar("bo_f64_to_i32_as")
+    assert f(float("nan")) == 0
+    assert f(3e9) == 2 ** 31 - 1 and f(-3e9) == -(2 ** 31)
+    assert f(-2.9) == -2 and f(2.9) == 2
+
+
+def test_sat_cast_s8_round_half_even_and_clamp():
+    f = O.scalar("bo_sat_cast_s8")
+    assert [f(v) for v in (0.5, 1.5, 2.5, -0.5, -2.5, 126.6, 200.0, -300.0)] == [0, 2, 2, 0, -2, 127, 127, -128]
+
+
+# ---- contraction (oracle.rs eval_contraction) ---------------------------------
+def test_contraction_reference_hand_vector():
+    # oracle.rs:2433-2480: [[1,2,3],[4,5,6]] . [[10,11],[12,13],[14,15]].
+    lhs = np.array([[1, 2, 3], [4, 5, 6]], np.float64)
+    rhs = np.array([[10, 11], [12, 13], [14, 15]], np.float64)
+    assert O.contraction_f64(lhs, rhs).tolist() == [[76, 82], [184, 199]]
+    # rhs stored transposed ([N,K] row-major) read through physical strides
+    rhs_t = np.ascontiguousarray(rhs.T).T
+    assert O.contraction_f64(lhs, rhs_t).tolist() == [[76, 82], [184, 199]]
+    assert O.contraction_s8_i32(lhs.astype(np.int8), rhs.astype(np.int8)).tolist() == [[76, 82], [184, 199]]
+
+
+def test_contraction_matches_golden_config1():
+    z = np.load(GOLD / "config1_s8_rcr_256.npz")
+    # B is [N,K] row-major == column-major [K,N]: pass the [K,N] view.
+    got = O.contraction_s8_i32(z["a"], z["b"].T)
+    assert np.array_equal(got, z["c"])
+    assert np.array_equal(O.gemm_s8_rcr_i32(z["a"], z["b"]), z["c"])
+    assert np.array_equal(O.gemm_s8_rcr_i32(z["a"], z["b"], nthreads=4), z["c"])
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 1), (3, 5, 7), (100, 70, 50), (64, 64, 32)])
+def test_gemm_i32_brute_force(shape):
+    m, n, k = shape
+    g = rng(sum(shape))
+    a, b = int8_uniform(g, (m, k)), int8_uniform(g, (n, k))
+    want = np.array([[sum(int(a[i, t]) * int(b[j, t]) for t in range(k)) for j in range(n)] for i in range(m)])
+    assert np.array_equal(O.gemm_s8_rcr_i32(a, b), want)
+
+
+def test_gemm_s8_sat_epilogue_reference_pattern():
+    # int8_smoke.rs:159-172 inputs, alpha = 0.125, beta = 0.
+    m = n = k = 128
+    a = ((np.arange(m * k) * 7) % 15 - 7).astype(np.int8).reshape(m, k)
+    b = ((np.arange(k * n) * 11) % 13 - 6).astype(np.int8).reshape(n, k)   # col-major [K,N]
+    acc = a.astype(np.int64) @ b.astype(np.int64).T
+    want = np.clip(np.rint(np.float32(0.125) * acc.astype(np.float32)), -128, 127).astype(np.int8)
+    assert np.array_equal(O.gemm_s8_rcr_s8(a, b, 0.125), want)
+    c = ((np.arange(m * n) * 3) % 9 - 4).astype(np.int8).reshape(m, n)
+    z = np.float32(0.125) * acc.astype(np.float32) + np.float32(0.5) * c.astype(np.float32)
+    assert np.array_equal(O.gemm_s8_rcr_s8(a, b, 0.125, 0.5, c), np.clip(np.rint(z), -128, 127).astype(np.int8))
+
+
+def test_w8a8_bf16_epilogue_against_torch():
+    g = rng(2)
+    m, n, k = 64, 96, 160
+    a, w = int8_uniform(g, (m, k)), int8_uniform(g, (n, k))
+    sa = g.uniform(0.005, 0.02, m).astype(np.float32)
+    sw = g.uniform(0.001, 0.01, n).astype(np.float32)
+    acc = (a.astype(np.int64) @ w.astype(np.int64).T).astype(np.float32)
+    y = (sa[:, None] * sw[None, :]).astype(np.float32) * acc
+    want = torch.from_numpy(y).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(O.gemm_w8a8_bf16(a, w, sa, sw), want)
+    assert np.array_equal(O.gemm_w8a8_bf16(a, w, sa, sw, rows=(5, 9), nthreads=2), want[5:9])
+
+
+def test_fp8_gemm_against_numpy():
+    g = rng(3)
+    m, n, k = 40, 24, 96
+    a = O.f32_to_e4m3(g.standard_normal((m, k)).astype(np.float32))
+    b = O.f32_to_e4m3(g.standard_normal((n, k)).astype(np.float32))
+    da, db = O.e4m3_to_f32(a).astype(np.float64), O.e4m3_to_f32(b).astype(np.float64)
+    assert np.allclose(O.gemm_fp8_e4m3_f64(a, b), da @ db.T, rtol=0, atol=1e-9)
+    # f32 K-ascending (fp8_e4m3_rcr_smoke.rs:51-76) vs an explicit float32 loop
+    want = np.zeros((m, n), np.float32)
+    for t in range(k):
+        want += (da[:, t:t + 1].astype(np.float32) * db[:, t].astype(np.float32)[None, :])
+    assert np.array_equal(O.gemm_fp8_e4m3_f32(a, b), want)
+
+
+def test_gemv_dense_f64_against_numpy():
+    g = rng(4)
+    n, k, batch = 37, 19, 3
+    a = g.standard_normal(batch * k)
+    b = g.standard_normal(k * n)          # stride_b = 0: GQA broadcast
+    d0 = g.standard_normal(batch * n)
+    got = O.gemv_dense_m1_f64(a, b, d0, n, k, batch, k, n, 0, n, 0.5, 0.25)
+    want = 0.5 * (a.reshape(batch, k) @ b.reshape(k, n)) + 0.25 * d0.reshape(batch, n)
+    assert np.allclose(got.reshape(batch, n), want, rtol=1e-12, atol=1e-12)
+
+
+def test_gemv_s8w_against_numpy():
+    g = rng(4)
+    n, k = 33, 1000
+    w = int8_uniform(g, (n, k))
+    xb = O.f32_to_bf16_bits_fast(g.standard_normal(k).astype(np.float32))
+    want = w.astype(np.float64) @ O.bf16_bits_to_f32(xb).astype(np.float64)
+    assert np.allclose(O.gemv_s8w_m1_f64(xb, w, nthreads=3), want, rtol=1e-13, atol=1e-12)
+
+
+def test_gather_rows_reference_golden_and_oob():
+    z = np.load(GOLD / "wte_gather.npz")
+    assert np.array_equal(O.gather_rows(z["table"], z["idx"]), z["expected"])
+    t = np.arange(20, dtype=np.uint16).reshape(5, 4)
+    got = O.gather_rows(t, np.array([4, 5, 0, 99], np.uint32))
+    assert got.tolist() == [[16, 17, 18, 19], [0, 0, 0, 0], [0, 1, 2, 3], [0, 0, 0, 0]]
+
+
+def test_moe_routing_offsets_and_grouped_gemm():
+    E, topk, tokens, n, k = 8, 2, 64, 24, 40
+    sorted_ids, expert_ids = moe_routing(tokens, E, topk, seed=5)
+    counts, offs = O.moe_expert_offsets(expert_ids, E)
+    assert np.array_equal(counts, np.bincount(expert_ids, minlength=E))
+    assert np.array_equal(offs, np.concatenate([[0], np.cumsum(counts)]))
+    g = rng(6)
+    x, w = int8_uniform(g, (tokens, k)), int8_uniform(g, (E, n, k))
+    got = O.moe_s8_grouped_i32(x, w, sorted_ids, offs, topk, tokens * topk)
+    for p, e in zip(sorted_ids, expert_ids):
+        want = w[e].astype(np.int64) @ x[p // topk].astype(np.int64)
+        assert np.array_equal(got[p], want)
+
+
+def test_moe_routing_is_zipf_and_topk_distinct():
+    sorted_ids, expert_ids = moe_routing(4096, 8, 2, seed=5)
+    assert sorted(sorted_ids.tolist()) == list(range(8192))
+    pair_e = np.empty(8192, np.int32)
+    pair_e[sorted_ids] = expert_ids
+    assert np.all(pair_e[0::2] != pair_e[1::2])
+    cnt = np.bincount(expert_ids, minlength=8)
+    assert cnt[0] > cnt[7] * 2
