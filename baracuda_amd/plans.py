@@ -354,7 +354,8 @@ class GemvS8wPlan:
         _need(x.dtype == torch.bfloat16 and x.numel() == self.k, "x must be bf16 [K]")
         _need(scale.dtype == torch.float32 and scale.numel() == self.n, "scale must be f32 [N]")
         _need(d.dtype == torch.bfloat16 and d.numel() == self.n, "d must be bf16 [N]")
-        st = lib().gemv_s8w_m1_bf16_gfx950_run(self.n, self.k, _ptr(x), _ptr(w), _ld(w), _ptr(scale),
+        ldw = _ld(w) if self.k > 0 else 1
+        st = lib().gemv_s8w_m1_bf16_gfx950_run(self.n, self.k, _ptr(x), _ptr(w), ldw, _ptr(scale),
                                                _ptr(d), None, 0, _stream(stream))
         check(st, "GemvS8wPlan::run")
 

@@ -79,7 +79,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="run only: w8a8|gemv|fp8|moe|gather (profiling)")
+    ap.add_argument("--only", default="",
+                    help="run only: w8a8|gemv|fp8|moe|gather|copy (profiling; copy = 256 MiB "
+                         "device copy used to calibrate the HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -96,6 +98,13 @@ def main():
     stream = torch.cuda.current_stream()
     only = args.only
     result = {}
+    if only == "copy":
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        cms = time_launches(lambda: dst.copy_(src), args.steps, args.warmup, stream)
+        print(json.dumps({"copy_bytes_each_way": 256 << 20, "us": round(cms * 1e3, 2),
+                          "GB_s_read_plus_write": round(2 * (256 << 20) / (cms * 1e-3) / 1e9, 1)}))
+        return
 
     # ---- headline: W8A8 4096^3 -------------------------------------------------
     M = N = K = 4096

@@ -164,11 +164,12 @@ BK_GATHER_DECL(f32)
 /* ======================= grouped MoE int8 GEMM ===========================
  * New SKU in the moe_wmma family; argument order of
  * baracuda_kernels_moe_wmma_bf16_run (crates/baracuda-kernels-sys/kernels/moe/moe_wmma.cu:154-175)
- * plus scale_a [tokens] and scale_w [E*N].  Routing: pairs grouped by expert
+ * plus scale_a (one f32 per input row) and scale_w [E*N].  Routing: pairs grouped by expert
  * through sorted_token_ids / expert_ids; input row = id / topk (id when
  * topk_weights != NULL); output row = id; expert_counts [E] and
  * expert_offsets [E+1] are caller buffers filled by the call.
- * out[id,n] = bf16_rne(((scale_a[in_row]*scale_w[e*N+n]) * acc) [* topk_weights[id]]). */
+ * out[id,n] = bf16_rne(((scale_a[in_row]*scale_w[e*N+n]) * acc) [* topk_weights[id]]).
+ * Each of the two products is rounded to f32 in that order. */
 int32_t baracuda_kernels_moe_s8_grouped_bf16_gfx950_run(
     const void *input, const void *weights, const int32_t *sorted_token_ids,
     const int32_t *expert_ids, const float *topk_weights, void *output,

@@ -42,11 +42,25 @@ def _gemv_run(w, scale, xb):
     return host_bits16(d)
 
 
-@pytest.mark.parametrize("shape", [(14336, 4096), (4096, 14336), (1, 1024), (77, 3000), (1000, 17), (33, 0)])
+@pytest.mark.parametrize("shape", [(14336, 4096), (4096, 14336), (1, 1024), (77, 3000), (1000, 17)])
 def test_gemv_s8w(gpu, shape):
     print(f"case: gemv_s8w {shape}", flush=True)
     w, scale, xb = _gemv_inputs(*shape)
     _gemv_check(_gemv_run(w, scale, xb), w, scale, xb)
+
+
+def test_gemv_s8w_empty_reduction(gpu):
+    # K == 0 with valid (non-null) buffers: every output is bf16(0 * scale) = 0.
+    n = 33
+    w = torch.empty((n, 1), dtype=torch.int8, device="cuda:0")[:, :0]
+    x = torch.empty(1, dtype=torch.bfloat16, device="cuda:0")[:0]
+    d = torch.full((n,), 5.0, dtype=torch.bfloat16, device="cuda:0")
+    scale = torch.ones(n, device="cuda:0")
+    st = lib().gemv_s8w_m1_bf16_gfx950_run(n, 0, x.data_ptr(), w.data_ptr(), 1,
+                                           scale.data_ptr(), d.data_ptr(),
+                                           None, 0, torch.cuda.current_stream().cuda_stream)
+    sync()
+    assert st == 0 and torch.all(d == 0)
 
 
 def test_gemv_s8w_graph_replay_bit_identical(gpu):

@@ -19,12 +19,14 @@ def _run(tokens, E, topk, n, k, seed, topk_w=False, pairs_check=None):
     sa = g.uniform(0.005, 0.02, tokens).astype(np.float32)
     sw = g.uniform(0.001, 0.01, E * n).astype(np.float32)
     tw = g.uniform(0.1, 1.0, size_m).astype(np.float32) if topk_w else None
-    xin = x if not topk_w else np.repeat(x, topk, axis=0)   # topk_weights form reads row = pair id
+    # topk_weights form reads input row = pair id: expand x and its per-row scales
+    xin = x if not topk_w else np.repeat(x, topk, axis=0)
+    sa_in = sa if not topk_w else np.repeat(sa, topk)
     out = torch.zeros((size_m, n), dtype=torch.bfloat16, device="cuda:0")
     counts = torch.zeros(E, dtype=torch.int32, device="cuda:0")
     offs = torch.zeros(E + 1, dtype=torch.int32, device="cuda:0")
     plan = P.MoeS8GroupedPlan.select(E, topk, size_m, n, k)
-    plan.run(dev(xin), dev(w), dev(sorted_ids), dev(expert_ids), out, counts, offs, dev(sa), dev(sw),
+    plan.run(dev(xin), dev(w), dev(sorted_ids), dev(expert_ids), out, counts, offs, dev(sa_in), dev(sw),
              topk_weights=dev(tw) if tw is not None else None)
     sync()
     c_ref, o_ref = O.moe_expert_offsets(expert_ids, E)
