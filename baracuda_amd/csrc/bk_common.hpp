@@ -41,6 +41,16 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float x) {
     return (uint16_t)((bits + bias) >> 16);
 }
 
+// Two f32 -> packed bf16x2 (low half = lo) with the gfx950 conversion
+// instruction v_cvt_pk_bf16_f32: round to nearest even, so finite values
+// round exactly like f32_to_bf16_rne (a NaN stays a quiet NaN, payload not
+// guaranteed).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
+}
+
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
     return __uint_as_float((uint32_t)b << 16);
 }

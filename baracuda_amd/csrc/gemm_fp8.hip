@@ -1,5 +1,7 @@
-// gemm_fp8.hip -- FP8 E4M3 (OCP e4m3fn) RCR GEMM SKUs for gfx950
-// (v_mfma_f32_16x16x128_f8f6f4 with both operands in e4m3, f32 accumulator).
+// gemm_fp8.hip -- FP8 E4M3 (OCP e4m3fn) RCR GEMM SKUs for gfx950, both
+// operands e4m3, f32 accumulator (v_mfma_f32_32x32x64_f8f6f4 on the LDS-DMA
+// path for whole 256x256 tiles, v_mfma_f32_16x16x128_f8f6f4 on the general
+// path).
 //
 // Replaces baracuda_kernels_gemm_fp8_e4m3_rcr_sm89_*
 // (crates/baracuda-kernels-sys/kernels/gemm/gemm_fp8_e4m3_rcr_sm89.cu:31-67,
@@ -8,6 +10,7 @@
 //   _bf16    D = bf16_rne((scale_a*scale_b) * acc)          new SKU (per-tensor scales)
 //   _f32     D = alpha * acc                                 new SKU (accumulator check)
 #include "gemm_mfma.hpp"
+#include "gemm_mfma2.hpp"
 
 namespace bk {
 namespace {
@@ -25,32 +28,14 @@ struct F8Args {
     float alpha, beta;
 };
 
-template <int EPI, bool Checked, bool VecOut>
-__global__ __launch_bounds__(NT, 1) void gemm_fp8_rcr_kernel(F8Args p) {
-    __shared__ __attribute__((aligned(16))) int8_t lds[4 * LDS_TILE];
-    const int tiles_m = (p.M + BM - 1) / BM;
-    const int tiles_n = (p.N + BN - 1) / BN;
-    int tm, tn;
-    tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
-    const int m_base = tm * BM, n_base = tn * BN;
-
-    const int tid = threadIdx.x;
-    RowSet as, bs;
-#pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-        const int r = i * LOAD_ROWS + (tid >> 3);
-        const int am = min(m_base + r, p.M - 1), bn = min(n_base + r, p.N - 1);
-        as.ptr[i] = p.a + (int64_t)am * p.lda;
-        bs.ptr[i] = p.b + (int64_t)bn * p.ldb;
-    }
-    v4f acc[TM][TN];
-    mainloop<Elem::E4M3, Checked>(lds, as, bs, p.K, acc);
-
-    for_each_fragment(acc, [&](int ml, int nl, const v4f &v) {
-        const int m = m_base + ml, n0 = n_base + nl;
+// Epilogue on one group of 4 consecutive output columns of row m.
+template <int EPI, bool VecOut>
+struct F8Epilogue {
+    const F8Args &p;
+    __device__ __forceinline__ void operator()(int m, int n0, const v4f &v) const {
         if (m >= p.M || n0 >= p.N) return;
-        const int count = p.N - n0 < 4 ? p.N - n0 : 4;
-        const bool vec = VecOut && count == 4;
+        const int count = VecOut ? 4 : (p.N - n0 < 4 ? p.N - n0 : 4);
+        const bool vec = VecOut;
         float y[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) y[r] = p.alpha * v[r];
@@ -75,27 +60,77 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_rcr_kernel(F8Args p) {
         } else {
             store4_f32(static_cast<float *>(p.d) + (int64_t)m * p.ldd + n0, y, vec, count);
         }
-    });
+    }
+};
+
+// General path: register-staged mainloop (K tail / unaligned / partial tiles).
+template <int EPI, bool VecOut>
+__global__ __launch_bounds__(NT, 1) void gemm_fp8_rcr_kernel(F8Args p) {
+    __shared__ __attribute__((aligned(16))) int8_t lds[4 * LDS_TILE];
+    const int tiles_m = (p.M + BM - 1) / BM;
+    const int tiles_n = (p.N + BN - 1) / BN;
+    int tm, tn;
+    tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int m_base = tm * BM, n_base = tn * BN;
+    const int tid = threadIdx.x;
+    RowSet as, bs;
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+        const int r = i * LOAD_ROWS + (tid >> 3);
+        const int am = min(m_base + r, p.M - 1), bn = min(n_base + r, p.N - 1);
+        as.ptr[i] = p.a + (int64_t)am * p.lda;
+        bs.ptr[i] = p.b + (int64_t)bn * p.ldb;
+    }
+    v4f acc[TM][TN];
+    mainloop<Elem::E4M3, true>(lds, as, bs, p.K, acc);
+    const F8Epilogue<EPI, VecOut> epi{p};
+    for_each_fragment(acc, [&](int ml, int nl, const v4f &v) { epi(m_base + ml, n_base + nl, v); });
 }
 
-template <int EPI, bool Checked>
-void launch_vec(const F8Args &p, bool vec, hipStream_t stream) {
-    const int tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
-    if (vec)
-        hipLaunchKernelGGL((gemm_fp8_rcr_kernel<EPI, Checked, true>), dim3(tiles), dim3(NT), 0, stream, p);
-    else
-        hipLaunchKernelGGL((gemm_fp8_rcr_kernel<EPI, Checked, false>), dim3(tiles), dim3(NT), 0, stream, p);
+// Fast path: whole 256x256 tiles, K % 128 == 0, 16-byte rows -> LDS-DMA
+// mainloop, 8 waves (2 x 4) of 128 x 64, v_mfma_f32_32x32x64_f8f6f4.
+typedef mfma2::Cfg<2, 4, 0> DmaCfg;
+
+template <int EPI, bool VecOut>
+__global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_fp8_rcr_dma_kernel(F8Args p) {
+    namespace M2 = mfma2;
+    typedef M2::PolicyF8<DmaCfg> P;
+    __shared__ __attribute__((aligned(1024))) int8_t stage0[2 * M2::OPER];
+    __shared__ __attribute__((aligned(1024))) int8_t stage1[2 * M2::OPER];
+    int tm, tn;
+    tile_coords(blockIdx.x, p.M / M2::BM, p.N / M2::BN, tm, tn);
+    const int m_base = tm * M2::BM, n_base = tn * M2::BN;
+    M2::DmaRows<false, false> d;
+    d.a = M2::make_dma_interior<DmaCfg>(p.a, (uint32_t)(p.M * p.lda), (int)p.lda, m_base * (int)p.lda);
+    d.b = M2::make_dma_interior<DmaCfg>(p.b, (uint32_t)(p.N * p.ldb), (int)p.ldb, n_base * (int)p.ldb);
+    M2::AccTile<P> acc;
+    M2::mainloop<P>(stage0, stage1, d, p.K, acc);
+    const F8Epilogue<EPI, VecOut> epi{p};
+    M2::for_each_quad<P>(acc, [&](int ml, int nl, const v4f &v) { epi(m_base + ml, n_base + nl, v); });
+}
+
+template <int EPI, bool VecOut>
+void launch_kernel(const F8Args &p, bool fast, hipStream_t stream) {
+    if (fast) {
+        const int tiles = (p.M / mfma2::BM) * (p.N / mfma2::BN);
+        hipLaunchKernelGGL((gemm_fp8_rcr_dma_kernel<EPI, VecOut>), dim3(tiles), dim3(DmaCfg::NT), 0, stream, p);
+    } else {
+        const int tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
+        hipLaunchKernelGGL((gemm_fp8_rcr_kernel<EPI, VecOut>), dim3(tiles), dim3(NT), 0, stream, p);
+    }
 }
 
 template <int EPI>
 int32_t launch(const F8Args &p, hipStream_t stream) {
     const int out_elem = EPI == EPI_F32 ? 4 : (EPI == EPI_BF16 ? 2 : 1);
-    const bool fast_k = p.K % BK == 0 && p.lda % 16 == 0 && p.ldb % 16 == 0 &&
-                        aligned16(p.a) && aligned16(p.b);
+    // The DMA path needs whole 256x256 tiles, whole K stages and 16-byte rows.
+    const bool fast = p.K % BK == 0 && p.lda % 16 == 0 && p.ldb % 16 == 0 && aligned16(p.a) &&
+                      aligned16(p.b) && p.M % mfma2::BM == 0 && p.N % mfma2::BN == 0 &&
+                      (int64_t)p.M * p.lda < (1ll << 31) && (int64_t)p.N * p.ldb < (1ll << 31);
     const bool vec = p.ldd % 4 == 0 && (reinterpret_cast<uintptr_t>(p.d) % (4 * out_elem)) == 0 &&
                      p.N % 4 == 0;
-    if (fast_k) launch_vec<EPI, false>(p, vec, stream);
-    else launch_vec<EPI, true>(p, vec, stream);
+    if (vec) launch_kernel<EPI, true>(p, fast, stream);
+    else launch_kernel<EPI, false>(p, fast, stream);
     return launch_status();
 }
 

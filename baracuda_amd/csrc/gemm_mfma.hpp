@@ -11,9 +11,12 @@
 //
 // LDS: A and B tiles are [256 rows][128 bytes], double buffered (128 KiB).
 // Rows are 128 B, so every row starts on the same bank; the 16-byte unit u
-// of row r is stored at unit u ^ swz(r), swz(r) = (r ^ (r >> 3)) & 7, which
-// makes the 16 rows read by one ds_read_b128 quarter-wave land on distinct
-// bank groups (and the 8 units written per row by a global-load row, too).
+// of row r is stored at unit u ^ swz(r), swz(r) = (r >> 1) & 7, the XOR
+// pattern measured bank-conflict free on gfx950 for these ds_read_b128 /
+// ds_write_b128 patterns.
+//
+// This register-staged mainloop serves the general case (K tail, unaligned
+// rows); aligned problems take the LDS-DMA mainloop of gemm_mfma2.hpp.
 //
 // MFMA operand roles are swapped (srcA = B rows, srcB = A rows) so the
 // 16x16 result lane l holds C[m = l%16][n = 4*(l/16) + r], r = 0..3: four
@@ -44,7 +47,7 @@ constexpr int LDS_TILE = BM * BK;   // 32 KiB per operand per stage
 constexpr int LOAD_ROWS = NT / 8;   // rows covered by one 16-byte load wave (64)
 constexpr int LOADS = BM / LOAD_ROWS;  // 4 loads per operand per stage
 
-__device__ __forceinline__ int swz(int r) { return (r ^ (r >> 3)) & 7; }
+__device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
 
 __device__ __forceinline__ int lds_off(int row, int unit) {
     return row * BK + ((unit ^ swz(row)) << 4);
@@ -214,8 +217,8 @@ __device__ __forceinline__ void for_each_fragment(const AccV (&acc)[TM][TN], F &
 __device__ __forceinline__ void store4_bf16(uint16_t *d, const float (&y)[4], bool vec, int count) {
     if (vec) {
         v2i w;
-        w[0] = (int)((uint32_t)f32_to_bf16_rne(y[0]) | ((uint32_t)f32_to_bf16_rne(y[1]) << 16));
-        w[1] = (int)((uint32_t)f32_to_bf16_rne(y[2]) | ((uint32_t)f32_to_bf16_rne(y[3]) << 16));
+        w[0] = (int)f32x2_to_bf16x2(y[0], y[1]);
+        w[1] = (int)f32x2_to_bf16x2(y[2], y[3]);
         *reinterpret_cast<v2i *>(d) = w;
     } else {
         for (int r = 0; r < 4; ++r) if (r < count) d[r] = f32_to_bf16_rne(y[r]);

@@ -1,0 +1,378 @@
+// gemm_mfma2.hpp -- the fast gfx950 MFMA mainloop (aligned problems) shared
+// by the int8 / FP8 RCR GEMMs and the grouped MoE GEMM.
+//
+// C[m,n] = sum_k A[m,k] * B[n,k]; A row-major [M,K], B row-major [N,K] (the
+// RCR "column-major [K,N]" operand).  Requirements checked by the launcher:
+// K % 128 == 0, lda % 16 == 0, ldb % 16 == 0, 16-byte aligned bases.
+//
+// Block tile 256(M) x 256(N), 256 threads = 4 wave64 (2 x 2), each wave owns
+// a 128 x 128 output tile (256 accumulator registers, kept in AGPRs; one wave
+// per SIMD).  K advances 128 bytes per stage, two stages in flight.
+//
+// Global -> LDS: direct DMA (global_load_lds_dwordx4), no staging registers.
+// One DMA instruction writes 1 KiB of LDS linearly (lane L -> bytes 16L..16L+15)
+// = 8 rows of 128 bytes; lane L fetches the logical 16-byte unit
+// u = (L % 8) ^ swz(row) of row (L / 8), so the LDS image is the row-major
+// tile with unit u of row r at physical unit u ^ swz(r).  swz(r) = (r >> 1) & 7
+// is the XOR pattern measured bank-conflict free on gfx950 for every
+// ds_read_b128 fragment pattern used below (16-row int8 and 32-row fp8 frags).
+//
+// Per stage and wave: 2 sub-steps of 64 bytes of K.  Fragments of the next
+// sub-step are read from LDS while the MFMAs of the current one run (two
+// register sets F0/F1); the only barrier per stage sits in the middle of the
+// second sub-step's MFMAs, after which the next stage's first fragments are
+// requested.  The two stage buffers are distinct __shared__ arrays and the
+// loop is unrolled by two, so the DMA into one buffer is never mistaken for a
+// write to the buffer being read (no spurious vmcnt waits before ds_reads).
+//
+// Both operand fragments use the same lane -> (row, k) mapping, so every k is
+// paired with itself whatever the hardware's intra-instruction K order is:
+// integer results are exact.
+#pragma once
+
+#include "bk_common.hpp"
+
+namespace bk {
+namespace mfma2 {
+
+constexpr int BM = 256;
+constexpr int BN = 256;
+constexpr int BK = 128;
+constexpr int OPER = BM * BK;        // 32 KiB per operand per stage
+
+// Block configuration: WAVES_M x WAVES_N wave64s, each owning a
+// (256 / WAVES_M) x (256 / WAVES_N) output tile.  PIPE 0: per sub-step,
+// read its fragments then issue its MFMAs (latency hidden by the other wave
+// of the SIMD); PIPE 1: two fragment register sets, the next sub-step's
+// fragments are read while the current sub-step's MFMAs run.
+template <int WAVES_M_, int WAVES_N_, int PIPE_>
+struct Cfg {
+    static constexpr int WAVES_M = WAVES_M_;
+    static constexpr int WAVES_N = WAVES_N_;
+    static constexpr int PIPE = PIPE_;
+    static constexpr int WAVES = WAVES_M * WAVES_N;
+    static constexpr int NT = 64 * WAVES;
+    static constexpr int WM = BM / WAVES_M;
+    static constexpr int WN = BN / WAVES_N;
+    static constexpr int ROWS_PER_WAVE = BM / WAVES;       // DMA rows per wave per operand
+    static constexpr int DMA_PER_WAVE = ROWS_PER_WAVE / 8;  // 1 KiB DMA instructions
+};
+
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
+__device__ __forceinline__ int lds_off(int row, int unit) { return row * BK + ((unit ^ swz(row)) << 4); }
+
+// ---------------------------------------------------------------------------
+// MFMA policies
+// ---------------------------------------------------------------------------
+// int8: v_mfma_i32_16x16x64_i8.  Wave tile = 8 x 8 tiles of 16x16.
+template <class C>
+struct PolicyI8 {
+    typedef C Cfg;
+    static constexpr int TI = C::WM / 16;    // 16x16 tiles per wave along M
+    static constexpr int TJ = C::WN / 16;    // ... along N
+    typedef v4i Acc;
+    typedef v4i Frag;
+    __device__ static Frag load(const int8_t *op, int row0, int t, int s, int lane) {
+        const int row = row0 + t * 16 + (lane & 15);
+        return *reinterpret_cast<const v4i *>(op + lds_off(row, s * 4 + (lane >> 4)));
+    }
+    static constexpr int H = 1;
+    __device__ static void mma(Acc &c, const Frag &b, const Frag &a, int) {
+        c = __builtin_amdgcn_mfma_i32_16x16x64_i8(b, a, c, 0, 0, 0);
+    }
+    __device__ static Acc zero() { return Acc{0, 0, 0, 0}; }
+    // Accumulator tile (i, j) -> groups of 4 consecutive columns.
+    template <class F>
+    __device__ static void visit(const Acc &c, int i, int j, int lane, F &&f) {
+        f(i * 16 + (lane & 15), j * 16 + (lane >> 4) * 4, v4i{c[0], c[1], c[2], c[3]});
+    }
+};
+
+// int8: v_mfma_i32_32x32x32_i8 (sustains ~25% more int8 ops/clk than the
+// 16x16x64 form on gfx950 with random operands).  Wave tile = TI x TJ tiles
+// of 32x32; a 64-byte sub-step of K is two instructions (h = 0, 1), lane l
+// supplying row l % 32 and the 16-byte unit s*4 + 2h + l/32.
+template <class C>
+struct PolicyI8x32 {
+    typedef C Cfg;
+    static constexpr int TI = C::WM / 32;
+    static constexpr int TJ = C::WN / 32;
+    typedef v16i Acc;
+    struct Frag { v4i h[2]; };
+    __device__ static Frag load(const int8_t *op, int row0, int t, int s, int lane) {
+        const int row = row0 + t * 32 + (lane & 31);
+        Frag f;
+        f.h[0] = *reinterpret_cast<const v4i *>(op + lds_off(row, s * 4 + (lane >> 5)));
+        f.h[1] = *reinterpret_cast<const v4i *>(op + lds_off(row, s * 4 + 2 + (lane >> 5)));
+        return f;
+    }
+    static constexpr int H = 2;   // instructions per sub-step per tile
+    __device__ static void mma(Acc &c, const Frag &b, const Frag &a, int h) {
+        c = __builtin_amdgcn_mfma_i32_32x32x32_i8(b.h[h], a.h[h], c, 0, 0, 0);
+    }
+    __device__ static Acc zero() { return Acc{0}; }
+    // 32x32 result: lane holds column m = lane % 32 and, for g = 0..3, rows
+    // n = 8g + 4*(lane/32) + 0..3 in registers 4g..4g+3.
+    template <class F>
+    __device__ static void visit(const Acc &c, int i, int j, int lane, F &&f) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+            f(i * 32 + (lane & 31), j * 32 + g * 8 + (lane >> 5) * 4,
+              v4i{c[4 * g], c[4 * g + 1], c[4 * g + 2], c[4 * g + 3]});
+    }
+};
+
+// fp8 e4m3: v_mfma_f32_32x32x64_f8f6f4.  Wave tile = 4 x 4 tiles of 32x32.
+template <class C>
+struct PolicyF8 {
+    typedef C Cfg;
+    static constexpr int TI = C::WM / 32;
+    static constexpr int TJ = C::WN / 32;
+    typedef v16f Acc;
+    typedef v8i Frag;
+    __device__ static Frag load(const int8_t *op, int row0, int t, int s, int lane) {
+        const int row = row0 + t * 32 + (lane & 31);
+        const int u = s * 4 + (lane >> 5) * 2;
+        const v4i lo = *reinterpret_cast<const v4i *>(op + lds_off(row, u));
+        const v4i hi = *reinterpret_cast<const v4i *>(op + lds_off(row, u + 1));
+        return Frag{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    }
+    static constexpr int H = 1;
+    __device__ static void mma(Acc &c, const Frag &b, const Frag &a, int) {
+        c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(b, a, c, 0, 0, 0, 0, 0, 0);
+    }
+    __device__ static Acc zero() { return Acc{0}; }
+    // 32x32 result: lane holds column m = lane % 32 and, for g = 0..3, rows
+    // n = 8g + 4*(lane/32) + 0..3 in registers 4g..4g+3.
+    template <class F>
+    __device__ static void visit(const Acc &c, int i, int j, int lane, F &&f) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+            f(i * 32 + (lane & 31), j * 32 + g * 8 + (lane >> 5) * 4,
+              v4f{c[4 * g], c[4 * g + 1], c[4 * g + 2], c[4 * g + 3]});
+    }
+};
+
+template <class P>
+struct Frags {
+    typename P::Frag a[P::TI];
+    typename P::Frag b[P::TJ];
+};
+
+template <class P>
+using AccTile = typename P::Acc[P::TI][P::TJ];
+
+template <class P>
+__device__ __forceinline__ void load_frags(Frags<P> &f, const int8_t *stage, int s, int wave_m,
+                                           int wave_n, int lane) {
+#pragma unroll
+    for (int t = 0; t < P::TJ; ++t) f.b[t] = P::load(stage + OPER, wave_n * P::Cfg::WN, t, s, lane);
+#pragma unroll
+    for (int t = 0; t < P::TI; ++t) f.a[t] = P::load(stage, wave_m * P::Cfg::WM, t, s, lane);
+}
+
+// MFMAs of one sub-step over tile columns J0..J1-1.  The instruction index h
+// is outermost so consecutive MFMAs never chain on the same accumulator.
+template <class P, int J0, int J1>
+__device__ __forceinline__ void mma_block(AccTile<P> &acc, const Frags<P> &f) {
+#pragma unroll
+    for (int h = 0; h < P::H; ++h)
+#pragma unroll
+        for (int j = J0; j < J1; ++j)
+#pragma unroll
+            for (int i = 0; i < P::TI; ++i) P::mma(acc[i][j], f.b[j], f.a[i], h);
+}
+
+// Buffer resource (V#) for a raw byte buffer: base, stride 0, num_records =
+// `bytes` (accesses at or past it read as zero), dword3 = the gfx9-family
+// raw-buffer format word.  Built wave-uniform so it lives in SGPRs.
+__device__ __forceinline__ v4i make_rsrc(const void *base, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    v4i r;
+    r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+    r[1] = __builtin_amdgcn_readfirstlane((int)(uint32_t)((a >> 32) & 0xffffu));
+    r[2] = __builtin_amdgcn_readfirstlane((int)bytes);
+    r[3] = 0x00020000;
+    return r;
+}
+
+// Per-thread DMA sources of one operand.  DMA instruction i (0..7) of a wave
+// covers tile rows wave*64 + 8i .. +7; lane L fetches row (L/8) of that
+// group at unit (L%8) ^ swz(row).
+//
+// Interior operand (every row of the tile is a real, evenly spaced row): swz
+// of the row depends on i only through (4i & 7), so the per-lane byte offset
+// is `even` (i even) or `odd` (i odd) plus the wave-uniform 8*i*ld, which
+// travels in the scalar offset with the K position: 2 VGPRs per operand.
+// Gathered operand (rows chosen by an index, e.g. MoE token rows): one
+// per-lane offset per instruction, 8 VGPRs.
+template <bool Gathered>
+struct DmaOperand;
+
+template <>
+struct DmaOperand<false> {
+    v4i rsrc;
+    int even, odd;
+    int row_stride;     // 8 * ld, bytes
+};
+
+template <>
+struct DmaOperand<true> {
+    v4i rsrc;
+    int off[8];         // DMA_PER_WAVE used
+};
+
+// Interior operand: tile rows r0 .. r0+255 of a row-major operand with
+// leading dimension ld (bytes), starting at byte `tile_off` of the buffer.
+template <class C>
+__device__ __forceinline__ DmaOperand<false> make_dma_interior(const int8_t *base, uint32_t bytes,
+                                                               int ld, int tile_off) {
+    constexpr int ROWS_PER_WAVE = C::ROWS_PER_WAVE;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    DmaOperand<false> d;
+    d.rsrc = make_rsrc(base, bytes);
+    d.row_stride = 8 * ld;
+    const int r0 = wave * ROWS_PER_WAVE + (lane >> 3);
+    const int u0 = (lane & 7) ^ swz(r0);
+    d.even = tile_off + r0 * ld + u0 * 16;
+    d.odd = tile_off + r0 * ld + (u0 ^ 4) * 16;
+    return d;
+}
+
+// Gathered operand: `row_off(r)` gives the byte offset of tile row r.
+template <class C, class RowOff>
+__device__ __forceinline__ DmaOperand<true> make_dma_gathered(const int8_t *base, uint32_t bytes,
+                                                              RowOff &&row_off) {
+    constexpr int ROWS_PER_WAVE = C::ROWS_PER_WAVE;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    DmaOperand<true> d;
+    d.rsrc = make_rsrc(base, bytes);
+#pragma unroll
+    for (int i = 0; i < C::DMA_PER_WAVE; ++i) {
+        const int r = wave * ROWS_PER_WAVE + i * 8 + (lane >> 3);
+        d.off[i] = row_off(r) + ((lane & 7) ^ swz(r)) * 16;
+    }
+    return d;
+}
+
+// One LDS-DMA transfer: 16 bytes per lane from rsrc[voff + soff] into LDS at
+// `lds_dst + 16 * lane` (lds_dst wave-uniform, passed through M0).  Issued as
+// inline asm so the compiler's wait-count pass does not treat consecutive
+// DMAs into one buffer as dependent (it would wait vmcnt(0) before each);
+// completion is awaited explicitly by wait_dma() before the stage barrier.
+__device__ __forceinline__ void dma16(const v4i &rsrc, int voff, int soff, const int8_t *lds_dst) {
+    const uint32_t lds = __builtin_amdgcn_readfirstlane(
+        (uint32_t)reinterpret_cast<uintptr_t>((lds_void *)lds_dst));
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :
+                 : "s"(lds), "v"(voff), "s"(rsrc), "s"(soff)
+                 : "memory", "m0");
+}
+
+__device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+template <class C>
+__device__ __forceinline__ void dma_operand(int8_t *dst, const DmaOperand<false> &d, int kbyte) {
+    constexpr int ROWS_PER_WAVE = C::ROWS_PER_WAVE;
+    const int wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int i = 0; i < C::DMA_PER_WAVE; ++i) {
+        const int soff = __builtin_amdgcn_readfirstlane(kbyte + i * d.row_stride);
+        dma16(d.rsrc, (i & 1) ? d.odd : d.even, soff, dst + (wave * ROWS_PER_WAVE + i * 8) * BK);
+    }
+}
+
+template <class C>
+__device__ __forceinline__ void dma_operand(int8_t *dst, const DmaOperand<true> &d, int kbyte) {
+    constexpr int ROWS_PER_WAVE = C::ROWS_PER_WAVE;
+    const int wave = threadIdx.x >> 6;
+    const int soff = __builtin_amdgcn_readfirstlane(kbyte);
+#pragma unroll
+    for (int i = 0; i < C::DMA_PER_WAVE; ++i) dma16(d.rsrc, d.off[i], soff, dst + (wave * ROWS_PER_WAVE + i * 8) * BK);
+}
+
+template <bool GA, bool GB>
+struct DmaRows {
+    DmaOperand<GA> a;
+    DmaOperand<GB> b;
+};
+
+template <class C, class D>
+__device__ __forceinline__ void dma_stage(int8_t *stage, const D &d, int kbyte) {
+    dma_operand<C>(stage, d.a, kbyte);
+    dma_operand<C>(stage + OPER, d.b, kbyte);
+}
+
+// One stage: compute from `cur`, stream the next stage into `nxt` (if any).
+// PIPE 1: F0 already holds `cur`'s sub-step 0 fragments on entry and holds
+// `nxt`'s on exit.
+template <class P, class D>
+__device__ __forceinline__ void stage_step(AccTile<P> &acc, Frags<P> &f0, Frags<P> &f1,
+                                           const int8_t *cur, int8_t *nxt, const D &d, int next_k,
+                                           bool has_next, int wave_m, int wave_n, int lane) {
+    typedef typename P::Cfg C;
+    if (has_next) dma_stage<C>(nxt, d, next_k);
+    if constexpr (C::PIPE == 0) {
+        load_frags<P>(f0, cur, 0, wave_m, wave_n, lane);
+        mma_block<P, 0, P::TJ>(acc, f0);
+        load_frags<P>(f1, cur, 1, wave_m, wave_n, lane);
+        mma_block<P, 0, P::TJ>(acc, f1);
+        wait_dma();        // this wave's DMA into `nxt` has landed
+        __syncthreads();   // ... and every wave's; every wave is done reading `cur`
+    } else {
+        load_frags<P>(f1, cur, 1, wave_m, wave_n, lane);
+        mma_block<P, 0, P::TJ>(acc, f0);
+        mma_block<P, 0, P::TJ / 2>(acc, f1);
+        wait_dma();
+        __syncthreads();
+        if (has_next) load_frags<P>(f0, nxt, 0, wave_m, wave_n, lane);
+        mma_block<P, P::TJ / 2, P::TJ>(acc, f1);
+    }
+}
+
+// Full K loop for one 256x256 tile.  s0 / s1 are the two stage buffers
+// (each 2 * OPER bytes: A then B).  Ends with a barrier.
+template <class P, class D>
+__device__ __forceinline__ void mainloop(int8_t *s0, int8_t *s1, const D &d, int K, AccTile<P> &acc) {
+    typedef typename P::Cfg C;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wave_m = wave / C::WAVES_N, wave_n = wave % C::WAVES_N;
+#pragma unroll
+    for (int i = 0; i < P::TI; ++i)
+#pragma unroll
+        for (int j = 0; j < P::TJ; ++j) acc[i][j] = P::zero();
+
+    const int KT = K / BK;
+    Frags<P> f0, f1;
+    dma_stage<C>(s0, d, 0);
+    wait_dma();
+    __syncthreads();
+    if constexpr (C::PIPE == 1) load_frags<P>(f0, s0, 0, wave_m, wave_n, lane);
+    int kt = 0;
+    for (; kt + 2 <= KT; kt += 2) {
+        stage_step<P>(acc, f0, f1, s0, s1, d, (kt + 1) * BK, true, wave_m, wave_n, lane);
+        stage_step<P>(acc, f0, f1, s1, s0, d, (kt + 2) * BK, kt + 2 < KT, wave_m, wave_n, lane);
+    }
+    if (kt < KT) stage_step<P>(acc, f0, f1, s0, s1, d, 0, false, wave_m, wave_n, lane);
+}
+
+// Visit this thread's accumulators: f(m_local, n0_local, quad) with quad the
+// values of columns n0..n0+3 of row m.
+template <class P, class F>
+__device__ __forceinline__ void for_each_quad(const AccTile<P> &acc, F &&f) {
+    typedef typename P::Cfg C;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = (wave / C::WAVES_N) * C::WM, wn = (wave % C::WAVES_N) * C::WN;
+#pragma unroll
+    for (int i = 0; i < P::TI; ++i)
+#pragma unroll
+        for (int j = 0; j < P::TJ; ++j)
+            P::visit(acc[i][j], i, j, lane, [&](int m, int n0, auto q) { f(wm + m, wn + n0, q); });
+}
+
+}  // namespace mfma2
+}  // namespace bk

@@ -14,6 +14,7 @@
 // saturates; the two agree whenever |acc| < 2^31, which holds for int8
 // operands in [-127,127] whenever K < 133143.
 #include "gemm_mfma.hpp"
+#include "gemm_mfma2.hpp"
 
 namespace bk {
 namespace {
@@ -32,32 +33,15 @@ struct S8Args {
     const float *sa; const float *sw;
 };
 
-template <int EPI, bool Checked, bool VecOut>
-__global__ __launch_bounds__(NT, 1) void gemm_s8_rcr_kernel(S8Args p) {
-    __shared__ __attribute__((aligned(16))) int8_t lds[4 * LDS_TILE];
-    const int tiles_m = (p.M + BM - 1) / BM;
-    const int tiles_n = (p.N + BN - 1) / BN;
-    int tm, tn;
-    tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
-    const int m_base = tm * BM, n_base = tn * BN;
-
-    const int tid = threadIdx.x;
-    RowSet as, bs;
-#pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-        const int r = i * LOAD_ROWS + (tid >> 3);
-        const int am = min(m_base + r, p.M - 1), bn = min(n_base + r, p.N - 1);
-        as.ptr[i] = p.a + (int64_t)am * p.lda;
-        bs.ptr[i] = p.b + (int64_t)bn * p.ldb;
-    }
-    v4i acc[TM][TN];
-    mainloop<Elem::S8, Checked>(lds, as, bs, p.K, acc);
-
-    for_each_fragment(acc, [&](int ml, int nl, const v4i &v) {
-        const int m = m_base + ml, n0 = n_base + nl;
+// Epilogue on one group of 4 consecutive output columns of row m.
+template <int EPI, bool VecOut>
+struct S8Epilogue {
+    const S8Args &p;
+    __device__ __forceinline__ void operator()(int m, int n0, const v4i &v) const {
         if (m >= p.M || n0 >= p.N) return;
-        const int count = p.N - n0 < 4 ? p.N - n0 : 4;
-        const bool vec = VecOut && count == 4;
+        // VecOut implies N % 4 == 0, so a group is then always complete.
+        const int count = VecOut ? 4 : (p.N - n0 < 4 ? p.N - n0 : 4);
+        const bool vec = VecOut;
         if constexpr (EPI == EPI_I32) {
             int32_t *d = static_cast<int32_t *>(p.d) + (int64_t)m * p.ldd + n0;
             if (vec) *reinterpret_cast<v4i *>(d) = v;
@@ -96,30 +80,129 @@ __global__ __launch_bounds__(NT, 1) void gemm_s8_rcr_kernel(S8Args p) {
             else
                 store4_f32(static_cast<float *>(p.d) + (int64_t)m * p.ldd + n0, y, vec, count);
         }
-    });
+    }
+};
+
+// General path: register-staged mainloop (K tail / unaligned operands).
+template <int EPI, bool VecOut>
+__global__ __launch_bounds__(NT, 1) void gemm_s8_rcr_kernel(S8Args p) {
+    __shared__ __attribute__((aligned(16))) int8_t lds[4 * LDS_TILE];
+    const int tiles_m = (p.M + BM - 1) / BM;
+    const int tiles_n = (p.N + BN - 1) / BN;
+    int tm, tn;
+    tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int m_base = tm * BM, n_base = tn * BN;
+
+    const int tid = threadIdx.x;
+    RowSet as, bs;
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+        const int r = i * LOAD_ROWS + (tid >> 3);
+        const int am = min(m_base + r, p.M - 1), bn = min(n_base + r, p.N - 1);
+        as.ptr[i] = p.a + (int64_t)am * p.lda;
+        bs.ptr[i] = p.b + (int64_t)bn * p.ldb;
+    }
+    v4i acc[TM][TN];
+    mainloop<Elem::S8, true>(lds, as, bs, p.K, acc);
+    const S8Epilogue<EPI, VecOut> epi{p};
+    for_each_fragment(acc, [&](int ml, int nl, const v4i &v) { epi(m_base + ml, n_base + nl, v); });
 }
 
-template <int EPI, bool Checked>
-void launch_vec(const S8Args &p, bool vec, hipStream_t stream) {
-    const int tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
-    if (vec)
-        hipLaunchKernelGGL((gemm_s8_rcr_kernel<EPI, Checked, true>), dim3(tiles), dim3(NT), 0, stream, p);
-    else
-        hipLaunchKernelGGL((gemm_s8_rcr_kernel<EPI, Checked, false>), dim3(tiles), dim3(NT), 0, stream, p);
+// Fast path: M, N multiples of 256, K % 128 == 0, 16-byte aligned rows ->
+// LDS-DMA mainloop, 8 waves (2 x 4) of 128 x 64, v_mfma_i32_16x16x64_i8.
+typedef mfma2::Cfg<2, 4, 0> DmaCfg;
+
+template <int EPI, bool VecOut>
+__global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_s8_rcr_dma_kernel(S8Args p) {
+    namespace M2 = mfma2;
+    typedef M2::PolicyI8<DmaCfg> P;
+    __shared__ __attribute__((aligned(1024))) int8_t stage0[2 * M2::OPER];
+    __shared__ __attribute__((aligned(1024))) int8_t stage1[2 * M2::OPER];
+    const int tiles_m = p.M / M2::BM, tiles_n = p.N / M2::BN;
+    int tm, tn;
+    tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int m_base = tm * M2::BM, n_base = tn * M2::BN;
+    M2::DmaRows<false, false> d;
+    d.a = M2::make_dma_interior<DmaCfg>(p.a, (uint32_t)(p.M * p.lda), (int)p.lda, m_base * (int)p.lda);
+    d.b = M2::make_dma_interior<DmaCfg>(p.b, (uint32_t)(p.N * p.ldb), (int)p.ldb, n_base * (int)p.ldb);
+    M2::AccTile<P> acc;
+    M2::mainloop<P>(stage0, stage1, d, p.K, acc);
+    if constexpr (EPI == EPI_W8A8_BF16 && VecOut) {
+        // Whole tiles.  The dequant scales this lane needs (one per 16-row
+        // tile i, four per 16-column tile j) are fetched in one batch, the
+        // wave's 128 x 64 bf16 tile is assembled in LDS (free after the
+        // mainloop's last barrier) and written back as full 128-byte rows.
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        const int wrow = (wave / DmaCfg::WAVES_N) * DmaCfg::WM;
+        const int wcol = (wave % DmaCfg::WAVES_N) * DmaCfg::WN;
+        float sam[P::TI];
+        v4f swv[P::TJ];
+#pragma unroll
+        for (int i = 0; i < P::TI; ++i) sam[i] = p.sa[m_base + wrow + i * 16 + (lane & 15)];
+#pragma unroll
+        for (int j = 0; j < P::TJ; ++j)
+            swv[j] = *reinterpret_cast<const v4f *>(p.sw + n_base + wcol + j * 16 + (lane >> 4) * 4);
+        // Per-wave 16 KiB staging area: row r (0..127) of 128 bytes, 16-byte
+        // unit u stored at unit u ^ (r & 7).
+        int8_t *stage = (wave < 4 ? stage0 : stage1) + (wave & 3) * (DmaCfg::WM * DmaCfg::WN * 2);
+#pragma unroll
+        for (int i = 0; i < P::TI; ++i)
+#pragma unroll
+            for (int j = 0; j < P::TJ; ++j) {
+                const int r = i * 16 + (lane & 15);
+                const int col = j * 16 + (lane >> 4) * 4;            // bf16 column 0..63
+                const int unit = col >> 3, half = (col >> 2) & 1;
+                v2i w;
+                w[0] = (int)f32x2_to_bf16x2((sam[i] * swv[j][0]) * (float)acc[i][j][0],
+                                            (sam[i] * swv[j][1]) * (float)acc[i][j][1]);
+                w[1] = (int)f32x2_to_bf16x2((sam[i] * swv[j][2]) * (float)acc[i][j][2],
+                                            (sam[i] * swv[j][3]) * (float)acc[i][j][3]);
+                *reinterpret_cast<v2i *>(stage + r * 128 + ((unit ^ (r & 7)) << 4) + half * 8) = w;
+            }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int q = 0; q < DmaCfg::WM / 8; ++q) {
+            const int r = q * 8 + (lane >> 3), u = lane & 7;
+            const v4i v = *reinterpret_cast<const v4i *>(stage + r * 128 + ((u ^ (r & 7)) << 4));
+            uint16_t *dst = static_cast<uint16_t *>(p.d) + (int64_t)(m_base + wrow + r) * p.ldd +
+                            n_base + wcol + u * 8;
+            *reinterpret_cast<v4i *>(dst) = v;
+        }
+    } else {
+        const S8Epilogue<EPI, VecOut> epi{p};
+        M2::for_each_quad<P>(acc, [&](int ml, int nl, const v4i &v) { epi(m_base + ml, n_base + nl, v); });
+    }
+}
+
+template <int EPI, bool VecOut>
+void launch_kernel(const S8Args &p, bool fast_k, hipStream_t stream) {
+    if (fast_k) {
+        const int tiles = ((p.M + mfma2::BM - 1) / mfma2::BM) * ((p.N + mfma2::BN - 1) / mfma2::BN);
+        hipLaunchKernelGGL((gemm_s8_rcr_dma_kernel<EPI, VecOut>), dim3(tiles), dim3(DmaCfg::NT), 0, stream, p);
+    } else {
+        const int tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
+        hipLaunchKernelGGL((gemm_s8_rcr_kernel<EPI, VecOut>), dim3(tiles), dim3(NT), 0, stream, p);
+    }
 }
 
 template <int EPI>
 int32_t launch(const S8Args &p, hipStream_t stream) {
     const int out_elem = (EPI == EPI_I32 || EPI == EPI_W8A8_F32) ? 4 : (EPI == EPI_S8 ? 1 : 2);
-    // Unchecked loads need K to be a whole number of stages and 16-byte rows.
+    // The DMA path needs whole 256x256 tiles, whole K stages and 16-byte rows.
     const bool fast_k = p.K > 0 && p.K % BK == 0 && p.lda % 16 == 0 && p.ldb % 16 == 0 &&
-                        aligned16(p.a) && aligned16(p.b);
-    // 4-wide vector stores need every 4-column group of D (and sw) aligned.
-    const bool vec = ((p.ldd * out_elem) % (4 * out_elem)) == 0 &&
-                     (reinterpret_cast<uintptr_t>(p.d) % (4 * out_elem)) == 0 &&
-                     (p.sw == nullptr || aligned16(p.sw)) && (p.N % 4 == 0);
-    if (fast_k) launch_vec<EPI, false>(p, vec, stream);
-    else launch_vec<EPI, true>(p, vec, stream);
+                        aligned16(p.a) && aligned16(p.b) &&
+                        (int64_t)p.M * p.lda < (1ll << 31) && (int64_t)p.N * p.ldb < (1ll << 31) &&
+                        p.M % mfma2::BM == 0 && p.N % mfma2::BN == 0;
+    // 4-wide vector stores need every 4-column group of D (and sw) aligned;
+    // the LDS-staged W8A8 bf16 store writes 16-byte units (8 columns).
+    bool vec = ((p.ldd * out_elem) % (4 * out_elem)) == 0 &&
+               (reinterpret_cast<uintptr_t>(p.d) % (4 * out_elem)) == 0 &&
+               (p.sw == nullptr || aligned16(p.sw)) && (p.N % 4 == 0);
+    if (EPI == EPI_W8A8_BF16) vec = vec && p.ldd % 8 == 0 && aligned16(p.d);
+    if (vec) launch_kernel<EPI, true>(p, fast_k, stream);
+    else launch_kernel<EPI, false>(p, fast_k, stream);
     return launch_status();
 }
 

@@ -16,6 +16,7 @@
 // LDS counters (no global atomics, no memset: graph-capturable), and the GEMM
 // is one launch whose workgroups walk the ragged per-expert tile list.
 #include "gemm_mfma.hpp"
+#include "gemm_mfma2.hpp"
 
 namespace bk {
 namespace {
@@ -60,28 +61,52 @@ struct MoeArgs {
     int E, topk, size_m, N, K;
 };
 
-template <bool Checked>
+// Ragged tile list: slot -> (expert, first pair of the tile, rows in it).
+// Workgroup-uniform walk over expert_offsets; false past the last tile.
+__device__ __forceinline__ bool moe_tile(const MoeArgs &p, int slot, int &e, int &seg0, int &rows_out) {
+    for (e = 0; e < p.E; ++e) {
+        const int o0 = p.offsets[e], o1 = min(p.offsets[e + 1], p.size_m);
+        const int rows = o1 > o0 ? o1 - o0 : 0;
+        const int tiles = (rows + 255) / 256;
+        if (slot < tiles) {
+            seg0 = o0 + slot * 256;
+            rows_out = min(256, rows - slot * 256);
+            return true;
+        }
+        slot -= tiles;
+    }
+    return false;
+}
+
+// W8A8 epilogue of one group of 4 columns of tile row ml.
+__device__ __forceinline__ void moe_store(const MoeArgs &p, const int32_t *rows_tok, int seg_rows,
+                                          int in_div, const float *swe, int ml, int n0,
+                                          const v4i &v) {
+    if (ml >= seg_rows || n0 >= p.N) return;
+    const int tok = rows_tok[ml];
+    const float sam = p.sa[tok / in_div];
+    const int count = p.N - n0 < 4 ? p.N - n0 : 4;
+    float y[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) y[r] = r < count ? (sam * swe[n0 + r]) * (float)v[r] : 0.0f;
+    if (p.topk_w) {
+        const float tw = p.topk_w[tok];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) y[r] = y[r] * tw;
+    }
+    store4_bf16(p.out + (int64_t)tok * p.N + n0, y, count == 4 && (p.N % 4 == 0), count);
+}
+
+// General path (K tail / unaligned / N not a multiple of 256).
 __global__ __launch_bounds__(NT, 1) void moe_s8_grouped_kernel(MoeArgs p) {
     __shared__ __attribute__((aligned(16))) int8_t lds[4 * LDS_TILE];
     __shared__ int32_t s_rows_tok[BM];
-
-    // Ragged tile list: slot -> (expert, m-tile).  Workgroup-uniform walk.
-    int slot = blockIdx.x;
-    int e = 0, seg0 = 0, seg_rows = 0;
-    for (; e < p.E; ++e) {
-        const int o0 = p.offsets[e], o1 = min(p.offsets[e + 1], p.size_m);
-        const int rows = o1 > o0 ? o1 - o0 : 0;
-        const int tiles = (rows + BM - 1) / BM;
-        if (slot < tiles) { seg0 = o0 + slot * BM; seg_rows = min(BM, rows - slot * BM); break; }
-        slot -= tiles;
-    }
-    if (e >= p.E) return;   // past the last real tile: whole workgroup exits
+    int e, seg0, seg_rows;
+    if (!moe_tile(p, blockIdx.x, e, seg0, seg_rows)) return;   // whole workgroup exits
     const int n_base = blockIdx.y * BN;
-
     const int tid = threadIdx.x;
     for (int r = tid; r < BM; r += NT) s_rows_tok[r] = p.sorted_ids[seg0 + min(r, seg_rows - 1)];
     __syncthreads();
-
     const int in_div = p.topk_w ? 1 : p.topk;
     const int8_t *we = p.w + (int64_t)e * p.N * p.K;
     RowSet as, bs;
@@ -92,24 +117,42 @@ __global__ __launch_bounds__(NT, 1) void moe_s8_grouped_kernel(MoeArgs p) {
         bs.ptr[i] = we + (int64_t)min(n_base + r, p.N - 1) * p.K;
     }
     v4i acc[TM][TN];
-    mainloop<Elem::S8, Checked>(lds, as, bs, p.K, acc);
-
+    mainloop<Elem::S8, true>(lds, as, bs, p.K, acc);
     const float *swe = p.sw + (int64_t)e * p.N;
     for_each_fragment(acc, [&](int ml, int nl, const v4i &v) {
-        const int n0 = n_base + nl;
-        if (ml >= seg_rows || n0 >= p.N) return;
-        const int tok = s_rows_tok[ml];
-        const float sam = p.sa[tok / in_div];
-        const int count = p.N - n0 < 4 ? p.N - n0 : 4;
-        float y[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) y[r] = r < count ? (sam * swe[n0 + r]) * (float)v[r] : 0.0f;
-        if (p.topk_w) {
-            const float tw = p.topk_w[tok];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) y[r] = y[r] * tw;
-        }
-        store4_bf16(p.out + (int64_t)tok * p.N + n0, y, count == 4 && (p.N % 4 == 0), count);
+        moe_store(p, s_rows_tok, seg_rows, in_div, swe, ml, n_base + nl, v);
+    });
+}
+
+// Fast path: K % 128 == 0, N % 256 == 0, 16-byte aligned operands.  A rows
+// are gathered per tile row (token rows of the expert's segment), B is the
+// expert's weight slab.
+typedef mfma2::Cfg<2, 4, 0> DmaCfg;
+
+__global__ __launch_bounds__(DmaCfg::NT, 1) void moe_s8_grouped_dma_kernel(MoeArgs p) {
+    namespace M2 = mfma2;
+    typedef M2::PolicyI8<DmaCfg> P;
+    __shared__ __attribute__((aligned(1024))) int8_t stage0[2 * M2::OPER];
+    __shared__ __attribute__((aligned(1024))) int8_t stage1[2 * M2::OPER];
+    __shared__ int32_t s_rows_tok[M2::BM];
+    int e, seg0, seg_rows;
+    if (!moe_tile(p, blockIdx.x, e, seg0, seg_rows)) return;   // whole workgroup exits
+    const int n_base = blockIdx.y * M2::BN;
+    for (int r = threadIdx.x; r < M2::BM; r += DmaCfg::NT)
+        s_rows_tok[r] = p.sorted_ids[seg0 + min(r, seg_rows - 1)];
+    __syncthreads();
+    const int in_div = p.topk_w ? 1 : p.topk;
+    const int x_rows = p.topk_w ? p.size_m : (p.size_m + p.topk - 1) / p.topk;
+    M2::DmaRows<true, false> d;
+    d.a = M2::make_dma_gathered<DmaCfg>(p.x, (uint32_t)((int64_t)x_rows * p.K),
+                                        [&](int r) { return (s_rows_tok[r] / in_div) * p.K; });
+    d.b = M2::make_dma_interior<DmaCfg>(p.w + (int64_t)e * p.N * p.K, (uint32_t)((int64_t)p.N * p.K),
+                                        p.K, n_base * p.K);
+    M2::AccTile<P> acc;
+    M2::mainloop<P>(stage0, stage1, d, p.K, acc);
+    const float *swe = p.sw + (int64_t)e * p.N;
+    M2::for_each_quad<P>(acc, [&](int ml, int nl, const v4i &v) {
+        moe_store(p, s_rows_tok, seg_rows, in_div, swe, ml, n_base + nl, v);
     });
 }
 
@@ -161,11 +204,16 @@ int32_t baracuda_kernels_moe_s8_grouped_bf16_gfx950_run(
     // Upper bound on ragged m-tiles: sum_e ceil(cnt_e / BM) <= ceil(size_m / BM) + E.
     const int slots = (size_m + BM - 1) / BM + num_experts;
     dim3 grid(slots, (size_n + BN - 1) / BN);
-    const bool fast_k = size_k % BK == 0 && mfma::aligned16(input) && mfma::aligned16(weights);
-    if (fast_k)
-        hipLaunchKernelGGL((moe_s8_grouped_kernel<false>), grid, dim3(NT), 0, stream, p);
+    // The DMA path needs whole K stages, N a multiple of 256, 16-byte aligned
+    // operands and byte offsets that fit 32 bits (per input / per expert slab).
+    const int64_t x_rows = topk_weights ? size_m : (size_m + topk - 1) / topk;
+    const bool fast = size_k % mfma2::BK == 0 && size_n % mfma2::BN == 0 &&
+                      mfma::aligned16(input) && mfma::aligned16(weights) &&
+                      x_rows * size_k < (1ll << 31) && (int64_t)size_n * size_k < (1ll << 31);
+    if (fast)
+        hipLaunchKernelGGL(moe_s8_grouped_dma_kernel, grid, dim3(DmaCfg::NT), 0, stream, p);
     else
-        hipLaunchKernelGGL((moe_s8_grouped_kernel<true>), grid, dim3(NT), 0, stream, p);
+        hipLaunchKernelGGL(moe_s8_grouped_kernel, grid, dim3(NT), 0, stream, p);
     return launch_status();
 }
 

@@ -52,8 +52,8 @@ def test_gemv_s8w(gpu, shape):
 def test_gemv_s8w_empty_reduction(gpu):
     # K == 0 with valid (non-null) buffers: every output is bf16(0 * scale) = 0.
     n = 33
-    w = torch.empty((n, 1), dtype=torch.int8, device="cuda:0")[:, :0]
-    x = torch.empty(1, dtype=torch.bfloat16, device="cuda:0")[:0]
+    w = torch.zeros((n, 1), dtype=torch.int8, device="cuda:0")    # non-null buffers, K = 0
+    x = torch.zeros(1, dtype=torch.bfloat16, device="cuda:0")
     d = torch.full((n,), 5.0, dtype=torch.bfloat16, device="cuda:0")
     scale = torch.ones(n, device="cuda:0")
     st = lib().gemv_s8w_m1_bf16_gfx950_run(n, 0, x.data_ptr(), w.data_ptr(), 1,

@@ -49,6 +49,41 @@ def test_i32_ragged_shapes(gpu, shape):
     assert np.array_equal(_i32(a, b), O.gemm_s8_rcr_i32(a, b, nthreads=8))
 
 
+# Shapes on the LDS-DMA path (whole 256x256 tiles, K % 128 == 0): one stage,
+# an even and an odd number of stages, several tiles per XCD group.
+DMA_SHAPES = [(256, 256, 128), (256, 512, 256), (512, 256, 384), (768, 1024, 640), (2048, 512, 1152)]
+
+
+@pytest.mark.parametrize("shape", DMA_SHAPES)
+def test_i32_dma_path_shapes(gpu, shape):
+    m, n, k = shape
+    print(f"case: i32 dma {shape}", flush=True)
+    g = rng(m + 3 * n + 7 * k)
+    a, b = int8_uniform(g, (m, k)), int8_uniform(g, (n, k))
+    assert np.array_equal(_i32(a, b), O.gemm_s8_rcr_i32(a, b, nthreads=8))
+
+
+@pytest.mark.parametrize("shape", DMA_SHAPES[:3])
+def test_w8a8_dma_path_shapes(gpu, shape):
+    a, w, sa, sw = w8a8(*shape, seed=13)
+    assert np.array_equal(_w8a8(a, w, sa, sw), O.gemm_w8a8_bf16(a, w, sa, sw, nthreads=8))
+
+
+@pytest.mark.parametrize("pad", [8, 4])
+def test_w8a8_dma_path_strided_output(gpu, pad):
+    # ldd = N + pad: pad 8 keeps the LDS-staged 16-byte stores, pad 4 takes
+    # the per-quad epilogue; padding columns must stay untouched.
+    m, n, k = 512, 256, 256
+    a, w, sa, sw = w8a8(m, n, k, seed=14)
+    d = torch.full((m, n + pad), 3.0, dtype=torch.bfloat16, device="cuda:0")
+    P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, output=P.ElementKind.Bf16)).run(
+        dev(a), dev(w), d[:, :n], scale_a=dev(sa), scale_b=dev(sw))
+    sync()
+    got = host_bits16(d)
+    assert np.array_equal(got[:, :n], O.gemm_w8a8_bf16(a, w, sa, sw, nthreads=8))
+    assert np.all(d[:, n:].float().cpu().numpy() == 3.0)
+
+
 def test_i32_extreme_values_no_overflow(gpu):
     # |acc| = 127*127*K stays < 2^31 for K < 133143: all -127 (and -128) inputs.
     m = n = 256
@@ -187,7 +222,7 @@ def _fp8_check_acc(got, a, b, alpha=1.0, rows=None):
     return exact
 
 
-@pytest.mark.parametrize("shape", REF_SHAPES + [(512, 384, 1024)])
+@pytest.mark.parametrize("shape", REF_SHAPES + [(512, 384, 1024)] + DMA_SHAPES[:4])
 def test_fp8_f32_accumulator(gpu, shape):
     print(f"case: fp8 f32 {shape}", flush=True)
     a, b, _, _ = _fp8_inputs(*shape)
@@ -197,7 +232,7 @@ def test_fp8_f32_accumulator(gpu, shape):
 
 def test_fp8_e4m3_out_reference_pattern(gpu):
     # fp8_e4m3_rcr_smoke.rs:113-126 patterns, alpha = 0.25; +-1 e4m3 grid step.
-    for (m, n, k) in REF_SHAPES:
+    for (m, n, k) in REF_SHAPES + [(256, 256, 128)]:
         a = O.f32_to_e4m3((((np.arange(m * k) * 5) % 13) - 6.0) * 0.125).reshape(m, k)
         b = O.f32_to_e4m3((((np.arange(k * n) * 7) % 11) - 5.0) * 0.125).reshape(n, k)
         got = O.e4m3_to_f32(_fp8_run(a, b, P.ElementKind.Fp8E4M3, alpha=0.25).cpu().numpy())
@@ -221,7 +256,7 @@ def test_fp8_bf16_config3_sampled(gpu):
         assert np.all(err <= bf16_ulp(exact) + 1e-4 * absum), (r, err.max())
 
 
-@pytest.mark.parametrize("shape", [(256, 128, 64), (512, 512, 1024)])
+@pytest.mark.parametrize("shape", [(256, 128, 64), (512, 512, 1024), (256, 512, 384)])
 def test_fp8_matches_hipblaslt(gpu, shape):
     # Independent library cross-check: hipBLASLt's FP8 GEMM (torch._scaled_mm) on
     # the same e4m3 operands, f32 out; both run the same MFMA instruction.

@@ -51,6 +51,16 @@ def test_moe_small_all_pairs(gpu):
     _run(tokens=300, E=8, topk=2, n=272, k=384, seed=5)
 
 
+def test_moe_dma_path_all_pairs(gpu):
+    # N % 256 == 0 and K % 128 == 0: the LDS-DMA grouped kernel.
+    print("case: moe dma path", flush=True)
+    _run(tokens=700, E=8, topk=2, n=512, k=384, seed=9)
+
+
+def test_moe_dma_path_topk_weights(gpu):
+    _run(tokens=200, E=4, topk=2, n=256, k=256, seed=10, topk_w=True)
+
+
 def test_moe_ragged_k_and_topk_weights(gpu):
     print("case: moe ragged k, topk weights", flush=True)
     _run(tokens=100, E=5, topk=3, n=100, k=200, seed=6, topk_w=True)
