@@ -25,6 +25,11 @@ METRIC = "int8/fp8 GEMM TOPS (% MFMA peak) at 4096³; m=1 GEMV HBM GB/s (% peak)
 PEAK_INT8_TOPS = 5000.0     # MI355X dense int8 MFMA, TOP/s
 PEAK_FP8_TFLOPS = 5000.0    # MI355X dense fp8 MFMA, TFLOP/s
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E, GB/s
+# HBM bytes per launch measured with rocprofv3 PMC (FETCH_SIZE x2.00 and
+# WRITE_SIZE x1.00, scales calibrated on a plain device copy); the runs and
+# raw readings are in profiles/path_kernels_hbm_traffic.md.
+TRAFFIC_W8A8_4096 = 49275.6 * 1024 * 2.0 + 32768.0 * 1024 * 1.0
+TRAFFIC_GEMV_14336x4096 = 28848.6 * 1024 * 2.0 + 56.0 * 1024 * 1.0
 
 
 def log(*a):
@@ -142,7 +147,8 @@ def main():
             gbs = nbytes / (gms * 1e-3) / 1e9
             extra["gemv_s8w_m1_14336x4096"] = {"us": round(gms * 1e3, 3), "GB_s": round(gbs, 1),
                                                "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),
-                                               "bytes_per_call": nbytes, "weight_copies_rotated": copies}
+                                               "bytes_per_call": nbytes, "weight_copies_rotated": copies,
+                                               "hbm_traffic_pmc": int(TRAFFIC_GEMV_14336x4096)}
             del ws
         if only in ("", "fp8"):
             log("bench: fp8 2048x14336x4096")
@@ -217,7 +223,7 @@ def main():
                    "m": M, "n": N, "k": K, "layout": "rcr", "out": "bf16"},
         "roofline": None if not ms else {
             "bound": "mfma", "achieved": round(tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
-            "frac": round(tops / PEAK_INT8_TOPS, 4), "traffic": None,
+            "frac": round(tops / PEAK_INT8_TOPS, 4), "traffic": int(TRAFFIC_W8A8_4096),
             "kernel": "gemm_s8_rcr_kernel<EPI_W8A8_BF16> (int8 tera-ops per second)"},
         "cpu_baseline": cpu,
         "extra": extra,
