@@ -323,6 +323,34 @@ __device__ __forceinline__ void stage_step(AccTile<P> &acc, Frags<P> &f0, Frags<
         mma_block<P, 0, P::TJ>(acc, f1);
         wait_dma();        // this wave's DMA into `nxt` has landed
         __syncthreads();   // ... and every wave's; every wave is done reading `cur`
+    } else if constexpr (C::PIPE >= 2) {
+        // Per sub-step: B fragments and A fragment 0 first, then each row i of
+        // MFMAs overlaps the read of A fragment i+1 (scheduler pinned).
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            Frags<P> &f = s ? f1 : f0;
+#pragma unroll
+            for (int t = 0; t < P::TJ; ++t) f.b[t] = P::load(cur + OPER, wave_n * C::WN, t, s, lane);
+            f.a[0] = P::load(cur, wave_m * C::WM, 0, s, lane);
+            if constexpr (C::PIPE == 3) __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+            for (int i = 0; i < P::TI; ++i) {
+                if (i + 1 < P::TI) f.a[i + 1] = P::load(cur, wave_m * C::WM, i + 1, s, lane);
+#pragma unroll
+                for (int h = 0; h < P::H; ++h)
+#pragma unroll
+                    for (int j = 0; j < P::TJ; ++j) P::mma(acc[i][j], f.b[j], f.a[i], h);
+            }
+            if constexpr (C::PIPE == 3) __builtin_amdgcn_s_setprio(0);
+            __builtin_amdgcn_sched_group_barrier(0x100, P::TJ + 1, 0);
+#pragma unroll
+            for (int i = 0; i < P::TI; ++i) {
+                if (i + 1 < P::TI) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, P::TJ * P::H, 0);
+            }
+        }
+        wait_dma();
+        __syncthreads();
     } else {
         load_frags<P>(f1, cur, 1, wave_m, wave_n, lane);
         mma_block<P, 0, P::TJ>(acc, f0);
@@ -358,6 +386,57 @@ __device__ __forceinline__ void mainloop(int8_t *s0, int8_t *s1, const D &d, int
         stage_step<P>(acc, f0, f1, s1, s0, d, (kt + 2) * BK, kt + 2 < KT, wave_m, wave_n, lane);
     }
     if (kt < KT) stage_step<P>(acc, f0, f1, s0, s1, d, 0, false, wave_m, wave_n, lane);
+}
+
+// W8A8 bf16 epilogue for the int8 16x16 policy, staged through LDS so each
+// output row segment of the wave tile (WN bf16 = 128 bytes for WN = 64) is
+// written with full-line 16-byte stores.
+//   sam[i]   dequant scale of this lane's row in 16-row tile i
+//   post[i]  optional second row factor (1 multiply after the dequant), only
+//            read when HasPost
+//   swv[j]   the 4 column scales of this lane's quad in 16-column tile j
+//   row_dst(r) destination of wave-tile row r (0..WM-1) at the wave's first
+//            column, or nullptr to skip the row
+// `scratch` holds WM*WN*2 bytes private to this wave; LDS must be free (the
+// mainloop ends with a barrier).  Products are rounded in the order
+// ((sam * sw) * acc) [* post], then packed with v_cvt_pk_bf16_f32.
+template <class P, bool HasPost, class RowDst>
+__device__ __forceinline__ void store_w8a8_bf16_staged(const AccTile<P> &acc, int8_t *scratch,
+                                                       const float (&sam)[P::TI],
+                                                       const float (&post)[P::TI],
+                                                       const v4f (&swv)[P::TJ], RowDst &&row_dst) {
+    typedef typename P::Cfg C;
+    static_assert(C::WN * 2 == 128, "staged store assumes 128-byte wave-tile rows");
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < P::TI; ++i)
+#pragma unroll
+        for (int j = 0; j < P::TJ; ++j) {
+            float y[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                y[r] = (sam[i] * swv[j][r]) * (float)acc[i][j][r];
+                if constexpr (HasPost) y[r] = y[r] * post[i];
+            }
+            const int row = i * 16 + (lane & 15);
+            const int col = j * 16 + (lane >> 4) * 4;              // bf16 column
+            const int unit = col >> 3, half = (col >> 2) & 1;
+            v2i w;
+            w[0] = (int)f32x2_to_bf16x2(y[0], y[1]);
+            w[1] = (int)f32x2_to_bf16x2(y[2], y[3]);
+            *reinterpret_cast<v2i *>(scratch + row * 128 + ((unit ^ (row & 7)) << 4) + half * 8) = w;
+        }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int q = 0; q < C::WM / 8; ++q) {
+        const int row = q * 8 + (lane >> 3), u = lane & 7;
+        uint16_t *dst = row_dst(row);
+        if (dst == nullptr) continue;
+        const v4i v = *reinterpret_cast<const v4i *>(scratch + row * 128 + ((u ^ (row & 7)) << 4));
+        *reinterpret_cast<v4i *>(dst + u * 8) = v;
+    }
 }
 
 // Visit this thread's accumulators: f(m_local, n0_local, quad) with quad the

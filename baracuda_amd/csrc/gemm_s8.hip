@@ -128,48 +128,22 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_s8_rcr_dma_kernel(S8Args p
     M2::AccTile<P> acc;
     M2::mainloop<P>(stage0, stage1, d, p.K, acc);
     if constexpr (EPI == EPI_W8A8_BF16 && VecOut) {
-        // Whole tiles.  The dequant scales this lane needs (one per 16-row
-        // tile i, four per 16-column tile j) are fetched in one batch, the
-        // wave's 128 x 64 bf16 tile is assembled in LDS (free after the
-        // mainloop's last barrier) and written back as full 128-byte rows.
+        // Whole tiles: scales fetched once per lane, output staged in LDS
+        // (free after the mainloop's last barrier) and written as full rows.
         const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-        const int wrow = (wave / DmaCfg::WAVES_N) * DmaCfg::WM;
-        const int wcol = (wave % DmaCfg::WAVES_N) * DmaCfg::WN;
-        float sam[P::TI];
+        const int wrow = m_base + (wave / DmaCfg::WAVES_N) * DmaCfg::WM;
+        const int wcol = n_base + (wave % DmaCfg::WAVES_N) * DmaCfg::WN;
+        float sam[P::TI], none[P::TI];
         v4f swv[P::TJ];
 #pragma unroll
-        for (int i = 0; i < P::TI; ++i) sam[i] = p.sa[m_base + wrow + i * 16 + (lane & 15)];
+        for (int i = 0; i < P::TI; ++i) sam[i] = p.sa[wrow + i * 16 + (lane & 15)];
 #pragma unroll
         for (int j = 0; j < P::TJ; ++j)
-            swv[j] = *reinterpret_cast<const v4f *>(p.sw + n_base + wcol + j * 16 + (lane >> 4) * 4);
-        // Per-wave 16 KiB staging area: row r (0..127) of 128 bytes, 16-byte
-        // unit u stored at unit u ^ (r & 7).
-        int8_t *stage = (wave < 4 ? stage0 : stage1) + (wave & 3) * (DmaCfg::WM * DmaCfg::WN * 2);
-#pragma unroll
-        for (int i = 0; i < P::TI; ++i)
-#pragma unroll
-            for (int j = 0; j < P::TJ; ++j) {
-                const int r = i * 16 + (lane & 15);
-                const int col = j * 16 + (lane >> 4) * 4;            // bf16 column 0..63
-                const int unit = col >> 3, half = (col >> 2) & 1;
-                v2i w;
-                w[0] = (int)f32x2_to_bf16x2((sam[i] * swv[j][0]) * (float)acc[i][j][0],
-                                            (sam[i] * swv[j][1]) * (float)acc[i][j][1]);
-                w[1] = (int)f32x2_to_bf16x2((sam[i] * swv[j][2]) * (float)acc[i][j][2],
-                                            (sam[i] * swv[j][3]) * (float)acc[i][j][3]);
-                *reinterpret_cast<v2i *>(stage + r * 128 + ((unit ^ (r & 7)) << 4) + half * 8) = w;
-            }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-        for (int q = 0; q < DmaCfg::WM / 8; ++q) {
-            const int r = q * 8 + (lane >> 3), u = lane & 7;
-            const v4i v = *reinterpret_cast<const v4i *>(stage + r * 128 + ((u ^ (r & 7)) << 4));
-            uint16_t *dst = static_cast<uint16_t *>(p.d) + (int64_t)(m_base + wrow + r) * p.ldd +
-                            n_base + wcol + u * 8;
-            *reinterpret_cast<v4i *>(dst) = v;
-        }
+            swv[j] = *reinterpret_cast<const v4f *>(p.sw + wcol + j * 16 + (lane >> 4) * 4);
+        int8_t *scratch = (wave < 4 ? stage0 : stage1) + (wave & 3) * (DmaCfg::WM * DmaCfg::WN * 2);
+        M2::store_w8a8_bf16_staged<P, false>(acc, scratch, sam, none, swv, [&](int r) {
+            return static_cast<uint16_t *>(p.d) + (int64_t)(wrow + r) * p.ldd + wcol;
+        });
     } else {
         const S8Epilogue<EPI, VecOut> epi{p};
         M2::for_each_quad<P>(acc, [&](int ml, int nl, const v4i &v) { epi(m_base + ml, n_base + nl, v); });

@@ -62,10 +62,14 @@ struct MoeArgs {
 };
 
 // Ragged tile list: slot -> (expert, first pair of the tile, rows in it).
-// Workgroup-uniform walk over expert_offsets; false past the last tile.
-__device__ __forceinline__ bool moe_tile(const MoeArgs &p, int slot, int &e, int &seg0, int &rows_out) {
+// The E+1 offsets are loaded in one parallel step into LDS, then every thread
+// walks them from LDS (workgroup-uniform result); false past the last tile.
+__device__ __forceinline__ bool moe_tile(const MoeArgs &p, int32_t *s_off, int slot, int &e,
+                                         int &seg0, int &rows_out) {
+    for (int i = threadIdx.x; i <= p.E; i += blockDim.x) s_off[i] = min(p.offsets[i], p.size_m);
+    __syncthreads();
     for (e = 0; e < p.E; ++e) {
-        const int o0 = p.offsets[e], o1 = min(p.offsets[e + 1], p.size_m);
+        const int o0 = s_off[e], o1 = s_off[e + 1];
         const int rows = o1 > o0 ? o1 - o0 : 0;
         const int tiles = (rows + 255) / 256;
         if (slot < tiles) {
@@ -101,8 +105,9 @@ __device__ __forceinline__ void moe_store(const MoeArgs &p, const int32_t *rows_
 __global__ __launch_bounds__(NT, 1) void moe_s8_grouped_kernel(MoeArgs p) {
     __shared__ __attribute__((aligned(16))) int8_t lds[4 * LDS_TILE];
     __shared__ int32_t s_rows_tok[BM];
+    __shared__ int32_t s_off[kMaxExperts + 1];
     int e, seg0, seg_rows;
-    if (!moe_tile(p, blockIdx.x, e, seg0, seg_rows)) return;   // whole workgroup exits
+    if (!moe_tile(p, s_off, blockIdx.x, e, seg0, seg_rows)) return;   // whole workgroup exits
     const int n_base = blockIdx.y * BN;
     const int tid = threadIdx.x;
     for (int r = tid; r < BM; r += NT) s_rows_tok[r] = p.sorted_ids[seg0 + min(r, seg_rows - 1)];
@@ -129,15 +134,31 @@ __global__ __launch_bounds__(NT, 1) void moe_s8_grouped_kernel(MoeArgs p) {
 // expert's weight slab.
 typedef mfma2::Cfg<2, 4, 0> DmaCfg;
 
-__global__ __launch_bounds__(DmaCfg::NT, 1) void moe_s8_grouped_dma_kernel(MoeArgs p) {
+// Workgroup id -> (slot, n-tile).  Workgroups are dispatched round-robin
+// over the 8 XCDs; the id is regrouped so each XCD owns a contiguous range of
+// n-tiles with every expert's m-tiles for them (slot fastest), so an expert's
+// weight panel is fetched into one XCD's L2 only.  Ids past the work exit.
+__device__ __forceinline__ bool moe_dma_coords(int pid, int total_padded, int slots, int n_tiles,
+                                               int &slot, int &ntile) {
+    constexpr int XCDS = 8;
+    const int t = (pid % XCDS) * (total_padded / XCDS) + pid / XCDS;
+    slot = t % slots;
+    ntile = t / slots;
+    return ntile < n_tiles;
+}
+
+__global__ __launch_bounds__(DmaCfg::NT, 1) void moe_s8_grouped_dma_kernel(MoeArgs p, int slots) {
     namespace M2 = mfma2;
     typedef M2::PolicyI8<DmaCfg> P;
     __shared__ __attribute__((aligned(1024))) int8_t stage0[2 * M2::OPER];
     __shared__ __attribute__((aligned(1024))) int8_t stage1[2 * M2::OPER];
     __shared__ int32_t s_rows_tok[M2::BM];
+    __shared__ int32_t s_off[kMaxExperts + 1];
+    int slot, ntile;
+    if (!moe_dma_coords(blockIdx.x, gridDim.x, slots, p.N / M2::BN, slot, ntile)) return;
     int e, seg0, seg_rows;
-    if (!moe_tile(p, blockIdx.x, e, seg0, seg_rows)) return;   // whole workgroup exits
-    const int n_base = blockIdx.y * M2::BN;
+    if (!moe_tile(p, s_off, slot, e, seg0, seg_rows)) return;   // whole workgroup exits
+    const int n_base = ntile * M2::BN;
     for (int r = threadIdx.x; r < M2::BM; r += DmaCfg::NT)
         s_rows_tok[r] = p.sorted_ids[seg0 + min(r, seg_rows - 1)];
     __syncthreads();
@@ -150,10 +171,29 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void moe_s8_grouped_dma_kernel(MoeAr
                                         p.K, n_base * p.K);
     M2::AccTile<P> acc;
     M2::mainloop<P>(stage0, stage1, d, p.K, acc);
+    // Epilogue: scales (per token row, per expert column) fetched once per
+    // lane; the wave tile is staged in LDS and written as full 128-byte rows
+    // of the token's output row; padding rows of a partial tile are skipped.
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wr = (wave / DmaCfg::WAVES_N) * DmaCfg::WM;
+    const int wc = n_base + (wave % DmaCfg::WAVES_N) * DmaCfg::WN;
     const float *swe = p.sw + (int64_t)e * p.N;
-    M2::for_each_quad<P>(acc, [&](int ml, int nl, const v4i &v) {
-        moe_store(p, s_rows_tok, seg_rows, in_div, swe, ml, n_base + nl, v);
-    });
+    float sam[P::TI], post[P::TI];
+    v4f swv[P::TJ];
+#pragma unroll
+    for (int i = 0; i < P::TI; ++i) {
+        const int tok = s_rows_tok[wr + i * 16 + (lane & 15)];
+        sam[i] = p.sa[tok / in_div];
+        post[i] = p.topk_w ? p.topk_w[tok] : 1.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < P::TJ; ++j) swv[j] = *reinterpret_cast<const v4f *>(swe + wc + j * 16 + (lane >> 4) * 4);
+    int8_t *scratch = (wave < 4 ? stage0 : stage1) + (wave & 3) * (DmaCfg::WM * DmaCfg::WN * 2);
+    auto dst = [&](int r) -> uint16_t * {
+        return wr + r < seg_rows ? p.out + (int64_t)s_rows_tok[wr + r] * p.N + wc : nullptr;
+    };
+    if (p.topk_w) M2::store_w8a8_bf16_staged<P, true>(acc, scratch, sam, post, swv, dst);
+    else M2::store_w8a8_bf16_staged<P, false>(acc, scratch, sam, post, swv, dst);
 }
 
 }  // namespace
@@ -205,13 +245,18 @@ int32_t baracuda_kernels_moe_s8_grouped_bf16_gfx950_run(
     const int slots = (size_m + BM - 1) / BM + num_experts;
     dim3 grid(slots, (size_n + BN - 1) / BN);
     // The DMA path needs whole K stages, N a multiple of 256, 16-byte aligned
-    // operands and byte offsets that fit 32 bits (per input / per expert slab).
+    // operands, byte offsets that fit 32 bits (per input / per expert slab) and
+    // 16-byte aligned output rows and column scales for the staged epilogue.
     const int64_t x_rows = topk_weights ? size_m : (size_m + topk - 1) / topk;
     const bool fast = size_k % mfma2::BK == 0 && size_n % mfma2::BN == 0 &&
                       mfma::aligned16(input) && mfma::aligned16(weights) &&
-                      x_rows * size_k < (1ll << 31) && (int64_t)size_n * size_k < (1ll << 31);
-    if (fast)
-        hipLaunchKernelGGL(moe_s8_grouped_dma_kernel, grid, dim3(DmaCfg::NT), 0, stream, p);
+                      x_rows * size_k < (1ll << 31) && (int64_t)size_n * size_k < (1ll << 31) &&
+                      mfma::aligned16(output) && mfma::aligned16(scale_w);
+    if (fast) {
+        const int work = slots * (size_n / mfma2::BN);
+        const int padded = (work + 7) / 8 * 8;   // whole XCD groups
+        hipLaunchKernelGGL(moe_s8_grouped_dma_kernel, dim3(padded), dim3(DmaCfg::NT), 0, stream, p, slots);
+    }
     else
         hipLaunchKernelGGL(moe_s8_grouped_kernel, grid, dim3(NT), 0, stream, p);
     return launch_status();
