@@ -1,0 +1,165 @@
+// quantize.hip -- per-token symmetric dynamic-range int8 quantization for
+// gfx950: the producer of the W8A8 GEMM's activation operand and its
+// per-token scale.
+//
+// Semantics of dynamic_range_quantize_per_token_sym
+// (crates/baracuda-kernels-sys/kernels/include/baracuda_quantize_compose.cuh:143-203):
+//   max_abs  = max_d |x[n, d]|
+//   scale[n] = max_abs > 0 ? max_abs / qmax : 1            (in the input type)
+//   inv      = 1 / scale                                    (f32)
+//   q[n, d]  = clamp(round_half_even(x[n, d] * inv), qmin, qmax)
+// For the f64 input the reference evaluates in f32 after a narrowing load
+// (qc_load_as_f32) and stores the scale back as f64; the same here.
+//
+// MI355X layout: one workgroup (256 threads) per row (grid-strided), the row
+// is read once into registers with workgroup-coalesced loads (up to 64
+// elements per thread, i.e. D <= 16384), reduced with a wave butterfly + LDS,
+// quantized from registers: one HBM read of x, one write of q.  Longer rows
+// take a two-pass loop over global memory.  Max is exact
+// in any order, so the result is bit-identical to the reference's.
+#include "bk_common.hpp"
+
+namespace bk {
+namespace {
+
+constexpr int kQBlock = 256;
+constexpr int kQMaxPerThread = 64;   // register-resident row: D <= 256 * 64
+
+// Load as f32 (qc_load_as_f32, baracuda_quantize_compose.cuh:69-89).
+template <typename T> struct QIn;
+template <> struct QIn<float> {
+    __device__ static float ld(const float *p) { return *p; }
+};
+template <> struct QIn<double> {
+    __device__ static float ld(const double *p) { return (float)*p; }
+};
+struct Bf16In { uint16_t bits; };   // element type: pointer steps of 2 bytes
+template <> struct QIn<Bf16In> {
+    __device__ static float ld(const Bf16In *p) { return bf16_to_f32(p->bits); }
+};
+
+__device__ __forceinline__ float block_max(float v, float *red) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float m = red[0];
+#pragma unroll
+    for (int w = 1; w < kQBlock / 64; ++w) m = fmaxf(m, red[w]);
+    return m;
+}
+
+__device__ __forceinline__ int8_t quant1(float v, float inv, float qmin, float qmax) {
+    float r = __builtin_rintf(v * inv);
+    r = r < qmin ? qmin : r;
+    r = r > qmax ? qmax : r;
+    return (int8_t)(int)r;
+}
+
+// T: element type of x; S: type of the scale output.
+template <typename T, typename S>
+__global__ __launch_bounds__(kQBlock) void quantize_per_token_kernel(
+    const T *__restrict__ x, S *__restrict__ scale, int8_t *__restrict__ q, int N, int D,
+    int qmin, int qmax) {
+    __shared__ float red[kQBlock / 64];
+    const float fqmin = (float)qmin, fqmax = (float)qmax;
+    for (int n = blockIdx.x; n < N; n += gridDim.x) {
+        const T *row = x + (int64_t)n * D;
+        int8_t *qrow = q + (int64_t)n * D;
+        float vals[kQMaxPerThread];
+        const bool resident = D <= kQBlock * kQMaxPerThread;
+        float m = 0.0f;
+        if (resident) {
+            // element e = tid + kQBlock * i: coalesced across the workgroup.
+#pragma unroll
+            for (int i = 0; i < kQMaxPerThread; ++i) {
+                const int e = threadIdx.x + kQBlock * i;
+                vals[i] = e < D ? QIn<T>::ld(row + e) : 0.0f;
+                m = fmaxf(m, fabsf(vals[i]));
+            }
+        } else {
+            for (int e = threadIdx.x; e < D; e += kQBlock) m = fmaxf(m, fabsf(QIn<T>::ld(row + e)));
+        }
+        const float max_abs = block_max(m, red);
+        const float s = max_abs > 0.0f ? max_abs / fqmax : 1.0f;
+        const float inv = s != 0.0f ? 1.0f / s : 0.0f;
+        if (threadIdx.x == 0) scale[n] = (S)s;
+        if (resident) {
+#pragma unroll
+            for (int i = 0; i < kQMaxPerThread; ++i) {
+                const int e = threadIdx.x + kQBlock * i;
+                if (e < D) qrow[e] = quant1(vals[i], inv, fqmin, fqmax);
+            }
+        } else {
+            for (int e = threadIdx.x; e < D; e += kQBlock)
+                qrow[e] = quant1(QIn<T>::ld(row + e), inv, fqmin, fqmax);
+        }
+        __syncthreads();   // `red` is reused by the next row
+    }
+}
+
+int32_t quant_check(int32_t N, int32_t D, int32_t qmin, int32_t qmax) {
+    if (N < 0 || D < 0) return kInvalid;
+    if (qmin > qmax) return kInvalid;
+    if (qmax <= 0) return kInvalid;
+    return kOk;   // N > 65535 is accepted (rows are grid-strided)
+}
+
+template <typename T, typename S>
+int32_t launch_quant(int32_t N, int32_t D, int32_t qmin, int32_t qmax, const void *input,
+                     void *scale, void *output, hipStream_t stream) {
+    const int32_t st = quant_check(N, D, qmin, qmax);
+    if (st != kOk) return st;
+    if ((int64_t)N * D == 0) return kOk;
+    if (!input || !scale || !output) return kInvalid;
+    const int grid = N < 65535 ? N : 65535;
+    hipLaunchKernelGGL((quantize_per_token_kernel<T, S>), dim3(grid), dim3(kQBlock), 0, stream,
+                       (const T *)input, (S *)scale, (int8_t *)output, N, D, qmin, qmax);
+    return launch_status();
+}
+
+}  // namespace
+}  // namespace bk
+
+using namespace bk;
+
+extern "C" {
+
+// Same ABI as baracuda_kernels_dynamic_range_quantize_per_token_sym_{f32,f64}_s8_*
+// (baracuda_quantize_compose.cuh:306-338 macro, compose.cu:19-22).
+#define BK_QUANT(TAG, TY)                                                                          \
+    int32_t baracuda_kernels_dynamic_range_quantize_per_token_sym_##TAG##_s8_run(                  \
+        int32_t N, int32_t D, int32_t qmin, int32_t qmax, const void *input, void *scale,          \
+        void *output, void *workspace, size_t workspace_bytes, void *stream) {                     \
+        (void)workspace; (void)workspace_bytes;                                                    \
+        return launch_quant<TY, TY>(N, D, qmin, qmax, input, scale, output, (hipStream_t)stream);  \
+    }                                                                                              \
+    int32_t baracuda_kernels_dynamic_range_quantize_per_token_sym_##TAG##_s8_can_implement(        \
+        int32_t N, int32_t D, int32_t qmin, int32_t qmax, const void *input, const void *scale,    \
+        const void *output) {                                                                      \
+        (void)input; (void)scale; (void)output;                                                    \
+        return quant_check(N, D, qmin, qmax);                                                      \
+    }
+
+BK_QUANT(f32, float)
+BK_QUANT(f64, double)
+#undef BK_QUANT
+
+// New SKU: bf16 activations in, f32 per-token scales out (what the W8A8 GEMM
+// epilogue consumes), int8 out.
+int32_t baracuda_kernels_dynamic_range_quantize_per_token_sym_bf16_s8_gfx950_run(
+    int32_t N, int32_t D, int32_t qmin, int32_t qmax, const void *input, void *scale,
+    void *output, void *workspace, size_t workspace_bytes, void *stream) {
+    (void)workspace; (void)workspace_bytes;
+    return launch_quant<Bf16In, float>(N, D, qmin, qmax, input, scale, output, (hipStream_t)stream);
+}
+
+int32_t baracuda_kernels_dynamic_range_quantize_per_token_sym_bf16_s8_gfx950_can_implement(
+    int32_t N, int32_t D, int32_t qmin, int32_t qmax, const void *input, const void *scale,
+    const void *output) {
+    (void)input; (void)scale; (void)output;
+    return quant_check(N, D, qmin, qmax);
+}
+
+}  // extern "C"

@@ -398,3 +398,81 @@ class MoeS8GroupedPlan:
             _ptr(expert_counts), _ptr(expert_offsets), self.E, self.topk, self.size_m, self.n, self.k,
             _ptr(scale_a), _ptr(scale_w), None, 0, _stream(stream))
         check(st, "MoeS8GroupedPlan::run")
+
+
+# ---- per-token dynamic quantization + quantized_linear ----------------------
+def dynamic_range_quantize_per_token_sym(x, scale, q, qmin=-127, qmax=127, stream=None) -> None:
+    """DynamicRangeQuantizePlan (baracuda_quantize_compose.cuh:143-203): per row,
+    scale = max|x|/qmax (1 for an all-zero row), q = clamp(rne(x/scale))."""
+    _need(x.dim() == 2 and x.is_contiguous() and q.is_contiguous(), "x, q contiguous [N, D]")
+    n, d = x.shape
+    _need(tuple(q.shape) == (n, d) and q.dtype == torch.int8 and scale.numel() == n, "q [N,D] int8, scale [N]")
+    L = lib()
+    if x.dtype == torch.float32:
+        _need(scale.dtype == torch.float32, "f32 input takes an f32 scale")
+        fn = L.dynamic_range_quantize_per_token_sym_f32_s8_run
+    elif x.dtype == torch.float64:
+        _need(scale.dtype == torch.float64, "f64 input takes an f64 scale")
+        fn = L.dynamic_range_quantize_per_token_sym_f64_s8_run
+    elif x.dtype == torch.bfloat16:
+        _need(scale.dtype == torch.float32, "bf16 input takes an f32 scale")
+        fn = L.dynamic_range_quantize_per_token_sym_bf16_s8_gfx950_run
+    else:
+        raise Unsupported(f"quantize input dtype {x.dtype}")
+    check(fn(n, d, qmin, qmax, _ptr(x), _ptr(scale), _ptr(q), None, 0, _stream(stream)),
+          "dynamic_range_quantize_per_token_sym")
+
+
+@dataclass(frozen=True)
+class QuantizedLinearDescriptor:
+    m: int
+    c_out: int
+    k: int
+    q_min: int = -127
+    q_max: int = 127
+
+
+class QuantizedLinearPlan:
+    """quantized_linear.rs QuantizedLinearPlan (:142-386): two launches on one
+    stream -- per-token activation quantization into caller scratch, then the
+    W8A8 GEMM with the (sa*sw)*acc dequant epilogue.  f32 activation -> f32
+    output (the reference's SKU); bf16 activation -> bf16 output (gfx950)."""
+
+    def __init__(self, desc: QuantizedLinearDescriptor):
+        self.desc = desc
+
+    @classmethod
+    def select(cls, desc: QuantizedLinearDescriptor) -> "QuantizedLinearPlan":
+        if desc.m < 0 or desc.c_out < 0 or desc.k < 0:
+            raise InvalidProblem("quantized_linear extents")
+        if desc.q_min > desc.q_max or desc.q_max <= 0:
+            raise InvalidProblem("quantized_linear q range")
+        return cls(desc)
+
+    def workspace_size(self) -> int:
+        return 0
+
+    def run(self, activation, weight_q, weight_scale, output, act_q_scratch, act_scale_scratch,
+            stream=None) -> None:
+        d = self.desc
+        if d.m * d.c_out == 0 or d.k == 0:
+            return
+        _need(tuple(activation.shape) == (d.m, d.k) and tuple(weight_q.shape) == (d.c_out, d.k),
+              "activation [M,K], weight_q [C_out,K]")
+        _need(tuple(output.shape) == (d.m, d.c_out), "output [M, C_out]")
+        dynamic_range_quantize_per_token_sym(activation, act_scale_scratch, act_q_scratch,
+                                             d.q_min, d.q_max, stream)
+        L, s = lib(), _stream(stream)
+        if activation.dtype == torch.float32:
+            _need(output.dtype == torch.float32 and weight_scale.dtype == torch.float32, "f32 output/scales")
+            st = L.quantized_linear_w8a8_f32_gfx950_run(d.m, d.c_out, d.k, _ptr(weight_q), _ptr(act_q_scratch),
+                                                         _ptr(act_scale_scratch), _ptr(weight_scale),
+                                                         _ptr(output), None, 0, s)
+        elif activation.dtype == torch.bfloat16:
+            _need(output.dtype == torch.bfloat16 and weight_scale.dtype == torch.float32, "bf16 output, f32 scales")
+            st = L.gemm_w8a8_rcr_gfx950_bf16_run(d.m, d.c_out, d.k, _ptr(act_q_scratch), d.k, _ptr(weight_q),
+                                                 _ld(weight_q), _ptr(act_scale_scratch), _ptr(weight_scale),
+                                                 _ptr(output), _ld(output), None, 0, s)
+        else:
+            raise Unsupported(f"quantized_linear activation dtype {activation.dtype}")
+        check(st, "QuantizedLinearPlan::run")

@@ -81,6 +81,31 @@ int32_t baracuda_kernels_quantized_linear_w8a8_f32_gfx950_can_implement(
     int32_t M, int32_t C_out, int32_t K, const void *weight_q, const void *act_q,
     const void *scale_a, const void *scale_w, const void *output);
 
+/* ======================= per-token dynamic int8 quantization =============
+ * Replaces baracuda_kernels_dynamic_range_quantize_per_token_sym_{f32,f64}_s8_{run,can_implement}
+ * (crates/baracuda-kernels-sys/kernels/include/baracuda_quantize_compose.cuh:143-203,306-338,
+ *  crates/baracuda-kernels-sys/kernels/quantize/compose.cu:19-22), same ABI:
+ * scale[n] = max|x[n,:]| / qmax (1 for an all-zero row), q = clamp(rne(x * (1/scale)), qmin, qmax).
+ * Accepts N > 65535 (the reference rejects it). */
+#define BK_QUANT_DECL(TAG)                                                                       \
+    int32_t baracuda_kernels_dynamic_range_quantize_per_token_sym_##TAG##_s8_run(               \
+        int32_t N, int32_t D, int32_t qmin, int32_t qmax, const void *input, void *scale,        \
+        void *output, void *workspace, size_t workspace_bytes, void *stream);                    \
+    int32_t baracuda_kernels_dynamic_range_quantize_per_token_sym_##TAG##_s8_can_implement(      \
+        int32_t N, int32_t D, int32_t qmin, int32_t qmax, const void *input, const void *scale,  \
+        const void *output);
+BK_QUANT_DECL(f32)
+BK_QUANT_DECL(f64)
+#undef BK_QUANT_DECL
+
+/* New SKU (same family): bf16 activations in, f32 per-token scales out. */
+int32_t baracuda_kernels_dynamic_range_quantize_per_token_sym_bf16_s8_gfx950_run(
+    int32_t N, int32_t D, int32_t qmin, int32_t qmax, const void *input, void *scale,
+    void *output, void *workspace, size_t workspace_bytes, void *stream);
+int32_t baracuda_kernels_dynamic_range_quantize_per_token_sym_bf16_s8_gfx950_can_implement(
+    int32_t N, int32_t D, int32_t qmin, int32_t qmax, const void *input, const void *scale,
+    const void *output);
+
 /* ======================= FP8 e4m3 GEMM, RCR layout ======================
  * OCP e4m3 (e4m3fn) operands, f32 accumulator. */
 

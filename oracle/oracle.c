@@ -297,6 +297,33 @@ void bo_gather_rows(void *dest, const void *table, const uint32_t *idx,
     }
 }
 
+/* baracuda_quantize_compose.cuh:143-203 dynamic_range_quantize_per_token_
+ * symmetric_kernel: max-abs over the row (NaN ignored by the `a > max`
+ * compare), scale = max/qmax (1 if max == 0), inv = 1/scale, then
+ * q = clamp(rne(x*inv)) cast to int8 (__float2int_rn(NaN) = 0). All in f32. */
+void bo_quantize_per_token_sym(const float *x, int64_t n, int64_t d, int32_t qmin,
+                               int32_t qmax, float *scale, int8_t *q) {
+    for (int64_t r = 0; r < n; ++r) {
+        const float *row = x + r * d;
+        float m = 0.0f;
+        for (int64_t c = 0; c < d; ++c) {
+            float a = fabsf(row[c]);
+            if (a > m) m = a;
+        }
+        volatile float s = m > 0.0f ? m / (float)qmax : 1.0f;
+        volatile float inv = s != 0.0f ? 1.0f / s : 0.0f;
+        scale[r] = s;
+        for (int64_t c = 0; c < d; ++c) {
+            volatile float p = row[c] * inv;
+            int32_t v = isnan(p) ? 0 : (int32_t)nearbyintf(p);
+            if (isnan(p)) v = 0;
+            if (v < qmin) v = qmin;
+            if (v > qmax) v = qmax;
+            q[r * d + c] = (int8_t)v;
+        }
+    }
+}
+
 /* baracuda_moe.cuh:1121-1162: histogram of expert_ids, then exclusive
  * prefix sum into offsets[0..E], offsets[0] = 0. */
 void bo_moe_expert_offsets(const int32_t *expert_ids, int64_t size_m,

@@ -102,6 +102,11 @@ void bo_gemv_s8w_m1_f64(int64_t n, int64_t k,
 void bo_gather_rows(void *dest, const void *table, const uint32_t *idx,
                     int64_t V, int64_t H, int64_t n, int64_t elem_size);
 
+/* dynamic_range_quantize_per_token_sym (baracuda_quantize_compose.cuh:143-203):
+ * x given as f32 (callers narrow f64 / widen bf16 first, like qc_load_as_f32). */
+void bo_quantize_per_token_sym(const float *x, int64_t n, int64_t d, int32_t qmin,
+                               int32_t qmax, float *scale, int8_t *q);
+
 /* MoE routing helpers (baracuda_moe.cuh:1121-1162). */
 void bo_moe_expert_offsets(const int32_t *expert_ids, int64_t size_m,
                            int32_t num_experts, int32_t *counts,

@@ -50,6 +50,7 @@ def _L():
             "bo_gemv_s8w_m1_f64": (None, [i64, i64, vp, vp, i64, vp, i32]),
             "bo_gather_rows": (None, [vp, vp, vp, i64, i64, i64, i64]),
             "bo_moe_expert_offsets": (None, [vp, i64, C.c_int32, vp, vp]),
+            "bo_quantize_per_token_sym": (None, [vp, i64, i64, C.c_int32, C.c_int32, vp, vp]),
             "bo_moe_s8_grouped_i32": (None, [vp, vp, vp, vp, C.c_int32, C.c_int32, i64, i64, i64, vp]),
         }
         for name, (res, args) in sig.items():
@@ -208,6 +209,16 @@ def gather_rows(table: np.ndarray, idx: np.ndarray) -> np.ndarray:
         if table.dtype.itemsize == 1 else np.empty((idx.size, H), dtype=table.dtype)
     _L().bo_gather_rows(_p(dest), _p(table), _p(idx), V, H, idx.size, table.dtype.itemsize)
     return dest
+
+
+def quantize_per_token_sym(x, qmin=-127, qmax=127):
+    """Returns (q int8 [N,D], scale f32 [N]); x is read as f32."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n, d = x.shape
+    q = np.zeros((n, d), dtype=np.int8)
+    s = np.zeros(n, dtype=np.float32)
+    _L().bo_quantize_per_token_sym(_p(x), n, d, qmin, qmax, _p(s), _p(q))
+    return q, s
 
 
 def moe_expert_offsets(expert_ids: np.ndarray, num_experts: int):

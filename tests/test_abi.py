@@ -15,10 +15,13 @@ HDR = Path(__file__).resolve().parents[1] / "include" / "baracuda_kernels.h"
 def _declared():
     text = re.sub(r"/\*.*?\*/", "", HDR.read_text(), flags=re.S)
     names = set(re.findall(r"\b(baracuda_kernels_\w+)\s*\(", text))
-    for tag_macro, body in (("BK_GEMV_DENSE_DECL", "gemv_dense_m1"), ("BK_GATHER_DECL", "gather_rows")):
+    for tag_macro, body, sufs in (
+            ("BK_GEMV_DENSE_DECL", "gemv_dense_m1_{}", ("run", "can_implement", "workspace_size")),
+            ("BK_GATHER_DECL", "gather_rows_{}", ("run", "can_implement", "workspace_size")),
+            ("BK_QUANT_DECL", "dynamic_range_quantize_per_token_sym_{}_s8", ("run", "can_implement"))):
         for tag in re.findall(tag_macro + r"\((\w+)\)", text):
-            for suf in ("run", "can_implement", "workspace_size"):
-                names.add(f"baracuda_kernels_{body}_{tag}_{suf}")
+            for suf in sufs:
+                names.add(f"baracuda_kernels_{body.format(tag)}_{suf}")
     return {n for n in names if "_TAG_" not in n}
 
 
@@ -84,6 +87,21 @@ def test_gemm_invalid_problems_rejected_before_launch():
     assert L.gemm_fp8_e4m3_rcr_gfx950_bf16_workspace_size(16, 16, 16) == 0
     assert L.quantized_linear_w8a8_f32_gfx950_can_implement(-1, 2, 2, None, None, None, None, None) == 2
     assert L.quantized_linear_w8a8_f32_gfx950_run(0, 2, 2, None, None, None, None, None, None, 0, None) == 0
+
+
+def test_quantize_can_implement():
+    # baracuda_quantize_compose.cuh:320-330 checks (N > 65535 accepted here).
+    L = ffi.lib()
+    for f in (L.dynamic_range_quantize_per_token_sym_f32_s8_can_implement,
+              L.dynamic_range_quantize_per_token_sym_f64_s8_can_implement,
+              L.dynamic_range_quantize_per_token_sym_bf16_s8_gfx950_can_implement):
+        assert f(4, 8, -127, 127, None, None, None) == 0
+        assert f(-1, 8, -127, 127, None, None, None) == 2
+        assert f(4, 8, 5, 3, None, None, None) == 2
+        assert f(4, 8, -5, 0, None, None, None) == 2
+        assert f(100000, 8, -127, 127, None, None, None) == 0
+    assert L.dynamic_range_quantize_per_token_sym_f32_s8_run(0, 8, -127, 127, None, None, None, None, 0, None) == 0
+    assert L.dynamic_range_quantize_per_token_sym_f32_s8_run(2, 8, -127, 127, None, None, None, None, 0, None) == 2
 
 
 def test_moe_can_implement():

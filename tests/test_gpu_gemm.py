@@ -271,3 +271,90 @@ def test_fp8_matches_hipblaslt(gpu, shape):
     ref = ref.cpu().numpy().astype(np.float64)
     absum = np.abs(O.e4m3_to_f32(a).astype(np.float64)) @ np.abs(O.e4m3_to_f32(b).astype(np.float64)).T
     assert np.all(np.abs(ours - ref) <= 1e-3 * np.abs(ref) + 1e-4 * absum)
+
+
+# ---- per-token dynamic quantization + the W8A8 pipeline ------------------------
+def _quant_gpu(x, dtype, qmin=-127, qmax=127):
+    from baracuda_amd.ffi import lib
+    n, dd = x.shape
+    tx = torch.from_numpy(x).to(dtype).cuda()
+    sdt = torch.float32 if dtype == torch.bfloat16 else dtype
+    scale = torch.zeros(n, dtype=sdt, device="cuda:0")
+    q = torch.zeros((n, dd), dtype=torch.int8, device="cuda:0")
+    L = lib()
+    fn = {torch.float32: L.dynamic_range_quantize_per_token_sym_f32_s8_run,
+          torch.float64: L.dynamic_range_quantize_per_token_sym_f64_s8_run,
+          torch.bfloat16: L.dynamic_range_quantize_per_token_sym_bf16_s8_gfx950_run}[dtype]
+    st = fn(n, dd, qmin, qmax, tx.data_ptr(), scale.data_ptr(), q.data_ptr(), None, 0,
+            torch.cuda.current_stream().cuda_stream)
+    assert st == 0
+    sync()
+    # the value the kernel reads, as f32 (qc_load_as_f32)
+    seen = tx.float().cpu().numpy()
+    return q.cpu().numpy(), scale.cpu().numpy(), seen
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(64, 4096), (7, 333), (3, 20000), (1, 1)])
+def test_quantize_per_token_bit_exact(gpu, dtype, shape):
+    print(f"case: quantize {dtype} {shape}", flush=True)
+    g = rng(shape[0] * 31 + shape[1])
+    x = (g.standard_normal(shape) * 10 ** g.uniform(-2, 2, (shape[0], 1))).astype(np.float64)
+    if shape[0] > 3:
+        x[2] = 0.0
+    q, s, seen = _quant_gpu(x, dtype)
+    wq, ws = O.quantize_per_token_sym(seen)
+    assert np.array_equal(q, wq)
+    assert np.array_equal(s.astype(np.float32), ws)
+
+
+def test_quantize_many_rows_grid_stride(gpu):
+    # N above the 65535-workgroup grid: rows are grid-strided.
+    x = rng(5).standard_normal((70000, 16)).astype(np.float32)
+    q, s, seen = _quant_gpu(x, torch.float32, -128, 127)
+    wq, ws = O.quantize_per_token_sym(seen, -128, 127)
+    assert np.array_equal(q, wq) and np.array_equal(s, ws)
+
+
+def test_quantize_then_w8a8_matches_fp_matmul(gpu):
+    # quantized_linear_smoke.rs: quantize activations per token, weights per
+    # channel, W8A8 GEMM; compare with the fp32 matmul (~2% relative).
+    g = rng(23)
+    m, n, k = 256, 512, 1024
+    a = g.standard_normal((m, k)).astype(np.float32)
+    w = (g.standard_normal((n, k)) * 0.05).astype(np.float32)
+    wq, ws = O.quantize_per_token_sym(w)          # per-output-channel symmetric
+    aq, sa, _ = _quant_gpu(a, torch.float32)
+    d = torch.empty((m, n), dtype=torch.bfloat16, device="cuda:0")
+    P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, output=P.ElementKind.Bf16)).run(
+        dev(aq), dev(wq), d, scale_a=dev(sa), scale_b=dev(ws))
+    sync()
+    got = O.bf16_bits_to_f32(host_bits16(d)).astype(np.float64)
+    ref = a.astype(np.float64) @ w.astype(np.float64).T
+    err = np.abs(got - ref)
+    assert err.max() <= 0.02 * np.abs(ref).max()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_quantized_linear_plan_two_pass(gpu, dtype):
+    # QuantizedLinearPlan::run = quantize (pass 1) + W8A8 GEMM (pass 2); the
+    # output equals the oracle chain on the same activation.
+    g = rng(29)
+    m, c_out, k = 96, 256, 512
+    a = g.standard_normal((m, k)).astype(np.float32)
+    wq, ws = O.quantize_per_token_sym((g.standard_normal((c_out, k)) * 0.1).astype(np.float32))
+    ta = torch.from_numpy(a).to(dtype).cuda()
+    out = torch.empty((m, c_out), dtype=dtype, device="cuda:0")
+    aq = torch.empty((m, k), dtype=torch.int8, device="cuda:0")
+    sa = torch.empty(m, dtype=torch.float32, device="cuda:0")
+    plan = P.QuantizedLinearPlan.select(P.QuantizedLinearDescriptor(m, c_out, k))
+    plan.run(ta, dev(wq), dev(ws), out, aq, sa)
+    sync()
+    qa, sa_ref = O.quantize_per_token_sym(ta.float().cpu().numpy())
+    assert np.array_equal(aq.cpu().numpy(), qa) and np.array_equal(sa.cpu().numpy(), sa_ref)
+    acc = O.gemm_s8_rcr_i32(qa, wq).astype(np.float32)
+    want = (sa_ref[:, None] * ws[None, :]).astype(np.float32) * acc
+    if dtype == torch.float32:
+        assert np.array_equal(out.cpu().numpy(), want)
+    else:
+        assert np.array_equal(host_bits16(out), O.f32_to_bf16_bits_fast(want))

@@ -218,3 +218,36 @@ def test_moe_routing_is_zipf_and_topk_distinct():
     assert np.all(pair_e[0::2] != pair_e[1::2])
     cnt = np.bincount(expert_ids, minlength=8)
     assert cnt[0] > cnt[7] * 2
+
+
+# ---- per-token dynamic quantization (baracuda_quantize_compose.cuh:143-203) --
+def _np_quant(x, qmin, qmax):
+    x = x.astype(np.float32)
+    m = np.abs(x).max(axis=1)
+    s = np.where(m > 0, m / np.float32(qmax), np.float32(1.0)).astype(np.float32)
+    inv = (np.float32(1.0) / s).astype(np.float32)
+    q = np.clip(np.rint((x * inv[:, None]).astype(np.float32)), qmin, qmax).astype(np.int8)
+    return q, s
+
+
+def test_quantize_per_token_reference_fixture():
+    # quantized_linear_smoke.rs:95-101 activation (two rows, per-token ranges).
+    a = np.array([[0.5, -0.3, 0.8, 1.2, -0.4, 0.6, 0.9, -0.7],
+                  [4.0, -2.5, 1.8, -3.2, 2.1, -1.4, 0.9, 3.6]], np.float32)
+    q, s = O.quantize_per_token_sym(a)
+    assert s.tolist() == [np.float32(1.2) / np.float32(127), np.float32(4.0) / np.float32(127)]
+    assert q[0, 3] == 127 and q[1, 0] == 127          # the row max maps to qmax
+    wq, ws = _np_quant(a, -127, 127)
+    assert np.array_equal(q, wq) and np.array_equal(s, ws)
+
+
+@pytest.mark.parametrize("qmin,qmax", [(-127, 127), (-128, 127), (-20, 20)])
+def test_quantize_per_token_against_numpy(qmin, qmax):
+    g = rng(17)
+    x = (g.standard_normal((40, 333)) * 10 ** g.uniform(-3, 3, (40, 1))).astype(np.float32)
+    x[3] = 0.0                    # all-zero row -> scale 1, q 0
+    x[5, 7] = 1e4                 # one dominant value
+    q, s = O.quantize_per_token_sym(x, qmin, qmax)
+    wq, ws = _np_quant(x, qmin, qmax)
+    assert np.array_equal(q, wq) and np.array_equal(s, ws)
+    assert s[3] == 1.0 and not q[3].any()
