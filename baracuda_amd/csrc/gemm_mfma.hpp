@@ -235,6 +235,104 @@ __device__ __forceinline__ void store4_f32(float *d, const float (&y)[4], bool v
 
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// ---- RRR: B is row-major [K, N] (n contiguous) ------------------------------
+// Per stage the B tile (256 n x 128 k) is loaded transposed: thread t owns
+// the 4 columns n = 4*(t % 64) .. +3 over the 16 rows k = 16*(t / 64) .. +15
+// (16 dword loads, workgroup-coalesced along n), byte-transposes them in
+// registers and writes 4 LDS rows of 16 k-bytes, so the LDS image is the same
+// [n][k] tile the RCR path builds and compute_stage is shared.
+template <bool Checked>
+__device__ __forceinline__ void load_b_rrr(v4i (&rb)[LOADS], const int8_t *b, int64_t ldb, int N,
+                                           int K, int n0, int kbyte, int tid) {
+    const int n = n0 + 4 * (tid & 63);
+    const int k0 = kbyte + 16 * (tid >> 6);
+    uint32_t w[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int k = k0 + r;
+        if constexpr (!Checked) {
+            w[r] = *reinterpret_cast<const uint32_t *>(b + (int64_t)k * ldb + n);
+        } else {
+            uint32_t v = 0;
+            if (k < K) {
+                const int8_t *p = b + (int64_t)k * ldb;
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    if (n + c < N) v |= (uint32_t)(uint8_t)p[n + c] << (8 * c);
+            }
+            w[r] = v;
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < LOADS; ++c) {
+        uint32_t o[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            o[q] = ((w[4 * q] >> (8 * c)) & 0xffu) | (((w[4 * q + 1] >> (8 * c)) & 0xffu) << 8) |
+                   (((w[4 * q + 2] >> (8 * c)) & 0xffu) << 16) | (((w[4 * q + 3] >> (8 * c)) & 0xffu) << 24);
+        rb[c] = v4i{(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
+    }
+}
+
+__device__ __forceinline__ void store_b_rrr(int8_t *lb, const v4i (&rb)[LOADS], int tid) {
+    const int unit = tid >> 6;                 // 16-byte k unit of the 128-byte row
+#pragma unroll
+    for (int c = 0; c < LOADS; ++c) {
+        const int row = 4 * (tid & 63) + c;    // n within the tile
+        *reinterpret_cast<v4i *>(lb + lds_off(row, unit)) = rb[c];
+    }
+}
+
+// K loop for one 256x256 RRR tile (A as in mainloop, B through load_b_rrr).
+// CheckedB: N tail / unaligned B rows / K tail on B.
+template <bool CheckedA, bool CheckedB>
+__device__ __forceinline__ void mainloop_rrr(int8_t *lds, const RowSet &as, const int8_t *b,
+                                             int64_t ldb, int N, int n0, int K,
+                                             v4i (&acc)[TM][TN]) {
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wave_m = wave / WAVES_N;
+    const int wave_n = wave % WAVES_N;
+    const int unit = tid & 7;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+    const int KT = (K + BK - 1) / BK;
+    v4i ra[LOADS], rb[LOADS];
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) ra[i] = load_chunk<CheckedA>(as.ptr[i], unit * 16, K);
+    load_b_rrr<CheckedB>(rb, b, ldb, N, K, n0, 0, tid);
+    {
+        const int row0 = tid >> 3;
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i)
+            *reinterpret_cast<v4i *>(lds + lds_off(i * LOAD_ROWS + row0, unit)) = ra[i];
+        store_b_rrr(lds + LDS_TILE, rb, tid);
+    }
+    __syncthreads();
+    for (int kt = 0; kt < KT; ++kt) {
+        int8_t *cur = lds + (kt & 1) * 2 * LDS_TILE;
+        int8_t *nxt = lds + ((kt + 1) & 1) * 2 * LDS_TILE;
+        const bool more = kt + 1 < KT;
+        if (more) {
+#pragma unroll
+            for (int i = 0; i < LOADS; ++i) ra[i] = load_chunk<CheckedA>(as.ptr[i], (kt + 1) * BK + unit * 16, K);
+            load_b_rrr<CheckedB>(rb, b, ldb, N, K, n0, (kt + 1) * BK, tid);
+        }
+        compute_stage<Elem::S8>(cur, cur + LDS_TILE, acc, wave_m, wave_n, lane);
+        if (more) {
+            const int row0 = tid >> 3;
+#pragma unroll
+            for (int i = 0; i < LOADS; ++i)
+                *reinterpret_cast<v4i *>(nxt + lds_off(i * LOAD_ROWS + row0, unit)) = ra[i];
+            store_b_rrr(nxt + LDS_TILE, rb, tid);
+        }
+        __syncthreads();
+    }
+}
+
 // Tile index -> (tile_m, tile_n).  Consecutive workgroups are dispatched
 // round-robin over the 8 XCDs, so the linear id is first regrouped so that
 // each XCD gets a contiguous run of tiles, and runs are laid out in groups

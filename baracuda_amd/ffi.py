@@ -68,6 +68,18 @@ _sig("baracuda_kernels_dynamic_range_quantize_per_token_sym_bf16_s8_gfx950_run",
 _sig("baracuda_kernels_dynamic_range_quantize_per_token_sym_bf16_s8_gfx950_can_implement", i32, i32, i32,
      i32, i32, vp, vp, vp)
 
+_RCR_RUN = (i32, i32, i32, vp, i64, vp, i64, vp, i64, vp, i64)
+for _e in ("bias", "bias_relu", "bias_gelu", "bias_silu"):
+    for _b in ("f32", "i32"):
+        _sig(f"baracuda_kernels_gemm_{_e}_{_b}bias_s8_rcr_gfx950_run", i32, *_RCR_RUN, vp, f32, f32, vp, sz, vp)
+        _sig(f"baracuda_kernels_gemm_{_e}_{_b}bias_s8_rcr_gfx950_workspace_size", sz, i32, i32, i32)
+        _sig(f"baracuda_kernels_gemm_{_e}_{_b}bias_s8_rcr_gfx950_can_implement", i32, *_RCR_RUN, vp)
+        _sig(f"baracuda_kernels_gemm_s8_rrr_gfx950_{_e}_{_b}_run", i32, *_RCR_RUN, vp, f32, f32, vp, sz, vp)
+        _sig(f"baracuda_kernels_gemm_s8_rrr_gfx950_{_e}_{_b}_can_implement", i32, *_RCR_RUN)
+_sig("baracuda_kernels_gemm_s8_rrr_gfx950_run", i32, *_RCR_RUN, f32, f32, vp, sz, vp)
+_sig("baracuda_kernels_gemm_s8_rrr_gfx950_workspace_size", sz, i32, i32, i32)
+_sig("baracuda_kernels_gemm_s8_rrr_gfx950_can_implement", i32, *_RCR_RUN)
+
 SYMBOLS = tuple(_SIGS)
 
 _lib = None

@@ -157,13 +157,17 @@ class IntGemmDescriptor:
     layout: LayoutSku = LayoutSku.Rcr
     epilogue: EpilogueKind = EpilogueKind.Identity
     output: ElementKind = ElementKind.S8     # S8 (reference), I32 or Bf16 (W8A8)
+    bias_element: ElementKind = ElementKind.F32   # BiasElementKind for Bias* epilogues: F32 / I32
 
 
 class IntGemmPlan:
     """int_gemm.rs IntGemmPlan: select / can_implement / workspace_size / sku / run.
 
-    RCR only on gfx950; outputs: S8 (sat(alpha*acc+beta*C)), I32 (raw acc),
-    Bf16 (W8A8 per-token x per-channel dequant, needs scale_a / scale_b)."""
+    RCR (int_gemm.rs:73-85, CUTLASS arm) and RRR (:86-124, bespoke arm) for S8
+    operands.  S8 output: D = sat_s8(rne(act(alpha*acc + beta*C + bias[n]))) for
+    the Identity and Bias / BiasRelu / BiasGelu / BiasSilu epilogues, bias f32
+    or i32 [N].  RCR additionally offers I32 (raw accumulator) and Bf16 (W8A8
+    per-token x per-channel dequant, needs scale_a / scale_b) with Identity."""
 
     def __init__(self, desc: IntGemmDescriptor, sku: GemmSku):
         self.desc, self._sku = desc, sku
@@ -172,13 +176,16 @@ class IntGemmPlan:
     def select(cls, desc: IntGemmDescriptor) -> "IntGemmPlan":
         if desc.m <= 0 or desc.n <= 0 or desc.k <= 0:
             raise InvalidProblem("int GEMM problem must have positive M, N, K")
-        if desc.layout != LayoutSku.Rcr:
-            raise Unsupported("gfx950 int8 GEMM implements the RCR layout")
-        if desc.epilogue != EpilogueKind.Identity:
-            raise Unsupported("gfx950 int8 GEMM implements the Identity epilogue")
         if desc.output not in (ElementKind.S8, ElementKind.I32, ElementKind.Bf16):
             raise Unsupported(f"int8 GEMM output {desc.output}")
-        return cls(desc, GemmSku(ArchSku.Gfx950, desc.layout, desc.epilogue, ElementKind.S8, desc.output))
+        if desc.output != ElementKind.S8 and (desc.layout != LayoutSku.Rcr or
+                                              desc.epilogue != EpilogueKind.Identity):
+            raise Unsupported("I32 / Bf16 outputs are RCR with the Identity epilogue")
+        has_bias = desc.epilogue != EpilogueKind.Identity
+        if has_bias and desc.bias_element not in (ElementKind.F32, ElementKind.I32):
+            raise Unsupported(f"bias element {desc.bias_element}")
+        return cls(desc, GemmSku(ArchSku.Gfx950, desc.layout, desc.epilogue, ElementKind.S8, desc.output,
+                                 desc.bias_element if has_bias else None))
 
     def sku(self) -> GemmSku:
         return self._sku
@@ -186,33 +193,57 @@ class IntGemmPlan:
     def precision_guarantee(self) -> PrecisionGuarantee:
         return self._sku.precision_guarantee()
 
-    def workspace_size(self) -> int:
+    def _symbol(self, suffix: str):
         d, L = self.desc, lib()
-        f = {ElementKind.S8: L.gemm_s8_rcr_gfx950_workspace_size,
-             ElementKind.I32: L.gemm_s8_rcr_gfx950_i32_workspace_size,
-             ElementKind.Bf16: L.gemm_w8a8_rcr_gfx950_bf16_workspace_size}[d.output]
-        return f(d.m, d.n, d.k)
+        if d.output == ElementKind.I32:
+            return getattr(L, f"gemm_s8_rcr_gfx950_i32_{suffix}")
+        if d.output == ElementKind.Bf16:
+            return getattr(L, f"gemm_w8a8_rcr_gfx950_bf16_{suffix}")
+        epi, bt = d.epilogue.value, d.bias_element.value
+        if d.layout == LayoutSku.Rcr:
+            if d.epilogue == EpilogueKind.Identity:
+                return getattr(L, f"gemm_s8_rcr_gfx950_{suffix}")
+            return getattr(L, f"gemm_{epi}_{bt}bias_s8_rcr_gfx950_{suffix}")
+        if d.epilogue == EpilogueKind.Identity:
+            return getattr(L, f"gemm_s8_rrr_gfx950_{suffix}")
+        if suffix == "workspace_size":
+            return None
+        return getattr(L, f"gemm_s8_rrr_gfx950_{epi}_{bt}_{suffix}")
 
-    def can_implement(self, a, b, d, c=None) -> None:
+    def workspace_size(self) -> int:
+        f = self._symbol("workspace_size")
+        return 0 if f is None else f(self.desc.m, self.desc.n, self.desc.k)
+
+    def can_implement(self, a, b, d, c=None, bias=None) -> None:
         desc = self.desc
         _need(tuple(a.shape) == (desc.m, desc.k), "A shape mismatch with descriptor (M, K)")
-        _need(tuple(b.shape) == (desc.n, desc.k), "B shape mismatch with descriptor ([N, K] = col-major [K, N])")
+        if desc.layout == LayoutSku.Rcr:
+            _need(tuple(b.shape) == (desc.n, desc.k), "B shape mismatch with descriptor ([N, K] = col-major [K, N])")
+        else:
+            _need(tuple(b.shape) == (desc.k, desc.n), "B shape mismatch with descriptor (K, N) (row-major)")
         _need(tuple(d.shape) == (desc.m, desc.n), "D shape mismatch with descriptor (M, N)")
         want = {ElementKind.S8: torch.int8, ElementKind.I32: torch.int32, ElementKind.Bf16: torch.bfloat16}[desc.output]
         _need(a.dtype == torch.int8 and b.dtype == torch.int8 and d.dtype == want, "dtype mismatch")
         if c is not None:
             _need(tuple(c.shape) == (desc.m, desc.n) and c.dtype == torch.int8, "C shape mismatch")
+        if desc.epilogue != EpilogueKind.Identity:
+            bdt = torch.float32 if desc.bias_element == ElementKind.F32 else torch.int32
+            _need(bias is not None, "Bias* epilogue needs a bias vector")
+            _need(bias.numel() >= desc.n and bias.dtype == bdt and bias.is_contiguous(),
+                  "bias must be a contiguous [N] vector of the descriptor's bias element")
 
     def run(self, a, b, d, c=None, alpha=1.0, beta=0.0, scale_a=None, scale_b=None,
-            workspace=None, stream=None) -> None:
-        self.can_implement(a, b, d, c)
+            bias=None, workspace=None, stream=None) -> None:
+        self.can_implement(a, b, d, c, bias)
         desc, L, s = self.desc, lib(), _stream(stream)
         if desc.output == ElementKind.S8:
             if c is None:
                 beta = 0.0
-            st = L.gemm_s8_rcr_gfx950_run(desc.m, desc.n, desc.k, _ptr(a), _ld(a), _ptr(b), _ld(b),
-                                          _ptr(c), _ld(c) if c is not None else 0, _ptr(d), _ld(d),
-                                          alpha, beta, _ptr(workspace), 0, s)
+            args = [desc.m, desc.n, desc.k, _ptr(a), _ld(a), _ptr(b), _ld(b),
+                    _ptr(c), _ld(c) if c is not None else 0, _ptr(d), _ld(d)]
+            if desc.epilogue != EpilogueKind.Identity:
+                args.append(_ptr(bias))
+            st = self._symbol("run")(*args, alpha, beta, _ptr(workspace), 0, s)
         elif desc.output == ElementKind.I32:
             st = L.gemm_s8_rcr_gfx950_i32_run(desc.m, desc.n, desc.k, _ptr(a), _ld(a), _ptr(b), _ld(b),
                                               _ptr(d), _ld(d), _ptr(workspace), 0, s)

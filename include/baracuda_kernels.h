@@ -81,6 +81,67 @@ int32_t baracuda_kernels_quantized_linear_w8a8_f32_gfx950_can_implement(
     int32_t M, int32_t C_out, int32_t K, const void *weight_q, const void *act_q,
     const void *scale_a, const void *scale_w, const void *output);
 
+/* int8 RCR with the bias / activation epilogue family.  Same ABI as
+ * baracuda_kernels_gemm_{bias,bias_relu,bias_gelu,bias_silu}_{f32bias,i32bias}_s8_rcr_sm80_*
+ * (crates/baracuda-cutlass-kernels-sys/kernels/gemm_s8_rcr_sm80_bias.cu:225-275,
+ *  crates/baracuda-kernels-sys/src/cutlass_reexport.rs:1025-):
+ * D = sat_s8(rne(act(alpha*acc + beta*C + bias[n]))), act in {identity, relu,
+ * gelu (erf), silu}, bias f32 or i32 [N]. */
+#define BK_S8_RCR_BIAS_DECL(EPI, BIAS)                                                          \
+    int32_t baracuda_kernels_gemm_##EPI##_##BIAS##_s8_rcr_gfx950_run(                           \
+        int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb, \
+        const void *c, int64_t ldc, void *d, int64_t ldd, const void *bias, float alpha,         \
+        float beta, void *workspace, size_t workspace_bytes, void *stream);                      \
+    size_t baracuda_kernels_gemm_##EPI##_##BIAS##_s8_rcr_gfx950_workspace_size(int32_t m,       \
+                                                                             int32_t n, int32_t k); \
+    int32_t baracuda_kernels_gemm_##EPI##_##BIAS##_s8_rcr_gfx950_can_implement(                 \
+        int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb, \
+        const void *c, int64_t ldc, void *d, int64_t ldd, const void *bias);
+BK_S8_RCR_BIAS_DECL(bias, f32bias)
+BK_S8_RCR_BIAS_DECL(bias_relu, f32bias)
+BK_S8_RCR_BIAS_DECL(bias_gelu, f32bias)
+BK_S8_RCR_BIAS_DECL(bias_silu, f32bias)
+BK_S8_RCR_BIAS_DECL(bias, i32bias)
+BK_S8_RCR_BIAS_DECL(bias_relu, i32bias)
+BK_S8_RCR_BIAS_DECL(bias_gelu, i32bias)
+BK_S8_RCR_BIAS_DECL(bias_silu, i32bias)
+#undef BK_S8_RCR_BIAS_DECL
+
+/* ======================= int8 GEMM, RRR layout ===========================
+ * A row-major [M,K] (lda), B row-major [K,N] (ldb), D row-major [M,N].
+ * Replaces baracuda_kernels_gemm_s8_rrr_sm80_{run,workspace_size,can_implement}
+ * (crates/baracuda-kernels-sys/kernels/gemm/gemm_s8_rrr_sm80.cu:28-64):
+ * D = sat_s8(rne(alpha*acc + beta*C)). */
+int32_t baracuda_kernels_gemm_s8_rrr_gfx950_run(
+    int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,
+    const void *c, int64_t ldc, void *d, int64_t ldd, float alpha, float beta,
+    void *workspace, size_t workspace_bytes, void *stream);
+size_t baracuda_kernels_gemm_s8_rrr_gfx950_workspace_size(int32_t m, int32_t n, int32_t k);
+int32_t baracuda_kernels_gemm_s8_rrr_gfx950_can_implement(
+    int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,
+    const void *c, int64_t ldc, void *d, int64_t ldd);
+
+/* RRR bias / activation family.  Same ABI as
+ * baracuda_kernels_gemm_s8_rrr_sm80_{bias,bias_relu,bias_gelu,bias_silu}_{f32,i32}_{run,can_implement}
+ * (crates/baracuda-kernels-sys/kernels/gemm/gemm_s8_rrr_sm80_bias.cu:48-267). */
+#define BK_S8_RRR_BIAS_DECL(EPI, BIAS)                                                          \
+    int32_t baracuda_kernels_gemm_s8_rrr_gfx950_##EPI##_##BIAS##_run(                           \
+        int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb, \
+        const void *c, int64_t ldc, void *d, int64_t ldd, const void *bias, float alpha,         \
+        float beta, void *workspace, size_t workspace_bytes, void *stream);                      \
+    int32_t baracuda_kernels_gemm_s8_rrr_gfx950_##EPI##_##BIAS##_can_implement(                 \
+        int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb, \
+        const void *c, int64_t ldc, const void *d, int64_t ldd);
+BK_S8_RRR_BIAS_DECL(bias, f32)
+BK_S8_RRR_BIAS_DECL(bias_relu, f32)
+BK_S8_RRR_BIAS_DECL(bias_gelu, f32)
+BK_S8_RRR_BIAS_DECL(bias_silu, f32)
+BK_S8_RRR_BIAS_DECL(bias, i32)
+BK_S8_RRR_BIAS_DECL(bias_relu, i32)
+BK_S8_RRR_BIAS_DECL(bias_gelu, i32)
+BK_S8_RRR_BIAS_DECL(bias_silu, i32)
+#undef BK_S8_RRR_BIAS_DECL
+
 /* ======================= per-token dynamic int8 quantization =============
  * Replaces baracuda_kernels_dynamic_range_quantize_per_token_sym_{f32,f64}_s8_{run,can_implement}
  * (crates/baracuda-kernels-sys/kernels/include/baracuda_quantize_compose.cuh:143-203,306-338,

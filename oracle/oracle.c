@@ -189,6 +189,46 @@ void bo_gemm_s8_rcr_s8(int64_t m, int64_t n, int64_t k,
         }
 }
 
+/* int8_rrr_smoke.rs:35-48 (erf_approx), f32 arithmetic in the test's order. */
+float bo_erf_as7126(float x) {
+    const float sign = x < 0.0f ? -1.0f : 1.0f;
+    const float ax = fabsf(x);
+    const float p = 0.3275911f, a1 = 0.254829592f, a2 = -0.284496736f, a3 = 1.421413741f,
+                a4 = -1.453152027f, a5 = 1.061405429f;
+    const float t = 1.0f / (1.0f + p * ax);
+    const float y = 1.0f - (((((a5 * t + a4) * t) + a3) * t + a2) * t + a1) * t * expf(-ax * ax);
+    return sign * y;
+}
+
+static float act_apply(int act, float x) {
+    switch (act) {
+    case 1: return x > 0.0f ? x : 0.0f;                                          /* relu :31-33 */
+    case 2: return 0.5f * x * (1.0f + bo_erf_as7126(x * (1.0f / 1.41421356237309504880f))); /* :50-53 */
+    case 3: return x / (1.0f + expf(-x));                                        /* silu :55-57 */
+    default: return x;
+    }
+}
+
+/* int8_rrr_smoke.rs:97-131 (cpu_int_gemm_rrr; the RCR twin indexes b[j*ldb+k]).
+ * The sum is exact in int64; for |a|,|b| <= 128 and k < 2^17 it equals the
+ * reference's saturating i32 sum. */
+void bo_gemm_s8_epi(int64_t m, int64_t n, int64_t k,
+                    const int8_t *a, int64_t lda,
+                    const int8_t *b, int64_t sbk, int64_t sbn,
+                    const int8_t *c, int64_t ldc, const float *bias, int act,
+                    int8_t *d, int64_t ldd, float alpha, float beta) {
+    for (int64_t i = 0; i < m; ++i)
+        for (int64_t j = 0; j < n; ++j) {
+            int64_t acc = 0;
+            for (int64_t kk = 0; kk < k; ++kk)
+                acc += (int64_t)a[i * lda + kk] * (int64_t)b[kk * sbk + j * sbn];
+            float z = alpha * (float)(int32_t)acc;
+            if (c != NULL) z += beta * (float)c[i * ldc + j];
+            if (bias != NULL) z += bias[j];
+            d[i * ldd + j] = bo_sat_cast_s8(act_apply(act, z));
+        }
+}
+
 /* baracuda_quantize_compose.cuh:265-274: y = sa*sw*(float)acc, evaluated
  * left to right in f32, i.e. (sa*sw)*acc; the bf16 store is oracle.rs:397-404. */
 void bo_gemm_w8a8_rcr_bf16(int64_t m, int64_t n, int64_t k,

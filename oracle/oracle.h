@@ -62,6 +62,20 @@ void bo_gemm_s8_rcr_s8(int64_t m, int64_t n, int64_t k,
                        int8_t *d, int64_t ldd,
                        float alpha, float beta);
 
+/* int8-out GEMM with the bias / activation epilogue of the reference's RRR
+ * and RCR smoke tests (crates/baracuda-kernels/tests/int8_rrr_smoke.rs:31-131):
+ *   acc = sum_k a[i,k]*b[k,j]   with b[k,j] at b[k*sbk + j*sbn]
+ *   z   = alpha*(f32)acc + beta*(f32)C[i,j] (when c) + bias[j] (when bias)
+ *   D   = sat_cast_s8(act(z))
+ * act: 0 none, 1 relu, 2 gelu (erf via Abramowitz-Stegun 7.1.26), 3 silu.
+ * Bias is passed as f32 (an i32 bias converts exactly for |bias| < 2^24). */
+void bo_gemm_s8_epi(int64_t m, int64_t n, int64_t k,
+                    const int8_t *a, int64_t lda,
+                    const int8_t *b, int64_t sbk, int64_t sbn,
+                    const int8_t *c, int64_t ldc, const float *bias, int act,
+                    int8_t *d, int64_t ldd, float alpha, float beta);
+float bo_erf_as7126(float x);
+
 /* W8A8: out = bf16( (sa[m]*sw[n]) * (f32)acc ) with f32 products. */
 void bo_gemm_w8a8_rcr_bf16(int64_t m, int64_t n, int64_t k,
                            const int8_t *a, int64_t lda,

@@ -43,6 +43,9 @@ def _L():
             "bo_contraction_f64": (None, [i64, i64, i64, vp, i64, i64, vp, i64, i64, vp, i64]),
             "bo_gemm_s8_rcr_i32": (None, [i64, i64, i64, vp, i64, vp, i64, vp, i64, i64, i64, i32]),
             "bo_gemm_s8_rcr_s8": (None, [i64, i64, i64, vp, i64, vp, i64, vp, i64, vp, i64, f32, f32]),
+            "bo_gemm_s8_epi": (None, [i64, i64, i64, vp, i64, vp, i64, i64, vp, i64, vp,
+                                      C.c_int, vp, i64, f32, f32]),
+            "bo_erf_as7126": (f32, [f32]),
             "bo_gemm_w8a8_rcr_bf16": (None, [i64, i64, i64, vp, i64, vp, i64, vp, vp, vp, i64, i64, i64, i32]),
             "bo_gemm_fp8_e4m3_rcr_f64": (None, [i64, i64, i64, vp, i64, vp, i64, vp, i64, i64, i64, i32]),
             "bo_gemm_fp8_e4m3_rcr_f32": (None, [i64, i64, i64, vp, i64, vp, i64, vp, i64]),
@@ -146,6 +149,35 @@ def gemm_s8_rcr_s8(a, b, alpha, beta=0.0, c=None) -> np.ndarray:
     _L().bo_gemm_s8_rcr_s8(m, n, k, _p(a), k, _p(b), k, None if cp is None else _p(cp), n,
                            _p(d), n, alpha, beta)
     return d
+
+
+ACTS = {None: 0, "relu": 1, "gelu": 2, "silu": 3}
+
+
+def gemm_s8_epi(a, b, layout, alpha, beta=0.0, c=None, bias=None, act=None) -> np.ndarray:
+    """int8-out GEMM with optional C, bias [N] (any numeric dtype, read as f32)
+    and activation. layout "rcr": b is [N, K]; "rrr": b is [K, N]."""
+    a = np.ascontiguousarray(a, dtype=np.int8)
+    b = np.ascontiguousarray(b, dtype=np.int8)
+    m, k = a.shape
+    if layout == "rcr":
+        n = b.shape[0]
+        sbk, sbn = 1, k
+    elif layout == "rrr":
+        n = b.shape[1]
+        sbk, sbn = n, 1
+    else:
+        raise ValueError(layout)
+    d = np.zeros((m, n), dtype=np.int8)
+    cp = None if c is None else np.ascontiguousarray(c, dtype=np.int8)
+    bp = None if bias is None else np.ascontiguousarray(np.asarray(bias).astype(np.float32))
+    _L().bo_gemm_s8_epi(m, n, k, _p(a), k, _p(b), sbk, sbn, None if cp is None else _p(cp), n,
+                        None if bp is None else _p(bp), ACTS[act], _p(d), n, alpha, beta)
+    return d
+
+
+def erf_as7126(x: float) -> float:
+    return _L().bo_erf_as7126(x)
 
 
 def gemm_w8a8_bf16(a, w, sa, sw, rows=None, nthreads=1) -> np.ndarray:

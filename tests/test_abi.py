@@ -22,7 +22,13 @@ def _declared():
         for tag in re.findall(tag_macro + r"\((\w+)\)", text):
             for suf in sufs:
                 names.add(f"baracuda_kernels_{body.format(tag)}_{suf}")
-    return {n for n in names if "_TAG_" not in n}
+    for epi, bias in re.findall(r"BK_S8_RCR_BIAS_DECL\((\w+), (\w+)\)", text):
+        for suf in ("run", "workspace_size", "can_implement"):
+            names.add(f"baracuda_kernels_gemm_{epi}_{bias}_s8_rcr_gfx950_{suf}")
+    for epi, bias in re.findall(r"BK_S8_RRR_BIAS_DECL\((\w+), (\w+)\)", text):
+        for suf in ("run", "can_implement"):
+            names.add(f"baracuda_kernels_gemm_s8_rrr_gfx950_{epi}_{bias}_{suf}")
+    return {n for n in names if "_TAG_" not in n and "##" not in n and "_EPI_" not in n}
 
 
 def test_header_and_binding_agree():
@@ -89,6 +95,30 @@ def test_gemm_invalid_problems_rejected_before_launch():
     assert L.quantized_linear_w8a8_f32_gfx950_run(0, 2, 2, None, None, None, None, None, None, 0, None) == 0
 
 
+
+def test_rrr_and_bias_can_implement():
+    # gemm_s8_rrr_sm80.cu:44-52: positive extents, lda >= K, ldb >= N, ldd >= N.
+    L = ffi.lib()
+    assert L.gemm_s8_rrr_gfx950_can_implement(4, 8, 16, None, 16, None, 8, None, 0, None, 8) == 0
+    assert L.gemm_s8_rrr_gfx950_can_implement(4, 8, 16, None, 16, None, 7, None, 0, None, 8) == 2
+    assert L.gemm_s8_rrr_gfx950_can_implement(4, 8, 16, None, 15, None, 8, None, 0, None, 8) == 2
+    assert L.gemm_s8_rrr_gfx950_can_implement(0, 8, 16, None, 16, None, 8, None, 0, None, 8) == 2
+    assert L.gemm_s8_rrr_gfx950_workspace_size(64, 64, 64) == 0
+    for epi in ("bias", "bias_relu", "bias_gelu", "bias_silu"):
+        for bt in ("f32", "i32"):
+            assert getattr(L, f"gemm_s8_rrr_gfx950_{epi}_{bt}_can_implement")(
+                4, 8, 16, None, 16, None, 8, None, 0, None, 8) == 0
+            # run refuses a missing bias before launching anything
+            assert getattr(L, f"gemm_s8_rrr_gfx950_{epi}_{bt}_run")(
+                4, 8, 16, None, 16, None, 8, None, 0, None, 8, None, 1.0, 0.0, None, 0, None) == 2
+            rcr = f"gemm_{epi}_{bt}bias_s8_rcr_gfx950_"
+            assert getattr(L, rcr + "can_implement")(4, 8, 16, None, 16, None, 16, None, 0, None, 8, None) == 0
+            assert getattr(L, rcr + "can_implement")(4, 8, 16, None, 16, None, 15, None, 0, None, 8, None) == 2
+            assert getattr(L, rcr + "workspace_size")(4, 8, 16) == 0
+            assert getattr(L, rcr + "run")(4, 8, 16, None, 16, None, 16, None, 0, None, 8, None,
+                                           1.0, 0.0, None, 0, None) == 2
+
+
 def test_quantize_can_implement():
     # baracuda_quantize_compose.cuh:320-330 checks (N > 65535 accepted here).
     L = ffi.lib()
@@ -122,8 +152,17 @@ def test_plan_select_and_sku():
     assert plan.workspace_size() == 0
     with pytest.raises(P.InvalidProblem):
         P.IntGemmPlan.select(P.IntGemmDescriptor(0, 1, 1))
+    rrr = P.IntGemmPlan.select(P.IntGemmDescriptor(8, 8, 8, layout=P.LayoutSku.Rrr,
+                                                   epilogue=P.EpilogueKind.BiasGelu,
+                                                   bias_element=P.ElementKind.I32))
+    assert rrr.sku().layout == P.LayoutSku.Rrr and rrr.sku().bias_element == P.ElementKind.I32
+    assert rrr.workspace_size() == 0
+    assert P.IntGemmPlan.select(P.IntGemmDescriptor(8, 8, 8)).sku().bias_element is None
+    with pytest.raises(P.Unsupported):   # raw accumulator is RCR / Identity only
+        P.IntGemmPlan.select(P.IntGemmDescriptor(8, 8, 8, layout=P.LayoutSku.Rrr, output=P.ElementKind.I32))
     with pytest.raises(P.Unsupported):
-        P.IntGemmPlan.select(P.IntGemmDescriptor(8, 8, 8, layout=P.LayoutSku.Rrr))
+        P.IntGemmPlan.select(P.IntGemmDescriptor(8, 8, 8, epilogue=P.EpilogueKind.Bias,
+                                                 bias_element=P.ElementKind.F16))
     f = P.Fp8GemmPlan.select(P.Fp8GemmDescriptor(2048, 14336, 4096, output=P.ElementKind.Bf16))
     assert f.sku().element == P.ElementKind.Fp8E4M3 and f.workspace_size() == 0
     with pytest.raises(P.InvalidProblem):

@@ -141,6 +141,50 @@ def test_gemm_s8_sat_epilogue_reference_pattern():
     assert np.array_equal(O.gemm_s8_rcr_s8(a, b, 0.125, 0.5, c), np.clip(np.rint(z), -128, 127).astype(np.int8))
 
 
+def test_erf_as7126_against_libm():
+    # A&S 7.1.26 has |error| <= 1.5e-7; f32 evaluation adds a few ulp.
+    xs = np.linspace(-6, 6, 2001, dtype=np.float32)
+    err = max(abs(O.erf_as7126(float(x)) - math.erf(float(x))) for x in xs)
+    assert err < 1e-6
+    assert O.erf_as7126(0.0) == 0.0 and O.erf_as7126(-2.0) == -O.erf_as7126(2.0)
+
+
+def _mk_bias(n, kind):
+    # int8_rrr_smoke.rs bias patterns: f32 ((j%5)-2)*0.5, i32 ((j%5)-2)*2.
+    j = np.arange(n)
+    return ((j % 5) - 2) * 0.5 if kind == "f32" else ((j % 5) - 2) * 2
+
+
+@pytest.mark.parametrize("act", [None, "relu", "gelu", "silu"])
+@pytest.mark.parametrize("shape", [(64, 64, 32), (100, 70, 50)])
+def test_gemm_s8_epi_closed_forms(act, shape):
+    m, n, k = shape
+    g = rng(m + n + k)
+    a, bt = int8_uniform(g, (m, k)), int8_uniform(g, (n, k))
+    c = int8_uniform(g, (m, n))
+    bias = _mk_bias(n, "f32")
+    acc = a.astype(np.int64) @ bt.astype(np.int64).T
+    z = (np.float32(0.125) * acc.astype(np.float32) + np.float32(0.5) * c.astype(np.float32)
+         + bias.astype(np.float32)).astype(np.float32)
+    if act == "relu":
+        z = np.maximum(z, np.float32(0))
+    elif act == "gelu":
+        z = np.float32(0.5) * z * (1 + np.vectorize(math.erf)(z / math.sqrt(2))).astype(np.float32)
+    elif act == "silu":
+        z = (z / (1 + np.exp(-z.astype(np.float64)))).astype(np.float32)
+    want = np.clip(np.rint(z), -128, 127).astype(np.int8)
+    rcr = O.gemm_s8_epi(a, bt, "rcr", 0.125, 0.5, c, bias, act)
+    rrr = O.gemm_s8_epi(a, np.ascontiguousarray(bt.T), "rrr", 0.125, 0.5, c, bias, act)
+    assert np.array_equal(rcr, rrr)               # layout only changes indexing
+    diff = np.abs(rcr.astype(int) - want.astype(int))
+    if act in (None, "relu"):
+        assert diff.max() == 0
+    else:                                         # approximated erf / f32 exp
+        assert diff.max() <= 1 and (diff != 0).mean() < 0.01
+    # no bias, no C: the plain int8 epilogue
+    assert np.array_equal(O.gemm_s8_epi(a, bt, "rcr", 0.125), O.gemm_s8_rcr_s8(a, bt, 0.125))
+
+
 def test_w8a8_bf16_epilogue_against_torch():
     g = rng(2)
     m, n, k = 64, 96, 160
