@@ -85,7 +85,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",
-                    help="run only: w8a8|gemv|fp8|moe|gather|copy (profiling; copy = 256 MiB "
+                    help="run only: w8a8|gemv|fp8|moe|int8epi|gather|copy (profiling; copy = 256 MiB "
                          "device copy used to calibrate the HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -186,6 +186,28 @@ def main():
                 "us": round(mms * 1e3, 1), "TOPS": round(mt, 1), "frac_int8_peak": round(mt / PEAK_INT8_TOPS, 4),
                 "expert_rows": np.bincount(eid, minlength=E).tolist()}
             del mx, mw, mo
+        if only in ("", "int8epi"):
+            log("bench: int8 s8-out RCR bias_gelu / RRR 4096^3")
+            ia = torch.randint(-127, 128, (M, K), dtype=torch.int8, device=dev)
+            ib = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev)
+            ibr = torch.randint(-127, 128, (K, N), dtype=torch.int8, device=dev)
+            ibias = torch.randn(N, device=dev)
+            idd = torch.empty((M, N), dtype=torch.int8, device=dev)
+            e = {}
+            for name, layout, epi, bmat in (
+                    ("rcr_identity", P.LayoutSku.Rcr, P.EpilogueKind.Identity, ib),
+                    ("rcr_bias_gelu_f32", P.LayoutSku.Rcr, P.EpilogueKind.BiasGelu, ib),
+                    ("rrr_identity", P.LayoutSku.Rrr, P.EpilogueKind.Identity, ibr),
+                    ("rrr_bias_silu_f32", P.LayoutSku.Rrr, P.EpilogueKind.BiasSilu, ibr)):
+                ip = P.IntGemmPlan.select(P.IntGemmDescriptor(M, N, K, layout=layout, epilogue=epi))
+                bias_arg = None if epi == P.EpilogueKind.Identity else ibias
+                ims = time_launches(lambda: ip.run(ia, bmat, idd, alpha=1.0 / 4096, bias=bias_arg,
+                                                   stream=stream), 20, 5, stream)
+                it_ = ops / (ims * 1e-3) / 1e12
+                e[name] = {"us": round(ims * 1e3, 2), "TOPS": round(it_, 1),
+                           "frac_int8_peak": round(it_ / PEAK_INT8_TOPS, 4)}
+            extra["int8_s8out_4096_cubed"] = e
+            del ia, ib, ibr, idd
         if only in ("", "gather"):
             log("bench: gather_rows bf16")
             V, H = 128256, 4096
