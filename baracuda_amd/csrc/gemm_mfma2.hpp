@@ -5,9 +5,10 @@
 // RCR "column-major [K,N]" operand).  Requirements checked by the launcher:
 // K % 128 == 0, lda % 16 == 0, ldb % 16 == 0, 16-byte aligned bases.
 //
-// Block tile 256(M) x 256(N), 256 threads = 4 wave64 (2 x 2), each wave owns
-// a 128 x 128 output tile (256 accumulator registers, kept in AGPRs; one wave
-// per SIMD).  K advances 128 bytes per stage, two stages in flight.
+// Block tile 256(M) x 256(N); Cfg<WAVES_M, WAVES_N, PIPE> picks the wave
+// grid (the int8 and FP8 kernels use 2 x 4 wave64s, each owning a 128 x 64
+// output tile, two waves per SIMD).  K advances 128 bytes per stage, two
+// stages in flight.
 //
 // Global -> LDS: direct DMA (global_load_lds_dwordx4), no staging registers.
 // One DMA instruction writes 1 KiB of LDS linearly (lane L -> bytes 16L..16L+15)
@@ -80,6 +81,9 @@ struct PolicyI8 {
         const int row = row0 + t * 16 + (lane & 15);
         return *reinterpret_cast<const v4i *>(op + lds_off(row, s * 4 + (lane >> 4)));
     }
+    __device__ static Frag load_b(const int8_t *op, int row0, int t, int s, int lane) {
+        return load(op, row0, t, s, lane);
+    }
     static constexpr int H = 1;
     __device__ static void mma(Acc &c, const Frag &b, const Frag &a, int) {
         c = __builtin_amdgcn_mfma_i32_16x16x64_i8(b, a, c, 0, 0, 0);
@@ -109,6 +113,9 @@ struct PolicyI8x32 {
         f.h[0] = *reinterpret_cast<const v4i *>(op + lds_off(row, s * 4 + (lane >> 5)));
         f.h[1] = *reinterpret_cast<const v4i *>(op + lds_off(row, s * 4 + 2 + (lane >> 5)));
         return f;
+    }
+    __device__ static Frag load_b(const int8_t *op, int row0, int t, int s, int lane) {
+        return load(op, row0, t, s, lane);
     }
     static constexpr int H = 2;   // instructions per sub-step per tile
     __device__ static void mma(Acc &c, const Frag &b, const Frag &a, int h) {
@@ -141,6 +148,9 @@ struct PolicyF8 {
         const v4i hi = *reinterpret_cast<const v4i *>(op + lds_off(row, u + 1));
         return Frag{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     }
+    __device__ static Frag load_b(const int8_t *op, int row0, int t, int s, int lane) {
+        return load(op, row0, t, s, lane);
+    }
     static constexpr int H = 1;
     __device__ static void mma(Acc &c, const Frag &b, const Frag &a, int) {
         c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(b, a, c, 0, 0, 0, 0, 0, 0);
@@ -157,6 +167,42 @@ struct PolicyF8 {
     }
 };
 
+// ---------------------------------------------------------------------------
+// Row-major B ([K, N], the RRR layout) kept in LDS as it lies in memory:
+// BK = 128 k-rows of BN = 256 bytes, 16-byte unit c of row k at physical unit
+// c ^ swz_t(k).  Fragments are read with ds_read_b64_tr_b8, whose 16-lane
+// groups see the 8-byte values of lanes (2j, 2j+1) as row j (16 bytes) of an
+// 8 x 16 byte block and return column i of it to lane i: lane i of group g
+// gets 8 consecutive k of output column n0 + i, so two reads rebuild exactly
+// the 16-byte, k-ascending operand that PolicyI8::load gives for A.
+// swz_t maps the 16 k-rows one 32-lane half-wave touches per read
+// ({0..7, 16..23} or {8..15, 24..31} plus multiples of 32) to distinct units.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int swz_t(int k) { return (k & 7) | (((k >> 4) & 1) << 3); }
+__device__ __forceinline__ int lds_off_t(int k, int unit) { return k * BN + ((unit ^ swz_t(k)) << 4); }
+
+typedef int v2i_t __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) v2i_t lds_v2i;
+
+__device__ __forceinline__ v2i_t ds_read_tr8(const int8_t *p) {
+    return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i *)(lds_void *)p);
+}
+
+template <class C>
+struct PolicyI8RowB : PolicyI8<C> {
+    typedef v4i Frag;
+    __device__ static Frag load_b(const int8_t *op, int row0, int t, int s, int lane) {
+        // k of this lane in sub-step 0; the sub-step (+64 rows) and the high
+        // half (+8 rows) leave swz_t unchanged, so they are constant offsets.
+        const int kb = 16 * (lane >> 4) + ((lane & 15) >> 1);
+        const int off = kb * BN + ((((row0 >> 4) + t) ^ swz_t(kb)) << 4) + ((lane & 1) << 3);
+        const int8_t *q = op + off + s * 64 * BN;
+        const v2i_t lo = ds_read_tr8(q);
+        const v2i_t hi = ds_read_tr8(q + 8 * BN);
+        return v4i{lo[0], lo[1], hi[0], hi[1]};
+    }
+};
+
 template <class P>
 struct Frags {
     typename P::Frag a[P::TI];
@@ -170,7 +216,7 @@ template <class P>
 __device__ __forceinline__ void load_frags(Frags<P> &f, const int8_t *stage, int s, int wave_m,
                                            int wave_n, int lane) {
 #pragma unroll
-    for (int t = 0; t < P::TJ; ++t) f.b[t] = P::load(stage + OPER, wave_n * P::Cfg::WN, t, s, lane);
+    for (int t = 0; t < P::TJ; ++t) f.b[t] = P::load_b(stage + OPER, wave_n * P::Cfg::WN, t, s, lane);
 #pragma unroll
     for (int t = 0; t < P::TI; ++t) f.a[t] = P::load(stage, wave_m * P::Cfg::WM, t, s, lane);
 }
@@ -295,6 +341,49 @@ __device__ __forceinline__ void dma_operand(int8_t *dst, const DmaOperand<true> 
     for (int i = 0; i < C::DMA_PER_WAVE; ++i) dma16(d.rsrc, d.off[i], soff, dst + (wave * ROWS_PER_WAVE + i * 8) * BK);
 }
 
+// Row-major B operand ([K, N], leading dimension ld): one DMA instruction
+// writes 4 k-rows of 256 bytes; lane L lands in row L/16 at physical unit
+// L%16 and so fetches logical unit (L%16) ^ swz_t(row).  For 8 waves a wave
+// owns 16 k-rows (4 instructions) and swz_t of its rows depends on the
+// instruction only through its parity, so as for the interior operand the
+// per-lane offset is `even` or `odd`, and the K position plus 4*i*ld travel
+// in the scalar offset.
+struct DmaOperandRowB {
+    v4i rsrc;
+    int even, odd;
+    int ld;
+};
+
+template <class C>
+__device__ __forceinline__ DmaOperandRowB make_dma_row_b(const int8_t *base, uint32_t bytes, int ld,
+                                                         int n_base) {
+    static_assert(BK / C::WAVES == 16, "row-major B DMA assumes 16 k-rows per wave");
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    DmaOperandRowB d;
+    d.rsrc = make_rsrc(base, bytes);
+    d.ld = ld;
+    const int r0 = wave * 16 + (lane >> 4);
+    const int p = lane & 15;
+    d.even = n_base + r0 * ld + ((p ^ swz_t(r0)) << 4);
+    d.odd = n_base + r0 * ld + ((p ^ swz_t(r0 + 4)) << 4);
+    return d;
+}
+
+template <class C>
+__device__ __forceinline__ void dma_operand(int8_t *dst, const DmaOperandRowB &d, int kbyte) {
+    const int wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int soff = __builtin_amdgcn_readfirstlane((kbyte + 4 * i) * d.ld);
+        dma16(d.rsrc, (i & 1) ? d.odd : d.even, soff, dst + (wave * 16 + 4 * i) * BN);
+    }
+}
+
+struct DmaRowsRrr {
+    DmaOperand<false> a;
+    DmaOperandRowB b;
+};
+
 template <bool GA, bool GB>
 struct DmaRows {
     DmaOperand<GA> a;
@@ -330,7 +419,7 @@ __device__ __forceinline__ void stage_step(AccTile<P> &acc, Frags<P> &f0, Frags<
         for (int s = 0; s < 2; ++s) {
             Frags<P> &f = s ? f1 : f0;
 #pragma unroll
-            for (int t = 0; t < P::TJ; ++t) f.b[t] = P::load(cur + OPER, wave_n * C::WN, t, s, lane);
+            for (int t = 0; t < P::TJ; ++t) f.b[t] = P::load_b(cur + OPER, wave_n * C::WN, t, s, lane);
             f.a[0] = P::load(cur, wave_m * C::WM, 0, s, lane);
             if constexpr (C::PIPE == 3) __builtin_amdgcn_s_setprio(1);
 #pragma unroll

@@ -167,7 +167,11 @@ __global__ __launch_bounds__(NT, 1) void gemm_s8_rrr_kernel(S8Args p) {
 }
 
 template <int ACT, typename BiasT>
+int32_t launch_rrr_dma(const S8Args &p, hipStream_t stream);
+
+template <int ACT, typename BiasT>
 int32_t launch_rrr(const S8Args &p, hipStream_t stream) {
+    if (launch_rrr_dma<ACT, BiasT>(p, stream) == kOk) return launch_status();
     const int tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
     const bool aligned = p.K % BK == 0 && p.N % BN == 0 && p.lda % 16 == 0 && p.ldb % 4 == 0 &&
                          aligned16(p.a) && (reinterpret_cast<uintptr_t>(p.b) & 3u) == 0;
@@ -220,6 +224,27 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_s8_rcr_dma_kernel(S8Args p
     }
 }
 
+// RRR fast path: A through the interior DMA, row-major B through the
+// transposing fragment reads (PolicyI8RowB); same tiles and epilogue as RCR.
+template <bool VecOut, int ACT, typename BiasT>
+__global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_s8_rrr_dma_kernel(S8Args p) {
+    namespace M2 = mfma2;
+    typedef M2::PolicyI8RowB<DmaCfg> P;
+    __shared__ __attribute__((aligned(1024))) int8_t stage0[2 * M2::OPER];
+    __shared__ __attribute__((aligned(1024))) int8_t stage1[2 * M2::OPER];
+    const int tiles_m = p.M / M2::BM, tiles_n = p.N / M2::BN;
+    int tm, tn;
+    tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int m_base = tm * M2::BM, n_base = tn * M2::BN;
+    M2::DmaRowsRrr d;
+    d.a = M2::make_dma_interior<DmaCfg>(p.a, (uint32_t)(p.M * p.lda), (int)p.lda, m_base * (int)p.lda);
+    d.b = M2::make_dma_row_b<DmaCfg>(p.b, (uint32_t)(p.K * p.ldb), (int)p.ldb, n_base);
+    M2::AccTile<P> acc;
+    M2::mainloop<P>(stage0, stage1, d, p.K, acc);
+    const S8Epilogue<EPI_S8, VecOut, ACT, BiasT> epi{p};
+    M2::for_each_quad<P>(acc, [&](int ml, int nl, const v4i &v) { epi(m_base + ml, n_base + nl, v); });
+}
+
 template <int EPI, bool VecOut, int ACT, typename BiasT>
 void launch_kernel(const S8Args &p, bool fast_k, hipStream_t stream) {
     if (fast_k) {
@@ -248,6 +273,25 @@ int32_t launch(const S8Args &p, hipStream_t stream) {
     if (vec) launch_kernel<EPI, true, ACT, BiasT>(p, fast_k, stream);
     else launch_kernel<EPI, false, ACT, BiasT>(p, fast_k, stream);
     return launch_status();
+}
+
+// Launches the RRR DMA kernel when the problem fits it (whole 256x256 tiles,
+// K % 128 == 0, 16-byte A / B rows and bases, buffer offsets below 2^31);
+// returns kOk if launched, kUnsupported to let the caller take the general
+// kernel.
+template <int ACT, typename BiasT>
+int32_t launch_rrr_dma(const S8Args &p, hipStream_t stream) {
+    const bool fits = p.K % mfma2::BK == 0 && p.M % mfma2::BM == 0 && p.N % mfma2::BN == 0 &&
+                      p.lda % 16 == 0 && p.ldb % 16 == 0 && aligned16(p.a) && aligned16(p.b) &&
+                      (int64_t)p.M * p.lda < (1ll << 31) && (int64_t)p.K * p.ldb < (1ll << 31);
+    if (!fits) return kUnsupported;
+    const int tiles = (p.M / mfma2::BM) * (p.N / mfma2::BN);
+    const bool vec = p.ldd % 4 == 0 && (reinterpret_cast<uintptr_t>(p.d) % 4) == 0;
+    if (vec)
+        hipLaunchKernelGGL((gemm_s8_rrr_dma_kernel<true, ACT, BiasT>), dim3(tiles), dim3(DmaCfg::NT), 0, stream, p);
+    else
+        hipLaunchKernelGGL((gemm_s8_rrr_dma_kernel<false, ACT, BiasT>), dim3(tiles), dim3(DmaCfg::NT), 0, stream, p);
+    return kOk;
 }
 
 int32_t check_rcr(int32_t m, int32_t n, int32_t k, int64_t lda, int64_t ldb, int64_t ldd) {
