@@ -80,6 +80,11 @@ _sig("baracuda_kernels_gemm_s8_rrr_gfx950_run", i32, *_RCR_RUN, f32, f32, vp, sz
 _sig("baracuda_kernels_gemm_s8_rrr_gfx950_workspace_size", sz, i32, i32, i32)
 _sig("baracuda_kernels_gemm_s8_rrr_gfx950_can_implement", i32, *_RCR_RUN)
 
+for _i in ("", "i64idx_"):
+    for _t in ("f32", "f64", "f16", "bf16"):
+        _sig(f"baracuda_kernels_embedding_{_i}{_t}_run", i32, i64, i32, i32, i64, vp, vp, vp, vp, sz, vp)
+        _sig(f"baracuda_kernels_embedding_{_i}{_t}_can_implement", i32, i64, i32, i32, i64, vp, vp, vp)
+
 SYMBOLS = tuple(_SIGS)
 
 _lib = None

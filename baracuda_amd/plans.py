@@ -48,6 +48,7 @@ class EpilogueKind(enum.Enum):
 
 
 class ElementKind(enum.Enum):
+    F64 = "f64"
     S8 = "s8"
     I32 = "i32"
     F32 = "f32"
@@ -64,6 +65,7 @@ class BackendKind(enum.Enum):
 class MathPrecision(enum.Enum):
     Int8 = "int8"
     Fp8E4M3 = "fp8_e4m3"
+    F64 = "f64"
     F32 = "f32"
     F16 = "f16"
     Bf16 = "bf16"
@@ -404,6 +406,87 @@ def gather_rows(dest: torch.Tensor, table: torch.Tensor, idx: torch.Tensor, stre
     _need(dest.numel() == n * H and dest.dtype == table.dtype, "dest must be [n, H] of table.dtype")
     fn = getattr(lib(), f"gather_rows_{_GATHER_TAG[table.dtype]}_run")
     check(fn(_ptr(dest), _ptr(table), _ptr(idx), V, H, n, _stream(stream)), "gather_rows")
+
+
+# ---- embedding forward -----------------------------------------------------
+PADDING_DISABLED = -(2 ** 31)   # embedding/mod.rs:57 (kPaddingDisabled)
+_EMBED_TAG = {torch.float32: "f32", torch.float64: "f64", torch.float16: "f16", torch.bfloat16: "bf16"}
+_EMBED_KIND = {torch.float32: ElementKind.F32, torch.float64: ElementKind.F64,
+               torch.float16: ElementKind.F16, torch.bfloat16: ElementKind.Bf16}
+
+
+@dataclass(frozen=True)
+class EmbeddingDescriptor:
+    num_embeddings: int
+    embedding_dim: int
+    num_indices: int
+    padding_idx: Optional[int] = None
+    element: ElementKind = ElementKind.F32
+
+
+@dataclass(frozen=True)
+class KernelSku:
+    op: str
+    element: ElementKind
+    aux_element: Optional[ElementKind]
+    arch: ArchSku
+    backend: BackendKind
+    precision_guarantee: PrecisionGuarantee
+
+
+class EmbeddingPlan:
+    """embedding.rs EmbeddingPlan (:90-360): out[n,:] = weight[idx[n],:], zero rows
+    for padding_idx and for negative / out-of-range indices; weight {f32, f64,
+    f16, bf16}, indices i32 or i64 (chosen by the index tensor at run time)."""
+
+    def __init__(self, desc: EmbeddingDescriptor, sku: KernelSku):
+        self.desc, self._sku = desc, sku
+
+    @classmethod
+    def select(cls, desc: EmbeddingDescriptor) -> "EmbeddingPlan":
+        if desc.num_embeddings < 0 or desc.embedding_dim < 0 or desc.num_indices < 0:
+            raise InvalidProblem("EmbeddingPlan: num_embeddings / embedding_dim / num_indices "
+                                 "must be non-negative")
+        if desc.element not in (ElementKind.F32, ElementKind.F64, ElementKind.F16, ElementKind.Bf16):
+            raise Unsupported("EmbeddingPlan: only f32, f64, f16, bf16")
+        mp = MathPrecision.F64 if desc.element == ElementKind.F64 else MathPrecision.F32
+        pg = PrecisionGuarantee(mp, desc.element, True, True)
+        return cls(desc, KernelSku("embedding", desc.element, ElementKind.I32, ArchSku.Gfx950,
+                                   BackendKind.Bespoke, pg))
+
+    def sku(self) -> KernelSku:
+        return self._sku
+
+    def precision_guarantee(self) -> PrecisionGuarantee:
+        return self._sku.precision_guarantee
+
+    def workspace_size(self) -> int:
+        return 0
+
+    def can_implement(self, weight, indices, output) -> None:
+        d = self.desc
+        _need(tuple(weight.shape) == (d.num_embeddings, d.embedding_dim),
+              "EmbeddingPlan: weight shape mismatch with descriptor")
+        _need(indices.dim() == 1 and indices.shape[0] == d.num_indices,
+              "EmbeddingPlan: indices.shape[0] mismatch with descriptor")
+        _need(tuple(output.shape) == (d.num_indices, d.embedding_dim),
+              "EmbeddingPlan: output shape must be [num_indices, embedding_dim]")
+        _need(weight.dtype in _EMBED_KIND and _EMBED_KIND[weight.dtype] == d.element and
+              output.dtype == weight.dtype, "EmbeddingPlan: element type mismatch")
+        _need(indices.dtype in (torch.int32, torch.int64), "EmbeddingPlan: indices must be i32 or i64")
+        _need(weight.is_contiguous() and indices.is_contiguous() and output.is_contiguous(),
+              "EmbeddingPlan: tensors must be contiguous")
+
+    def run(self, weight, indices, output, workspace=None, stream=None) -> None:
+        self.can_implement(weight, indices, output)
+        d = self.desc
+        if d.num_indices == 0 or d.embedding_dim == 0:
+            return
+        pad = PADDING_DISABLED if d.padding_idx is None else d.padding_idx
+        ix = "i64idx_" if indices.dtype == torch.int64 else ""
+        fn = getattr(lib(), f"embedding_{ix}{_EMBED_TAG[weight.dtype]}_run")
+        check(fn(d.num_indices, d.num_embeddings, d.embedding_dim, pad, _ptr(weight), _ptr(indices),
+                 _ptr(output), _ptr(workspace), 0, _stream(stream)), "EmbeddingPlan::run")
 
 
 # ---- grouped MoE int8 -------------------------------------------------------

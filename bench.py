@@ -85,7 +85,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",
-                    help="run only: w8a8|gemv|fp8|moe|int8epi|gather|copy (profiling; copy = 256 MiB "
+                    help="run only: w8a8|gemv|fp8|moe|int8epi|embedding|gather|copy (profiling; copy = 256 MiB "
                          "device copy used to calibrate the HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -208,6 +208,19 @@ def main():
                            "frac_int8_peak": round(it_ / PEAK_INT8_TOPS, 4)}
             extra["int8_s8out_4096_cubed"] = e
             del ia, ib, ibr, idd
+        if only in ("", "embedding"):
+            log("bench: embedding V=32000 D=4096 N=1")
+            e = {}
+            for dt, name in ((torch.float16, "f16"), (torch.float32, "f32")):
+                V, D = 32000, 4096
+                ew = torch.randn((V, D), device=dev).to(dt)
+                eidx = torch.randint(0, V, (1,), dtype=torch.int32, device=dev)
+                eo = torch.empty((1, D), dtype=dt, device=dev)
+                ep = P.EmbeddingPlan.select(P.EmbeddingDescriptor(V, D, 1, None, P._EMBED_KIND[dt]))
+                ems = time_launches(lambda: ep.run(ew, eidx, eo, stream=stream), 200, 20, stream)
+                e[name] = {"us": round(ems * 1e3, 2)}
+                del ew
+            extra["embedding_v32000_d4096_n1"] = e
         if only in ("", "gather"):
             log("bench: gather_rows bf16")
             V, H = 128256, 4096

@@ -142,6 +142,31 @@ BK_S8_RRR_BIAS_DECL(bias_gelu, i32)
 BK_S8_RRR_BIAS_DECL(bias_silu, i32)
 #undef BK_S8_RRR_BIAS_DECL
 
+/* ======================= embedding forward ===============================
+ * out[n,:] = weight[idx[n],:], zero row when idx[n] == padding_idx, < 0 or
+ * >= V; idx i32 (embedding_<T>) or i64 (embedding_i64idx_<T>), padding_idx
+ * as i64 (INT32_MIN = none).  Same ABI as baracuda_kernels_embedding_*
+ * (crates/baracuda-kernels-sys/kernels/include/baracuda_embedding.cuh:513-556,
+ *  kernels/embedding/embedding.cu:7-15). */
+#define BK_EMBED_DECL(NAME)                                                                     \
+    int32_t baracuda_kernels_##NAME##_run(int64_t num_indices, int32_t num_embeddings,          \
+                                          int32_t embedding_dim, int64_t padding_idx,           \
+                                          const void *weight, const void *indices, void *out,   \
+                                          void *workspace, size_t workspace_bytes, void *stream); \
+    int32_t baracuda_kernels_##NAME##_can_implement(int64_t num_indices, int32_t num_embeddings, \
+                                                    int32_t embedding_dim, int64_t padding_idx, \
+                                                    const void *weight, const void *indices,    \
+                                                    const void *out);
+BK_EMBED_DECL(embedding_f32)
+BK_EMBED_DECL(embedding_f64)
+BK_EMBED_DECL(embedding_f16)
+BK_EMBED_DECL(embedding_bf16)
+BK_EMBED_DECL(embedding_i64idx_f32)
+BK_EMBED_DECL(embedding_i64idx_f64)
+BK_EMBED_DECL(embedding_i64idx_f16)
+BK_EMBED_DECL(embedding_i64idx_bf16)
+#undef BK_EMBED_DECL
+
 /* ======================= per-token dynamic int8 quantization =============
  * Replaces baracuda_kernels_dynamic_range_quantize_per_token_sym_{f32,f64}_s8_{run,can_implement}
  * (crates/baracuda-kernels-sys/kernels/include/baracuda_quantize_compose.cuh:143-203,306-338,

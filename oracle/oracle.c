@@ -189,6 +189,18 @@ void bo_gemm_s8_rcr_s8(int64_t m, int64_t n, int64_t k,
         }
 }
 
+/* baracuda_embedding.cuh:61-88 (embedding_kernel), one row at a time. */
+void bo_embedding(void *out, const void *weight, const void *idx, int64_t idx_size, int64_t n,
+                  int64_t V, int64_t D, int64_t elem_size, int64_t padding_idx) {
+    const int64_t rb = D * elem_size;
+    for (int64_t r = 0; r < n; ++r) {
+        const int64_t v = idx_size == 8 ? ((const int64_t *)idx)[r] : (int64_t)((const int32_t *)idx)[r];
+        uint8_t *dst = (uint8_t *)out + r * rb;
+        if (v == padding_idx || v < 0 || v >= V) memset(dst, 0, (size_t)rb);
+        else memcpy(dst, (const uint8_t *)weight + v * rb, (size_t)rb);
+    }
+}
+
 /* int8_rrr_smoke.rs:35-48 (erf_approx), f32 arithmetic in the test's order. */
 float bo_erf_as7126(float x) {
     const float sign = x < 0.0f ? -1.0f : 1.0f;

@@ -116,6 +116,12 @@ void bo_gemv_s8w_m1_f64(int64_t n, int64_t k,
 void bo_gather_rows(void *dest, const void *table, const uint32_t *idx,
                     int64_t V, int64_t H, int64_t n, int64_t elem_size);
 
+/* embedding forward (baracuda_embedding.cuh:61-88): out[r,:] = weight[idx[r],:],
+ * zero when idx[r] == padding_idx, idx[r] < 0 or idx[r] >= V.  idx_size 4
+ * (i32) or 8 (i64); elem_size in bytes. */
+void bo_embedding(void *out, const void *weight, const void *idx, int64_t idx_size, int64_t n,
+                  int64_t V, int64_t D, int64_t elem_size, int64_t padding_idx);
+
 /* dynamic_range_quantize_per_token_sym (baracuda_quantize_compose.cuh:143-203):
  * x given as f32 (callers narrow f64 / widen bf16 first, like qc_load_as_f32). */
 void bo_quantize_per_token_sym(const float *x, int64_t n, int64_t d, int32_t qmin,

@@ -46,6 +46,7 @@ def _L():
             "bo_gemm_s8_epi": (None, [i64, i64, i64, vp, i64, vp, i64, i64, vp, i64, vp,
                                       C.c_int, vp, i64, f32, f32]),
             "bo_erf_as7126": (f32, [f32]),
+            "bo_embedding": (None, [vp, vp, vp, i64, i64, i64, i64, i64, i64]),
             "bo_gemm_w8a8_rcr_bf16": (None, [i64, i64, i64, vp, i64, vp, i64, vp, vp, vp, i64, i64, i64, i32]),
             "bo_gemm_fp8_e4m3_rcr_f64": (None, [i64, i64, i64, vp, i64, vp, i64, vp, i64, i64, i64, i32]),
             "bo_gemm_fp8_e4m3_rcr_f32": (None, [i64, i64, i64, vp, i64, vp, i64, vp, i64]),
@@ -174,6 +175,22 @@ def gemm_s8_epi(a, b, layout, alpha, beta=0.0, c=None, bias=None, act=None) -> n
     _L().bo_gemm_s8_epi(m, n, k, _p(a), k, _p(b), sbk, sbn, None if cp is None else _p(cp), n,
                         None if bp is None else _p(bp), ACTS[act], _p(d), n, alpha, beta)
     return d
+
+
+PADDING_DISABLED = -(2 ** 31)
+
+
+def embedding(weight, idx, padding_idx=None) -> np.ndarray:
+    """weight [V, D] (any 2/4/8-byte dtype), idx i32 or i64 [N] -> [N, D]."""
+    weight = np.ascontiguousarray(weight)
+    idx = np.ascontiguousarray(idx)
+    assert idx.dtype in (np.int32, np.int64)
+    V, D = weight.shape
+    out = np.empty((idx.shape[0], D), dtype=weight.dtype)
+    pad = PADDING_DISABLED if padding_idx is None else padding_idx
+    _L().bo_embedding(_p(out), _p(weight), _p(idx), idx.itemsize, idx.shape[0], V, D,
+                      weight.itemsize, pad)
+    return out
 
 
 def erf_as7126(x: float) -> float:

@@ -22,13 +22,17 @@ def _declared():
         for tag in re.findall(tag_macro + r"\((\w+)\)", text):
             for suf in sufs:
                 names.add(f"baracuda_kernels_{body.format(tag)}_{suf}")
+    for tag in re.findall(r"BK_EMBED_DECL\((\w+)\)", text):
+        for suf in ("run", "can_implement"):
+            names.add(f"baracuda_kernels_{tag}_{suf}")
     for epi, bias in re.findall(r"BK_S8_RCR_BIAS_DECL\((\w+), (\w+)\)", text):
         for suf in ("run", "workspace_size", "can_implement"):
             names.add(f"baracuda_kernels_gemm_{epi}_{bias}_s8_rcr_gfx950_{suf}")
     for epi, bias in re.findall(r"BK_S8_RRR_BIAS_DECL\((\w+), (\w+)\)", text):
         for suf in ("run", "can_implement"):
             names.add(f"baracuda_kernels_gemm_s8_rrr_gfx950_{epi}_{bias}_{suf}")
-    return {n for n in names if "_TAG_" not in n and "##" not in n and "_EPI_" not in n}
+    return {n for n in names if "_TAG_" not in n and "##" not in n and "_EPI_" not in n
+            and "_NAME_" not in n}
 
 
 def test_header_and_binding_agree():
@@ -117,6 +121,24 @@ def test_rrr_and_bias_can_implement():
             assert getattr(L, rcr + "workspace_size")(4, 8, 16) == 0
             assert getattr(L, rcr + "run")(4, 8, 16, None, 16, None, 16, None, 0, None, 8, None,
                                            1.0, 0.0, None, 0, None) == 2
+
+
+
+def test_embedding_can_implement_and_empty():
+    # baracuda_embedding.cuh:513-556: negative extents -> 2, N == 0 -> 0 before
+    # the pointer check, null pointers -> 2.
+    L = ffi.lib()
+    for i in ("", "i64idx_"):
+        for t in ("f32", "f64", "f16", "bf16"):
+            can = getattr(L, f"embedding_{i}{t}_can_implement")
+            run = getattr(L, f"embedding_{i}{t}_run")
+            assert can(4, 10, 8, -(2 ** 31), None, None, None) == 0
+            assert can(-1, 10, 8, 0, None, None, None) == 2
+            assert can(4, -1, 8, 0, None, None, None) == 2
+            assert can(4, 10, -8, 0, None, None, None) == 2
+            assert run(0, 10, 8, 0, None, None, None, None, 0, None) == 0
+            assert run(-1, 10, 8, 0, None, None, None, None, 0, None) == 2
+            assert run(3, 10, 8, 0, None, None, None, None, 0, None) == 2
 
 
 def test_quantize_can_implement():

@@ -295,3 +295,36 @@ def test_quantize_per_token_against_numpy(qmin, qmax):
     wq, ws = _np_quant(x, qmin, qmax)
     assert np.array_equal(q, wq) and np.array_equal(s, ws)
     assert s[3] == 1.0 and not q[3].any()
+
+
+# ---- embedding ---------------------------------------------------------------
+# embedding_smoke.rs cases: (V, D, weight(i), idx, padding_idx).
+EMBED_REF_CASES = [
+    (5, 4, lambda i: i * 0.25 + 1.0, [1, 3, 0], None, np.float32),
+    (5, 3, lambda i: i * -0.5 + 2.0, [4, 2, 0, 1], None, np.float64),
+    (5, 4, lambda i: i + 1.0, [0, 2, 4, -1], 0, np.float32),
+    (4, 3, lambda i: i * 0.5 - 1.0, [3, 0, 1], None, np.float16),
+]
+
+
+@pytest.mark.parametrize("case", range(len(EMBED_REF_CASES)))
+@pytest.mark.parametrize("idx_dtype", [np.int32, np.int64])
+def test_embedding_reference_cases(case, idx_dtype):
+    V, D, f, idx, pad, dt = EMBED_REF_CASES[case]
+    w = np.array([f(i) for i in range(V * D)], dtype=dt).reshape(V, D)
+    got = O.embedding(w, np.array(idx, dtype=idx_dtype), pad)
+    want = np.zeros((len(idx), D), dt)
+    for r, v in enumerate(idx):
+        if v != pad and 0 <= v < V:
+            want[r] = w[v]
+    assert got.tobytes() == want.tobytes()
+
+
+def test_embedding_padding_literal():
+    # embedding_f32_padding_idx_zeros_row written out: weight[i] = i + 1.
+    w = (np.arange(20, dtype=np.float32) + 1).reshape(5, 4)
+    got = O.embedding(w, np.array([0, 2, 4, -1], np.int32), 0)
+    assert got.tolist() == [[0] * 4, [9, 10, 11, 12], [17, 18, 19, 20], [0] * 4]
+    # the i32 sentinel never matches a valid row; a huge i64 index is out of range
+    big = np.array([2 ** 40, 3, -(2 ** 31)], np.int64)
+    assert O.embedding(w, big).tolist() == [[0] * 4, [13, 14, 15, 16], [0] * 4]
