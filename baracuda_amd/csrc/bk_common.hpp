@@ -98,6 +98,46 @@ __device__ __forceinline__ float e4m3_to_f32(uint8_t b) {
     return __uint_as_float(s | ((e - 7 + 127) << 23) | (m << 20));
 }
 
+// OCP E5M2 saturating encode with round-to-nearest-even (the satfinite cast
+// of baracuda_dtype.cuh:54-57): NaN stays NaN, |x| > 57344 (and inf) -> the
+// max finite 0x7b, 2 mantissa bits kept with RNE on the f32 bit pattern,
+// subnormals on the 2^-16 grid.
+__device__ __forceinline__ uint8_t f32_to_e5m2_satfinite(float x) {
+    uint32_t bits = __float_as_uint(x);
+    uint8_t sign = (uint8_t)((bits >> 24) & 0x80u);
+    uint32_t abs = bits & 0x7fffffffu;
+    if (abs > 0x7f800000u) return (uint8_t)(sign | 0x7f);
+    if (abs > 0x47600000u) return (uint8_t)(sign | 0x7b);   // > 57344 (incl. inf)
+    if (abs < 0x38800000u) {                                  // < 2^-14: subnormal grid
+        float q = __builtin_rintf(__uint_as_float(abs) * 65536.0f);
+        return (uint8_t)(sign | (uint8_t)q);                  // q == 4 -> min normal
+    }
+    uint32_t lsb = (abs >> 21) & 1u;
+    uint32_t r = abs + 0xfffffu + lsb;
+    uint32_t e = (r >> 23) - 127 + 15;
+    uint32_t m = (r >> 21) & 3u;
+    if (e > 30) return (uint8_t)(sign | 0x7b);
+    return (uint8_t)(sign | (uint8_t)(e << 2) | (uint8_t)m);
+}
+
+// E5M2 is the top byte of an IEEE binary16.
+__device__ __forceinline__ float e5m2_to_f32(uint8_t b) { return f16_to_f32((uint16_t)((uint16_t)b << 8)); }
+
+// fp8 format selector shared by the kernels and the MFMA cbsz / blgp fields.
+enum Fp8Fmt : int { FMT_E4M3 = 0, FMT_E5M2 = 1 };
+
+template <int FMT>
+__device__ __forceinline__ float fp8_to_f32(uint8_t b) {
+    if constexpr (FMT == FMT_E5M2) return e5m2_to_f32(b);
+    else return e4m3_to_f32(b);
+}
+
+template <int FMT>
+__device__ __forceinline__ uint8_t f32_to_fp8_satfinite(float x) {
+    if constexpr (FMT == FMT_E5M2) return f32_to_e5m2_satfinite(x);
+    else return f32_to_e4m3_satfinite(x);
+}
+
 __device__ __forceinline__ int8_t sat_cast_s8(float x) {
     float r = __builtin_rintf(x);   // round half to even
     r = r < -128.0f ? -128.0f : r;

@@ -1,0 +1,221 @@
+// gemm_fp8_kernels.hpp -- the FP8 GEMM kernels and launchers shared by the
+// FP8 SKU translation units (gemm_fp8.hip, gemm_fp8_bias.hip,
+// gemm_fp8_bias_e5m2.hip).
+//
+// Operands e4m3 (FMT_E4M3) or e5m2 (FMT_E5M2), both of one encoding; A
+// row-major [M,K]; B [N,K] (RCR) or row-major [K,N] (RRR); f32 accumulator.
+// Outputs:
+//   F8_OUT   D = sat_fp8(act(alpha*acc + beta*dec(C) [+ bias[n]]))   reference SKUs
+//   F8_BF16  D = bf16_rne(alpha * acc)                                 new SKU
+//   F8_F32   D = alpha * acc                                           new SKU
+// (baracuda_fp8_rcr_sm89.cuh:102-323, baracuda_fp8_rrr_sm89.cuh:60-272).
+//
+// Whole 256x256 tiles with K % 128 == 0 and 16-byte rows take the LDS-DMA
+// mainloop (v_mfma_f32_32x32x64_f8f6f4; RRR reads B with transposing LDS
+// reads); everything else the register-staged mainloop (16x16x128).
+#pragma once
+
+#include "gemm_mfma.hpp"
+#include "gemm_mfma2.hpp"
+#include "act.hpp"
+
+namespace bk {
+namespace {
+
+using namespace mfma;
+
+enum F8Epi : int { F8_OUT = 0, F8_BF16 = 1, F8_F32 = 2 };
+enum F8Layout : int { F8_RCR = 0, F8_RRR = 1 };
+
+struct F8Args {
+    int M, N, K;
+    const int8_t *a; int64_t lda;
+    const int8_t *b; int64_t ldb;
+    const uint8_t *c; int64_t ldc;
+    void *d; int64_t ldd;
+    float alpha, beta;
+    const float *bias;   // [N], for ACT != ACT_NONE
+};
+
+// Epilogue on one group of 4 consecutive output columns of row m.
+template <int FMT, int EPI, bool VecOut, int ACT>
+struct F8Epilogue {
+    const F8Args &p;
+    __device__ __forceinline__ void operator()(int m, int n0, const v4f &v) const {
+        if (m >= p.M || n0 >= p.N) return;
+        const int count = VecOut ? 4 : (p.N - n0 < 4 ? p.N - n0 : 4);
+        float y[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) y[r] = p.alpha * v[r];
+        if constexpr (EPI == F8_OUT) {
+            uint8_t *d = static_cast<uint8_t *>(p.d) + (int64_t)m * p.ldd + n0;
+            uint8_t o[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float z = y[r];
+                if (p.beta != 0.0f && p.c != nullptr && r < count)
+                    z += p.beta * fp8_to_f32<FMT>(p.c[(int64_t)m * p.ldc + n0 + r]);
+                if constexpr (ACT != ACT_NONE) {
+                    if (r < count) z += p.bias[n0 + r];
+                    z = activation<ACT>(z);
+                }
+                o[r] = f32_to_fp8_satfinite<FMT>(z);
+            }
+            if constexpr (VecOut) {
+                *reinterpret_cast<uint32_t *>(d) = (uint32_t)o[0] | ((uint32_t)o[1] << 8) |
+                                                   ((uint32_t)o[2] << 16) | ((uint32_t)o[3] << 24);
+            } else {
+                for (int r = 0; r < count; ++r) d[r] = o[r];
+            }
+        } else if constexpr (EPI == F8_BF16) {
+            store4_bf16(static_cast<uint16_t *>(p.d) + (int64_t)m * p.ldd + n0, y, VecOut, count);
+        } else {
+            store4_f32(static_cast<float *>(p.d) + (int64_t)m * p.ldd + n0, y, VecOut, count);
+        }
+    }
+};
+
+// General path: register-staged mainloop (K tail / unaligned / partial tiles).
+template <int FMT, int LAYOUT, int EPI, int ACT>
+__global__ __launch_bounds__(NT, 1) void gemm_fp8_kernel(F8Args p) {
+    constexpr Elem E = FMT == FMT_E5M2 ? Elem::E5M2 : Elem::E4M3;
+    __shared__ __attribute__((aligned(16))) int8_t lds[4 * LDS_TILE];
+    const int tiles_m = (p.M + BM - 1) / BM;
+    const int tiles_n = (p.N + BN - 1) / BN;
+    int tm, tn;
+    tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int m_base = tm * BM, n_base = tn * BN;
+    const int tid = threadIdx.x;
+    RowSet as, bs;
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+        const int r = i * LOAD_ROWS + (tid >> 3);
+        as.ptr[i] = p.a + (int64_t)min(m_base + r, p.M - 1) * p.lda;
+        bs.ptr[i] = p.b + (int64_t)min(n_base + r, p.N - 1) * p.ldb;
+    }
+    v4f acc[TM][TN];
+    if constexpr (LAYOUT == F8_RCR) mainloop<E, true>(lds, as, bs, p.K, acc);
+    else mainloop_rrr<E, true, true>(lds, as, p.b, p.ldb, p.N, n_base, p.K, acc);
+    const F8Epilogue<FMT, EPI, false, ACT> epi{p};
+    for_each_fragment(acc, [&](int ml, int nl, const v4f &v) { epi(m_base + ml, n_base + nl, v); });
+}
+
+typedef mfma2::Cfg<2, 4, 0> F8DmaCfg;
+
+template <int FMT, int LAYOUT>
+struct F8DmaPolicy { typedef mfma2::PolicyF8<F8DmaCfg, FMT> type; };
+template <int FMT>
+struct F8DmaPolicy<FMT, F8_RRR> { typedef mfma2::PolicyF8RowB<F8DmaCfg, FMT> type; };
+
+// Fast path: whole 256x256 tiles, K % 128 == 0, 16-byte rows, vector stores.
+template <int FMT, int LAYOUT, int EPI, int ACT>
+__global__ __launch_bounds__(F8DmaCfg::NT, 1) void gemm_fp8_dma_kernel(F8Args p) {
+    namespace M2 = mfma2;
+    typedef typename F8DmaPolicy<FMT, LAYOUT>::type P;
+    __shared__ __attribute__((aligned(1024))) int8_t stage0[2 * M2::OPER];
+    __shared__ __attribute__((aligned(1024))) int8_t stage1[2 * M2::OPER];
+    int tm, tn;
+    tile_coords(blockIdx.x, p.M / M2::BM, p.N / M2::BN, tm, tn);
+    const int m_base = tm * M2::BM, n_base = tn * M2::BN;
+    M2::AccTile<P> acc;
+    if constexpr (LAYOUT == F8_RCR) {
+        M2::DmaRows<false, false> d;
+        d.a = M2::make_dma_interior<F8DmaCfg>(p.a, (uint32_t)(p.M * p.lda), (int)p.lda, m_base * (int)p.lda);
+        d.b = M2::make_dma_interior<F8DmaCfg>(p.b, (uint32_t)(p.N * p.ldb), (int)p.ldb, n_base * (int)p.ldb);
+        M2::mainloop<P>(stage0, stage1, d, p.K, acc);
+    } else {
+        M2::DmaRowsRrr d;
+        d.a = M2::make_dma_interior<F8DmaCfg>(p.a, (uint32_t)(p.M * p.lda), (int)p.lda, m_base * (int)p.lda);
+        d.b = M2::make_dma_row_b<F8DmaCfg>(p.b, (uint32_t)(p.K * p.ldb), (int)p.ldb, n_base);
+        M2::mainloop<P>(stage0, stage1, d, p.K, acc);
+    }
+    const F8Epilogue<FMT, EPI, true, ACT> epi{p};
+    M2::for_each_quad<P>(acc, [&](int ml, int nl, const v4f &v) { epi(m_base + ml, n_base + nl, v); });
+}
+
+template <int FMT, int LAYOUT, int EPI, int ACT>
+int32_t launch_fp8(const F8Args &p, hipStream_t stream) {
+    const int out_elem = EPI == F8_F32 ? 4 : (EPI == F8_BF16 ? 2 : 1);
+    const int64_t b_rows = LAYOUT == F8_RCR ? p.N : p.K;
+    const bool fast = p.K % mfma2::BK == 0 && p.lda % 16 == 0 && p.ldb % 16 == 0 && aligned16(p.a) &&
+                      aligned16(p.b) && p.M % mfma2::BM == 0 && p.N % mfma2::BN == 0 &&
+                      (int64_t)p.M * p.lda < (1ll << 31) && b_rows * p.ldb < (1ll << 31) &&
+                      p.ldd % 4 == 0 && (reinterpret_cast<uintptr_t>(p.d) % (4 * out_elem)) == 0;
+    if (fast) {
+        const int tiles = (p.M / mfma2::BM) * (p.N / mfma2::BN);
+        hipLaunchKernelGGL((gemm_fp8_dma_kernel<FMT, LAYOUT, EPI, ACT>), dim3(tiles), dim3(F8DmaCfg::NT),
+                           0, stream, p);
+    } else {
+        const int tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
+        hipLaunchKernelGGL((gemm_fp8_kernel<FMT, LAYOUT, EPI, ACT>), dim3(tiles), dim3(NT), 0, stream, p);
+    }
+    return launch_status();
+}
+
+// Extent / leading-dimension checks of the reference launchers plus the
+// row-length bounds the kernels index with: B rows are K bytes (RCR) or N
+// bytes (RRR).
+template <int LAYOUT>
+int32_t check_fp8(int32_t m, int32_t n, int32_t k, int64_t lda, int64_t ldb, const void *c,
+                  int64_t ldc, int64_t ldd) {
+    if (m <= 0 || n <= 0 || k <= 0) return kInvalid;
+    if (lda < k || ldd < n) return kInvalid;
+    if (ldb < (LAYOUT == F8_RCR ? k : n)) return kInvalid;
+    if (c != nullptr && ldc < n) return kInvalid;
+    return kOk;
+}
+
+}  // namespace
+}  // namespace bk
+
+// Entry points of one fp8-out SKU: baracuda_kernels_gemm_fp8_<ENC>_<LAY>_gfx950[_<EPI>]_*.
+#define BK_FP8_IDENTITY_SKU(ENC, LAY, FMT, LAYOUT)                                                 \
+    int32_t baracuda_kernels_gemm_fp8_##ENC##_##LAY##_gfx950_can_implement(                        \
+        int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,    \
+        const void *c, int64_t ldc, const void *d, int64_t ldd) {                                   \
+        (void)a; (void)b; (void)d;                                                                  \
+        return bk::check_fp8<LAYOUT>(m, n, k, lda, ldb, c, ldc, ldd);                               \
+    }                                                                                               \
+    size_t baracuda_kernels_gemm_fp8_##ENC##_##LAY##_gfx950_workspace_size(int32_t m, int32_t n,   \
+                                                                          int32_t k) {             \
+        (void)m; (void)n; (void)k;                                                                  \
+        return 0;                                                                                   \
+    }                                                                                               \
+    int32_t baracuda_kernels_gemm_fp8_##ENC##_##LAY##_gfx950_run(                                  \
+        int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,    \
+        const void *c, int64_t ldc, void *d, int64_t ldd, float alpha, float beta,                  \
+        void *workspace, size_t workspace_bytes, void *stream) {                                    \
+        (void)workspace; (void)workspace_bytes;                                                     \
+        int32_t st = bk::check_fp8<LAYOUT>(m, n, k, lda, ldb, c, ldc, ldd);                         \
+        if (st != bk::kOk) return st;                                                               \
+        if (!a || !b || !d) return bk::kInvalid;                                                    \
+        bk::F8Args p{m, n, k, (const int8_t *)a, lda, (const int8_t *)b, ldb, (const uint8_t *)c,   \
+                     ldc, d, ldd, alpha, beta, nullptr};                                            \
+        return bk::launch_fp8<FMT, LAYOUT, bk::F8_OUT, bk::ACT_NONE>(p, (hipStream_t)stream);       \
+    }
+
+#define BK_FP8_BIAS_SKU(ENC, LAY, EPISFX, FMT, LAYOUT, ACTV)                                       \
+    int32_t baracuda_kernels_gemm_fp8_##ENC##_##LAY##_gfx950_##EPISFX##_can_implement(              \
+        int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,    \
+        const void *c, int64_t ldc, const void *d, int64_t ldd) {                                   \
+        (void)a; (void)b; (void)d;                                                                  \
+        return bk::check_fp8<LAYOUT>(m, n, k, lda, ldb, c, ldc, ldd);                               \
+    }                                                                                               \
+    int32_t baracuda_kernels_gemm_fp8_##ENC##_##LAY##_gfx950_##EPISFX##_run(                        \
+        int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,    \
+        const void *c, int64_t ldc, void *d, int64_t ldd, const void *bias, float alpha,            \
+        float beta, void *workspace, size_t workspace_bytes, void *stream) {                        \
+        (void)workspace; (void)workspace_bytes;                                                     \
+        int32_t st = bk::check_fp8<LAYOUT>(m, n, k, lda, ldb, c, ldc, ldd);                         \
+        if (st != bk::kOk) return st;                                                               \
+        if (!a || !b || !d || !bias) return bk::kInvalid;                                           \
+        bk::F8Args p{m, n, k, (const int8_t *)a, lda, (const int8_t *)b, ldb, (const uint8_t *)c,   \
+                     ldc, d, ldd, alpha, beta, (const float *)bias};                                \
+        return bk::launch_fp8<FMT, LAYOUT, bk::F8_OUT, ACTV>(p, (hipStream_t)stream);               \
+    }
+
+#define BK_FP8_BIAS_FAMILY(ENC, LAY, FMT, LAYOUT)                                                  \
+    BK_FP8_BIAS_SKU(ENC, LAY, bias, FMT, LAYOUT, bk::ACT_BIAS)                                     \
+    BK_FP8_BIAS_SKU(ENC, LAY, bias_relu, FMT, LAYOUT, bk::ACT_BIAS_RELU)                           \
+    BK_FP8_BIAS_SKU(ENC, LAY, bias_gelu, FMT, LAYOUT, bk::ACT_BIAS_GELU)                           \
+    BK_FP8_BIAS_SKU(ENC, LAY, bias_silu, FMT, LAYOUT, bk::ACT_BIAS_SILU)

@@ -53,11 +53,10 @@ __device__ __forceinline__ int lds_off(int row, int unit) {
     return row * BK + ((unit ^ swz(row)) << 4);
 }
 
-enum class Elem { S8, E4M3 };
+enum class Elem { S8, E4M3, E5M2 };
 
-template <Elem E> struct AccT;
+template <Elem E> struct AccT { typedef v4f type; };   // FP8: f32 accumulators
 template <> struct AccT<Elem::S8> { typedef v4i type; };
-template <> struct AccT<Elem::E4M3> { typedef v4f type; };
 
 // Per-thread view of the rows this thread stages into LDS.  Each of the 4
 // loads of a stage covers row (i * 64 + tid / 8), 16-byte unit tid % 8.
@@ -137,8 +136,9 @@ __device__ __forceinline__ void compute_stage(const int8_t *la, const int8_t *lb
             }
         }
     } else {
-        // v_mfma_f32_16x16x128_f8f6f4 (e4m3 x e4m3): 32 bytes of K per lane,
-        // one instruction covers the whole 128-byte stage.
+        // v_mfma_f32_16x16x128_f8f6f4 (cbsz = blgp = 0: e4m3 x e4m3, 1: e5m2 x
+        // e5m2): 32 bytes of K per lane, one instruction covers the stage.
+        constexpr int F = E == Elem::E5M2 ? 1 : 0;
         const int u0 = grp * 2;
         v8i bf[TN];
 #pragma unroll
@@ -157,7 +157,7 @@ __device__ __forceinline__ void compute_stage(const int8_t *la, const int8_t *lb
 #pragma unroll
             for (int j = 0; j < TN; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                    bf[j], af, acc[i][j], 0, 0, 0, 0, 0, 0);
+                    bf[j], af, acc[i][j], F, F, 0, 0, 0, 0);
         }
     }
 }
@@ -285,10 +285,10 @@ __device__ __forceinline__ void store_b_rrr(int8_t *lb, const v4i (&rb)[LOADS], 
 
 // K loop for one 256x256 RRR tile (A as in mainloop, B through load_b_rrr).
 // CheckedB: N tail / unaligned B rows / K tail on B.
-template <bool CheckedA, bool CheckedB>
+template <Elem E, bool CheckedA, bool CheckedB>
 __device__ __forceinline__ void mainloop_rrr(int8_t *lds, const RowSet &as, const int8_t *b,
                                              int64_t ldb, int N, int n0, int K,
-                                             v4i (&acc)[TM][TN]) {
+                                             typename AccT<E>::type (&acc)[TM][TN]) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -298,7 +298,7 @@ __device__ __forceinline__ void mainloop_rrr(int8_t *lds, const RowSet &as, cons
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+        for (int j = 0; j < TN; ++j) acc[i][j] = typename AccT<E>::type{0, 0, 0, 0};
     const int KT = (K + BK - 1) / BK;
     v4i ra[LOADS], rb[LOADS];
 #pragma unroll
@@ -321,7 +321,7 @@ __device__ __forceinline__ void mainloop_rrr(int8_t *lds, const RowSet &as, cons
             for (int i = 0; i < LOADS; ++i) ra[i] = load_chunk<CheckedA>(as.ptr[i], (kt + 1) * BK + unit * 16, K);
             load_b_rrr<CheckedB>(rb, b, ldb, N, K, n0, (kt + 1) * BK, tid);
         }
-        compute_stage<Elem::S8>(cur, cur + LDS_TILE, acc, wave_m, wave_n, lane);
+        compute_stage<E>(cur, cur + LDS_TILE, acc, wave_m, wave_n, lane);
         if (more) {
             const int row0 = tid >> 3;
 #pragma unroll

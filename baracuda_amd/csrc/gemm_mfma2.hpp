@@ -133,8 +133,9 @@ struct PolicyI8x32 {
     }
 };
 
-// fp8 e4m3: v_mfma_f32_32x32x64_f8f6f4.  Wave tile = 4 x 4 tiles of 32x32.
-template <class C>
+// fp8: v_mfma_f32_32x32x64_f8f6f4, FMT 0 = e4m3, 1 = e5m2 (the cbsz / blgp
+// operand-format fields).  Wave tile = TI x TJ tiles of 32x32.
+template <class C, int FMT = 0>
 struct PolicyF8 {
     typedef C Cfg;
     static constexpr int TI = C::WM / 32;
@@ -153,7 +154,7 @@ struct PolicyF8 {
     }
     static constexpr int H = 1;
     __device__ static void mma(Acc &c, const Frag &b, const Frag &a, int) {
-        c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(b, a, c, 0, 0, 0, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(b, a, c, FMT, FMT, 0, 0, 0, 0);
     }
     __device__ static Acc zero() { return Acc{0}; }
     // 32x32 result: lane holds column m = lane % 32 and, for g = 0..3, rows
@@ -175,10 +176,12 @@ struct PolicyF8 {
 // 8 x 16 byte block and return column i of it to lane i: lane i of group g
 // gets 8 consecutive k of output column n0 + i, so two reads rebuild exactly
 // the 16-byte, k-ascending operand that PolicyI8::load gives for A.
-// swz_t maps the 16 k-rows one 32-lane half-wave touches per read
-// ({0..7, 16..23} or {8..15, 24..31} plus multiples of 32) to distinct units.
+// swz_t(k) = 2*(k%8) + bit 4 of k gives distinct units to every set of
+// (k-row, unit) pairs one 32-lane half-wave touches per read: the int8
+// fragment's rows {8q..8q+7} and {8q+16..8q+23} at one unit, and the fp8
+// fragment's rows {8q..8q+7} at units c and c^1.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ int swz_t(int k) { return (k & 7) | (((k >> 4) & 1) << 3); }
+__device__ __forceinline__ int swz_t(int k) { return ((k & 7) << 1) | ((k >> 4) & 1); }
 __device__ __forceinline__ int lds_off_t(int k, int unit) { return k * BN + ((unit ^ swz_t(k)) << 4); }
 
 typedef int v2i_t __attribute__((ext_vector_type(2)));
@@ -200,6 +203,28 @@ struct PolicyI8RowB : PolicyI8<C> {
         const v2i_t lo = ds_read_tr8(q);
         const v2i_t hi = ds_read_tr8(q + 8 * BN);
         return v4i{lo[0], lo[1], hi[0], hi[1]};
+    }
+};
+
+// fp8 row-major B for the 32x32x64 policy: lane l needs the 32 k-bytes
+// 64s + 32*(l/32) .. +31 of column n0 + l%32.  16-lane group g covers columns
+// 16*(g%2) .. +15 and the k half g/2; four transposing reads of 8 k-rows each.
+// Rows 8q + j for q = 0, 1 share swz_t, as do q = 2, 3 (unit xor 1).
+template <class C, int FMT>
+struct PolicyF8RowB : PolicyF8<C, FMT> {
+    typedef v8i Frag;
+    __device__ static Frag load_b(const int8_t *op, int row0, int t, int s, int lane) {
+        const int g = lane >> 4;
+        const int kb = 32 * (g >> 1) + ((lane & 15) >> 1);
+        const int unit = ((row0 + t * 32) >> 4) + (g & 1);
+        const int half = (lane & 1) << 3;
+        const int8_t *q0 = op + kb * BN + ((unit ^ swz_t(kb)) << 4) + half + s * 64 * BN;
+        const int8_t *q2 = op + (kb + 16) * BN + ((unit ^ swz_t(kb + 16)) << 4) + half + s * 64 * BN;
+        const v2i_t r0 = ds_read_tr8(q0);
+        const v2i_t r1 = ds_read_tr8(q0 + 8 * BN);
+        const v2i_t r2 = ds_read_tr8(q2);
+        const v2i_t r3 = ds_read_tr8(q2 + 8 * BN);
+        return Frag{r0[0], r0[1], r1[0], r1[1], r2[0], r2[1], r3[0], r3[1]};
     }
 };
 

@@ -80,6 +80,17 @@ _sig("baracuda_kernels_gemm_s8_rrr_gfx950_run", i32, *_RCR_RUN, f32, f32, vp, sz
 _sig("baracuda_kernels_gemm_s8_rrr_gfx950_workspace_size", sz, i32, i32, i32)
 _sig("baracuda_kernels_gemm_s8_rrr_gfx950_can_implement", i32, *_RCR_RUN)
 
+for _enc in ("e4m3", "e5m2"):
+    for _lay in ("rcr", "rrr"):
+        _pre = f"baracuda_kernels_gemm_fp8_{_enc}_{_lay}_gfx950"
+        if (_enc, _lay) != ("e4m3", "rcr"):
+            _sig(f"{_pre}_run", i32, *_RCR_RUN, f32, f32, vp, sz, vp)
+            _sig(f"{_pre}_workspace_size", sz, i32, i32, i32)
+            _sig(f"{_pre}_can_implement", i32, *_RCR_RUN)
+        for _e in ("bias", "bias_relu", "bias_gelu", "bias_silu"):
+            _sig(f"{_pre}_{_e}_run", i32, *_RCR_RUN, vp, f32, f32, vp, sz, vp)
+            _sig(f"{_pre}_{_e}_can_implement", i32, *_RCR_RUN)
+
 for _i in ("", "i64idx_"):
     for _t in ("f32", "f64", "f16", "bf16"):
         _sig(f"baracuda_kernels_embedding_{_i}{_t}_run", i32, i64, i32, i32, i64, vp, vp, vp, vp, sz, vp)

@@ -55,6 +55,7 @@ class ElementKind(enum.Enum):
     F16 = "f16"
     Bf16 = "bf16"
     Fp8E4M3 = "fp8_e4m3"
+    Fp8E5M2 = "fp8_e5m2"
     U32 = "u32"
 
 
@@ -65,6 +66,7 @@ class BackendKind(enum.Enum):
 class MathPrecision(enum.Enum):
     Int8 = "int8"
     Fp8E4M3 = "fp8_e4m3"
+    Fp8E5M2 = "fp8_e5m2"
     F64 = "f64"
     F32 = "f32"
     F16 = "f16"
@@ -94,7 +96,8 @@ class GemmSku:
         # atomics) and therefore also bit-stable on the same hardware.
         if self.element == ElementKind.S8:
             return PrecisionGuarantee(MathPrecision.Int8, ElementKind.I32, True, True)
-        return PrecisionGuarantee(MathPrecision.Fp8E4M3, ElementKind.F32, True, True)
+        mp = MathPrecision.Fp8E5M2 if self.element == ElementKind.Fp8E5M2 else MathPrecision.Fp8E4M3
+        return PrecisionGuarantee(mp, ElementKind.F32, True, True)
 
 
 # ---- errors (status codes, crates/baracuda-kernels-sys/src/lib.rs:19-27) ----
@@ -260,6 +263,9 @@ class IntGemmPlan:
 
 
 # ---- FP8 GEMM --------------------------------------------------------------
+_FP8_ENC = {ElementKind.Fp8E4M3: "e4m3", ElementKind.Fp8E5M2: "e5m2"}
+
+
 @dataclass(frozen=True)
 class Fp8GemmDescriptor:
     m: int
@@ -267,11 +273,15 @@ class Fp8GemmDescriptor:
     k: int
     layout: LayoutSku = LayoutSku.Rcr
     epilogue: EpilogueKind = EpilogueKind.Identity
-    output: ElementKind = ElementKind.Fp8E4M3   # Fp8E4M3 (reference), Bf16, F32
+    output: ElementKind = ElementKind.Fp8E4M3   # the operand encoding (reference), or Bf16 / F32
+    element: ElementKind = ElementKind.Fp8E4M3  # operand encoding: Fp8E4M3 or Fp8E5M2
 
 
 class Fp8GemmPlan:
-    """fp8_gemm.rs Fp8GemmPlan for E4M3 RCR on gfx950."""
+    """fp8_gemm.rs Fp8GemmPlan (:104-750): {E4M3, E5M2} x {RCR, RRR} x {Identity,
+    Bias, BiasRelu, BiasGelu, BiasSilu}, fp8 out in the operand encoding:
+    D = sat_fp8(act(alpha*acc + beta*dequant(C) [+ bias[n]])), bias f32 [N].
+    E4M3 RCR Identity also offers Bf16 (scale_a*scale_b*acc) and F32 outputs."""
 
     def __init__(self, desc: Fp8GemmDescriptor, sku: GemmSku):
         self.desc, self._sku = desc, sku
@@ -280,13 +290,16 @@ class Fp8GemmPlan:
     def select(cls, desc: Fp8GemmDescriptor) -> "Fp8GemmPlan":
         if desc.m <= 0 or desc.n <= 0 or desc.k <= 0:
             raise InvalidProblem("FP8 GEMM problem must have positive M, N, K")
-        if desc.layout != LayoutSku.Rcr:
-            raise Unsupported("gfx950 FP8 GEMM implements the RCR layout")
-        if desc.epilogue != EpilogueKind.Identity:
-            raise Unsupported("gfx950 FP8 GEMM implements the Identity epilogue")
-        if desc.output not in (ElementKind.Fp8E4M3, ElementKind.Bf16, ElementKind.F32):
-            raise Unsupported(f"FP8 GEMM output {desc.output}")
-        return cls(desc, GemmSku(ArchSku.Gfx950, desc.layout, desc.epilogue, ElementKind.Fp8E4M3, desc.output))
+        if desc.element not in _FP8_ENC:
+            raise Unsupported(f"FP8 GEMM operand element {desc.element}")
+        if desc.output in (ElementKind.Bf16, ElementKind.F32):
+            if (desc.element, desc.layout, desc.epilogue) != (ElementKind.Fp8E4M3, LayoutSku.Rcr,
+                                                               EpilogueKind.Identity):
+                raise Unsupported("Bf16 / F32 outputs are E4M3 RCR with the Identity epilogue")
+        elif desc.output != desc.element:
+            raise Unsupported("fp8 output must use the operand encoding")
+        bias = ElementKind.F32 if desc.epilogue != EpilogueKind.Identity else None
+        return cls(desc, GemmSku(ArchSku.Gfx950, desc.layout, desc.epilogue, desc.element, desc.output, bias))
 
     def sku(self) -> GemmSku:
         return self._sku
@@ -297,18 +310,33 @@ class Fp8GemmPlan:
     def workspace_size(self) -> int:
         return 0
 
-    def run(self, a, b, d, c=None, alpha=1.0, beta=0.0, scale_a=1.0, scale_b=1.0,
+    def _prefix(self) -> str:
+        d = self.desc
+        return f"gemm_fp8_{_FP8_ENC[d.element]}_{d.layout.value}_gfx950"
+
+    def run(self, a, b, d, c=None, alpha=1.0, beta=0.0, scale_a=1.0, scale_b=1.0, bias=None,
             workspace=None, stream=None) -> None:
         desc, L, s = self.desc, lib(), _stream(stream)
-        _need(tuple(a.shape) == (desc.m, desc.k) and tuple(b.shape) == (desc.n, desc.k)
+        bshape = (desc.n, desc.k) if desc.layout == LayoutSku.Rcr else (desc.k, desc.n)
+        _need(tuple(a.shape) == (desc.m, desc.k) and tuple(b.shape) == bshape
               and tuple(d.shape) == (desc.m, desc.n), "shape mismatch with descriptor")
         _need(a.element_size() == 1 and b.element_size() == 1, "FP8 operands are 1-byte")
-        if desc.output == ElementKind.Fp8E4M3:
+        if desc.output == desc.element:
+            _need(d.element_size() == 1, "D must be 1-byte fp8")
             if c is None:
                 beta = 0.0
-            st = L.gemm_fp8_e4m3_rcr_gfx950_run(desc.m, desc.n, desc.k, _ptr(a), _ld(a), _ptr(b), _ld(b),
-                                                _ptr(c), _ld(c) if c is not None else 0, _ptr(d), _ld(d),
-                                                alpha, beta, _ptr(workspace), 0, s)
+            else:
+                _need(tuple(c.shape) == (desc.m, desc.n) and c.element_size() == 1, "C shape mismatch")
+            args = [desc.m, desc.n, desc.k, _ptr(a), _ld(a), _ptr(b), _ld(b),
+                    _ptr(c), _ld(c) if c is not None else 0, _ptr(d), _ld(d)]
+            if desc.epilogue == EpilogueKind.Identity:
+                fn = getattr(L, f"{self._prefix()}_run")
+            else:
+                _need(bias is not None and bias.dtype == torch.float32 and bias.numel() >= desc.n
+                      and bias.is_contiguous(), "Bias* epilogue needs a contiguous f32 [N] bias")
+                fn = getattr(L, f"{self._prefix()}_{desc.epilogue.value}_run")
+                args.append(_ptr(bias))
+            st = fn(*args, alpha, beta, _ptr(workspace), 0, s)
         elif desc.output == ElementKind.Bf16:
             _need(d.dtype == torch.bfloat16, "D must be bf16")
             st = L.gemm_fp8_e4m3_rcr_gfx950_bf16_run(desc.m, desc.n, desc.k, _ptr(a), _ld(a), _ptr(b), _ld(b),

@@ -142,6 +142,50 @@ BK_S8_RRR_BIAS_DECL(bias_gelu, i32)
 BK_S8_RRR_BIAS_DECL(bias_silu, i32)
 #undef BK_S8_RRR_BIAS_DECL
 
+/* FP8 fp8-out SKUs in both encodings and layouts (B [N,K] for rcr, row-major
+ * [K,N] for rrr), D = sat_fp8(alpha*acc + beta*dequant(C)).  Same ABI as
+ * baracuda_kernels_gemm_fp8_{e4m3,e5m2}_{rcr,rrr}_sm89_{run,workspace_size,can_implement}
+ * (crates/baracuda-kernels-sys/kernels/gemm/gemm_fp8_{e4m3,e5m2}_{rcr,rrr}_sm89.cu). */
+#define BK_FP8_DECL(ENC, LAY)                                                                   \
+    int32_t baracuda_kernels_gemm_fp8_##ENC##_##LAY##_gfx950_run(                               \
+        int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb, \
+        const void *c, int64_t ldc, void *d, int64_t ldd, float alpha, float beta,               \
+        void *workspace, size_t workspace_bytes, void *stream);                                  \
+    size_t baracuda_kernels_gemm_fp8_##ENC##_##LAY##_gfx950_workspace_size(int32_t m, int32_t n, \
+                                                                          int32_t k);           \
+    int32_t baracuda_kernels_gemm_fp8_##ENC##_##LAY##_gfx950_can_implement(                     \
+        int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb, \
+        const void *c, int64_t ldc, const void *d, int64_t ldd);
+BK_FP8_DECL(e4m3, rrr)
+BK_FP8_DECL(e5m2, rcr)
+BK_FP8_DECL(e5m2, rrr)
+#undef BK_FP8_DECL
+
+/* FP8 bias / activation family: D = sat_fp8(act(alpha*acc + beta*dequant(C) +
+ * bias[n])), bias f32 [N].  Same ABI as
+ * baracuda_kernels_gemm_fp8_{e4m3,e5m2}_{rcr,rrr}_sm89_{bias,bias_relu,bias_gelu,bias_silu}_*
+ * (crates/baracuda-kernels-sys/kernels/gemm/gemm_fp8_*_sm89_bias.cu,
+ *  crates/baracuda-kernels-sys/src/lib.rs:964-1460). */
+#define BK_FP8_BIAS_DECL(ENC, LAY, EPI)                                                         \
+    int32_t baracuda_kernels_gemm_fp8_##ENC##_##LAY##_gfx950_##EPI##_run(                       \
+        int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb, \
+        const void *c, int64_t ldc, void *d, int64_t ldd, const void *bias, float alpha,         \
+        float beta, void *workspace, size_t workspace_bytes, void *stream);                      \
+    int32_t baracuda_kernels_gemm_fp8_##ENC##_##LAY##_gfx950_##EPI##_can_implement(             \
+        int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb, \
+        const void *c, int64_t ldc, const void *d, int64_t ldd);
+#define BK_FP8_BIAS_DECL4(ENC, LAY)                                                             \
+    BK_FP8_BIAS_DECL(ENC, LAY, bias)                                                            \
+    BK_FP8_BIAS_DECL(ENC, LAY, bias_relu)                                                       \
+    BK_FP8_BIAS_DECL(ENC, LAY, bias_gelu)                                                       \
+    BK_FP8_BIAS_DECL(ENC, LAY, bias_silu)
+BK_FP8_BIAS_DECL4(e4m3, rcr)
+BK_FP8_BIAS_DECL4(e4m3, rrr)
+BK_FP8_BIAS_DECL4(e5m2, rcr)
+BK_FP8_BIAS_DECL4(e5m2, rrr)
+#undef BK_FP8_BIAS_DECL4
+#undef BK_FP8_BIAS_DECL
+
 /* ======================= embedding forward ===============================
  * out[n,:] = weight[idx[n],:], zero row when idx[n] == padding_idx, < 0 or
  * >= V; idx i32 (embedding_<T>) or i64 (embedding_i64idx_<T>), padding_idx

@@ -97,6 +97,38 @@ uint8_t bo_f32_to_e4m3_satfinite(float x) {
     return (uint8_t)(sign | (uint8_t)(ef << 3) | (uint8_t)q);
 }
 
+/* OCP 8-bit floating point spec, E5M2: bias 15, IEEE-style inf (S.11111.00)
+ * and NaN (S.11111.xx, xx != 0), max finite 57344, subnormals m/4 * 2^-14. */
+float bo_e5m2_to_f32(uint8_t b) {
+    int s = b >> 7, e = (b >> 2) & 0x1f, m = b & 3;
+    double v;
+    if (e == 31) v = m ? NAN : INFINITY;
+    else if (e == 0) v = ldexp((double)m, -16);
+    else v = ldexp(1.0 + m / 4.0, e - 15);
+    return (float)(s ? -v : v);
+}
+
+/* Saturating RNE encode to E5M2 (baracuda_dtype.cuh:48-57: SATFINITE, so
+ * inf and |x| beyond 57344 clamp to max-finite; NaN -> NaN). */
+uint8_t bo_f32_to_e5m2_satfinite(float x) {
+    uint8_t sign = (f32_bits(x) >> 24) & 0x80u;
+    if (isnan(x)) return (uint8_t)(sign | 0x7f);
+    double a = fabs((double)x);
+    if (a < ldexp(1.0, -14)) {                 /* subnormal: units of 2^-16 */
+        double q = nearbyint(a * 65536.0);     /* q in 0..4, 4 == min normal */
+        return (uint8_t)(sign | (uint8_t)q);
+    }
+    if (isinf(x)) return (uint8_t)(sign | 0x7b);
+    int e;
+    double m = frexp(a, &e);
+    e -= 1; m *= 2.0;
+    double q = nearbyint((m - 1.0) * 4.0);
+    if (q >= 4.0) { q = 0.0; e += 1; }
+    int ef = e + 15;
+    if (ef > 30) return (uint8_t)(sign | 0x7b);
+    return (uint8_t)(sign | (uint8_t)(ef << 2) | (uint8_t)q);
+}
+
 /* oracle.rs:922-935 encode_float(.., I32): Rust `f as i32` truncates toward
  * zero, saturates at the i32 range and maps NaN to 0. */
 int32_t bo_f64_to_i32_as(double f) {
@@ -281,6 +313,43 @@ void bo_gemm_fp8_e4m3_rcr_f64(int64_t m, int64_t n, int64_t k,
             for (int64_t kk = 0; kk < k; ++kk)
                 s += (double)lut[a[i * lda + kk]] * (double)lut[b[j * ldb + kk]];
             acc[i * ldacc + j] = s;
+        }
+}
+
+/* FP8 GEMM exact accumulator, either encoding (fmt 0 e4m3, 1 e5m2) and
+ * either B layout (b[k,j] at b[k*sbk + j*sbn]); the products and the sum are
+ * exact in f64 for every K used here. */
+void bo_gemm_fp8_f64(int fmt, int64_t m, int64_t n, int64_t k,
+                     const uint8_t *a, int64_t lda, const uint8_t *b, int64_t sbk, int64_t sbn,
+                     double *acc, int64_t ldacc, int64_t row0, int64_t row1, int nthreads) {
+    (void)m;
+    float lut[256];
+    for (int i = 0; i < 256; ++i) lut[i] = fmt ? bo_e5m2_to_f32((uint8_t)i) : bo_e4m3_to_f32((uint8_t)i);
+    int nt = pick_threads(nthreads);
+#pragma omp parallel for schedule(static) num_threads(nt) if (nt > 1)
+    for (int64_t i = row0; i < row1; ++i)
+        for (int64_t j = 0; j < n; ++j) {
+            double s = 0.0;
+            for (int64_t kk = 0; kk < k; ++kk)
+                s += (double)lut[a[i * lda + kk]] * (double)lut[b[kk * sbk + j * sbn]];
+            acc[(i - row0) * ldacc + j] = s;
+        }
+}
+
+/* FP8-out epilogue of gemm_fp8_{rcr,rrr}_sm89 (baracuda_fp8_rrr_sm89.cuh:190-235,
+ * fp8_bias_smoke.rs:125-160):
+ *   z = alpha*(f32)acc [+ beta*dec(C)] [+ bias[j]] ; D = sat_fp8(act(z))
+ * acc is the exact sum rounded once to f32. */
+void bo_fp8_epilogue(int fmt, int64_t m, int64_t n, const double *acc, int64_t ldacc,
+                     const uint8_t *c, int64_t ldc, const float *bias, int act,
+                     float alpha, float beta, uint8_t *d, int64_t ldd) {
+    for (int64_t i = 0; i < m; ++i)
+        for (int64_t j = 0; j < n; ++j) {
+            float z = alpha * (float)acc[i * ldacc + j];
+            if (c != NULL) z += beta * (fmt ? bo_e5m2_to_f32(c[i * ldc + j]) : bo_e4m3_to_f32(c[i * ldc + j]));
+            if (bias != NULL) z += bias[j];
+            z = act_apply(act, z);
+            d[i * ldd + j] = fmt ? bo_f32_to_e5m2_satfinite(z) : bo_f32_to_e4m3_satfinite(z);
         }
 }
 

@@ -29,6 +29,8 @@ uint16_t bo_f32_to_f16_bits(float x);
 float    bo_f16_bits_to_f32(uint16_t h);
 float    bo_e4m3_to_f32(uint8_t b);
 uint8_t  bo_f32_to_e4m3_satfinite(float x);
+float    bo_e5m2_to_f32(uint8_t b);
+uint8_t  bo_f32_to_e5m2_satfinite(float x);
 int32_t  bo_f64_to_i32_as(double f);     /* Rust `f as i32` (saturating, NaN->0) */
 int8_t   bo_sat_cast_s8(float x);        /* RNE + clamp to [-128,127]            */
 
@@ -91,6 +93,16 @@ void bo_gemm_fp8_e4m3_rcr_f64(int64_t m, int64_t n, int64_t k,
                               const uint8_t *b, int64_t ldb,
                               double *acc, int64_t ldacc,
                               int64_t row0, int64_t row1, int nthreads);
+/* Either encoding (fmt 0 e4m3, 1 e5m2) and layout (b[k,j] at b[k*sbk+j*sbn]);
+ * rows [row0,row1) written from acc row 0. */
+void bo_gemm_fp8_f64(int fmt, int64_t m, int64_t n, int64_t k,
+                     const uint8_t *a, int64_t lda, const uint8_t *b, int64_t sbk, int64_t sbn,
+                     double *acc, int64_t ldacc, int64_t row0, int64_t row1, int nthreads);
+/* FP8-out epilogue: D = sat_fp8(act(alpha*(f32)acc + beta*dec(C) + bias)),
+ * c / bias may be NULL; act as in bo_gemm_s8_epi. */
+void bo_fp8_epilogue(int fmt, int64_t m, int64_t n, const double *acc, int64_t ldacc,
+                     const uint8_t *c, int64_t ldc, const float *bias, int act,
+                     float alpha, float beta, uint8_t *d, int64_t ldd);
 /* The reference smoke test's own f32 K-ascending accumulation. */
 void bo_gemm_fp8_e4m3_rcr_f32(int64_t m, int64_t n, int64_t k,
                               const uint8_t *a, int64_t lda,

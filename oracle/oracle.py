@@ -46,6 +46,10 @@ def _L():
             "bo_gemm_s8_epi": (None, [i64, i64, i64, vp, i64, vp, i64, i64, vp, i64, vp,
                                       C.c_int, vp, i64, f32, f32]),
             "bo_erf_as7126": (f32, [f32]),
+            "bo_e5m2_to_f32": (f32, [C.c_uint8]),
+            "bo_f32_to_e5m2_satfinite": (C.c_uint8, [f32]),
+            "bo_gemm_fp8_f64": (None, [C.c_int, i64, i64, i64, vp, i64, vp, i64, i64, vp, i64, i64, i64, i32]),
+            "bo_fp8_epilogue": (None, [C.c_int, i64, i64, vp, i64, vp, i64, vp, C.c_int, f32, f32, vp, i64]),
             "bo_embedding": (None, [vp, vp, vp, i64, i64, i64, i64, i64, i64]),
             "bo_gemm_w8a8_rcr_bf16": (None, [i64, i64, i64, vp, i64, vp, i64, vp, vp, vp, i64, i64, i64, i32]),
             "bo_gemm_fp8_e4m3_rcr_f64": (None, [i64, i64, i64, vp, i64, vp, i64, vp, i64, i64, i64, i32]),
@@ -174,6 +178,51 @@ def gemm_s8_epi(a, b, layout, alpha, beta=0.0, c=None, bias=None, act=None) -> n
     bp = None if bias is None else np.ascontiguousarray(np.asarray(bias).astype(np.float32))
     _L().bo_gemm_s8_epi(m, n, k, _p(a), k, _p(b), sbk, sbn, None if cp is None else _p(cp), n,
                         None if bp is None else _p(bp), ACTS[act], _p(d), n, alpha, beta)
+    return d
+
+
+FP8_FMT = {"e4m3": 0, "e5m2": 1}
+
+
+def e5m2_table() -> np.ndarray:
+    f = _L().bo_e5m2_to_f32
+    return np.array([f(i) for i in range(256)], dtype=np.float32)
+
+
+def fp8_to_f32(b, fmt: str) -> np.ndarray:
+    t = e4m3_table() if fmt == "e4m3" else e5m2_table()
+    return t[np.asarray(b, dtype=np.uint8)]
+
+
+def f32_to_fp8(x, fmt: str) -> np.ndarray:
+    f = _L().bo_f32_to_e4m3_satfinite if fmt == "e4m3" else _L().bo_f32_to_e5m2_satfinite
+    x = np.asarray(x, dtype=np.float32)
+    return np.array([f(float(v)) for v in x.ravel()], dtype=np.uint8).reshape(x.shape)
+
+
+def gemm_fp8_f64(a_bits, b_bits, fmt: str, layout: str = "rcr", rows=None, nthreads=1) -> np.ndarray:
+    """Exact f64 accumulator; layout "rcr": b is [N, K]; "rrr": b is [K, N]."""
+    a = np.ascontiguousarray(a_bits, dtype=np.uint8)
+    b = np.ascontiguousarray(b_bits, dtype=np.uint8)
+    m, k = a.shape
+    if layout == "rcr":
+        n, sbk, sbn = b.shape[0], 1, k
+    else:
+        n, sbk, sbn = b.shape[1], b.shape[1], 1
+    r0, r1 = rows if rows is not None else (0, m)
+    acc = np.zeros((r1 - r0, n), dtype=np.float64)
+    _L().bo_gemm_fp8_f64(FP8_FMT[fmt], m, n, k, _p(a), k, _p(b), sbk, sbn, _p(acc), n, r0, r1, nthreads)
+    return acc
+
+
+def fp8_epilogue(acc, fmt: str, alpha, beta=0.0, c=None, bias=None, act=None) -> np.ndarray:
+    acc = np.ascontiguousarray(acc, dtype=np.float64)
+    m, n = acc.shape
+    d = np.zeros((m, n), dtype=np.uint8)
+    cp = None if c is None else np.ascontiguousarray(c, dtype=np.uint8)
+    bp = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    _L().bo_fp8_epilogue(FP8_FMT[fmt], m, n, _p(acc), n, None if cp is None else _p(cp), n,
+                         None if bp is None else _p(bp), ACTS[act], alpha, beta, _p(d), n)
     return d
 
 

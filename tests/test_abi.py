@@ -22,6 +22,13 @@ def _declared():
         for tag in re.findall(tag_macro + r"\((\w+)\)", text):
             for suf in sufs:
                 names.add(f"baracuda_kernels_{body.format(tag)}_{suf}")
+    for enc, lay in re.findall(r"BK_FP8_DECL\((\w+), (\w+)\)", text):
+        for suf in ("run", "workspace_size", "can_implement"):
+            names.add(f"baracuda_kernels_gemm_fp8_{enc}_{lay}_gfx950_{suf}")
+    for enc, lay in re.findall(r"BK_FP8_BIAS_DECL4\((\w+), (\w+)\)", text):
+        for epi in ("bias", "bias_relu", "bias_gelu", "bias_silu"):
+            for suf in ("run", "can_implement"):
+                names.add(f"baracuda_kernels_gemm_fp8_{enc}_{lay}_gfx950_{epi}_{suf}")
     for tag in re.findall(r"BK_EMBED_DECL\((\w+)\)", text):
         for suf in ("run", "can_implement"):
             names.add(f"baracuda_kernels_{tag}_{suf}")
@@ -32,7 +39,7 @@ def _declared():
         for suf in ("run", "can_implement"):
             names.add(f"baracuda_kernels_gemm_s8_rrr_gfx950_{epi}_{bias}_{suf}")
     return {n for n in names if "_TAG_" not in n and "##" not in n and "_EPI_" not in n
-            and "_NAME_" not in n}
+            and "_NAME_" not in n and "_ENC_" not in n}
 
 
 def test_header_and_binding_agree():

@@ -328,3 +328,57 @@ def test_embedding_padding_literal():
     # the i32 sentinel never matches a valid row; a huge i64 index is out of range
     big = np.array([2 ** 40, 3, -(2 ** 31)], np.int64)
     assert O.embedding(w, big).tolist() == [[0] * 4, [13, 14, 15, 16], [0] * 4]
+
+
+# ---- e5m2 / FP8 epilogue -------------------------------------------------------
+def test_e5m2_decode_table_matches_torch_float8_e5m2():
+    ref = torch.arange(256, dtype=torch.uint8).view(torch.float8_e5m2).float().numpy()
+    got = O.e5m2_table()
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    ok = ~np.isnan(ref)
+    assert np.array_equal(got[ok], ref[ok])     # includes +-inf at 0x7c / 0xfc
+
+
+def test_e5m2_encode_matches_torch_in_range_and_saturates():
+    x = _specials()
+    x = x[np.isfinite(x) & (np.abs(x) <= 57344.0)]
+    want = torch.from_numpy(x).to(torch.float8_e5m2).view(torch.uint8).numpy()
+    assert np.array_equal(O.f32_to_fp8(x, "e5m2"), want)
+    # satfinite: beyond max-finite (incl. the values RNE would send to inf) -> 0x7b
+    sat = np.array([61440.0, 1e6, np.inf, -70000.0, -np.inf], np.float32)
+    assert O.f32_to_fp8(sat, "e5m2").tolist() == [0x7B, 0x7B, 0x7B, 0xFB, 0xFB]
+    assert O.f32_to_fp8(np.array([np.nan], np.float32), "e5m2")[0] & 0x7F == 0x7F
+    # ties to even on the 2^-16 subnormal grid and at a normal midpoint
+    assert O.f32_to_fp8(np.array([2 ** -17, 3 * 2 ** -17, 1.125, 1.375], np.float32), "e5m2").tolist() == \
+        [0x00, 0x02, 0x3C, 0x3E]
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("act", [None, "relu", "gelu", "silu"])
+def test_fp8_gemm_and_epilogue_closed_forms(fmt, act):
+    m, n, k = 37, 29, 45
+    g = rng(9)
+    a = O.f32_to_fp8(g.standard_normal((m, k)).astype(np.float32), fmt)
+    bt = O.f32_to_fp8(g.standard_normal((n, k)).astype(np.float32), fmt)
+    c = O.f32_to_fp8(g.standard_normal((m, n)).astype(np.float32), fmt)
+    fa, fb = O.fp8_to_f32(a, fmt).astype(np.float64), O.fp8_to_f32(bt, fmt).astype(np.float64)
+    acc = O.gemm_fp8_f64(a, bt, fmt, "rcr")
+    assert np.array_equal(acc, fa @ fb.T)
+    assert np.array_equal(O.gemm_fp8_f64(a, np.ascontiguousarray(bt.T), fmt, "rrr"), acc)
+    assert np.array_equal(O.gemm_fp8_f64(a, bt, fmt, rows=(5, 9)), acc[5:9])
+    bias = (((np.arange(n) % 5) - 2) * 0.5).astype(np.float32)
+    z = (np.float32(0.25) * acc.astype(np.float32) + np.float32(0.5) * O.fp8_to_f32(c, fmt)
+         + bias).astype(np.float32)
+    if act == "relu":
+        z = np.maximum(z, np.float32(0))
+    elif act == "gelu":
+        z = (np.float32(0.5) * z * (1 + np.vectorize(math.erf)(z / math.sqrt(2)))).astype(np.float32)
+    elif act == "silu":
+        z = (z / (1 + np.exp(-z.astype(np.float64)))).astype(np.float32)
+    want = O.f32_to_fp8(z, fmt)
+    got = O.fp8_epilogue(acc, fmt, 0.25, 0.5, c, bias, act)
+    if act in (None, "relu"):
+        assert np.array_equal(got, want)
+    else:   # approximated erf / f32 exp: at most one grid step, rarely
+        step = np.abs(O.fp8_to_f32(got, fmt) - O.fp8_to_f32(want, fmt))
+        assert (step > 0).mean() < 0.02
