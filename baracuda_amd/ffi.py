@@ -96,6 +96,18 @@ for _i in ("", "i64idx_"):
         _sig(f"baracuda_kernels_embedding_{_i}{_t}_run", i32, i64, i32, i32, i64, vp, vp, vp, vp, sz, vp)
         _sig(f"baracuda_kernels_embedding_{_i}{_t}_can_implement", i32, i64, i32, i32, i64, vp, vp, vp)
 
+_sig("baracuda_te_fp8_format_e4m3", i32)
+_sig("baracuda_te_fp8_format_e5m2", i32)
+_sig("baracuda_te_fp8_max_representable", f32, i32)
+_sig("baracuda_te_fused_cast_amax_run", i32, vp, vp, vp, vp, i32, i64, i32, i32, vp)
+_sig("baracuda_te_fused_cast_amax_can_implement", i32, vp, vp, vp, vp, i32, i64, i32, i32)
+_sig("baracuda_te_dequant_run", i32, vp, vp, vp, i64, i32, i32, vp)
+_sig("baracuda_te_dequant_can_implement", i32, vp, vp, vp, i64, i32, i32)
+_sig("baracuda_te_recipe_update_run", i32, vp, vp, vp, i32, i32, i32, vp)
+_sig("baracuda_te_recipe_update_can_implement", i32, vp, vp, vp, i32, i32, i32)
+_sig("baracuda_te_recipe_init_run", i32, vp, vp, vp, i32, vp)
+_sig("baracuda_te_recipe_init_can_implement", i32, vp, vp, vp, i32)
+
 SYMBOLS = tuple(_SIGS)
 
 _lib = None

@@ -618,3 +618,102 @@ class QuantizedLinearPlan:
         else:
             raise Unsupported(f"quantized_linear activation dtype {activation.dtype}")
         check(st, "QuantizedLinearPlan::run")
+
+
+# ---- FP8 delayed-scaling quantizer (transformer-engine shim) -----------------
+class TeInvalidArgument(KernelError):
+    """The shim's status 1 (baracuda-transformer-engine Error::ShimInvalidArgument)."""
+    status = 1
+
+
+def _te_check(status: int, what: str) -> None:
+    if status == 1:
+        raise TeInvalidArgument(f"{what}: status 1")
+    if status == 5:
+        raise LaunchFailed(f"{what}: status 5")
+    if status != 0:
+        raise KernelError(f"{what}: status {status}")
+
+
+class Fp8Format(enum.Enum):
+    """baracuda-transformer-engine lib.rs Fp8Format (FFI tags 0 / 1)."""
+    E4M3 = 0
+    E5M2 = 1
+
+    def max_representable(self) -> float:
+        return 448.0 if self is Fp8Format.E4M3 else 57344.0
+
+
+_TE_DTYPE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+
+
+class Fp8Recipe:
+    """lib.rs Fp8Recipe: amax history ring + device scale / scale_inv scalars.
+
+    new() zeroes the history and sets scale = scale_inv = 1; each cast folds
+    max|x| into history[write_pos]; update_after_pass() publishes
+    scale = max_repr / max(history) and advances write_pos (wrapping)."""
+
+    def __init__(self, fmt: Fp8Format, history_len: int, device="cuda:0", stream=None):
+        if history_len <= 0 or history_len > 8192:
+            raise TeInvalidArgument("amax history length must be in 1..=8192")
+        self.format, self.history_len, self.write_pos = fmt, history_len, 0
+        self.amax_history = torch.empty(history_len, dtype=torch.float32, device=device)
+        self.scale = torch.empty(1, dtype=torch.float32, device=device)
+        self.scale_inv = torch.empty(1, dtype=torch.float32, device=device)
+        _te_check(lib().baracuda_te_recipe_init_run(_ptr(self.amax_history), _ptr(self.scale),
+                                                    _ptr(self.scale_inv), history_len, _stream(stream)),
+                  "Fp8Recipe::new")
+
+    def update_after_pass(self, stream=None) -> None:
+        _te_check(lib().baracuda_te_recipe_update_run(_ptr(self.amax_history), _ptr(self.scale),
+                                                      _ptr(self.scale_inv), self.history_len,
+                                                      self.write_pos, self.format.value, _stream(stream)),
+                  "Fp8Recipe::update_after_pass")
+        self.write_pos = (self.write_pos + 1) % self.history_len
+
+    def scale_host(self) -> float:
+        torch.cuda.synchronize()
+        return float(self.scale.item())
+
+    def scale_inv_host(self) -> float:
+        torch.cuda.synchronize()
+        return float(self.scale_inv.item())
+
+
+class Fp8CastPlan:
+    """lib.rs Fp8CastPlan: output = sat_fp8(input * scale), amax folded into the recipe."""
+
+    @classmethod
+    def select(cls) -> "Fp8CastPlan":
+        return cls()
+
+    def run(self, inp: torch.Tensor, out: torch.Tensor, recipe: Fp8Recipe, stream=None) -> None:
+        if inp.numel() != out.numel():
+            raise TeInvalidArgument("Fp8CastPlan::run: input.len() != output.len()")
+        if inp.numel() == 0:
+            raise TeInvalidArgument("Fp8CastPlan::run: empty input")
+        _need(inp.dtype in _TE_DTYPE and out.element_size() == 1 and inp.is_contiguous()
+              and out.is_contiguous(), "Fp8CastPlan: f32/f16/bf16 contiguous input, 1-byte output")
+        _te_check(lib().baracuda_te_fused_cast_amax_run(
+            _ptr(inp), _ptr(out), _ptr(recipe.scale), _ptr(recipe.amax_history), recipe.write_pos,
+            inp.numel(), recipe.format.value, _TE_DTYPE[inp.dtype], _stream(stream)), "Fp8CastPlan::run")
+
+
+class Fp8DequantPlan:
+    """lib.rs Fp8DequantPlan: output = dec(input) * scale_inv."""
+
+    @classmethod
+    def select(cls) -> "Fp8DequantPlan":
+        return cls()
+
+    def run(self, inp: torch.Tensor, out: torch.Tensor, recipe: Fp8Recipe, stream=None) -> None:
+        if inp.numel() != out.numel():
+            raise TeInvalidArgument("Fp8DequantPlan::run: input.len() != output.len()")
+        if inp.numel() == 0:
+            raise TeInvalidArgument("Fp8DequantPlan::run: empty input")
+        _need(out.dtype in _TE_DTYPE and inp.element_size() == 1 and inp.is_contiguous()
+              and out.is_contiguous(), "Fp8DequantPlan: 1-byte input, f32/f16/bf16 contiguous output")
+        _te_check(lib().baracuda_te_dequant_run(
+            _ptr(inp), _ptr(out), _ptr(recipe.scale_inv), inp.numel(), recipe.format.value,
+            _TE_DTYPE[out.dtype], _stream(stream)), "Fp8DequantPlan::run")

@@ -85,7 +85,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",
-                    help="run only: w8a8|gemv|fp8|moe|int8epi|embedding|gather|copy (profiling; copy = 256 MiB "
+                    help="run only: w8a8|gemv|fp8|moe|int8epi|te|embedding|gather|copy (profiling; copy = 256 MiB "
                          "device copy used to calibrate the HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -208,6 +208,19 @@ def main():
                            "frac_int8_peak": round(it_ / PEAK_INT8_TOPS, 4)}
             extra["int8_s8out_4096_cubed"] = e
             del ia, ib, ibr, idd
+        if only in ("", "te"):
+            log("bench: fp8 fused cast+amax bf16 14336x4096 -> e4m3")
+            tn = 14336 * 4096
+            tx = torch.randn(tn, device=dev).to(torch.bfloat16)
+            tq = torch.empty(tn, dtype=torch.uint8, device=dev)
+            trec = P.Fp8Recipe(P.Fp8Format.E4M3, 16)
+            tcast = P.Fp8CastPlan.select()
+            tms = time_launches(lambda: tcast.run(tx, tq, trec, stream=stream), 50, 10, stream)
+            tbytes = tn * 3
+            extra["te_fp8_cast_amax_bf16_14336x4096"] = {
+                "us": round(tms * 1e3, 2), "GB_s": round(tbytes / (tms * 1e-3) / 1e9, 1),
+                "frac_hbm_peak": round(tbytes / (tms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+            del tx, tq
         if only in ("", "embedding"):
             log("bench: embedding V=32000 D=4096 N=1")
             e = {}

@@ -186,6 +186,39 @@ BK_FP8_BIAS_DECL4(e5m2, rrr)
 #undef BK_FP8_BIAS_DECL4
 #undef BK_FP8_BIAS_DECL
 
+/* ======================= FP8 delayed-scaling quantizer ===================
+ * Same ABI as crates/baracuda-transformer-engine-sys/csrc/baracuda_te_shim.cu
+ * (bound in crates/baracuda-transformer-engine-sys/src/lib.rs:95-257).
+ * Status 0 ok, 1 invalid argument, 5 launch failure.  fmt 0 = e4m3, 1 = e5m2;
+ * dtype 0 = f32, 1 = f16, 2 = bf16. */
+int32_t baracuda_te_fp8_format_e4m3(void);
+int32_t baracuda_te_fp8_format_e5m2(void);
+float baracuda_te_fp8_max_representable(int32_t fmt);
+/* out[i] = sat_fp8(x[i] * scale[0]); amax_history[write_pos] = max(., max|x|) */
+int32_t baracuda_te_fused_cast_amax_run(const void *x_in, void *x_out, const float *scale,
+                                        float *amax_history, int32_t write_pos, int64_t numel,
+                                        int32_t fmt, int32_t in_dtype, void *stream);
+int32_t baracuda_te_fused_cast_amax_can_implement(const void *x_in, const void *x_out,
+                                                  const float *scale, const float *amax_history,
+                                                  int32_t write_pos, int64_t numel, int32_t fmt,
+                                                  int32_t in_dtype);
+/* y[i] = dec(x[i]) * scale_inv[0] */
+int32_t baracuda_te_dequant_run(const void *x_in, void *y_out, const float *scale_inv, int64_t numel,
+                                int32_t fmt, int32_t out_dtype, void *stream);
+int32_t baracuda_te_dequant_can_implement(const void *x_in, const void *y_out, const float *scale_inv,
+                                          int64_t numel, int32_t fmt, int32_t out_dtype);
+/* scale = max_repr / max(history) (0 -> 1, inf -> max_repr), scale_inv = 1/that;
+ * history[write_pos] = 0 */
+int32_t baracuda_te_recipe_update_run(float *amax_history, float *scale, float *scale_inv,
+                                      int32_t hist_len, int32_t write_pos, int32_t fmt, void *stream);
+int32_t baracuda_te_recipe_update_can_implement(const float *amax_history, const float *scale,
+                                                const float *scale_inv, int32_t hist_len,
+                                                int32_t write_pos, int32_t fmt);
+int32_t baracuda_te_recipe_init_run(float *amax_history, float *scale, float *scale_inv,
+                                    int32_t hist_len, void *stream);
+int32_t baracuda_te_recipe_init_can_implement(const float *amax_history, const float *scale,
+                                              const float *scale_inv, int32_t hist_len);
+
 /* ======================= embedding forward ===============================
  * out[n,:] = weight[idx[n],:], zero row when idx[n] == padding_idx, < 0 or
  * >= V; idx i32 (embedding_<T>) or i64 (embedding_i64idx_<T>), padding_idx

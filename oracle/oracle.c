@@ -221,6 +221,28 @@ void bo_gemm_s8_rcr_s8(int64_t m, int64_t n, int64_t k,
         }
 }
 
+/* baracuda_te_shim.cu fused_cast_amax_kernel: out = sat_fp8(v * s) in f32,
+ * amax = max |v| with NaN never winning (`av > tmax`). */
+void bo_te_cast_amax(const float *x, int64_t n, float scale, int fmt, uint8_t *out, float *amax) {
+    float m = 0.0f;
+    for (int64_t i = 0; i < n; ++i) {
+        const float av = fabsf(x[i]);
+        if (av > m) m = av;
+        volatile float vs = x[i] * scale;
+        out[i] = fmt ? bo_f32_to_e5m2_satfinite(vs) : bo_f32_to_e4m3_satfinite(vs);
+    }
+    *amax = m;
+}
+
+/* baracuda_te_shim.cu dequant_kernel: y = dec(x) * si in f32 (callers round
+ * to f16 / bf16 with the RNE codecs above). */
+void bo_te_dequant(const uint8_t *x, int64_t n, float scale_inv, int fmt, float *y) {
+    for (int64_t i = 0; i < n; ++i) {
+        volatile float v = (fmt ? bo_e5m2_to_f32(x[i]) : bo_e4m3_to_f32(x[i])) * scale_inv;
+        y[i] = v;
+    }
+}
+
 /* baracuda_embedding.cuh:61-88 (embedding_kernel), one row at a time. */
 void bo_embedding(void *out, const void *weight, const void *idx, int64_t idx_size, int64_t n,
                   int64_t V, int64_t D, int64_t elem_size, int64_t padding_idx) {

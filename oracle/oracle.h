@@ -128,6 +128,11 @@ void bo_gemv_s8w_m1_f64(int64_t n, int64_t k,
 void bo_gather_rows(void *dest, const void *table, const uint32_t *idx,
                     int64_t V, int64_t H, int64_t n, int64_t elem_size);
 
+/* FP8 delayed-scaling quantizer (baracuda_te_shim.cu fused_cast_amax_kernel,
+ * dequant_kernel): x widened to f32 by the caller. */
+void bo_te_cast_amax(const float *x, int64_t n, float scale, int fmt, uint8_t *out, float *amax);
+void bo_te_dequant(const uint8_t *x, int64_t n, float scale_inv, int fmt, float *y);
+
 /* embedding forward (baracuda_embedding.cuh:61-88): out[r,:] = weight[idx[r],:],
  * zero when idx[r] == padding_idx, idx[r] < 0 or idx[r] >= V.  idx_size 4
  * (i32) or 8 (i64); elem_size in bytes. */

@@ -50,6 +50,8 @@ def _L():
             "bo_f32_to_e5m2_satfinite": (C.c_uint8, [f32]),
             "bo_gemm_fp8_f64": (None, [C.c_int, i64, i64, i64, vp, i64, vp, i64, i64, vp, i64, i64, i64, i32]),
             "bo_fp8_epilogue": (None, [C.c_int, i64, i64, vp, i64, vp, i64, vp, C.c_int, f32, f32, vp, i64]),
+            "bo_te_cast_amax": (None, [vp, i64, f32, C.c_int, vp, vp]),
+            "bo_te_dequant": (None, [vp, i64, f32, C.c_int, vp]),
             "bo_embedding": (None, [vp, vp, vp, i64, i64, i64, i64, i64, i64]),
             "bo_gemm_w8a8_rcr_bf16": (None, [i64, i64, i64, vp, i64, vp, i64, vp, vp, vp, i64, i64, i64, i32]),
             "bo_gemm_fp8_e4m3_rcr_f64": (None, [i64, i64, i64, vp, i64, vp, i64, vp, i64, i64, i64, i32]),
@@ -224,6 +226,42 @@ def fp8_epilogue(acc, fmt: str, alpha, beta=0.0, c=None, bias=None, act=None) ->
     _L().bo_fp8_epilogue(FP8_FMT[fmt], m, n, _p(acc), n, None if cp is None else _p(cp), n,
                          None if bp is None else _p(bp), ACTS[act], alpha, beta, _p(d), n)
     return d
+
+
+def te_cast_amax(x_f32, scale: float, fmt: str):
+    """fused_cast_amax on f32-widened input: (fp8 bits, amax)."""
+    x = np.ascontiguousarray(x_f32, dtype=np.float32).ravel()
+    out = np.zeros(x.size, dtype=np.uint8)
+    amax = np.zeros(1, dtype=np.float32)
+    _L().bo_te_cast_amax(_p(x), x.size, scale, FP8_FMT[fmt], _p(out), _p(amax))
+    return out, float(amax[0])
+
+
+def te_dequant_f32(bits, scale_inv: float, fmt: str) -> np.ndarray:
+    b = np.ascontiguousarray(bits, dtype=np.uint8).ravel()
+    y = np.zeros(b.size, dtype=np.float32)
+    _L().bo_te_dequant(_p(b), b.size, scale_inv, FP8_FMT[fmt], _p(y))
+    return y
+
+
+TE_MAX_REPR = {"e4m3": 448.0, "e5m2": 57344.0}
+
+
+def te_recipe_update(history, fmt: str, write_pos: int):
+    """recipe_update_kernel: (scale, scale_inv, new history) in f32."""
+    h = np.asarray(history, dtype=np.float32).copy()
+    amax = np.float32(0.0)
+    for v in h:
+        if v > amax:
+            amax = v
+    if not amax > 0:
+        amax = np.float32(1.0)
+    if not np.isfinite(amax):
+        amax = np.float32(TE_MAX_REPR[fmt])
+    mr = np.float32(TE_MAX_REPR[fmt])
+    scale, scale_inv = np.float32(mr / amax), np.float32(amax / mr)
+    h[write_pos] = 0.0
+    return float(scale), float(scale_inv), h
 
 
 PADDING_DISABLED = -(2 ** 31)

@@ -14,7 +14,7 @@ HDR = Path(__file__).resolve().parents[1] / "include" / "baracuda_kernels.h"
 
 def _declared():
     text = re.sub(r"/\*.*?\*/", "", HDR.read_text(), flags=re.S)
-    names = set(re.findall(r"\b(baracuda_kernels_\w+)\s*\(", text))
+    names = set(re.findall(r"\b(baracuda_(?:kernels|te)_\w+)\s*\(", text))
     for tag_macro, body, sufs in (
             ("BK_GEMV_DENSE_DECL", "gemv_dense_m1_{}", ("run", "can_implement", "workspace_size")),
             ("BK_GATHER_DECL", "gather_rows_{}", ("run", "can_implement", "workspace_size")),
@@ -146,6 +146,36 @@ def test_embedding_can_implement_and_empty():
             assert run(0, 10, 8, 0, None, None, None, None, 0, None) == 0
             assert run(-1, 10, 8, 0, None, None, None, None, 0, None) == 2
             assert run(3, 10, 8, 0, None, None, None, None, 0, None) == 2
+
+
+
+def test_te_shim_argument_checks():
+    # baracuda_te_shim.cu can_implement / run guards (status 1 = invalid).
+    L = ffi.lib()
+    assert L.baracuda_te_fp8_format_e4m3() == 0 and L.baracuda_te_fp8_format_e5m2() == 1
+    assert L.baracuda_te_fp8_max_representable(0) == 448.0
+    assert L.baracuda_te_fp8_max_representable(1) == 57344.0
+    assert L.baracuda_te_fp8_max_representable(7) == 1.0
+    can = L.baracuda_te_fused_cast_amax_can_implement
+    assert can(None, None, None, None, 0, 16, 0, 2) == 0
+    assert can(None, None, None, None, -1, 16, 0, 2) == 1
+    assert can(None, None, None, None, 0, -1, 0, 2) == 1
+    assert can(None, None, None, None, 0, 16, 2, 0) == 1
+    assert can(None, None, None, None, 0, 16, 1, 3) == 1
+    assert L.baracuda_te_fused_cast_amax_run(None, None, None, None, 0, 16, 0, 0, None) == 1
+    assert L.baracuda_te_dequant_can_implement(None, None, None, 16, 1, 2) == 0
+    assert L.baracuda_te_dequant_can_implement(None, None, None, 16, 1, -1) == 1
+    assert L.baracuda_te_dequant_run(None, None, None, 16, 0, 0, None) == 1
+    upd = L.baracuda_te_recipe_update_can_implement
+    assert upd(None, None, None, 8, 7, 0) == 0
+    assert upd(None, None, None, 8, 8, 0) == 1
+    assert upd(None, None, None, 0, 0, 0) == 1
+    assert upd(None, None, None, 8193, 0, 0) == 1
+    assert L.baracuda_te_recipe_init_can_implement(None, None, None, 8192) == 0
+    assert L.baracuda_te_recipe_init_can_implement(None, None, None, 0) == 1
+    assert L.baracuda_te_recipe_init_run(None, None, None, 8, None) == 1
+    with pytest.raises(P.TeInvalidArgument):
+        P.Fp8Recipe(P.Fp8Format.E4M3, 0, device="cpu")
 
 
 def test_quantize_can_implement():

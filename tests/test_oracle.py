@@ -382,3 +382,41 @@ def test_fp8_gemm_and_epilogue_closed_forms(fmt, act):
     else:   # approximated erf / f32 exp: at most one grid step, rarely
         step = np.abs(O.fp8_to_f32(got, fmt) - O.fp8_to_f32(want, fmt))
         assert (step > 0).mean() < 0.02
+
+
+# ---- FP8 delayed-scaling quantizer -------------------------------------------
+@pytest.mark.parametrize("fmt,tdt", [("e4m3", torch.float8_e4m3fn), ("e5m2", torch.float8_e5m2)])
+def test_te_cast_matches_torch_in_range(fmt, tdt):
+    g = rng(4)
+    x = (g.standard_normal(5000) * 3).astype(np.float32)
+    x[17] = np.nan
+    s = 7.5
+    bits, amax = O.te_cast_amax(x, s, fmt)
+    xs = (x * np.float32(s)).astype(np.float32)
+    ok = np.isfinite(xs) & (np.abs(xs) <= O.TE_MAX_REPR[fmt])
+    want = torch.from_numpy(xs[ok]).to(tdt).view(torch.uint8).numpy()
+    assert np.array_equal(bits[ok], want)
+    assert bits[17] & 0x7F == 0x7F                      # NaN stays NaN
+    assert amax == np.nanmax(np.abs(x))                 # NaN never wins the max
+    big = O.te_cast_amax(np.array([1e6, -1e6], np.float32), 1.0, fmt)[0]
+    assert big.tolist() == ([0x7E, 0xFE] if fmt == "e4m3" else [0x7B, 0xFB])   # satfinite
+
+
+def test_te_recipe_scale_formula_reference_cases():
+    # recipe_scale_compute_smoke.rs: amax 10 (e4m3) -> 44.8, amax 100 (e5m2)
+    # -> 573.44, empty history -> amax floored at 1 -> scale = 448.
+    s, si, h = O.te_recipe_update([0, 0, 10.0, 0], "e4m3", 2)
+    assert abs(s - 44.8) / 44.8 < 1e-6 and abs(s * si - 1) < 1e-6 and h[2] == 0
+    s, si, _ = O.te_recipe_update([100.0], "e5m2", 0)
+    assert abs(s - 573.44) / 573.44 < 1e-6
+    assert O.te_recipe_update([0.0] * 8, "e4m3", 0)[:2] == (448.0, float(np.float32(1.0) / np.float32(448.0)))
+    assert O.te_recipe_update([np.inf], "e4m3", 0)[:2] == (1.0, 1.0)
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+def test_te_dequant_is_decode_times_scale_inv(fmt):
+    b = np.arange(256, dtype=np.uint8)
+    y = O.te_dequant_f32(b, 0.125, fmt)
+    ref = O.fp8_to_f32(b, fmt) * np.float32(0.125)
+    both_nan = np.isnan(y) & np.isnan(ref)
+    assert np.array_equal(y[~both_nan], ref[~both_nan])
