@@ -138,6 +138,37 @@ __device__ __forceinline__ uint8_t f32_to_fp8_satfinite(float x) {
     else return f32_to_e4m3_satfinite(x);
 }
 
+// Four f32 -> four satfinite fp8 bytes (byte i = element i) through the
+// hardware packed conversion (v_cvt_pk_fp8_f32 / v_cvt_pk_bf8_f32, RNE).
+// Measured on gfx950 to equal f32_to_fp8_satfinite bit for bit for every
+// |x| <= max finite (2^24 patterns spanning all exponents, ties and
+// subnormals); beyond that the instruction overflows to NaN / inf and gives
+// NaN the sign bit, so the input is clamped to +-max first and NaN inputs
+// take the software code (sign | 0x7f).
+template <int FMT>
+__device__ __forceinline__ uint32_t f32x4_to_fp8x4_satfinite(float a, float b, float c, float d) {
+    constexpr float M = FMT == FMT_E5M2 ? 57344.0f : 448.0f;
+    const float ca = fminf(fmaxf(a, -M), M), cb = fminf(fmaxf(b, -M), M);
+    const float cc = fminf(fmaxf(c, -M), M), cd = fminf(fmaxf(d, -M), M);
+    uint32_t w;
+    if constexpr (FMT == FMT_E5M2) {
+        w = (uint32_t)__builtin_amdgcn_cvt_pk_bf8_f32(ca, cb, 0, false);
+        w = (uint32_t)__builtin_amdgcn_cvt_pk_bf8_f32(cc, cd, (int)w, true);
+    } else {
+        w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(ca, cb, 0, false);
+        w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(cc, cd, (int)w, true);
+    }
+    const float v[4] = {a, b, c, d};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if (v[i] != v[i]) {
+            const uint32_t nan = ((__float_as_uint(v[i]) >> 24) & 0x80u) | 0x7fu;
+            w = (w & ~(0xffu << (8 * i))) | (nan << (8 * i));
+        }
+    }
+    return w;
+}
+
 __device__ __forceinline__ int8_t sat_cast_s8(float x) {
     float r = __builtin_rintf(x);   // round half to even
     r = r < -128.0f ? -128.0f : r;

@@ -49,23 +49,22 @@ struct F8Epilogue {
         for (int r = 0; r < 4; ++r) y[r] = p.alpha * v[r];
         if constexpr (EPI == F8_OUT) {
             uint8_t *d = static_cast<uint8_t *>(p.d) + (int64_t)m * p.ldd + n0;
-            uint8_t o[4];
+            float z[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                float z = y[r];
+                z[r] = y[r];
                 if (p.beta != 0.0f && p.c != nullptr && r < count)
-                    z += p.beta * fp8_to_f32<FMT>(p.c[(int64_t)m * p.ldc + n0 + r]);
+                    z[r] += p.beta * fp8_to_f32<FMT>(p.c[(int64_t)m * p.ldc + n0 + r]);
                 if constexpr (ACT != ACT_NONE) {
-                    if (r < count) z += p.bias[n0 + r];
-                    z = activation<ACT>(z);
+                    if (r < count) z[r] += p.bias[n0 + r];
+                    z[r] = activation<ACT>(z[r]);
                 }
-                o[r] = f32_to_fp8_satfinite<FMT>(z);
             }
+            const uint32_t w = f32x4_to_fp8x4_satfinite<FMT>(z[0], z[1], z[2], z[3]);
             if constexpr (VecOut) {
-                *reinterpret_cast<uint32_t *>(d) = (uint32_t)o[0] | ((uint32_t)o[1] << 8) |
-                                                   ((uint32_t)o[2] << 16) | ((uint32_t)o[3] << 24);
+                *reinterpret_cast<uint32_t *>(d) = w;
             } else {
-                for (int r = 0; r < count; ++r) d[r] = o[r];
+                for (int r = 0; r < count; ++r) d[r] = (uint8_t)(w >> (8 * r));
             }
         } else if constexpr (EPI == F8_BF16) {
             store4_bf16(static_cast<uint16_t *>(p.d) + (int64_t)m * p.ldd + n0, y, VecOut, count);

@@ -14,8 +14,9 @@
 // 1 = e5m2.
 //
 // MI355X layout: the cast and dequant are HBM-bound streams; each thread
-// moves 8 elements per step with 16-byte (or 2 x 16-byte for f32) loads and
-// an 8-byte fp8 store, grid-strided over at most 2048 workgroups.  The amax
+// moves 4 units of 8 elements per step (16-byte, or 2 x 16-byte for f32,
+// loads, all issued before the first conversion, and 8-byte fp8 stores),
+// grid-strided over at most 2048 workgroups.  The amax
 // is reduced across the wave with DPP-free shuffles, across the workgroup in
 // LDS, and folded into the history slot with one integer atomicMax per
 // workgroup on the bits of a non-negative float (order-preserving).  Init is
@@ -28,6 +29,7 @@ namespace {
 constexpr int kTeBlock = 256;
 constexpr int kTeMaxHistory = 8192;
 constexpr int kTeMaxGrid = 2048;
+constexpr int kTeUnroll = 4;
 enum TeStatus : int32_t { kTeOk = 0, kTeInvalid = 1, kTeLaunch = 5 };
 
 __host__ __device__ inline float te_max_repr(int32_t fmt) {
@@ -93,19 +95,30 @@ __global__ __launch_bounds__(kTeBlock) void te_cast_amax_kernel(const T *__restr
     const int64_t tid = (int64_t)blockIdx.x * kTeBlock + threadIdx.x;
     const int64_t step = (int64_t)gridDim.x * kTeBlock;
     if constexpr (Vec) {
+        // kTeUnroll independent 8-element units per thread per step, all
+        // loads issued before any conversion: 4x the bytes in flight.
         const int64_t units = numel >> 3;
-        for (int64_t u = tid; u < units; u += step) {
-            float v[8];
-            te_ld8<T>(x + 8 * u, v);
-            uint32_t lo = 0, hi = 0;
+        for (int64_t u0 = tid; u0 < units; u0 += kTeUnroll * step) {
+            float v[kTeUnroll][8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                tmax = fmaxf(tmax, fabsf(v[i]));
-                const uint32_t q = f32_to_fp8_satfinite<FMT>(v[i] * s);
-                if (i < 4) lo |= q << (8 * i);
-                else hi |= q << (8 * (i - 4));
+            for (int j = 0; j < kTeUnroll; ++j) {
+                const int64_t u = u0 + j * step;
+                if (u < units) te_ld8<T>(x + 8 * u, v[j]);
             }
-            *reinterpret_cast<v2i *>(out + 8 * u) = v2i{(int)lo, (int)hi};
+#pragma unroll
+            for (int j = 0; j < kTeUnroll; ++j) {
+                const int64_t u = u0 + j * step;
+                if (u >= units) break;
+                float y[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    tmax = fmaxf(tmax, fabsf(v[j][i]));
+                    y[i] = v[j][i] * s;
+                }
+                const uint32_t lo = f32x4_to_fp8x4_satfinite<FMT>(y[0], y[1], y[2], y[3]);
+                const uint32_t hi = f32x4_to_fp8x4_satfinite<FMT>(y[4], y[5], y[6], y[7]);
+                *reinterpret_cast<v2i *>(out + 8 * u) = v2i{(int)lo, (int)hi};
+            }
         }
         const int64_t t0 = units << 3;
         if (blockIdx.x == 0 && t0 + threadIdx.x < numel) {
@@ -134,19 +147,29 @@ __global__ __launch_bounds__(kTeBlock) void te_dequant_kernel(const uint8_t *__r
     const int64_t step = (int64_t)gridDim.x * kTeBlock;
     if constexpr (Vec) {
         const int64_t units = numel >> 3;
-        for (int64_t u = tid; u < units; u += step) {
-            const v2i w = *reinterpret_cast<const v2i *>(x + 8 * u);
-            T o[8];
+        for (int64_t u0 = tid; u0 < units; u0 += kTeUnroll * step) {
+            v2i w[kTeUnroll];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const uint8_t b = (uint8_t)((uint32_t)w[i >> 2] >> (8 * (i & 3)));
-                te_st<T>(&o[i], fp8_to_f32<FMT>(b) * si);
+            for (int j = 0; j < kTeUnroll; ++j) {
+                const int64_t u = u0 + j * step;
+                if (u < units) w[j] = *reinterpret_cast<const v2i *>(x + 8 * u);
             }
-            if constexpr (sizeof(T) == 4) {
-                *reinterpret_cast<v4f *>(y + 8 * u) = *reinterpret_cast<const v4f *>(&o[0]);
-                *reinterpret_cast<v4f *>(y + 8 * u + 4) = *reinterpret_cast<const v4f *>(&o[4]);
-            } else {
-                *reinterpret_cast<v4i *>(y + 8 * u) = *reinterpret_cast<const v4i *>(&o[0]);
+#pragma unroll
+            for (int j = 0; j < kTeUnroll; ++j) {
+                const int64_t u = u0 + j * step;
+                if (u >= units) break;
+                T o[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const uint8_t b = (uint8_t)((uint32_t)w[j][i >> 2] >> (8 * (i & 3)));
+                    te_st<T>(&o[i], fp8_to_f32<FMT>(b) * si);
+                }
+                if constexpr (sizeof(T) == 4) {
+                    *reinterpret_cast<v4f *>(y + 8 * u) = *reinterpret_cast<const v4f *>(&o[0]);
+                    *reinterpret_cast<v4f *>(y + 8 * u + 4) = *reinterpret_cast<const v4f *>(&o[4]);
+                } else {
+                    *reinterpret_cast<v4i *>(y + 8 * u) = *reinterpret_cast<const v4i *>(&o[0]);
+                }
             }
         }
         const int64_t t0 = units << 3;
@@ -203,7 +226,7 @@ int32_t te_cast(const void *x, void *out, const float *scale, float *slot, int64
     const bool vec = (reinterpret_cast<uintptr_t>(x) & 15u) == 0 &&
                      (reinterpret_cast<uintptr_t>(out) & 7u) == 0;
     if (vec)
-        hipLaunchKernelGGL((te_cast_amax_kernel<T, FMT, true>), dim3(te_grid(numel >> 3)), dim3(kTeBlock),
+        hipLaunchKernelGGL((te_cast_amax_kernel<T, FMT, true>), dim3(te_grid(((numel >> 3) + kTeUnroll - 1) / kTeUnroll)), dim3(kTeBlock),
                            0, s, (const T *)x, (uint8_t *)out, scale, slot, numel);
     else
         hipLaunchKernelGGL((te_cast_amax_kernel<T, FMT, false>), dim3(te_grid(numel)), dim3(kTeBlock), 0,
@@ -216,7 +239,7 @@ int32_t te_dequant(const void *x, void *y, const float *scale_inv, int64_t numel
     const bool vec = (reinterpret_cast<uintptr_t>(x) & 7u) == 0 &&
                      (reinterpret_cast<uintptr_t>(y) & 15u) == 0;
     if (vec)
-        hipLaunchKernelGGL((te_dequant_kernel<T, FMT, true>), dim3(te_grid(numel >> 3)), dim3(kTeBlock), 0,
+        hipLaunchKernelGGL((te_dequant_kernel<T, FMT, true>), dim3(te_grid(((numel >> 3) + kTeUnroll - 1) / kTeUnroll)), dim3(kTeBlock), 0,
                            s, (const uint8_t *)x, (T *)y, scale_inv, numel);
     else
         hipLaunchKernelGGL((te_dequant_kernel<T, FMT, false>), dim3(te_grid(numel)), dim3(kTeBlock), 0, s,

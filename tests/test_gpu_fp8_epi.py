@@ -119,3 +119,19 @@ def test_e5m2_rrr_dma_matches_rcr_bitwise(gpu):
     rcr = _run("e5m2", P.LayoutSku.Rcr, P.EpilogueKind.Identity, a, bt, alpha=1.0 / 32)
     rrr = _run("e5m2", P.LayoutSku.Rrr, P.EpilogueKind.Identity, a, np.ascontiguousarray(bt.T), alpha=1.0 / 32)
     assert np.array_equal(rcr, rrr)
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("shape", [(100, 70, 50), (256, 256, 128)])
+def test_saturating_outputs(gpu, fmt, shape):
+    # A large alpha pushes most outputs past max finite: satfinite clamps to
+    # +-max (0x7e / 0x7b), never inf or NaN; exact pattern sums keep it bit-exact.
+    m, n, k = shape
+    a = O.f32_to_fp8((((np.arange(m * k) * 5) % 13) - 6.0) * 0.125, fmt).reshape(m, k)
+    b = O.f32_to_fp8((((np.arange(k * n) * 7) % 11) - 5.0) * 0.125, fmt).reshape(n, k)
+    alpha = 4096.0 if fmt == "e4m3" else 2.0 ** 19
+    got = _run(fmt, P.LayoutSku.Rcr, P.EpilogueKind.Identity, a, b, alpha=alpha)
+    want = _want(fmt, P.LayoutSku.Rcr, P.EpilogueKind.Identity, a, b, None, None, alpha, 0.0)
+    assert np.array_equal(got, want)
+    mx = 0x7E if fmt == "e4m3" else 0x7B
+    assert ((got & 0x7F) == mx).mean() > 0.3
