@@ -169,6 +169,27 @@ __device__ __forceinline__ uint32_t f32x4_to_fp8x4_satfinite(float a, float b, f
     return w;
 }
 
+// u8 -> s8 operand flip for the signed int8 MFMA: each byte u becomes
+// s = u - 128 (xor 0x80) and `sum` accumulates the flipped bytes
+// (v_dot4_i32_i8 with ones).  Summing the flipped value lets the raw one die
+// at the xor, which keeps the fragment registers from doubling.
+__device__ __forceinline__ v4i u8_flip_and_sum(const v4i &f, int &sum) {
+    v4i o;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        o[w] = f[w] ^ (int)0x80808080u;
+        sum = __builtin_amdgcn_sdot4(o[w], 0x01010101, sum, false);
+    }
+    return o;
+}
+
+__device__ __forceinline__ uint8_t sat_cast_u8(float x) {
+    float r = __builtin_rintf(x);   // round half to even
+    r = r < 0.0f ? 0.0f : r;
+    r = r > 255.0f ? 255.0f : r;
+    return (uint8_t)(int)r;
+}
+
 __device__ __forceinline__ int8_t sat_cast_s8(float x) {
     float r = __builtin_rintf(x);   // round half to even
     r = r < -128.0f ? -128.0f : r;

@@ -53,10 +53,22 @@ __device__ __forceinline__ int lds_off(int row, int unit) {
     return row * BK + ((unit ^ swz(row)) << 4);
 }
 
-enum class Elem { S8, E4M3, E5M2 };
+enum class Elem { S8, U8, E4M3, E5M2 };
 
 template <Elem E> struct AccT { typedef v4f type; };   // FP8: f32 accumulators
 template <> struct AccT<Elem::S8> { typedef v4i type; };
+template <> struct AccT<Elem::U8> { typedef v4i type; };
+
+// u8 operands through the signed int8 MFMA: each fragment word is flipped to
+// s = u - 128 (xor 0x80 per byte) and the flipped bytes are summed per row of
+// A (ra[i], tile row i of the wave) and per column of B (cb[j]) with v_dot4;
+// the epilogue restores sum(u_a*u_b) = acc_s + 128*(ra + cb) + 16384*K_pad.
+// Each lane holds partial sums over its k-group (lane / 16).
+struct FragSums {
+    int ra[TM];
+    int cb[TN];
+};
+
 
 // Per-thread view of the rows this thread stages into LDS.  Each of the 4
 // loads of a stage covers row (i * 64 + tid / 8), 16-byte unit tid % 8.
@@ -112,10 +124,11 @@ __device__ __forceinline__ void store_stage(int8_t *la, int8_t *lb, const v4i (&
 template <Elem E>
 __device__ __forceinline__ void compute_stage(const int8_t *la, const int8_t *lb,
                                               typename AccT<E>::type (&acc)[TM][TN],
-                                              int wave_m, int wave_n, int lane) {
+                                              int wave_m, int wave_n, int lane,
+                                              FragSums *sums = nullptr) {
     const int r16 = lane & 15;
     const int grp = lane >> 4;
-    if constexpr (E == Elem::S8) {
+    if constexpr (E == Elem::S8 || E == Elem::U8) {
         // v_mfma_i32_16x16x64_i8: 16 bytes of K per lane, 2 sub-steps per stage.
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
@@ -125,11 +138,13 @@ __device__ __forceinline__ void compute_stage(const int8_t *la, const int8_t *lb
             for (int j = 0; j < TN; ++j) {
                 const int row = wave_n * WN + j * 16 + r16;
                 bf[j] = *reinterpret_cast<const v4i *>(lb + lds_off(row, unit));
+                if constexpr (E == Elem::U8) bf[j] = u8_flip_and_sum(bf[j], sums->cb[j]);
             }
 #pragma unroll
             for (int i = 0; i < TM; ++i) {
                 const int row = wave_m * WM + i * 16 + r16;
                 v4i af = *reinterpret_cast<const v4i *>(la + lds_off(row, unit));
+                if constexpr (E == Elem::U8) af = u8_flip_and_sum(af, sums->ra[i]);
 #pragma unroll
                 for (int j = 0; j < TN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[j], af, acc[i][j], 0, 0, 0);
@@ -288,7 +303,8 @@ __device__ __forceinline__ void store_b_rrr(int8_t *lb, const v4i (&rb)[LOADS], 
 template <Elem E, bool CheckedA, bool CheckedB>
 __device__ __forceinline__ void mainloop_rrr(int8_t *lds, const RowSet &as, const int8_t *b,
                                              int64_t ldb, int N, int n0, int K,
-                                             typename AccT<E>::type (&acc)[TM][TN]) {
+                                             typename AccT<E>::type (&acc)[TM][TN],
+                                             FragSums *sums = nullptr) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -299,6 +315,12 @@ __device__ __forceinline__ void mainloop_rrr(int8_t *lds, const RowSet &as, cons
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = typename AccT<E>::type{0, 0, 0, 0};
+    if constexpr (E == Elem::U8) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) sums->ra[i] = 0;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) sums->cb[j] = 0;
+    }
     const int KT = (K + BK - 1) / BK;
     v4i ra[LOADS], rb[LOADS];
 #pragma unroll
@@ -321,7 +343,7 @@ __device__ __forceinline__ void mainloop_rrr(int8_t *lds, const RowSet &as, cons
             for (int i = 0; i < LOADS; ++i) ra[i] = load_chunk<CheckedA>(as.ptr[i], (kt + 1) * BK + unit * 16, K);
             load_b_rrr<CheckedB>(rb, b, ldb, N, K, n0, (kt + 1) * BK, tid);
         }
-        compute_stage<E>(cur, cur + LDS_TILE, acc, wave_m, wave_n, lane);
+        compute_stage<E>(cur, cur + LDS_TILE, acc, wave_m, wave_n, lane, sums);
         if (more) {
             const int row0 = tid >> 3;
 #pragma unroll

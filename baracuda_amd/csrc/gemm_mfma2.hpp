@@ -73,6 +73,10 @@ __device__ __forceinline__ int lds_off(int row, int unit) { return row * BK + ((
 template <class C>
 struct PolicyI8 {
     typedef C Cfg;
+    static constexpr bool SUMS = false;   // u8 operand correction (PolicyU8RowB)
+    struct Sums {};
+    template <class F> __device__ static void fixup(F &, Sums &) {}
+
     static constexpr int TI = C::WM / 16;    // 16x16 tiles per wave along M
     static constexpr int TJ = C::WN / 16;    // ... along N
     typedef v4i Acc;
@@ -103,6 +107,10 @@ struct PolicyI8 {
 template <class C>
 struct PolicyI8x32 {
     typedef C Cfg;
+    static constexpr bool SUMS = false;   // u8 operand correction (PolicyU8RowB)
+    struct Sums {};
+    template <class F> __device__ static void fixup(F &, Sums &) {}
+
     static constexpr int TI = C::WM / 32;
     static constexpr int TJ = C::WN / 32;
     typedef v16i Acc;
@@ -138,6 +146,10 @@ struct PolicyI8x32 {
 template <class C, int FMT = 0>
 struct PolicyF8 {
     typedef C Cfg;
+    static constexpr bool SUMS = false;   // u8 operand correction (PolicyU8RowB)
+    struct Sums {};
+    template <class F> __device__ static void fixup(F &, Sums &) {}
+
     static constexpr int TI = C::WM / 32;
     static constexpr int TJ = C::WN / 32;
     typedef v16f Acc;
@@ -203,6 +215,26 @@ struct PolicyI8RowB : PolicyI8<C> {
         const v2i_t lo = ds_read_tr8(q);
         const v2i_t hi = ds_read_tr8(q + 8 * BN);
         return v4i{lo[0], lo[1], hi[0], hi[1]};
+    }
+};
+
+// u8 x u8 RRR through the signed MFMA: fragments are flipped to u - 128 and
+// the flipped bytes summed per A row (ra[i]) and B column (cb[j]) on the way
+// in; the epilogue adds 128*(row sum + column sum) + 16384*K back.
+template <class C>
+struct PolicyU8RowB : PolicyI8RowB<C> {
+    typedef PolicyI8<C> Base;
+    static constexpr bool SUMS = true;
+    struct Sums {
+        int ra[Base::TI];
+        int cb[Base::TJ];
+    };
+    template <class F>
+    __device__ static void fixup(F &f, Sums &s) {
+#pragma unroll
+        for (int t = 0; t < Base::TI; ++t) f.a[t] = u8_flip_and_sum(f.a[t], s.ra[t]);
+#pragma unroll
+        for (int t = 0; t < Base::TJ; ++t) f.b[t] = u8_flip_and_sum(f.b[t], s.cb[t]);
     }
 };
 
@@ -427,13 +459,17 @@ __device__ __forceinline__ void dma_stage(int8_t *stage, const D &d, int kbyte) 
 template <class P, class D>
 __device__ __forceinline__ void stage_step(AccTile<P> &acc, Frags<P> &f0, Frags<P> &f1,
                                            const int8_t *cur, int8_t *nxt, const D &d, int next_k,
-                                           bool has_next, int wave_m, int wave_n, int lane) {
+                                           bool has_next, int wave_m, int wave_n, int lane,
+                                           typename P::Sums &sums) {
     typedef typename P::Cfg C;
+    static_assert(!P::SUMS || C::PIPE == 0, "operand sums are wired into PIPE 0 only");
     if (has_next) dma_stage<C>(nxt, d, next_k);
     if constexpr (C::PIPE == 0) {
         load_frags<P>(f0, cur, 0, wave_m, wave_n, lane);
+        if constexpr (P::SUMS) P::fixup(f0, sums);
         mma_block<P, 0, P::TJ>(acc, f0);
         load_frags<P>(f1, cur, 1, wave_m, wave_n, lane);
+        if constexpr (P::SUMS) P::fixup(f1, sums);
         mma_block<P, 0, P::TJ>(acc, f1);
         wait_dma();        // this wave's DMA into `nxt` has landed
         __syncthreads();   // ... and every wave's; every wave is done reading `cur`
@@ -479,7 +515,8 @@ __device__ __forceinline__ void stage_step(AccTile<P> &acc, Frags<P> &f0, Frags<
 // Full K loop for one 256x256 tile.  s0 / s1 are the two stage buffers
 // (each 2 * OPER bytes: A then B).  Ends with a barrier.
 template <class P, class D>
-__device__ __forceinline__ void mainloop(int8_t *s0, int8_t *s1, const D &d, int K, AccTile<P> &acc) {
+__device__ __forceinline__ void mainloop(int8_t *s0, int8_t *s1, const D &d, int K, AccTile<P> &acc,
+                                         typename P::Sums &sums) {
     typedef typename P::Cfg C;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wave_m = wave / C::WAVES_N, wave_n = wave % C::WAVES_N;
@@ -496,10 +533,17 @@ __device__ __forceinline__ void mainloop(int8_t *s0, int8_t *s1, const D &d, int
     if constexpr (C::PIPE == 1) load_frags<P>(f0, s0, 0, wave_m, wave_n, lane);
     int kt = 0;
     for (; kt + 2 <= KT; kt += 2) {
-        stage_step<P>(acc, f0, f1, s0, s1, d, (kt + 1) * BK, true, wave_m, wave_n, lane);
-        stage_step<P>(acc, f0, f1, s1, s0, d, (kt + 2) * BK, kt + 2 < KT, wave_m, wave_n, lane);
+        stage_step<P>(acc, f0, f1, s0, s1, d, (kt + 1) * BK, true, wave_m, wave_n, lane, sums);
+        stage_step<P>(acc, f0, f1, s1, s0, d, (kt + 2) * BK, kt + 2 < KT, wave_m, wave_n, lane, sums);
     }
-    if (kt < KT) stage_step<P>(acc, f0, f1, s0, s1, d, 0, false, wave_m, wave_n, lane);
+    if (kt < KT) stage_step<P>(acc, f0, f1, s0, s1, d, 0, false, wave_m, wave_n, lane, sums);
+}
+
+template <class P, class D>
+__device__ __forceinline__ void mainloop(int8_t *s0, int8_t *s1, const D &d, int K, AccTile<P> &acc) {
+    static_assert(!P::SUMS, "this policy needs its operand sums");
+    typename P::Sums none;
+    mainloop<P>(s0, s1, d, K, acc, none);
 }
 
 // W8A8 bf16 epilogue for the int8 16x16 policy, staged through LDS so each

@@ -215,6 +215,154 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_s8_rrr_dma_kernel(S8Args p
     M2::for_each_quad<P>(acc, [&](int ml, int nl, const v4i &v) { epi(m_base + ml, n_base + nl, v); });
 }
 
+// ---- u8 x u8 RRR (B row-major [K,N]) ----------------------------------------
+// Operands flipped to s = u - 128 on the fragments; with the per-row sums of
+// A and per-column sums of B taken over the flipped values, the unsigned
+// accumulator is restored exactly modulo 2^32:
+//   sum_k u_a*u_b = acc_s + 128*(rowsum_s + colsum_s) + 16384*K_pad,
+// K_pad = the k extent of the stages run (zero-padded k contribute
+// (-128+128)*(-128+128) = 0 on the left and cancel on the right).
+// D = sat_u8(rne(act(alpha*acc_u + beta*C + bias[n]))) (gemm_u8_rrr_sm80 /
+// ..._bias semantics, baracuda_int8_rrr_sm80.cuh).
+template <bool VecOut, int ACT, typename BiasT>
+struct U8Epilogue {
+    const S8Args &p;
+    const int *rs;        // [256] tile row sums of A
+    const int *cs;        // [256] tile column sums of B
+    uint32_t kcorr;       // 16384 * K_pad (mod 2^32), added
+    __device__ __forceinline__ void operator()(int ml, int nl, const v4i &v, int m_base,
+                                               int n_base) const {
+        const int m = m_base + ml, n0 = n_base + nl;
+        if (m >= p.M || n0 >= p.N) return;
+        const int count = VecOut ? 4 : (p.N - n0 < 4 ? p.N - n0 : 4);
+        const uint32_t rsum = (uint32_t)rs[ml];
+        uint8_t *d = static_cast<uint8_t *>(p.d) + (int64_t)m * p.ldd + n0;
+        const uint8_t *c = reinterpret_cast<const uint8_t *>(p.c);
+        uint8_t o[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t au = (uint32_t)v[r] + 128u * (rsum + (uint32_t)cs[nl + r]) + kcorr;
+            float z = p.alpha * (float)(int32_t)au;
+            if (p.beta != 0.0f && c != nullptr && r < count)
+                z += p.beta * (float)c[(int64_t)m * p.ldc + n0 + r];
+            if constexpr (ACT != ACT_NONE) {
+                if (r < count) z += (float)static_cast<const BiasT *>(p.bias)[n0 + r];
+                z = activation<ACT>(z);
+            }
+            o[r] = sat_cast_u8(z);
+        }
+        if constexpr (VecOut) {
+            *reinterpret_cast<uint32_t *>(d) = (uint32_t)o[0] | ((uint32_t)o[1] << 8) |
+                                               ((uint32_t)o[2] << 16) | ((uint32_t)o[3] << 24);
+        } else {
+            for (int r = 0; r < count; ++r) d[r] = o[r];
+        }
+    }
+};
+
+// Reduce a wave's per-lane partial sums (lane groups = k-groups) and park the
+// tile's 256 row and 256 column sums in LDS.  `scratch` must be free LDS;
+// ends with a barrier.
+template <int TI_, int TJ_>
+__device__ __forceinline__ void park_sums(const int (&ra)[TI_], const int (&cb)[TJ_], int *scratch,
+                                          int wave_m, int wave_n, int wm, int wn, int lane) {
+#pragma unroll
+    for (int i = 0; i < TI_; ++i) {
+        int v = ra[i];
+        v += __shfl_xor(v, 16, 64);
+        v += __shfl_xor(v, 32, 64);
+        if (wave_n == 0 && lane < 16) scratch[wave_m * wm + i * 16 + lane] = v;
+    }
+#pragma unroll
+    for (int j = 0; j < TJ_; ++j) {
+        int v = cb[j];
+        v += __shfl_xor(v, 16, 64);
+        v += __shfl_xor(v, 32, 64);
+        if (wave_m == 0 && lane < 16) scratch[256 + wave_n * wn + j * 16 + lane] = v;
+    }
+    __syncthreads();
+}
+
+template <bool VecOut, int ACT, typename BiasT>
+__global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_u8_rrr_dma_kernel(S8Args p) {
+    namespace M2 = mfma2;
+    typedef M2::PolicyU8RowB<DmaCfg> P;
+    __shared__ __attribute__((aligned(1024))) int8_t stage0[2 * M2::OPER];
+    __shared__ __attribute__((aligned(1024))) int8_t stage1[2 * M2::OPER];
+    const int tiles_m = p.M / M2::BM, tiles_n = p.N / M2::BN;
+    int tm, tn;
+    tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int m_base = tm * M2::BM, n_base = tn * M2::BN;
+    M2::DmaRowsRrr d;
+    d.a = M2::make_dma_interior<DmaCfg>(p.a, (uint32_t)(p.M * p.lda), (int)p.lda, m_base * (int)p.lda);
+    d.b = M2::make_dma_row_b<DmaCfg>(p.b, (uint32_t)(p.K * p.ldb), (int)p.ldb, n_base);
+    M2::AccTile<P> acc;
+    typename P::Sums sums;
+#pragma unroll
+    for (int i = 0; i < P::TI; ++i) sums.ra[i] = 0;
+#pragma unroll
+    for (int j = 0; j < P::TJ; ++j) sums.cb[j] = 0;
+    M2::mainloop<P>(stage0, stage1, d, p.K, acc, sums);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int *sc = reinterpret_cast<int *>(stage0);
+    park_sums(sums.ra, sums.cb, sc, wave / DmaCfg::WAVES_N, wave % DmaCfg::WAVES_N, DmaCfg::WM,
+              DmaCfg::WN, lane);
+    const U8Epilogue<VecOut, ACT, BiasT> epi{p, sc, sc + 256, 16384u * (uint32_t)p.K};
+    M2::for_each_quad<P>(acc, [&](int ml, int nl, const v4i &v) { epi(ml, nl, v, m_base, n_base); });
+}
+
+template <bool Aligned, int ACT, typename BiasT>
+__global__ __launch_bounds__(NT, 1) void gemm_u8_rrr_kernel(S8Args p) {
+    __shared__ __attribute__((aligned(16))) int8_t lds[4 * LDS_TILE];
+    const int tiles_m = (p.M + BM - 1) / BM;
+    const int tiles_n = (p.N + BN - 1) / BN;
+    int tm, tn;
+    tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int m_base = tm * BM, n_base = tn * BN;
+    const int tid = threadIdx.x;
+    RowSet as;
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+        const int r = i * LOAD_ROWS + (tid >> 3);
+        as.ptr[i] = p.a + (int64_t)min(m_base + r, p.M - 1) * p.lda;
+    }
+    v4i acc[TM][TN];
+    FragSums sums;
+    mainloop_rrr<Elem::U8, !Aligned, !Aligned>(lds, as, p.b, p.ldb, p.N, n_base, p.K, acc, &sums);
+    const int lane = tid & 63, wave = tid >> 6;
+    int *sc = reinterpret_cast<int *>(lds);
+    park_sums(sums.ra, sums.cb, sc, wave / WAVES_N, wave % WAVES_N, WM, WN, lane);
+    const uint32_t kpad = (uint32_t)((p.K + BK - 1) / BK) * (uint32_t)BK;
+    const U8Epilogue<false, ACT, BiasT> epi{p, sc, sc + 256, 16384u * kpad};
+    for_each_fragment(acc, [&](int ml, int nl, const v4i &v) { epi(ml, nl, v, m_base, n_base); });
+}
+
+template <int ACT, typename BiasT>
+int32_t launch_u8_rrr(const S8Args &p, hipStream_t stream) {
+    const bool dma = p.K % mfma2::BK == 0 && p.M % mfma2::BM == 0 && p.N % mfma2::BN == 0 &&
+                     p.lda % 16 == 0 && p.ldb % 16 == 0 && aligned16(p.a) && aligned16(p.b) &&
+                     (int64_t)p.M * p.lda < (1ll << 31) && (int64_t)p.K * p.ldb < (1ll << 31);
+    if (dma) {
+        const int tiles = (p.M / mfma2::BM) * (p.N / mfma2::BN);
+        const bool vec = p.ldd % 4 == 0 && (reinterpret_cast<uintptr_t>(p.d) % 4) == 0;
+        if (vec)
+            hipLaunchKernelGGL((gemm_u8_rrr_dma_kernel<true, ACT, BiasT>), dim3(tiles), dim3(DmaCfg::NT), 0,
+                               stream, p);
+        else
+            hipLaunchKernelGGL((gemm_u8_rrr_dma_kernel<false, ACT, BiasT>), dim3(tiles), dim3(DmaCfg::NT), 0,
+                               stream, p);
+        return launch_status();
+    }
+    const int tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
+    const bool aligned = p.K % BK == 0 && p.N % BN == 0 && p.lda % 16 == 0 && p.ldb % 4 == 0 &&
+                         aligned16(p.a) && (reinterpret_cast<uintptr_t>(p.b) & 3u) == 0;
+    if (aligned)
+        hipLaunchKernelGGL((gemm_u8_rrr_kernel<true, ACT, BiasT>), dim3(tiles), dim3(NT), 0, stream, p);
+    else
+        hipLaunchKernelGGL((gemm_u8_rrr_kernel<false, ACT, BiasT>), dim3(tiles), dim3(NT), 0, stream, p);
+    return launch_status();
+}
+
 template <int EPI, bool VecOut, int ACT, typename BiasT>
 void launch_kernel(const S8Args &p, bool fast_k, hipStream_t stream) {
     if (fast_k) {

@@ -1,0 +1,79 @@
+// gemm_u8_rrr.hip -- u8 x u8 RRR GEMM (B row-major [K, N]) and its bias /
+// activation family for gfx950: D = sat_u8(rne(act(alpha*acc + beta*C
+// [+ bias[n]]))), acc the exact int32 sum of u8 products.
+//
+// gfx950's int8 MFMA is signed, so operands run through it as u - 128 and the
+// kernels add the row / column-sum correction back (gemm_s8_kernels.hpp).
+#include "gemm_s8_kernels.hpp"
+
+using namespace bk;
+
+extern "C" {
+
+// Same ABI as baracuda_kernels_gemm_u8_rrr_sm80_* and its bias family
+// (crates/baracuda-kernels-sys/kernels/gemm/gemm_u8_rrr_sm80.cu,
+//  gemm_u8_rrr_sm80_bias.cu; bound in crates/baracuda-kernels-sys/src/lib.rs:120-160,462-).
+static int32_t check_u8_rrr(int32_t m, int32_t n, int32_t k, int64_t lda, int64_t ldb,
+                            const void *c, int64_t ldc, int64_t ldd) {
+    if (m <= 0 || n <= 0 || k <= 0) return kInvalid;
+    if (lda < k || ldb < n || ldd < n) return kInvalid;
+    if (c != nullptr && ldc < n) return kInvalid;
+    return kOk;
+}
+
+int32_t baracuda_kernels_gemm_u8_rrr_gfx950_can_implement(
+    int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,
+    const void *c, int64_t ldc, void *d, int64_t ldd) {
+    (void)a; (void)b; (void)d;
+    return check_u8_rrr(m, n, k, lda, ldb, c, ldc, ldd);
+}
+
+size_t baracuda_kernels_gemm_u8_rrr_gfx950_workspace_size(int32_t m, int32_t n, int32_t k) {
+    (void)m; (void)n; (void)k;
+    return 0;
+}
+
+int32_t baracuda_kernels_gemm_u8_rrr_gfx950_run(
+    int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,
+    const void *c, int64_t ldc, void *d, int64_t ldd, float alpha, float beta,
+    void *workspace, size_t workspace_bytes, void *stream) {
+    (void)workspace; (void)workspace_bytes;
+    int32_t st = check_u8_rrr(m, n, k, lda, ldb, c, ldc, ldd);
+    if (st != kOk) return st;
+    if (!a || !b || !d) return kInvalid;
+    S8Args p{m, n, k, (const int8_t *)a, lda, (const int8_t *)b, ldb, (const int8_t *)c, ldc, d, ldd,
+             alpha, beta, nullptr, nullptr, nullptr};
+    return launch_u8_rrr<ACT_NONE, float>(p, (hipStream_t)stream);
+}
+
+#define BK_U8_RRR_BIAS(EPISFX, ACTV, BSFX, BTY)                                                      \
+    int32_t baracuda_kernels_gemm_u8_rrr_gfx950_##EPISFX##_##BSFX##_can_implement(                  \
+        int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,     \
+        const void *c, int64_t ldc, const void *d, int64_t ldd) {                                    \
+        (void)a; (void)b; (void)d;                                                                   \
+        return check_u8_rrr(m, n, k, lda, ldb, c, ldc, ldd);                                         \
+    }                                                                                                \
+    int32_t baracuda_kernels_gemm_u8_rrr_gfx950_##EPISFX##_##BSFX##_run(                            \
+        int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,     \
+        const void *c, int64_t ldc, void *d, int64_t ldd, const void *bias, float alpha, float beta, \
+        void *workspace, size_t workspace_bytes, void *stream) {                                     \
+        (void)workspace; (void)workspace_bytes;                                                      \
+        int32_t st = check_u8_rrr(m, n, k, lda, ldb, c, ldc, ldd);                                   \
+        if (st != kOk) return st;                                                                    \
+        if (!a || !b || !d || !bias) return kInvalid;                                                \
+        S8Args p{m, n, k, (const int8_t *)a, lda, (const int8_t *)b, ldb, (const int8_t *)c, ldc, d, \
+                 ldd, alpha, beta, nullptr, nullptr, bias};                                          \
+        return launch_u8_rrr<ACTV, BTY>(p, (hipStream_t)stream);                                     \
+    }
+
+BK_U8_RRR_BIAS(bias, ACT_BIAS, f32, float)
+BK_U8_RRR_BIAS(bias_relu, ACT_BIAS_RELU, f32, float)
+BK_U8_RRR_BIAS(bias_gelu, ACT_BIAS_GELU, f32, float)
+BK_U8_RRR_BIAS(bias_silu, ACT_BIAS_SILU, f32, float)
+BK_U8_RRR_BIAS(bias, ACT_BIAS, i32, int32_t)
+BK_U8_RRR_BIAS(bias_relu, ACT_BIAS_RELU, i32, int32_t)
+BK_U8_RRR_BIAS(bias_gelu, ACT_BIAS_GELU, i32, int32_t)
+BK_U8_RRR_BIAS(bias_silu, ACT_BIAS_SILU, i32, int32_t)
+#undef BK_U8_RRR_BIAS
+
+}  // extern "C"

@@ -50,6 +50,7 @@ class EpilogueKind(enum.Enum):
 class ElementKind(enum.Enum):
     F64 = "f64"
     S8 = "s8"
+    U8 = "u8"
     I32 = "i32"
     F32 = "f32"
     F16 = "f16"
@@ -94,7 +95,7 @@ class GemmSku:
         # types.rs:296-369: int8 accumulates in i32 and is bit-stable; the
         # gfx950 FP8 MFMA path is deterministic (fixed per-tile K order, no
         # atomics) and therefore also bit-stable on the same hardware.
-        if self.element == ElementKind.S8:
+        if self.element in (ElementKind.S8, ElementKind.U8):
             return PrecisionGuarantee(MathPrecision.Int8, ElementKind.I32, True, True)
         mp = MathPrecision.Fp8E5M2 if self.element == ElementKind.Fp8E5M2 else MathPrecision.Fp8E4M3
         return PrecisionGuarantee(mp, ElementKind.F32, True, True)
@@ -161,8 +162,9 @@ class IntGemmDescriptor:
     k: int
     layout: LayoutSku = LayoutSku.Rcr
     epilogue: EpilogueKind = EpilogueKind.Identity
-    output: ElementKind = ElementKind.S8     # S8 (reference), I32 or Bf16 (W8A8)
+    output: ElementKind = ElementKind.S8     # S8 / U8 (the element, reference), I32 or Bf16 (W8A8)
     bias_element: ElementKind = ElementKind.F32   # BiasElementKind for Bias* epilogues: F32 / I32
+    element: ElementKind = ElementKind.S8    # operand element (IntElement): S8, or U8 (RRR only)
 
 
 class IntGemmPlan:
@@ -181,6 +183,17 @@ class IntGemmPlan:
     def select(cls, desc: IntGemmDescriptor) -> "IntGemmPlan":
         if desc.m <= 0 or desc.n <= 0 or desc.k <= 0:
             raise InvalidProblem("int GEMM problem must have positive M, N, K")
+        if desc.element == ElementKind.U8:
+            # int_gemm.rs:93-101: U8 is a bespoke RRR SKU with a u8 output.
+            if desc.layout != LayoutSku.Rrr or desc.output != ElementKind.U8:
+                raise Unsupported("U8 int GEMM is RRR with a U8 output")
+            has_bias = desc.epilogue != EpilogueKind.Identity
+            if has_bias and desc.bias_element not in (ElementKind.F32, ElementKind.I32):
+                raise Unsupported(f"bias element {desc.bias_element}")
+            return cls(desc, GemmSku(ArchSku.Gfx950, desc.layout, desc.epilogue, ElementKind.U8, ElementKind.U8,
+                                     desc.bias_element if has_bias else None))
+        if desc.element != ElementKind.S8:
+            raise Unsupported(f"int GEMM element {desc.element}: S8 / U8 only")
         if desc.output not in (ElementKind.S8, ElementKind.I32, ElementKind.Bf16):
             raise Unsupported(f"int8 GEMM output {desc.output}")
         if desc.output != ElementKind.S8 and (desc.layout != LayoutSku.Rcr or
@@ -205,6 +218,10 @@ class IntGemmPlan:
         if d.output == ElementKind.Bf16:
             return getattr(L, f"gemm_w8a8_rcr_gfx950_bf16_{suffix}")
         epi, bt = d.epilogue.value, d.bias_element.value
+        if d.element == ElementKind.U8:
+            if d.epilogue == EpilogueKind.Identity:
+                return getattr(L, f"gemm_u8_rrr_gfx950_{suffix}")
+            return None if suffix == "workspace_size" else getattr(L, f"gemm_u8_rrr_gfx950_{epi}_{bt}_{suffix}")
         if d.layout == LayoutSku.Rcr:
             if d.epilogue == EpilogueKind.Identity:
                 return getattr(L, f"gemm_s8_rcr_gfx950_{suffix}")
@@ -227,10 +244,12 @@ class IntGemmPlan:
         else:
             _need(tuple(b.shape) == (desc.k, desc.n), "B shape mismatch with descriptor (K, N) (row-major)")
         _need(tuple(d.shape) == (desc.m, desc.n), "D shape mismatch with descriptor (M, N)")
-        want = {ElementKind.S8: torch.int8, ElementKind.I32: torch.int32, ElementKind.Bf16: torch.bfloat16}[desc.output]
-        _need(a.dtype == torch.int8 and b.dtype == torch.int8 and d.dtype == want, "dtype mismatch")
+        want = {ElementKind.S8: torch.int8, ElementKind.U8: torch.uint8, ElementKind.I32: torch.int32,
+                ElementKind.Bf16: torch.bfloat16}[desc.output]
+        op = torch.uint8 if desc.element == ElementKind.U8 else torch.int8
+        _need(a.dtype == op and b.dtype == op and d.dtype == want, "dtype mismatch")
         if c is not None:
-            _need(tuple(c.shape) == (desc.m, desc.n) and c.dtype == torch.int8, "C shape mismatch")
+            _need(tuple(c.shape) == (desc.m, desc.n) and c.dtype == op, "C shape mismatch")
         if desc.epilogue != EpilogueKind.Identity:
             bdt = torch.float32 if desc.bias_element == ElementKind.F32 else torch.int32
             _need(bias is not None, "Bias* epilogue needs a bias vector")
@@ -241,7 +260,7 @@ class IntGemmPlan:
             bias=None, workspace=None, stream=None) -> None:
         self.can_implement(a, b, d, c, bias)
         desc, L, s = self.desc, lib(), _stream(stream)
-        if desc.output == ElementKind.S8:
+        if desc.output in (ElementKind.S8, ElementKind.U8):
             if c is None:
                 beta = 0.0
             args = [desc.m, desc.n, desc.k, _ptr(a), _ld(a), _ptr(b), _ld(b),

@@ -206,7 +206,15 @@ def main():
                 it_ = ops / (ims * 1e-3) / 1e12
                 e[name] = {"us": round(ims * 1e3, 2), "TOPS": round(it_, 1),
                            "frac_int8_peak": round(it_ / PEAK_INT8_TOPS, 4)}
+            ua = torch.randint(0, 256, (M, K), dtype=torch.uint8, device=dev)
+            ub = torch.randint(0, 256, (K, N), dtype=torch.uint8, device=dev)
+            ud = torch.empty((M, N), dtype=torch.uint8, device=dev)
+            up = P.IntGemmPlan.select(P.IntGemmDescriptor(M, N, K, layout=P.LayoutSku.Rrr, element=P.ElementKind.U8,
+                                                          output=P.ElementKind.U8))
+            ums = time_launches(lambda: up.run(ua, ub, ud, alpha=1.0 / 65536, stream=stream), 20, 5, stream)
+            e["rrr_u8_identity"] = {"us": round(ums * 1e3, 2), "TOPS": round(ops / (ums * 1e-3) / 1e12, 1)}
             extra["int8_s8out_4096_cubed"] = e
+            del ua, ub, ud
             del ia, ib, ibr, idd
         if only in ("", "te"):
             log("bench: fp8 fused cast+amax bf16 14336x4096 -> e4m3")

@@ -186,6 +186,38 @@ BK_FP8_BIAS_DECL4(e5m2, rrr)
 #undef BK_FP8_BIAS_DECL4
 #undef BK_FP8_BIAS_DECL
 
+/* ======================= u8 GEMM, RRR layout ============================
+ * u8 x u8, int32 accumulator, D = sat_u8(rne(act(alpha*acc + beta*C [+ bias])))
+ * with C and D u8.  Replaces baracuda_kernels_gemm_u8_rrr_sm80_{run,workspace_size,
+ * can_implement} and baracuda_kernels_gemm_u8_rrr_sm80_{bias,...}_{f32,i32}_*
+ * (crates/baracuda-kernels-sys/kernels/gemm/gemm_u8_rrr_sm80{,_bias}.cu;
+ *  crates/baracuda-kernels-sys/src/lib.rs:120-160, 462-). */
+int32_t baracuda_kernels_gemm_u8_rrr_gfx950_run(
+    int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,
+    const void *c, int64_t ldc, void *d, int64_t ldd, float alpha, float beta,
+    void *workspace, size_t workspace_bytes, void *stream);
+size_t baracuda_kernels_gemm_u8_rrr_gfx950_workspace_size(int32_t m, int32_t n, int32_t k);
+int32_t baracuda_kernels_gemm_u8_rrr_gfx950_can_implement(
+    int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,
+    const void *c, int64_t ldc, void *d, int64_t ldd);
+#define BK_U8_RRR_BIAS_DECL(EPI, BIAS)                                                          \
+    int32_t baracuda_kernels_gemm_u8_rrr_gfx950_##EPI##_##BIAS##_run(                           \
+        int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb, \
+        const void *c, int64_t ldc, void *d, int64_t ldd, const void *bias, float alpha,         \
+        float beta, void *workspace, size_t workspace_bytes, void *stream);                      \
+    int32_t baracuda_kernels_gemm_u8_rrr_gfx950_##EPI##_##BIAS##_can_implement(                 \
+        int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb, \
+        const void *c, int64_t ldc, const void *d, int64_t ldd);
+BK_U8_RRR_BIAS_DECL(bias, f32)
+BK_U8_RRR_BIAS_DECL(bias_relu, f32)
+BK_U8_RRR_BIAS_DECL(bias_gelu, f32)
+BK_U8_RRR_BIAS_DECL(bias_silu, f32)
+BK_U8_RRR_BIAS_DECL(bias, i32)
+BK_U8_RRR_BIAS_DECL(bias_relu, i32)
+BK_U8_RRR_BIAS_DECL(bias_gelu, i32)
+BK_U8_RRR_BIAS_DECL(bias_silu, i32)
+#undef BK_U8_RRR_BIAS_DECL
+
 /* ======================= FP8 delayed-scaling quantizer ===================
  * Same ABI as crates/baracuda-transformer-engine-sys/csrc/baracuda_te_shim.cu
  * (bound in crates/baracuda-transformer-engine-sys/src/lib.rs:95-257).

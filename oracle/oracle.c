@@ -295,6 +295,30 @@ void bo_gemm_s8_epi(int64_t m, int64_t n, int64_t k,
         }
 }
 
+static uint8_t sat_cast_u8(float x) {
+    float r = nearbyintf(x);
+    if (r < 0.0f) r = 0.0f;
+    if (r > 255.0f) r = 255.0f;
+    return (uint8_t)(int)r;
+}
+
+void bo_gemm_u8_epi(int64_t m, int64_t n, int64_t k,
+                    const uint8_t *a, int64_t lda,
+                    const uint8_t *b, int64_t sbk, int64_t sbn,
+                    const uint8_t *c, int64_t ldc, const float *bias, int act,
+                    uint8_t *d, int64_t ldd, float alpha, float beta) {
+    for (int64_t i = 0; i < m; ++i)
+        for (int64_t j = 0; j < n; ++j) {
+            int64_t acc = 0;
+            for (int64_t kk = 0; kk < k; ++kk)
+                acc += (int64_t)a[i * lda + kk] * (int64_t)b[kk * sbk + j * sbn];
+            float z = alpha * (float)(int32_t)acc;
+            if (c != NULL) z += beta * (float)c[i * ldc + j];
+            if (bias != NULL) z += bias[j];
+            d[i * ldd + j] = sat_cast_u8(act_apply(act, z));
+        }
+}
+
 /* baracuda_quantize_compose.cuh:265-274: y = sa*sw*(float)acc, evaluated
  * left to right in f32, i.e. (sa*sw)*acc; the bf16 store is oracle.rs:397-404. */
 void bo_gemm_w8a8_rcr_bf16(int64_t m, int64_t n, int64_t k,

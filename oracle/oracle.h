@@ -77,6 +77,13 @@ void bo_gemm_s8_epi(int64_t m, int64_t n, int64_t k,
                     const int8_t *c, int64_t ldc, const float *bias, int act,
                     int8_t *d, int64_t ldd, float alpha, float beta);
 float bo_erf_as7126(float x);
+/* The same for u8 operands / C / D (gemm_u8_rrr_sm80: sat_cast_u8 = RNE +
+ * clamp to [0, 255], int8_rrr_smoke.rs:79-81). */
+void bo_gemm_u8_epi(int64_t m, int64_t n, int64_t k,
+                    const uint8_t *a, int64_t lda,
+                    const uint8_t *b, int64_t sbk, int64_t sbn,
+                    const uint8_t *c, int64_t ldc, const float *bias, int act,
+                    uint8_t *d, int64_t ldd, float alpha, float beta);
 
 /* W8A8: out = bf16( (sa[m]*sw[n]) * (f32)acc ) with f32 products. */
 void bo_gemm_w8a8_rcr_bf16(int64_t m, int64_t n, int64_t k,

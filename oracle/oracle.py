@@ -46,6 +46,8 @@ def _L():
             "bo_gemm_s8_epi": (None, [i64, i64, i64, vp, i64, vp, i64, i64, vp, i64, vp,
                                       C.c_int, vp, i64, f32, f32]),
             "bo_erf_as7126": (f32, [f32]),
+            "bo_gemm_u8_epi": (None, [i64, i64, i64, vp, i64, vp, i64, i64, vp, i64, vp,
+                                      C.c_int, vp, i64, f32, f32]),
             "bo_e5m2_to_f32": (f32, [C.c_uint8]),
             "bo_f32_to_e5m2_satfinite": (C.c_uint8, [f32]),
             "bo_gemm_fp8_f64": (None, [C.c_int, i64, i64, i64, vp, i64, vp, i64, i64, vp, i64, i64, i64, i32]),
@@ -278,6 +280,23 @@ def embedding(weight, idx, padding_idx=None) -> np.ndarray:
     _L().bo_embedding(_p(out), _p(weight), _p(idx), idx.itemsize, idx.shape[0], V, D,
                       weight.itemsize, pad)
     return out
+
+
+def gemm_u8_epi(a, b, layout, alpha, beta=0.0, c=None, bias=None, act=None) -> np.ndarray:
+    """u8 twin of gemm_s8_epi (u8 operands, C and output)."""
+    a = np.ascontiguousarray(a, dtype=np.uint8)
+    b = np.ascontiguousarray(b, dtype=np.uint8)
+    m, k = a.shape
+    if layout == "rcr":
+        n, sbk, sbn = b.shape[0], 1, k
+    else:
+        n, sbk, sbn = b.shape[1], b.shape[1], 1
+    d = np.zeros((m, n), dtype=np.uint8)
+    cp = None if c is None else np.ascontiguousarray(c, dtype=np.uint8)
+    bp = None if bias is None else np.ascontiguousarray(np.asarray(bias).astype(np.float32))
+    _L().bo_gemm_u8_epi(m, n, k, _p(a), k, _p(b), sbk, sbn, None if cp is None else _p(cp), n,
+                        None if bp is None else _p(bp), ACTS[act], _p(d), n, alpha, beta)
+    return d
 
 
 def erf_as7126(x: float) -> float:

@@ -135,3 +135,67 @@ def test_rrr_large_k_sum_identity(gpu):
     assert np.array_equal(got, want)
     rows = np.arange(0, m, 97)
     assert np.array_equal(got[rows], O.gemm_s8_epi(a[rows], b, "rrr", 1.0 / 4096))
+
+
+# ---- U8 RRR (int8_rrr_smoke.rs run_u8_smoke: a = (7i)%16, b = (11i)%14) ------
+def _run_u8(epi, bias_kind, a, b, c=None, bias=None, alpha=0.125, beta=0.0):
+    m, k = a.shape
+    n = b.shape[1]
+    plan = P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, layout=P.LayoutSku.Rrr, epilogue=epi,
+                                                    bias_element=bias_kind, element=P.ElementKind.U8,
+                                                    output=P.ElementKind.U8))
+    d = torch.full((m, n), 99, dtype=torch.uint8, device="cuda:0")
+    plan.run(dev(a), dev(b), d, c=None if c is None else dev(c), alpha=alpha, beta=beta,
+             bias=None if bias is None else dev(bias))
+    sync()
+    return d.cpu().numpy()
+
+
+@pytest.mark.parametrize("bias_kind", [P.ElementKind.F32, P.ElementKind.I32])
+@pytest.mark.parametrize("epi", EPIS)
+@pytest.mark.parametrize("shape", REF_SHAPES + [(256, 256, 128), (512, 512, 256)])
+def test_u8_reference_smoke_pattern(gpu, shape, epi, bias_kind):
+    if epi == P.EpilogueKind.Identity and bias_kind == P.ElementKind.I32:
+        pytest.skip("Identity has no bias")
+    m, n, k = shape
+    print(f"case: u8 rrr {epi.value} {bias_kind.value} {shape}", flush=True)
+    a = ((np.arange(m * k) * 7) % 16).astype(np.uint8).reshape(m, k)
+    b = ((np.arange(k * n) * 11) % 14).astype(np.uint8).reshape(k, n)
+    bias = _bias(n, bias_kind)
+    got = _run_u8(epi, bias_kind, a, b, bias=bias)
+    want = O.gemm_u8_epi(a, b, "rrr", 0.125, 0.0, None, None if epi == P.EpilogueKind.Identity else bias,
+                         ACT[epi])
+    _check(got, want, epi)
+
+
+@pytest.mark.parametrize("epi", EPIS)
+@pytest.mark.parametrize("shape", [(256, 256, 128), (512, 768, 384), (300, 520, 200), (130, 260, 1000)])
+def test_u8_full_range_with_c(gpu, shape, epi):
+    # Full-range bytes (the flipped sign bit matters) on the DMA and the
+    # general path, including a K tail (200, 1000) whose zero padding the
+    # correction accounts for.
+    m, n, k = shape
+    print(f"case: u8 random {epi.value} {shape}", flush=True)
+    g = rng(m * 3 + n + k)
+    a = g.integers(0, 256, (m, k), dtype=np.uint8)
+    b = g.integers(0, 256, (k, n), dtype=np.uint8)
+    c = g.integers(0, 256, (m, n), dtype=np.uint8)
+    bias = (g.standard_normal(n) * 30).astype(np.float32)
+    alpha = 1.0 / (64.0 * k)
+    got = _run_u8(epi, P.ElementKind.F32, a, b, c=c, bias=bias, alpha=alpha, beta=0.5)
+    want = O.gemm_u8_epi(a, b, "rrr", alpha, 0.5, c, None if epi == P.EpilogueKind.Identity else bias,
+                         ACT[epi])
+    _check(got, want, epi)
+
+
+def test_u8_large_k_exact_accumulator(gpu):
+    # alpha = 1 / 2^k-scale keeps the u8 output informative at K = 8192
+    # (acc up to 255^2 * 8192 ~ 5.3e8 < 2^31): checks the 16384*K term.
+    m, n, k = 256, 256, 8192
+    g = rng(99)
+    a = g.integers(0, 256, (m, k), dtype=np.uint8)
+    b = g.integers(0, 256, (k, n), dtype=np.uint8)
+    alpha = 255.0 / (255.0 * 255.0 * k)
+    got = _run_u8(P.EpilogueKind.Identity, P.ElementKind.F32, a, b, alpha=alpha)
+    want = O.gemm_u8_epi(a, b, "rrr", alpha)
+    assert np.array_equal(got, want)

@@ -420,3 +420,30 @@ def test_te_dequant_is_decode_times_scale_inv(fmt):
     ref = O.fp8_to_f32(b, fmt) * np.float32(0.125)
     both_nan = np.isnan(y) & np.isnan(ref)
     assert np.array_equal(y[~both_nan], ref[~both_nan])
+
+
+@pytest.mark.parametrize("act", [None, "relu", "gelu", "silu"])
+def test_gemm_u8_epi_closed_forms(act):
+    m, n, k = 37, 45, 70
+    g = rng(12)
+    a = g.integers(0, 256, (m, k), dtype=np.uint8)
+    b = g.integers(0, 256, (k, n), dtype=np.uint8)
+    c = g.integers(0, 256, (m, n), dtype=np.uint8)
+    bias = (g.standard_normal(n) * 30).astype(np.float32)
+    acc = a.astype(np.int64) @ b.astype(np.int64)
+    alpha = 1.0 / 2048
+    z = (np.float32(alpha) * acc.astype(np.float32) + np.float32(0.5) * c.astype(np.float32) + bias).astype(np.float32)
+    if act == "relu":
+        z = np.maximum(z, np.float32(0))
+    elif act == "gelu":
+        z = (np.float32(0.5) * z * (1 + np.vectorize(math.erf)(z / math.sqrt(2)))).astype(np.float32)
+    elif act == "silu":
+        z = (z / (1 + np.exp(-z.astype(np.float64)))).astype(np.float32)
+    want = np.clip(np.rint(z), 0, 255).astype(np.uint8)
+    got = O.gemm_u8_epi(a, b, "rrr", alpha, 0.5, c, bias, act)
+    assert np.array_equal(got, O.gemm_u8_epi(a, np.ascontiguousarray(b.T), "rcr", alpha, 0.5, c, bias, act))
+    diff = np.abs(got.astype(int) - want.astype(int))
+    if act in (None, "relu"):
+        assert diff.max() == 0
+    else:
+        assert diff.max() <= 1 and (diff != 0).mean() < 0.01
