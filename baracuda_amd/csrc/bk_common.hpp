@@ -170,17 +170,17 @@ __device__ __forceinline__ uint32_t f32x4_to_fp8x4_satfinite(float a, float b, f
 }
 
 // u8 -> s8 operand flip for the signed int8 MFMA: each byte u becomes
-// s = u - 128 (xor 0x80) and `sum` accumulates the flipped bytes
-// (v_dot4_i32_i8 with ones).  Summing the flipped value lets the raw one die
-// at the xor, which keeps the fragment registers from doubling.
-__device__ __forceinline__ v4i u8_flip_and_sum(const v4i &f, int &sum) {
-    v4i o;
+// s = u - 128 (xor 0x80).
+__device__ __forceinline__ v4i u8_flip(const v4i &f) {
+    return v4i{f[0] ^ (int)0x80808080u, f[1] ^ (int)0x80808080u, f[2] ^ (int)0x80808080u,
+               f[3] ^ (int)0x80808080u};
+}
+
+// Sum of the 16 raw bytes of a 16-byte chunk added to acc (v_dot4_u32_u8).
+__device__ __forceinline__ uint32_t u8_sum16(const v4i &f, uint32_t acc) {
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-        o[w] = f[w] ^ (int)0x80808080u;
-        sum = __builtin_amdgcn_sdot4(o[w], 0x01010101, sum, false);
-    }
-    return o;
+    for (int w = 0; w < 4; ++w) acc = __builtin_amdgcn_udot4((uint32_t)f[w], 0x01010101u, acc, false);
+    return acc;
 }
 
 __device__ __forceinline__ uint8_t sat_cast_u8(float x) {

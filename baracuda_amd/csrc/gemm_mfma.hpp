@@ -59,16 +59,16 @@ template <Elem E> struct AccT { typedef v4f type; };   // FP8: f32 accumulators
 template <> struct AccT<Elem::S8> { typedef v4i type; };
 template <> struct AccT<Elem::U8> { typedef v4i type; };
 
-// u8 operands through the signed int8 MFMA: each fragment word is flipped to
-// s = u - 128 (xor 0x80 per byte) and the flipped bytes are summed per row of
-// A (ra[i], tile row i of the wave) and per column of B (cb[j]) with v_dot4;
-// the epilogue restores sum(u_a*u_b) = acc_s + 128*(ra + cb) + 16384*K_pad.
-// Each lane holds partial sums over its k-group (lane / 16).
-struct FragSums {
-    int ra[TM];
-    int cb[TN];
+// u8 operands through the signed int8 MFMA: fragments are flipped to
+// s = u - 128 (xor 0x80 per byte) right before the MFMA, and once per stage
+// each wave sums the raw bytes of its slice of the LDS tile: rows
+// 32*wave .. +31 of A and of B (stored [n][k]), two lanes per row.  The
+// epilogue restores sum(u_a*u_b) = acc_s + 128*(rowsum + colsum) - 16384*K_pad
+// (zero-padded k are 0 in the raw sums and -128*-128 in acc_s).
+struct U8Sums {
+    uint32_t ra;   // raw-byte sum, A row 32*wave + lane/2, half lane%2 of each stage
+    uint32_t cb;   // the same for B row (= output column) 32*wave + lane/2
 };
-
 
 // Per-thread view of the rows this thread stages into LDS.  Each of the 4
 // loads of a stage covers row (i * 64 + tid / 8), 16-byte unit tid % 8.
@@ -125,7 +125,7 @@ template <Elem E>
 __device__ __forceinline__ void compute_stage(const int8_t *la, const int8_t *lb,
                                               typename AccT<E>::type (&acc)[TM][TN],
                                               int wave_m, int wave_n, int lane,
-                                              FragSums *sums = nullptr) {
+                                              U8Sums *sums = nullptr) {
     const int r16 = lane & 15;
     const int grp = lane >> 4;
     if constexpr (E == Elem::S8 || E == Elem::U8) {
@@ -138,16 +138,26 @@ __device__ __forceinline__ void compute_stage(const int8_t *la, const int8_t *lb
             for (int j = 0; j < TN; ++j) {
                 const int row = wave_n * WN + j * 16 + r16;
                 bf[j] = *reinterpret_cast<const v4i *>(lb + lds_off(row, unit));
-                if constexpr (E == Elem::U8) bf[j] = u8_flip_and_sum(bf[j], sums->cb[j]);
+                if constexpr (E == Elem::U8) bf[j] = u8_flip(bf[j]);
             }
 #pragma unroll
             for (int i = 0; i < TM; ++i) {
                 const int row = wave_m * WM + i * 16 + r16;
                 v4i af = *reinterpret_cast<const v4i *>(la + lds_off(row, unit));
-                if constexpr (E == Elem::U8) af = u8_flip_and_sum(af, sums->ra[i]);
+                if constexpr (E == Elem::U8) af = u8_flip(af);
 #pragma unroll
                 for (int j = 0; j < TN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[j], af, acc[i][j], 0, 0, 0);
+            }
+        }
+        if constexpr (E == Elem::U8) {
+            // Raw-byte sums of this wave's slice of the stage (fragments dead here).
+            const int row = 32 * (threadIdx.x >> 6) + (lane >> 1);
+            const int u0 = (lane & 1) * 4;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                sums->ra = u8_sum16(*reinterpret_cast<const v4i *>(la + lds_off(row, u0 + u)), sums->ra);
+                sums->cb = u8_sum16(*reinterpret_cast<const v4i *>(lb + lds_off(row, u0 + u)), sums->cb);
             }
         }
     } else {
@@ -304,7 +314,7 @@ template <Elem E, bool CheckedA, bool CheckedB>
 __device__ __forceinline__ void mainloop_rrr(int8_t *lds, const RowSet &as, const int8_t *b,
                                              int64_t ldb, int N, int n0, int K,
                                              typename AccT<E>::type (&acc)[TM][TN],
-                                             FragSums *sums = nullptr) {
+                                             U8Sums *sums = nullptr) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -315,12 +325,7 @@ __device__ __forceinline__ void mainloop_rrr(int8_t *lds, const RowSet &as, cons
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = typename AccT<E>::type{0, 0, 0, 0};
-    if constexpr (E == Elem::U8) {
-#pragma unroll
-        for (int i = 0; i < TM; ++i) sums->ra[i] = 0;
-#pragma unroll
-        for (int j = 0; j < TN; ++j) sums->cb[j] = 0;
-    }
+    if constexpr (E == Elem::U8) sums->ra = sums->cb = 0;
     const int KT = (K + BK - 1) / BK;
     v4i ra[LOADS], rb[LOADS];
 #pragma unroll

@@ -76,6 +76,7 @@ struct PolicyI8 {
     static constexpr bool SUMS = false;   // u8 operand correction (PolicyU8RowB)
     struct Sums {};
     template <class F> __device__ static void fixup(F &, Sums &) {}
+    __device__ static void stage_hook(const int8_t *, Sums &) {}
 
     static constexpr int TI = C::WM / 16;    // 16x16 tiles per wave along M
     static constexpr int TJ = C::WN / 16;    // ... along N
@@ -110,6 +111,7 @@ struct PolicyI8x32 {
     static constexpr bool SUMS = false;   // u8 operand correction (PolicyU8RowB)
     struct Sums {};
     template <class F> __device__ static void fixup(F &, Sums &) {}
+    __device__ static void stage_hook(const int8_t *, Sums &) {}
 
     static constexpr int TI = C::WM / 32;
     static constexpr int TJ = C::WN / 32;
@@ -149,6 +151,7 @@ struct PolicyF8 {
     static constexpr bool SUMS = false;   // u8 operand correction (PolicyU8RowB)
     struct Sums {};
     template <class F> __device__ static void fixup(F &, Sums &) {}
+    __device__ static void stage_hook(const int8_t *, Sums &) {}
 
     static constexpr int TI = C::WM / 32;
     static constexpr int TJ = C::WN / 32;
@@ -218,23 +221,50 @@ struct PolicyI8RowB : PolicyI8<C> {
     }
 };
 
-// u8 x u8 RRR through the signed MFMA: fragments are flipped to u - 128 and
-// the flipped bytes summed per A row (ra[i]) and B column (cb[j]) on the way
-// in; the epilogue adds 128*(row sum + column sum) + 16384*K back.
+// u8 x u8 RRR through the signed MFMA: fragments are flipped to u - 128
+// right before the MFMA (fixup); once per stage (stage_hook) each wave sums
+// the raw bytes of its slice of the freshly landed tile -- A rows
+// 32*wave .. +31 (two lanes per row, ds_read_b128) and the B columns of k-rows
+// 16*wave .. +15 (transposing reads: lane i of group g gets 8 k of column
+// 16u + i, u = g, g+4, g+8, g+12) -- so no per-fragment sums stay live
+// through the MFMA sequence.  The epilogue restores
+// sum(u_a*u_b) = acc_s + 128*(rowsum + colsum) - 16384*K.
 template <class C>
 struct PolicyU8RowB : PolicyI8RowB<C> {
     typedef PolicyI8<C> Base;
     static constexpr bool SUMS = true;
     struct Sums {
-        int ra[Base::TI];
-        int cb[Base::TJ];
+        uint32_t ra;
+        uint32_t cb[4];
     };
     template <class F>
-    __device__ static void fixup(F &f, Sums &s) {
+    __device__ static void fixup(F &f, Sums &) {
 #pragma unroll
-        for (int t = 0; t < Base::TI; ++t) f.a[t] = u8_flip_and_sum(f.a[t], s.ra[t]);
+        for (int t = 0; t < Base::TI; ++t) f.a[t] = u8_flip(f.a[t]);
 #pragma unroll
-        for (int t = 0; t < Base::TJ; ++t) f.b[t] = u8_flip_and_sum(f.b[t], s.cb[t]);
+        for (int t = 0; t < Base::TJ; ++t) f.b[t] = u8_flip(f.b[t]);
+    }
+    __device__ static void stage_hook(const int8_t *stage, Sums &s) {
+        static_assert(C::WAVES == 8, "slices assume 8 waves");
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        const int row = 32 * wave + (lane >> 1);
+        const int u0 = (lane & 1) * 4;
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            s.ra = u8_sum16(*reinterpret_cast<const v4i *>(stage + lds_off(row, u0 + u)), s.ra);
+        const int8_t *b = stage + OPER;
+        const int g = lane >> 4;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int unit = g + 4 * q;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int k = 16 * wave + 8 * h + ((lane & 15) >> 1);
+                const v2i_t v = ds_read_tr8(b + lds_off_t(k, unit) + ((lane & 1) << 3));
+                s.cb[q] = __builtin_amdgcn_udot4((uint32_t)v[0], 0x01010101u, s.cb[q], false);
+                s.cb[q] = __builtin_amdgcn_udot4((uint32_t)v[1], 0x01010101u, s.cb[q], false);
+            }
+        }
     }
 };
 
@@ -471,6 +501,8 @@ __device__ __forceinline__ void stage_step(AccTile<P> &acc, Frags<P> &f0, Frags<
         load_frags<P>(f1, cur, 1, wave_m, wave_n, lane);
         if constexpr (P::SUMS) P::fixup(f1, sums);
         mma_block<P, 0, P::TJ>(acc, f1);
+        // `cur` stays valid until the barrier below; the fragments are dead here.
+        if constexpr (P::SUMS) P::stage_hook(cur, sums);
         wait_dma();        // this wave's DMA into `nxt` has landed
         __syncthreads();   // ... and every wave's; every wave is done reading `cur`
     } else if constexpr (C::PIPE >= 2) {

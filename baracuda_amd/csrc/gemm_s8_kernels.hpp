@@ -216,20 +216,19 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_s8_rrr_dma_kernel(S8Args p
 }
 
 // ---- u8 x u8 RRR (B row-major [K,N]) ----------------------------------------
-// Operands flipped to s = u - 128 on the fragments; with the per-row sums of
-// A and per-column sums of B taken over the flipped values, the unsigned
-// accumulator is restored exactly modulo 2^32:
-//   sum_k u_a*u_b = acc_s + 128*(rowsum_s + colsum_s) + 16384*K_pad,
-// K_pad = the k extent of the stages run (zero-padded k contribute
-// (-128+128)*(-128+128) = 0 on the left and cancel on the right).
-// D = sat_u8(rne(act(alpha*acc_u + beta*C + bias[n]))) (gemm_u8_rrr_sm80 /
+// Operands run through the signed MFMA as s = u - 128; with the raw-byte sums
+// of each A row and B column the unsigned accumulator is restored exactly
+// modulo 2^32:  sum_k u_a*u_b = acc_s + 128*(rowsum + colsum) - 16384*K_pad,
+// K_pad = the k extent of the stages run (zero-padded k are 0 in the sums and
+// (-128)*(-128) in acc_s).
+// D = sat_u8(rne(act(alpha*acc + beta*C [+ bias[n]]))) (gemm_u8_rrr_sm80 /
 // ..._bias semantics, baracuda_int8_rrr_sm80.cuh).
 template <bool VecOut, int ACT, typename BiasT>
 struct U8Epilogue {
     const S8Args &p;
     const int *rs;        // [256] tile row sums of A
     const int *cs;        // [256] tile column sums of B
-    uint32_t kcorr;       // 16384 * K_pad (mod 2^32), added
+    uint32_t kcorr;       // 16384 * K_pad (mod 2^32), subtracted
     __device__ __forceinline__ void operator()(int ml, int nl, const v4i &v, int m_base,
                                                int n_base) const {
         const int m = m_base + ml, n0 = n_base + nl;
@@ -241,7 +240,7 @@ struct U8Epilogue {
         uint8_t o[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const uint32_t au = (uint32_t)v[r] + 128u * (rsum + (uint32_t)cs[nl + r]) + kcorr;
+            const uint32_t au = (uint32_t)v[r] + 128u * (rsum + (uint32_t)cs[nl + r]) - kcorr;
             float z = p.alpha * (float)(int32_t)au;
             if (p.beta != 0.0f && c != nullptr && r < count)
                 z += p.beta * (float)c[(int64_t)m * p.ldc + n0 + r];
@@ -260,27 +259,12 @@ struct U8Epilogue {
     }
 };
 
-// Reduce a wave's per-lane partial sums (lane groups = k-groups) and park the
-// tile's 256 row and 256 column sums in LDS.  `scratch` must be free LDS;
-// ends with a barrier.
-template <int TI_, int TJ_>
-__device__ __forceinline__ void park_sums(const int (&ra)[TI_], const int (&cb)[TJ_], int *scratch,
-                                          int wave_m, int wave_n, int wm, int wn, int lane) {
-#pragma unroll
-    for (int i = 0; i < TI_; ++i) {
-        int v = ra[i];
-        v += __shfl_xor(v, 16, 64);
-        v += __shfl_xor(v, 32, 64);
-        if (wave_n == 0 && lane < 16) scratch[wave_m * wm + i * 16 + lane] = v;
-    }
-#pragma unroll
-    for (int j = 0; j < TJ_; ++j) {
-        int v = cb[j];
-        v += __shfl_xor(v, 16, 64);
-        v += __shfl_xor(v, 32, 64);
-        if (wave_m == 0 && lane < 16) scratch[256 + wave_n * wn + j * 16 + lane] = v;
-    }
-    __syncthreads();
+// Row sums of a [256][*] tile slice: lanes 2r, 2r+1 of wave w hold halves of
+// row 32w + r.  Writes dst[32w + r].
+__device__ __forceinline__ void park_row_sums(uint32_t v, int *dst) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    v += __shfl_xor(v, 1, 64);
+    if ((lane & 1) == 0) dst[32 * wave + (lane >> 1)] = (int)v;
 }
 
 template <bool VecOut, int ACT, typename BiasT>
@@ -298,15 +282,26 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_u8_rrr_dma_kernel(S8Args p
     d.b = M2::make_dma_row_b<DmaCfg>(p.b, (uint32_t)(p.K * p.ldb), (int)p.ldb, n_base);
     M2::AccTile<P> acc;
     typename P::Sums sums;
+    sums.ra = 0;
 #pragma unroll
-    for (int i = 0; i < P::TI; ++i) sums.ra[i] = 0;
-#pragma unroll
-    for (int j = 0; j < P::TJ; ++j) sums.cb[j] = 0;
+    for (int q = 0; q < 4; ++q) sums.cb[q] = 0;
     M2::mainloop<P>(stage0, stage1, d, p.K, acc, sums);
+    // Park: row sums directly; column partials per wave in [8][256], then summed.
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    int *sc = reinterpret_cast<int *>(stage0);
-    park_sums(sums.ra, sums.cb, sc, wave / DmaCfg::WAVES_N, wave % DmaCfg::WAVES_N, DmaCfg::WM,
-              DmaCfg::WN, lane);
+    int *sc = reinterpret_cast<int *>(stage0);           // rs[256] | cs[256] | part[8][256]
+    park_row_sums(sums.ra, sc);
+    // Lane i of group g holds column 16*(g + 4q) + i over this wave's 16 k-rows
+    // in cb[q]: every column exactly once per wave.
+#pragma unroll
+    for (int q = 0; q < 4; ++q) sc[512 + 256 * wave + 16 * ((lane >> 4) + 4 * q) + (lane & 15)] = (int)sums.cb[q];
+    __syncthreads();
+    if (threadIdx.x < 256) {
+        int t = 0;
+#pragma unroll
+        for (int w = 0; w < 8; ++w) t += sc[512 + 256 * w + threadIdx.x];
+        sc[256 + threadIdx.x] = t;
+    }
+    __syncthreads();
     const U8Epilogue<VecOut, ACT, BiasT> epi{p, sc, sc + 256, 16384u * (uint32_t)p.K};
     M2::for_each_quad<P>(acc, [&](int ml, int nl, const v4i &v) { epi(ml, nl, v, m_base, n_base); });
 }
@@ -327,11 +322,12 @@ __global__ __launch_bounds__(NT, 1) void gemm_u8_rrr_kernel(S8Args p) {
         as.ptr[i] = p.a + (int64_t)min(m_base + r, p.M - 1) * p.lda;
     }
     v4i acc[TM][TN];
-    FragSums sums;
+    U8Sums sums;
     mainloop_rrr<Elem::U8, !Aligned, !Aligned>(lds, as, p.b, p.ldb, p.N, n_base, p.K, acc, &sums);
-    const int lane = tid & 63, wave = tid >> 6;
     int *sc = reinterpret_cast<int *>(lds);
-    park_sums(sums.ra, sums.cb, sc, wave / WAVES_N, wave % WAVES_N, WM, WN, lane);
+    park_row_sums(sums.ra, sc);
+    park_row_sums(sums.cb, sc + 256);
+    __syncthreads();
     const uint32_t kpad = (uint32_t)((p.K + BK - 1) / BK) * (uint32_t)BK;
     const U8Epilogue<false, ACT, BiasT> epi{p, sc, sc + 256, 16384u * kpad};
     for_each_fragment(acc, [&](int ml, int nl, const v4i &v) { epi(ml, nl, v, m_base, n_base); });
