@@ -28,7 +28,7 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E, GB/s
 # HBM bytes per launch measured with rocprofv3 PMC (FETCH_SIZE x2.00 and
 # WRITE_SIZE x1.00, scales calibrated on a plain device copy); the runs and
 # raw readings are in profiles/path_kernels_hbm_traffic.md.
-TRAFFIC_W8A8_4096 = 49275.6 * 1024 * 2.0 + 32768.0 * 1024 * 1.0
+TRAFFIC_W8A8_4096 = 49682.4 * 1024 * 2 + 33280.0 * 1024   # FETCH_SIZE x2 + WRITE_SIZE (KiB), profiles/path_kernels_hbm_traffic.md
 TRAFFIC_GEMV_14336x4096 = 28848.6 * 1024 * 2.0 + 56.0 * 1024 * 1.0
 
 
@@ -280,7 +280,7 @@ def main():
         "roofline": None if not ms else {
             "bound": "mfma", "achieved": round(tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
             "frac": round(tops / PEAK_INT8_TOPS, 4), "traffic": int(TRAFFIC_W8A8_4096),
-            "kernel": "gemm_s8_rcr_kernel<EPI_W8A8_BF16> (int8 tera-ops per second)"},
+            "kernel": "gemm_s8_rcr_dma_kernel<EPI_W8A8_BF16, vec> (int8 tera-ops per second)"},
         "cpu_baseline": cpu,
         "extra": extra,
     }
