@@ -169,6 +169,21 @@ __device__ __forceinline__ uint32_t f32x4_to_fp8x4_satfinite(float a, float b, f
     return w;
 }
 
+// 16-bit float MFMA operands: 8 elements = one 16-byte fragment word group.
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+
+// v_mfma_f32_16x16x32_{bf16,f16} on 16-byte fragments (srcA, srcB as raw words).
+template <bool IsBf16>
+__device__ __forceinline__ v4f mfma16x16x32_h(const v4i &a, const v4i &b, const v4f &c) {
+    if constexpr (IsBf16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                       __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                      __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+
 // u8 -> s8 operand flip for the signed int8 MFMA: each byte u becomes
 // s = u - 128 (xor 0x80).
 __device__ __forceinline__ v4i u8_flip(const v4i &f) {

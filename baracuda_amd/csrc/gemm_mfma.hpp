@@ -53,7 +53,7 @@ __device__ __forceinline__ int lds_off(int row, int unit) {
     return row * BK + ((unit ^ swz(row)) << 4);
 }
 
-enum class Elem { S8, U8, E4M3, E5M2 };
+enum class Elem { S8, U8, E4M3, E5M2, BF16, F16 };
 
 template <Elem E> struct AccT { typedef v4f type; };   // FP8: f32 accumulators
 template <> struct AccT<Elem::S8> { typedef v4i type; };
@@ -128,8 +128,9 @@ __device__ __forceinline__ void compute_stage(const int8_t *la, const int8_t *lb
                                               U8Sums *sums = nullptr) {
     const int r16 = lane & 15;
     const int grp = lane >> 4;
-    if constexpr (E == Elem::S8 || E == Elem::U8) {
-        // v_mfma_i32_16x16x64_i8: 16 bytes of K per lane, 2 sub-steps per stage.
+    if constexpr (E == Elem::S8 || E == Elem::U8 || E == Elem::BF16 || E == Elem::F16) {
+        // v_mfma_i32_16x16x64_i8 / v_mfma_f32_16x16x32_{bf16,f16}: 16 bytes of
+        // K per lane, 2 sub-steps per stage.
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
             const int unit = s * 4 + grp;
@@ -146,8 +147,12 @@ __device__ __forceinline__ void compute_stage(const int8_t *la, const int8_t *lb
                 v4i af = *reinterpret_cast<const v4i *>(la + lds_off(row, unit));
                 if constexpr (E == Elem::U8) af = u8_flip(af);
 #pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[j], af, acc[i][j], 0, 0, 0);
+                for (int j = 0; j < TN; ++j) {
+                    if constexpr (E == Elem::BF16 || E == Elem::F16)
+                        acc[i][j] = mfma16x16x32_h<E == Elem::BF16>(bf[j], af, acc[i][j]);
+                    else
+                        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[j], af, acc[i][j], 0, 0, 0);
+                }
             }
         }
         if constexpr (E == Elem::U8) {

@@ -46,17 +46,22 @@ constexpr int OPER = BM * BK;        // 32 KiB per operand per stage
 // read its fragments then issue its MFMAs (latency hidden by the other wave
 // of the SIMD); PIPE 1: two fragment register sets, the next sub-step's
 // fragments are read while the current sub-step's MFMAs run.
-template <int WAVES_M_, int WAVES_N_, int PIPE_>
+// TB: square block tile edge (256 by default; the A and B stage regions are
+// TB x BK bytes each, B at stage + OPER).
+template <int WAVES_M_, int WAVES_N_, int PIPE_, int TB_ = 256>
 struct Cfg {
     static constexpr int WAVES_M = WAVES_M_;
     static constexpr int WAVES_N = WAVES_N_;
     static constexpr int PIPE = PIPE_;
+    static constexpr int TB = TB_;
+    static constexpr int OPER = TB * BK;                    // bytes per operand per stage
     static constexpr int WAVES = WAVES_M * WAVES_N;
     static constexpr int NT = 64 * WAVES;
-    static constexpr int WM = BM / WAVES_M;
-    static constexpr int WN = BN / WAVES_N;
-    static constexpr int ROWS_PER_WAVE = BM / WAVES;       // DMA rows per wave per operand
+    static constexpr int WM = TB / WAVES_M;
+    static constexpr int WN = TB / WAVES_N;
+    static constexpr int ROWS_PER_WAVE = TB / WAVES;       // DMA rows per wave per operand
     static constexpr int DMA_PER_WAVE = ROWS_PER_WAVE / 8;  // 1 KiB DMA instructions
+    static_assert(ROWS_PER_WAVE % 8 == 0, "whole 1 KiB DMA groups per wave");
 };
 
 typedef float v16f __attribute__((ext_vector_type(16)));
@@ -98,6 +103,21 @@ struct PolicyI8 {
     template <class F>
     __device__ static void visit(const Acc &c, int i, int j, int lane, F &&f) {
         f(i * 16 + (lane & 15), j * 16 + (lane >> 4) * 4, v4i{c[0], c[1], c[2], c[3]});
+    }
+};
+
+// bf16 / f16: v_mfma_f32_16x16x32_{bf16,f16} takes the same 16 bytes of K
+// per lane as the int8 16x16x64 form, so the fragment layout, swizzle and
+// sub-step structure are PolicyI8's; only the instruction and the f32
+// accumulators differ.
+template <class C, bool IsBf16>
+struct PolicyH16 : PolicyI8<C> {
+    typedef v4f Acc;
+    __device__ static void mma(Acc &c, const v4i &b, const v4i &a, int) { c = mfma16x16x32_h<IsBf16>(b, a, c); }
+    __device__ static Acc zero() { return Acc{0.0f, 0.0f, 0.0f, 0.0f}; }
+    template <class F>
+    __device__ static void visit(const Acc &c, int i, int j, int lane, F &&f) {
+        f(i * 16 + (lane & 15), j * 16 + (lane >> 4) * 4, c);
     }
 };
 
@@ -208,6 +228,7 @@ __device__ __forceinline__ v2i_t ds_read_tr8(const int8_t *p) {
 
 template <class C>
 struct PolicyI8RowB : PolicyI8<C> {
+    static_assert(C::TB == 256, "row-major B tiles are 256 columns wide");
     typedef v4i Frag;
     __device__ static Frag load_b(const int8_t *op, int row0, int t, int s, int lane) {
         // k of this lane in sub-step 0; the sub-step (+64 rows) and the high
@@ -274,6 +295,7 @@ struct PolicyU8RowB : PolicyI8RowB<C> {
 // Rows 8q + j for q = 0, 1 share swz_t, as do q = 2, 3 (unit xor 1).
 template <class C, int FMT>
 struct PolicyF8RowB : PolicyF8<C, FMT> {
+    static_assert(C::TB == 256, "row-major B tiles are 256 columns wide");
     typedef v8i Frag;
     __device__ static Frag load_b(const int8_t *op, int row0, int t, int s, int lane) {
         const int g = lane >> 4;
@@ -303,7 +325,7 @@ template <class P>
 __device__ __forceinline__ void load_frags(Frags<P> &f, const int8_t *stage, int s, int wave_m,
                                            int wave_n, int lane) {
 #pragma unroll
-    for (int t = 0; t < P::TJ; ++t) f.b[t] = P::load_b(stage + OPER, wave_n * P::Cfg::WN, t, s, lane);
+    for (int t = 0; t < P::TJ; ++t) f.b[t] = P::load_b(stage + P::Cfg::OPER, wave_n * P::Cfg::WN, t, s, lane);
 #pragma unroll
     for (int t = 0; t < P::TI; ++t) f.a[t] = P::load(stage, wave_m * P::Cfg::WM, t, s, lane);
 }
@@ -480,7 +502,7 @@ struct DmaRows {
 template <class C, class D>
 __device__ __forceinline__ void dma_stage(int8_t *stage, const D &d, int kbyte) {
     dma_operand<C>(stage, d.a, kbyte);
-    dma_operand<C>(stage + OPER, d.b, kbyte);
+    dma_operand<C>(stage + C::OPER, d.b, kbyte);
 }
 
 // One stage: compute from `cur`, stream the next stage into `nxt` (if any).
@@ -512,7 +534,7 @@ __device__ __forceinline__ void stage_step(AccTile<P> &acc, Frags<P> &f0, Frags<
         for (int s = 0; s < 2; ++s) {
             Frags<P> &f = s ? f1 : f0;
 #pragma unroll
-            for (int t = 0; t < P::TJ; ++t) f.b[t] = P::load_b(cur + OPER, wave_n * C::WN, t, s, lane);
+            for (int t = 0; t < P::TJ; ++t) f.b[t] = P::load_b(cur + C::OPER, wave_n * C::WN, t, s, lane);
             f.a[0] = P::load(cur, wave_m * C::WM, 0, s, lane);
             if constexpr (C::PIPE == 3) __builtin_amdgcn_s_setprio(1);
 #pragma unroll

@@ -1,0 +1,367 @@
+// moe_grouped.hip -- grouped MoE expert GEMMs for gfx950, one GEMM launch
+// over all experts:
+//   int8 x int8 with the W8A8 dequant epilogue to bf16 (new SKU), and
+//   bf16 x bf16 / f16 x f16 with f32 accumulation (the reference's moe_wmma).
+//
+// Routing contract of the reference MoE path
+// (crates/baracuda-kernels-sys/kernels/moe/moe_wmma.cu:121-175,
+//  crates/baracuda-kernels-sys/kernels/include/baracuda_moe.cuh:827-944,1121-1162):
+//   sorted_token_ids[size_m]  pair ids (token*topk + slot) grouped by expert
+//   expert_ids[size_m]        expert of each sorted position
+//   expert_counts[E], expert_offsets[E+1]   caller-provided, filled here
+//   input row of pair p       = sorted_token_ids[p] / topk   (topk_weights == NULL)
+//                             = sorted_token_ids[p]          (topk_weights != NULL)
+//   output row of pair p      = sorted_token_ids[p]
+//   int8:      out[row, n] = bf16( ((sa[in_row] * sw[e*N + n]) * acc) [* topk_weights[row]] )
+//   bf16/f16:  out[row, n] = T( acc [* topk_weights[row]] )   (baracuda_moe.cuh:929-941)
+//
+// Differences by design: expert offsets are computed by one workgroup with
+// LDS counters (no global atomics, no memset: graph-capturable), and the GEMM
+// is one launch whose workgroups walk the ragged per-expert tile list.
+#include "gemm_mfma.hpp"
+#include "gemm_mfma2.hpp"
+
+namespace bk {
+namespace {
+
+using namespace mfma;
+
+constexpr int kMaxExperts = 1024;
+
+// expert_counts / expert_offsets from expert_ids (one workgroup, 1024 threads).
+__global__ __launch_bounds__(1024) void moe_offsets_kernel(const int32_t *__restrict__ expert_ids,
+                                                           int32_t size_m, int32_t num_experts,
+                                                           int32_t *__restrict__ counts,
+                                                           int32_t *__restrict__ offsets) {
+    __shared__ int32_t cnt[kMaxExperts];
+    for (int e = threadIdx.x; e < num_experts; e += blockDim.x) cnt[e] = 0;
+    __syncthreads();
+    for (int i = threadIdx.x; i < size_m; i += blockDim.x) {
+        const int e = expert_ids[i];
+        if (e >= 0 && e < num_experts) atomicAdd(&cnt[e], 1);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int run = 0;
+        offsets[0] = 0;
+        for (int e = 0; e < num_experts; ++e) {
+            counts[e] = cnt[e];
+            run += cnt[e];
+            offsets[e + 1] = run;
+        }
+    }
+}
+
+// Operand kinds: int8 (W8A8 epilogue), bf16, f16 (16-bit float elements).
+enum MoeKind : int { MOE_S8 = 0, MOE_BF16 = 1, MOE_F16 = 2 };
+
+template <int KIND> struct MoeElem;
+template <> struct MoeElem<MOE_S8> { static constexpr Elem E = Elem::S8; static constexpr int SIZE = 1; };
+template <> struct MoeElem<MOE_BF16> { static constexpr Elem E = Elem::BF16; static constexpr int SIZE = 2; };
+template <> struct MoeElem<MOE_F16> { static constexpr Elem E = Elem::F16; static constexpr int SIZE = 2; };
+
+struct MoeArgs {
+    const int8_t *x;            // [tokens, K] elements (bytes addressed)
+    const int8_t *w;            // [E, N, K]
+    const int32_t *sorted_ids;  // [size_m]
+    const int32_t *offsets;     // [E+1]
+    const float *topk_w;        // [size_m] or nullptr
+    const float *sa;            // [tokens]   (int8 only)
+    const float *sw;            // [E, N]     (int8 only)
+    uint16_t *out;              // [size_m, N] bf16 / f16
+    int E, topk, size_m, N, K;  // K in elements
+};
+
+// Ragged tile list: slot -> (expert, first pair of the tile, rows in it).
+// The E+1 offsets are loaded in one parallel step into LDS, then every thread
+// walks them from LDS (workgroup-uniform result); false past the last tile.
+__device__ __forceinline__ bool moe_tile(const MoeArgs &p, int32_t *s_off, int slot, int &e,
+                                         int &seg0, int &rows_out) {
+    for (int i = threadIdx.x; i <= p.E; i += blockDim.x) s_off[i] = min(p.offsets[i], p.size_m);
+    __syncthreads();
+    for (e = 0; e < p.E; ++e) {
+        const int o0 = s_off[e], o1 = s_off[e + 1];
+        const int rows = o1 > o0 ? o1 - o0 : 0;
+        const int tiles = (rows + 255) / 256;
+        if (slot < tiles) {
+            seg0 = o0 + slot * 256;
+            rows_out = min(256, rows - slot * 256);
+            return true;
+        }
+        slot -= tiles;
+    }
+    return false;
+}
+
+// W8A8 epilogue of one group of 4 columns of tile row ml.
+__device__ __forceinline__ void moe_store(const MoeArgs &p, const int32_t *rows_tok, int seg_rows,
+                                          int in_div, const float *swe, int ml, int n0,
+                                          const v4i &v) {
+    if (ml >= seg_rows || n0 >= p.N) return;
+    const int tok = rows_tok[ml];
+    const float sam = p.sa[tok / in_div];
+    const int count = p.N - n0 < 4 ? p.N - n0 : 4;
+    float y[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) y[r] = r < count ? (sam * swe[n0 + r]) * (float)v[r] : 0.0f;
+    if (p.topk_w) {
+        const float tw = p.topk_w[tok];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) y[r] = y[r] * tw;
+    }
+    store4_bf16(p.out + (int64_t)tok * p.N + n0, y, count == 4 && (p.N % 4 == 0), count);
+}
+
+// bf16 / f16 epilogue of one group of 4 columns: out = T(acc [* topk_w]).
+template <int KIND, class AccV>
+__device__ __forceinline__ void moe_store_h(const MoeArgs &p, const int32_t *rows_tok, int seg_rows,
+                                            int ml, int n0, const AccV &v) {
+    if (ml >= seg_rows || n0 >= p.N) return;
+    const int tok = rows_tok[ml];
+    const int count = p.N - n0 < 4 ? p.N - n0 : 4;
+    const float tw = p.topk_w ? p.topk_w[tok] : 1.0f;
+    uint16_t h[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float y = p.topk_w ? v[r] * tw : v[r];
+        h[r] = KIND == MOE_BF16 ? f32_to_bf16_rne(y) : f32_to_f16_rne(y);
+    }
+    uint16_t *d = p.out + (int64_t)tok * p.N + n0;
+    if (count == 4 && (reinterpret_cast<uintptr_t>(d) & 7u) == 0) {
+        *reinterpret_cast<v2i *>(d) = v2i{(int)((uint32_t)h[0] | ((uint32_t)h[1] << 16)),
+                                          (int)((uint32_t)h[2] | ((uint32_t)h[3] << 16))};
+    } else {
+        for (int r = 0; r < count; ++r) d[r] = h[r];
+    }
+}
+
+// General path (K tail / unaligned / N not a multiple of 256).
+template <int KIND>
+__global__ __launch_bounds__(NT, 1) void moe_grouped_kernel(MoeArgs p) {
+    constexpr int ES = MoeElem<KIND>::SIZE;
+    __shared__ __attribute__((aligned(16))) int8_t lds[4 * LDS_TILE];
+    __shared__ int32_t s_rows_tok[BM];
+    __shared__ int32_t s_off[kMaxExperts + 1];
+    int e, seg0, seg_rows;
+    if (!moe_tile(p, s_off, blockIdx.x, e, seg0, seg_rows)) return;   // whole workgroup exits
+    const int n_base = blockIdx.y * BN;
+    const int tid = threadIdx.x;
+    for (int r = tid; r < BM; r += NT) s_rows_tok[r] = p.sorted_ids[seg0 + min(r, seg_rows - 1)];
+    __syncthreads();
+    const int in_div = p.topk_w ? 1 : p.topk;
+    const int64_t kb = (int64_t)p.K * ES;   // row length in bytes
+    const int8_t *we = p.w + (int64_t)e * p.N * kb;
+    RowSet as, bs;
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+        const int r = i * LOAD_ROWS + (tid >> 3);
+        as.ptr[i] = p.x + (int64_t)(s_rows_tok[r] / in_div) * kb;
+        bs.ptr[i] = we + (int64_t)min(n_base + r, p.N - 1) * kb;
+    }
+    typename AccT<MoeElem<KIND>::E>::type acc[TM][TN];
+    mainloop<MoeElem<KIND>::E, true>(lds, as, bs, (int)kb, acc);
+    if constexpr (KIND == MOE_S8) {
+        const float *swe = p.sw + (int64_t)e * p.N;
+        for_each_fragment(acc, [&](int ml, int nl, const v4i &v) {
+            moe_store(p, s_rows_tok, seg_rows, in_div, swe, ml, n_base + nl, v);
+        });
+    } else {
+        for_each_fragment(acc, [&](int ml, int nl, const v4f &v) {
+            moe_store_h<KIND>(p, s_rows_tok, seg_rows, ml, n_base + nl, v);
+        });
+    }
+}
+
+// Fast path: K % 128 == 0, N % 256 == 0, 16-byte aligned operands.  A rows
+// are gathered per tile row (token rows of the expert's segment), B is the
+// expert's weight slab.
+typedef mfma2::Cfg<2, 4, 0> DmaCfg;
+
+// Workgroup id -> (slot, n-tile).  Workgroups are dispatched round-robin
+// over the 8 XCDs; the id is regrouped so each XCD owns a contiguous range of
+// n-tiles with every expert's m-tiles for them (slot fastest), so an expert's
+// weight panel is fetched into one XCD's L2 only.  Ids past the work exit.
+__device__ __forceinline__ bool moe_dma_coords(int pid, int total_padded, int slots, int n_tiles,
+                                               int &slot, int &ntile) {
+    constexpr int XCDS = 8;
+    const int t = (pid % XCDS) * (total_padded / XCDS) + pid / XCDS;
+    slot = t % slots;
+    ntile = t / slots;
+    return ntile < n_tiles;
+}
+
+template <int KIND> struct MoePolicy { typedef mfma2::PolicyI8<DmaCfg> type; };
+template <> struct MoePolicy<MOE_BF16> { typedef mfma2::PolicyH16<DmaCfg, true> type; };
+template <> struct MoePolicy<MOE_F16> { typedef mfma2::PolicyH16<DmaCfg, false> type; };
+
+template <int KIND>
+__global__ __launch_bounds__(DmaCfg::NT, 1) void moe_grouped_dma_kernel(MoeArgs p, int slots) {
+    namespace M2 = mfma2;
+    typedef typename MoePolicy<KIND>::type P;
+    constexpr int ES = MoeElem<KIND>::SIZE;
+    __shared__ __attribute__((aligned(1024))) int8_t stage0[2 * M2::OPER];
+    __shared__ __attribute__((aligned(1024))) int8_t stage1[2 * M2::OPER];
+    __shared__ int32_t s_rows_tok[M2::BM];
+    __shared__ int32_t s_off[kMaxExperts + 1];
+    int slot, ntile;
+    if (!moe_dma_coords(blockIdx.x, gridDim.x, slots, p.N / M2::BN, slot, ntile)) return;
+    int e, seg0, seg_rows;
+    if (!moe_tile(p, s_off, slot, e, seg0, seg_rows)) return;   // whole workgroup exits
+    const int n_base = ntile * M2::BN;
+    for (int r = threadIdx.x; r < M2::BM; r += DmaCfg::NT)
+        s_rows_tok[r] = p.sorted_ids[seg0 + min(r, seg_rows - 1)];
+    __syncthreads();
+    const int in_div = p.topk_w ? 1 : p.topk;
+    const int x_rows = p.topk_w ? p.size_m : (p.size_m + p.topk - 1) / p.topk;
+    const int kb = p.K * ES;   // row length in bytes
+    M2::DmaRows<true, false> d;
+    d.a = M2::make_dma_gathered<DmaCfg>(p.x, (uint32_t)((int64_t)x_rows * kb),
+                                        [&](int r) { return (s_rows_tok[r] / in_div) * kb; });
+    d.b = M2::make_dma_interior<DmaCfg>(p.w + (int64_t)e * p.N * kb, (uint32_t)((int64_t)p.N * kb),
+                                        kb, n_base * kb);
+    M2::AccTile<P> acc;
+    M2::mainloop<P>(stage0, stage1, d, kb, acc);
+    if constexpr (KIND != MOE_S8) {
+        M2::for_each_quad<P>(acc, [&](int ml, int nl, const v4f &v) {
+            moe_store_h<KIND>(p, s_rows_tok, seg_rows, ml, n_base + nl, v);
+        });
+        return;
+    } else {
+        // Epilogue: scales (per token row, per expert column) fetched once per
+        // lane; the wave tile is staged in LDS and written as full 128-byte rows
+        // of the token's output row; padding rows of a partial tile are skipped.
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        const int wr = (wave / DmaCfg::WAVES_N) * DmaCfg::WM;
+        const int wc = n_base + (wave % DmaCfg::WAVES_N) * DmaCfg::WN;
+        const float *swe = p.sw + (int64_t)e * p.N;
+        float sam[P::TI], post[P::TI];
+        v4f swv[P::TJ];
+#pragma unroll
+        for (int i = 0; i < P::TI; ++i) {
+            const int tok = s_rows_tok[wr + i * 16 + (lane & 15)];
+            sam[i] = p.sa[tok / in_div];
+            post[i] = p.topk_w ? p.topk_w[tok] : 1.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < P::TJ; ++j) swv[j] = *reinterpret_cast<const v4f *>(swe + wc + j * 16 + (lane >> 4) * 4);
+        int8_t *scratch = (wave < 4 ? stage0 : stage1) + (wave & 3) * (DmaCfg::WM * DmaCfg::WN * 2);
+        auto dst = [&](int r) -> uint16_t * {
+            return wr + r < seg_rows ? p.out + (int64_t)s_rows_tok[wr + r] * p.N + wc : nullptr;
+        };
+        if (p.topk_w) M2::store_w8a8_bf16_staged<P, true>(acc, scratch, sam, post, swv, dst);
+        else M2::store_w8a8_bf16_staged<P, false>(acc, scratch, sam, post, swv, dst);
+    }
+}
+
+// Offsets, then the grouped GEMM (DMA path when the problem fits it).
+template <int KIND>
+int32_t launch_moe(const MoeArgs &p, const int32_t *expert_ids, int32_t *expert_counts,
+                   bool out_ok, hipStream_t stream) {
+    constexpr int ES = MoeElem<KIND>::SIZE;
+    hipLaunchKernelGGL(moe_offsets_kernel, dim3(1), dim3(1024), 0, stream, expert_ids, p.size_m, p.E,
+                       expert_counts, const_cast<int32_t *>(p.offsets));
+    if (hipPeekAtLastError() != hipSuccess) return kLaunch;
+    // Upper bound on ragged m-tiles: sum_e ceil(cnt_e / BM) <= ceil(size_m / BM) + E.
+    const int slots = (p.size_m + BM - 1) / BM + p.E;
+    // The DMA path needs whole 128-byte K stages, N a multiple of 256, 16-byte
+    // aligned operands, byte offsets that fit 32 bits (per input / per expert
+    // slab) and what its epilogue needs (out_ok).
+    const int64_t kb = (int64_t)p.K * ES;
+    const int64_t x_rows = p.topk_w ? p.size_m : (p.size_m + p.topk - 1) / p.topk;
+    const bool fast = kb % mfma2::BK == 0 && p.N % mfma2::BN == 0 && mfma::aligned16(p.x) &&
+                      mfma::aligned16(p.w) && x_rows * kb < (1ll << 31) &&
+                      (int64_t)p.N * kb < (1ll << 31) && out_ok;
+    if (fast) {
+        const int work = slots * (p.N / mfma2::BN);
+        const int padded = (work + 7) / 8 * 8;   // whole XCD groups
+        hipLaunchKernelGGL((moe_grouped_dma_kernel<KIND>), dim3(padded), dim3(DmaCfg::NT), 0, stream, p, slots);
+    } else {
+        dim3 grid(slots, (p.N + BN - 1) / BN);
+        hipLaunchKernelGGL((moe_grouped_kernel<KIND>), grid, dim3(NT), 0, stream, p);
+    }
+    return launch_status();
+}
+
+}  // namespace
+}  // namespace bk
+
+using namespace bk;
+
+extern "C" {
+
+int32_t baracuda_kernels_moe_s8_grouped_bf16_gfx950_can_implement(
+    int32_t num_experts, int32_t topk, int32_t size_m, int32_t size_n, int32_t size_k) {
+    if (num_experts <= 0 || topk <= 0) return kInvalid;
+    if (size_m <= 0 || size_n <= 0 || size_k <= 0) return kInvalid;
+    if (topk > num_experts) return kInvalid;
+    if (num_experts > kMaxExperts) return kUnsupported;
+    return kOk;
+}
+
+size_t baracuda_kernels_moe_s8_grouped_bf16_gfx950_workspace_size(
+    int32_t num_experts, int32_t topk, int32_t size_m, int32_t size_n, int32_t size_k) {
+    (void)num_experts; (void)topk; (void)size_m; (void)size_n; (void)size_k;
+    return 0;
+}
+
+// Argument order follows baracuda_kernels_moe_wmma_bf16_run (moe_wmma.cu:154-175)
+// with the two W8A8 scale vectors inserted before the workspace.
+int32_t baracuda_kernels_moe_s8_grouped_bf16_gfx950_run(
+    const void *input, const void *weights, const int32_t *sorted_token_ids,
+    const int32_t *expert_ids, const float *topk_weights, void *output,
+    int32_t *expert_counts, int32_t *expert_offsets, int32_t num_experts, int32_t topk,
+    int32_t size_m, int32_t size_n, int32_t size_k, const float *scale_a, const float *scale_w,
+    void *workspace, size_t workspace_bytes, void *stream_ptr) {
+    (void)workspace; (void)workspace_bytes;
+    if (!input || !weights || !sorted_token_ids || !expert_ids || !output || !expert_counts ||
+        !expert_offsets || !scale_a || !scale_w)
+        return kInvalid;
+    int32_t st = baracuda_kernels_moe_s8_grouped_bf16_gfx950_can_implement(num_experts, topk, size_m,
+                                                                           size_n, size_k);
+    if (st != kOk) return st;
+    MoeArgs p{(const int8_t *)input, (const int8_t *)weights, sorted_token_ids, expert_offsets,
+              topk_weights, scale_a, scale_w, (uint16_t *)output, num_experts, topk, size_m,
+              size_n, size_k};
+    // The staged W8A8 epilogue writes 16-byte units of output rows and reads
+    // 16-byte groups of column scales.
+    return launch_moe<MOE_S8>(p, expert_ids, expert_counts,
+                              mfma::aligned16(output) && mfma::aligned16(scale_w),
+                              (hipStream_t)stream_ptr);
+}
+
+// Same ABI as baracuda_kernels_moe_wmma_{f16,bf16}_{run,can_implement}
+// (crates/baracuda-kernels-sys/kernels/moe/moe_wmma.cu:121-209): bf16 / f16
+// input [*, K] and weights [E, N, K], f32 accumulation, out[row, n] in the
+// input type; is_prefill (a tile-shape hint there) has no effect here.
+#define BK_MOE_WMMA(TAG, KIND)                                                                     \
+    int32_t baracuda_kernels_moe_wmma_##TAG##_can_implement(int32_t num_experts, int32_t topk,    \
+                                                            int32_t size_m, int32_t size_n,       \
+                                                            int32_t size_k, int32_t is_prefill) { \
+        (void)is_prefill;                                                                          \
+        return baracuda_kernels_moe_s8_grouped_bf16_gfx950_can_implement(num_experts, topk, size_m,\
+                                                                         size_n, size_k);         \
+    }                                                                                              \
+    int32_t baracuda_kernels_moe_wmma_##TAG##_run(                                                 \
+        const void *input, const void *weights, const int32_t *sorted_token_ids,                   \
+        const int32_t *expert_ids, const float *topk_weights, void *output,                        \
+        int32_t *expert_counts, int32_t *expert_offsets, int32_t num_experts, int32_t topk,        \
+        int32_t size_m, int32_t size_n, int32_t size_k, int32_t is_prefill, void *workspace,       \
+        size_t workspace_bytes, void *stream_ptr) {                                                \
+        (void)is_prefill; (void)workspace; (void)workspace_bytes;                                  \
+        if (!input || !weights || !sorted_token_ids || !expert_ids || !output || !expert_counts ||  \
+            !expert_offsets)                                                                       \
+            return kInvalid;                                                                       \
+        int32_t st = baracuda_kernels_moe_s8_grouped_bf16_gfx950_can_implement(                   \
+            num_experts, topk, size_m, size_n, size_k);                                            \
+        if (st != kOk) return st;                                                                  \
+        MoeArgs p{(const int8_t *)input, (const int8_t *)weights, sorted_token_ids, expert_offsets, \
+                  topk_weights, nullptr, nullptr, (uint16_t *)output, num_experts, topk, size_m,   \
+                  size_n, size_k};                                                                 \
+        return launch_moe<KIND>(p, expert_ids, expert_counts, true, (hipStream_t)stream_ptr);      \
+    }
+
+BK_MOE_WMMA(bf16, MOE_BF16)
+BK_MOE_WMMA(f16, MOE_F16)
+#undef BK_MOE_WMMA
+
+}  // extern "C"

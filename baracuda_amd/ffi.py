@@ -103,6 +103,10 @@ for _i in ("", "i64idx_"):
         _sig(f"baracuda_kernels_embedding_{_i}{_t}_run", i32, i64, i32, i32, i64, vp, vp, vp, vp, sz, vp)
         _sig(f"baracuda_kernels_embedding_{_i}{_t}_can_implement", i32, i64, i32, i32, i64, vp, vp, vp)
 
+for _t in ("bf16", "f16"):
+    _sig(f"baracuda_kernels_moe_wmma_{_t}_run", i32, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32,
+         i32, vp, sz, vp)
+    _sig(f"baracuda_kernels_moe_wmma_{_t}_can_implement", i32, i32, i32, i32, i32, i32, i32)
 _sig("baracuda_te_fp8_format_e4m3", i32)
 _sig("baracuda_te_fp8_format_e5m2", i32)
 _sig("baracuda_te_fp8_max_representable", f32, i32)

@@ -736,3 +736,66 @@ class Fp8DequantPlan:
         _te_check(lib().baracuda_te_dequant_run(
             _ptr(inp), _ptr(out), _ptr(recipe.scale_inv), inp.numel(), recipe.format.value,
             _TE_DTYPE[out.dtype], _stream(stream)), "Fp8DequantPlan::run")
+
+
+# ---- float MoE (moe_wmma) ----------------------------------------------------
+class MoeVariant(enum.Enum):
+    """moe/mod.rs:68-76."""
+    ScalarGguf = "scalar_gguf"
+    Wmma = "wmma"
+    WmmaGguf = "wmma_gguf"
+
+
+@dataclass(frozen=True)
+class MoeDescriptor:
+    """moe/mod.rs:80-100 MoeDescriptor (d_model = size_k, d_expert = size_n)."""
+    num_tokens: int
+    num_experts: int
+    top_k: int
+    d_model: int
+    d_expert: int
+    variant: MoeVariant = MoeVariant.Wmma
+    element: ElementKind = ElementKind.Bf16
+    is_prefill: bool = True
+
+
+class MoePlan:
+    """moe/mod.rs:218- MoePlan for the Wmma variant over bf16 / f16 experts:
+    out[sorted_token_ids[p], n] = T(sum_k x[in_row, k] * w[e, n, k] [* topk_weights])."""
+
+    def __init__(self, desc: MoeDescriptor):
+        self.desc = desc
+
+    @classmethod
+    def select(cls, desc: MoeDescriptor) -> "MoePlan":
+        if (desc.num_tokens < 0 or desc.num_experts <= 0 or desc.top_k <= 0 or desc.d_model <= 0
+                or desc.d_expert <= 0):
+            raise InvalidProblem("MoePlan: non-positive dims")
+        if desc.variant != MoeVariant.Wmma:
+            raise Unsupported("gfx950 MoePlan implements the Wmma variant (GGUF blocks are out of scope)")
+        if desc.element not in (ElementKind.Bf16, ElementKind.F16):
+            raise Unsupported("MoePlan Wmma: bf16 or f16 elements")
+        size_m = max(desc.num_tokens * desc.top_k, 1)
+        check(getattr(lib(), f"moe_wmma_{desc.element.value}_can_implement")(
+            desc.num_experts, desc.top_k, size_m, desc.d_expert, desc.d_model, int(desc.is_prefill)),
+            "MoePlan::select")
+        return cls(desc)
+
+    def workspace_size(self) -> int:
+        return 0
+
+    def run(self, x, w, sorted_token_ids, expert_ids, out, expert_counts, expert_offsets,
+            topk_weights=None, stream=None) -> None:
+        d = self.desc
+        dt = torch.bfloat16 if d.element == ElementKind.Bf16 else torch.float16
+        _need(x.dtype == dt and w.dtype == dt and out.dtype == dt, "MoePlan: element type mismatch")
+        _need(w.numel() == d.num_experts * d.d_expert * d.d_model and x.shape[-1] == d.d_model,
+              "MoePlan: shapes")
+        size_m = sorted_token_ids.numel()
+        if size_m == 0:
+            return
+        st = getattr(lib(), f"moe_wmma_{d.element.value}_run")(
+            _ptr(x), _ptr(w), _ptr(sorted_token_ids), _ptr(expert_ids), _ptr(topk_weights), _ptr(out),
+            _ptr(expert_counts), _ptr(expert_offsets), d.num_experts, d.top_k, size_m, d.d_expert,
+            d.d_model, int(d.is_prefill), None, 0, _stream(stream))
+        check(st, "MoePlan::run")

@@ -186,6 +186,16 @@ def main():
                 "us": round(mms * 1e3, 1), "TOPS": round(mt, 1), "frac_int8_peak": round(mt / PEAK_INT8_TOPS, 4),
                 "expert_rows": np.bincount(eid, minlength=E).tolist()}
             del mx, mw, mo
+            log("bench: moe grouped bf16 (moe_wmma ABI)")
+            bx = torch.randn((tokens, k), device=dev).to(torch.bfloat16)
+            bw = (torch.randn((E, n, k), device=dev) * 0.05).to(torch.bfloat16)
+            bo = torch.empty((tokens * topk, n), dtype=torch.bfloat16, device=dev)
+            bp = P.MoePlan.select(P.MoeDescriptor(tokens, E, topk, k, n, element=P.ElementKind.Bf16))
+            bms = time_launches(lambda: bp.run(bx, bw, dsid, deid, bo, cnt, off, stream=stream), 10, 3, stream)
+            bt = 2.0 * tokens * topk * n * k / (bms * 1e-3) / 1e12
+            extra["moe_wmma_bf16_e8_top2_4096x14336x4096"] = {
+                "us": round(bms * 1e3, 1), "TFLOPS": round(bt, 1), "frac_bf16_peak": round(bt / 2500.0, 4)}
+            del bx, bw, bo
         if only in ("", "int8epi"):
             log("bench: int8 s8-out RCR bias_gelu / RRR 4096^3")
             ia = torch.randint(-127, 128, (M, K), dtype=torch.int8, device=dev)

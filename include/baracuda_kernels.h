@@ -218,6 +218,26 @@ BK_U8_RRR_BIAS_DECL(bias_gelu, i32)
 BK_U8_RRR_BIAS_DECL(bias_silu, i32)
 #undef BK_U8_RRR_BIAS_DECL
 
+/* ======================= MoE grouped GEMM, bf16 / f16 (reference ABI) =====
+ * Same names and ABI as baracuda_kernels_moe_wmma_{f16,bf16}_{run,can_implement}
+ * (crates/baracuda-kernels-sys/kernels/moe/moe_wmma.cu:121-209): input
+ * [*, size_k], weights [num_experts, size_n, size_k] in the element type,
+ * f32 accumulation, out[sorted_token_ids[p], n] = T(acc [* topk_weights[...]]).
+ * expert_counts / expert_offsets are filled here; is_prefill is a hint. */
+#define BK_MOE_WMMA_DECL(TAG)                                                                   \
+    int32_t baracuda_kernels_moe_wmma_##TAG##_run(                                              \
+        const void *input, const void *weights, const int32_t *sorted_token_ids,                \
+        const int32_t *expert_ids, const float *topk_weights, void *output,                     \
+        int32_t *expert_counts, int32_t *expert_offsets, int32_t num_experts, int32_t topk,     \
+        int32_t size_m, int32_t size_n, int32_t size_k, int32_t is_prefill, void *workspace,    \
+        size_t workspace_bytes, void *stream);                                                  \
+    int32_t baracuda_kernels_moe_wmma_##TAG##_can_implement(int32_t num_experts, int32_t topk, \
+                                                            int32_t size_m, int32_t size_n,    \
+                                                            int32_t size_k, int32_t is_prefill);
+BK_MOE_WMMA_DECL(bf16)
+BK_MOE_WMMA_DECL(f16)
+#undef BK_MOE_WMMA_DECL
+
 /* ======================= FP8 delayed-scaling quantizer ===================
  * Same ABI as crates/baracuda-transformer-engine-sys/csrc/baracuda_te_shim.cu
  * (bound in crates/baracuda-transformer-engine-sys/src/lib.rs:95-257).

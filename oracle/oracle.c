@@ -524,3 +524,21 @@ void bo_moe_s8_grouped_i32(const int8_t *x, const int8_t *w,
         }
     }
 }
+
+/* baracuda_moe.cuh:827-944: the float (WMMA) MoE GEMM restated in f64. */
+void bo_moe_grouped_f64(const float *x, const float *w, const int32_t *sorted_token_ids,
+                        const int32_t *offsets, int32_t num_experts, int32_t topk,
+                        const float *topk_w, int64_t n, int64_t k, double *out) {
+    for (int32_t e = 0; e < num_experts; ++e)
+        for (int32_t p = offsets[e]; p < offsets[e + 1]; ++p) {
+            const int64_t tok = sorted_token_ids[p];
+            const int64_t in_row = topk_w ? tok : tok / topk;
+            const double tw = topk_w ? (double)topk_w[tok] : 1.0;
+            for (int64_t j = 0; j < n; ++j) {
+                double acc = 0.0;
+                for (int64_t kk = 0; kk < k; ++kk)
+                    acc += (double)x[in_row * k + kk] * (double)w[((int64_t)e * n + j) * k + kk];
+                out[tok * n + j] = acc * tw;
+            }
+        }
+}

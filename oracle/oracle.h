@@ -164,6 +164,15 @@ void bo_moe_s8_grouped_i32(const int8_t *x, const int8_t *w,
                            int32_t topk, int64_t size_m, int64_t n,
                            int64_t k, int32_t *acc_out);
 
+/* Float MoE (baracuda_moe.cuh:827-944, moe_gemm_wmma_kernel): for each
+ * segment e and pair p in it: tok = sorted_token_ids[p],
+ * in_row = topk_w ? tok : tok / topk,
+ * out[tok, n] = (topk_w ? topk_w[tok] : 1) * sum_k x[in_row,k]*w[e,n,k] in f64
+ * (inputs given as f32, decoded from bf16/f16 by the caller). */
+void bo_moe_grouped_f64(const float *x, const float *w, const int32_t *sorted_token_ids,
+                        const int32_t *offsets, int32_t num_experts, int32_t topk,
+                        const float *topk_w, int64_t n, int64_t k, double *out);
+
 #ifdef __cplusplus
 }
 #endif

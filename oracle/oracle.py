@@ -54,6 +54,7 @@ def _L():
             "bo_fp8_epilogue": (None, [C.c_int, i64, i64, vp, i64, vp, i64, vp, C.c_int, f32, f32, vp, i64]),
             "bo_te_cast_amax": (None, [vp, i64, f32, C.c_int, vp, vp]),
             "bo_te_dequant": (None, [vp, i64, f32, C.c_int, vp]),
+            "bo_moe_grouped_f64": (None, [vp, vp, vp, vp, i32, i32, vp, i64, i64, vp]),
             "bo_embedding": (None, [vp, vp, vp, i64, i64, i64, i64, i64, i64]),
             "bo_gemm_w8a8_rcr_bf16": (None, [i64, i64, i64, vp, i64, vp, i64, vp, vp, vp, i64, i64, i64, i32]),
             "bo_gemm_fp8_e4m3_rcr_f64": (None, [i64, i64, i64, vp, i64, vp, i64, vp, i64, i64, i64, i32]),
@@ -297,6 +298,20 @@ def gemm_u8_epi(a, b, layout, alpha, beta=0.0, c=None, bias=None, act=None) -> n
     _L().bo_gemm_u8_epi(m, n, k, _p(a), k, _p(b), sbk, sbn, None if cp is None else _p(cp), n,
                         None if bp is None else _p(bp), ACTS[act], _p(d), n, alpha, beta)
     return d
+
+
+def moe_grouped_f64(x_f32, w_f32, sorted_ids, offsets, topk, topk_w=None, out_rows=None) -> np.ndarray:
+    """Float MoE reference: x [rows, K], w [E, N, K] (f32 values), f64 out [out_rows, N]."""
+    x = np.ascontiguousarray(x_f32, dtype=np.float32)
+    w = np.ascontiguousarray(w_f32, dtype=np.float32)
+    sid = np.ascontiguousarray(sorted_ids, dtype=np.int32)
+    off = np.ascontiguousarray(offsets, dtype=np.int32)
+    E, n, k = w.shape
+    rows = out_rows if out_rows is not None else int(sid.max()) + 1
+    out = np.full((rows, n), np.nan)
+    tw = None if topk_w is None else np.ascontiguousarray(topk_w, dtype=np.float32)
+    _L().bo_moe_grouped_f64(_p(x), _p(w), _p(sid), _p(off), E, topk, None if tw is None else _p(tw), n, k, _p(out))
+    return out
 
 
 def erf_as7126(x: float) -> float:

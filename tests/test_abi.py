@@ -29,6 +29,9 @@ def _declared():
         for epi in ("bias", "bias_relu", "bias_gelu", "bias_silu"):
             for suf in ("run", "can_implement"):
                 names.add(f"baracuda_kernels_gemm_fp8_{enc}_{lay}_gfx950_{epi}_{suf}")
+    for tag in re.findall(r"BK_MOE_WMMA_DECL\((\w+)\)", text):
+        for suf in ("run", "can_implement"):
+            names.add(f"baracuda_kernels_moe_wmma_{tag}_{suf}")
     for tag in re.findall(r"BK_EMBED_DECL\((\w+)\)", text):
         for suf in ("run", "can_implement"):
             names.add(f"baracuda_kernels_{tag}_{suf}")
@@ -42,7 +45,7 @@ def _declared():
         for suf in ("run", "can_implement"):
             names.add(f"baracuda_kernels_gemm_s8_rrr_gfx950_{epi}_{bias}_{suf}")
     return {n for n in names if "_TAG_" not in n and "##" not in n and "_EPI_" not in n
-            and "_NAME_" not in n and "_ENC_" not in n}
+            and "_NAME_" not in n and "_ENC_" not in n and "wmma_TAG" not in n}
 
 
 def test_header_and_binding_agree():
@@ -198,6 +201,12 @@ def test_quantize_can_implement():
 
 def test_moe_can_implement():
     L = ffi.lib()
+    for t in ("bf16", "f16"):   # moe_wmma.cu:189-209
+        assert getattr(L, f"moe_wmma_{t}_can_implement")(8, 2, 64, 64, 64, 1) == 0
+        assert getattr(L, f"moe_wmma_{t}_can_implement")(2, 3, 64, 64, 64, 0) == 2
+        assert getattr(L, f"moe_wmma_{t}_can_implement")(2048, 2, 64, 64, 64, 0) == 3
+        assert getattr(L, f"moe_wmma_{t}_run")(None, None, None, None, None, None, None, None,
+                                                8, 2, 64, 64, 64, 1, None, 0, None) == 2
     # moe_wmma.cu:177-187
     assert L.moe_s8_grouped_bf16_gfx950_can_implement(8, 2, 8192, 14336, 4096) == 0
     assert L.moe_s8_grouped_bf16_gfx950_can_implement(2, 3, 16, 16, 16) == 2

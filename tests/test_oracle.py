@@ -447,3 +447,23 @@ def test_gemm_u8_epi_closed_forms(act):
         assert diff.max() == 0
     else:
         assert diff.max() <= 1 and (diff != 0).mean() < 0.01
+
+
+def test_moe_grouped_f64_against_numpy():
+    g = rng(21)
+    E, topk, tokens, n, k = 4, 2, 24, 9, 13
+    sid, eid = moe_routing(tokens, E, topk, seed=3)
+    off = np.concatenate([[0], np.cumsum(np.bincount(eid, minlength=E))]).astype(np.int32)
+    x = g.standard_normal((tokens, k)).astype(np.float32)
+    w = g.standard_normal((E, n, k)).astype(np.float32)
+    got = O.moe_grouped_f64(x, w, sid, off, topk, out_rows=tokens * topk)
+    for p in range(len(sid)):
+        tok, e = sid[p], eid[p]
+        assert np.allclose(got[tok], w[e].astype(np.float64) @ x[tok // topk].astype(np.float64), rtol=1e-12)
+    # with topk_weights the input row is the pair id and the result is scaled
+    xp = g.standard_normal((tokens * topk, k)).astype(np.float32)
+    tw = g.random(tokens * topk).astype(np.float32)
+    got = O.moe_grouped_f64(xp, w, sid, off, topk, tw, out_rows=tokens * topk)
+    for p in range(len(sid)):
+        tok, e = sid[p], eid[p]
+        assert np.allclose(got[tok], (w[e].astype(np.float64) @ xp[tok].astype(np.float64)) * tw[tok], rtol=1e-12)
