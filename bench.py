@@ -77,6 +77,71 @@ def cpu_baseline_w8a8(a, w, sa, sw, budget_s=15.0):
                       "oracle/oracle.c bo_gemm_w8a8_rcr_bf16, OpenMP"}
 
 
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baselines_extra(budget_s=4.0):
+    """The oracle on the other configs (bounded samples), same host cores:
+    config 1 serial at full size; GEMV / gather full size; FP8 on a row sample."""
+    import numpy as np
+    from oracle import oracle as O
+    from oracle.inputs import int8_uniform, rng
+    cores = cpu_cores()
+    out = {"cpu_model": cpu_model(), "cores": cores, "kind": "port"}
+    g = rng(7)
+    a, b = int8_uniform(g, (256, 256)), int8_uniform(g, (256, 256))
+    t0 = time.perf_counter()
+    O.gemm_s8_rcr_i32(a, b, nthreads=1)
+    dt = time.perf_counter() - t0
+    out["config1_int8_256_cubed_serial"] = {"s": round(dt, 4), "GOPS": round(2 * 256 ** 3 / dt / 1e9, 2),
+                                            "threads": 1}
+    n, k = 14336, 4096
+    w = int8_uniform(g, (n, k))
+    x = (g.standard_normal(k).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    reps, t0 = 0, time.perf_counter()
+    while reps < 3 or time.perf_counter() - t0 < 0.5:
+        O.gemv_s8w_m1_f64(x, w, nthreads=cores)
+        reps += 1
+    dt = (time.perf_counter() - t0) / reps
+    out["gemv_s8w_m1_14336x4096"] = {"us": round(dt * 1e6, 1), "GB_s": round((n * k + 2 * k + 6 * n) / dt / 1e9, 2)}
+    del w
+    m, n, k = 2048, 14336, 4096
+    fa = g.integers(0, 126, (m, k), dtype=np.uint8)
+    fb = g.integers(0, 126, (n, k), dtype=np.uint8)
+    t0 = time.perf_counter()
+    O.gemm_fp8_e4m3_f64(fa, fb, rows=(0, cores), nthreads=cores)
+    dt = time.perf_counter() - t0
+    rows = int(max(cores, min(m, cores * max(1, int(budget_s / max(dt, 1e-3))))))
+    t0 = time.perf_counter()
+    O.gemm_fp8_e4m3_f64(fa, fb, rows=(0, rows), nthreads=cores)
+    dt = time.perf_counter() - t0
+    out["fp8_e4m3_2048x14336x4096"] = {"TFLOPS": round(2.0 * rows * n * k / dt / 1e12, 6),
+                                       "sample_rows": rows, "s": round(dt, 2)}
+    del fa, fb
+    V, H = 128256, 4096
+    table = np.zeros((V, H), dtype=np.uint16)   # pages touched only where gathered
+    gr = {}
+    for nr in (1, 8, 64):
+        idx = g.integers(0, V, nr).astype(np.uint32)
+        reps, t0 = 0, time.perf_counter()
+        while reps < 5 or time.perf_counter() - t0 < 0.2:
+            O.gather_rows(table, idx)
+            reps += 1
+        dt = (time.perf_counter() - t0) / reps
+        gr[f"n{nr}"] = {"us": round(dt * 1e6, 2)}
+    out["gather_rows_bf16_128256x4096"] = gr
+    out["note"] = ("W8A8 is the headline cpu_baseline; the grouped MoE config is not sampled "
+                   "(its 470 MB expert slab dominates host set-up time)")
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -267,9 +332,14 @@ def main():
             del table
 
     cpu = None
+    cpu_extra = None
     if not args.no_cpu and ms is not None:
         log("bench: cpu baseline")
         cpu = cpu_baseline_w8a8(a, w, sa, sw)
+        cpu["cpu_model"] = cpu_model()
+        if not args.no_extra:
+            log("bench: cpu baselines of the other configs")
+            cpu_extra = cpu_baselines_extra()
 
     result = {
         "metric": METRIC,
@@ -292,6 +362,7 @@ def main():
             "frac": round(tops / PEAK_INT8_TOPS, 4), "traffic": int(TRAFFIC_W8A8_4096),
             "kernel": "gemm_s8_rcr_dma_kernel<EPI_W8A8_BF16, vec> (int8 tera-ops per second)"},
         "cpu_baseline": cpu,
+        "cpu_baseline_extra": cpu_extra,
         "extra": extra,
     }
     print(json.dumps(result), flush=True)
