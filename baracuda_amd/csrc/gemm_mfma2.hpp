@@ -593,9 +593,98 @@ __device__ __forceinline__ void mainloop(int8_t *s0, int8_t *s1, const D &d, int
     if (kt < KT) stage_step<P>(acc, f0, f1, s0, s1, d, 0, false, wave_m, wave_n, lane, sums);
 }
 
+// PIPE 4: one barrier per stage, placed halfway through the second
+// sub-step's MFMA rows, so the post-barrier fragment reads of the next stage
+// overlap MFMAs instead of idling the MFMA pipe.  Per stage k (buffer cur):
+//   sub-step 0: A rows streamed one ahead of the MFMA rows (B already loaded)
+//   sub-step 1: B + A rows streamed; after half of the rows every remaining
+//               A fragment of `cur` is read, then wait for this wave's DMA
+//               of stage k+1, barrier (every wave is done with `cur` and
+//               stage k+1 has landed), DMA stage k+2 into `cur`, read stage
+//               k+1's sub-step-0 B fragments, finish the MFMA rows.
+// Register peak: accumulators + one B set + half the A rows + the next B set.
+template <class P, class D>
+__device__ __forceinline__ void mainloop_p4(int8_t *s0, int8_t *s1, const D &d, int K, AccTile<P> &acc) {
+    typedef typename P::Cfg C;
+    static_assert(!P::SUMS, "operand sums are wired into PIPE 0 only");
+    constexpr int TI = P::TI, TJ = P::TJ;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wave_m = wave / C::WAVES_N, wave_n = wave % C::WAVES_N;
+    const int row_a = wave_m * C::WM, row_b = wave_n * C::WN;
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) acc[i][j] = P::zero();
+    const int KT = K / BK;
+    dma_stage<C>(s0, d, 0);
+    if (KT > 1) dma_stage<C>(s1, d, BK);
+    if (KT > 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * C::DMA_PER_WAVE) : "memory");
+    else wait_dma();
+    __syncthreads();
+    typename P::Frag bnext[TJ];
+#pragma unroll
+    for (int t = 0; t < TJ; ++t) bnext[t] = P::load_b(s0 + C::OPER, row_b, t, 0, lane);
+    auto stage = [&](int8_t *cur, int8_t *nxt, int kt) {
+        // sub-step 0
+        {
+            typename P::Frag a0 = P::load(cur, row_a, 0, 0, lane);
+#pragma unroll
+            for (int i = 0; i < TI; ++i) {
+                typename P::Frag a1;
+                if (i + 1 < TI) a1 = P::load(cur, row_a, i + 1, 0, lane);
+#pragma unroll
+                for (int h = 0; h < P::H; ++h)
+#pragma unroll
+                    for (int j = 0; j < TJ; ++j) P::mma(acc[i][j], bnext[j], a0, h);
+                if (i + 1 < TI) a0 = a1;
+            }
+        }
+        // sub-step 1
+        typename P::Frag b1[TJ];
+#pragma unroll
+        for (int t = 0; t < TJ; ++t) b1[t] = P::load_b(cur + C::OPER, row_b, t, 1, lane);
+        typename P::Frag a[TI];
+        a[0] = P::load(cur, row_a, 0, 1, lane);
+#pragma unroll
+        for (int i = 0; i < TI / 2; ++i) {
+            a[i + 1] = P::load(cur, row_a, i + 1, 1, lane);
+#pragma unroll
+            for (int h = 0; h < P::H; ++h)
+#pragma unroll
+                for (int j = 0; j < TJ; ++j) P::mma(acc[i][j], b1[j], a[i], h);
+        }
+#pragma unroll
+        for (int i = TI / 2 + 1; i < TI; ++i) a[i] = P::load(cur, row_a, i, 1, lane);
+        wait_dma();        // this wave's DMA of stage kt+1 has landed
+        __syncthreads();   // ... and every wave's; every wave has read all of `cur`
+        if (kt + 2 < KT) dma_stage<C>(cur, d, (kt + 2) * BK);
+        if (kt + 1 < KT) {
+#pragma unroll
+            for (int t = 0; t < TJ; ++t) bnext[t] = P::load_b(nxt + C::OPER, row_b, t, 0, lane);
+        }
+#pragma unroll
+        for (int i = TI / 2; i < TI; ++i)
+#pragma unroll
+            for (int h = 0; h < P::H; ++h)
+#pragma unroll
+                for (int j = 0; j < TJ; ++j) P::mma(acc[i][j], b1[j], a[i], h);
+    };
+    int kt = 0;
+    for (; kt + 2 <= KT; kt += 2) {
+        stage(s0, s1, kt);
+        stage(s1, s0, kt + 1);
+    }
+    if (kt < KT) stage(s0, s1, kt);
+    __syncthreads();   // LDS free for the caller's epilogue
+}
+
 template <class P, class D>
 __device__ __forceinline__ void mainloop(int8_t *s0, int8_t *s1, const D &d, int K, AccTile<P> &acc) {
     static_assert(!P::SUMS, "this policy needs its operand sums");
+    if constexpr (P::Cfg::PIPE == 4) {
+        mainloop_p4<P>(s0, s1, d, K, acc);
+        return;
+    }
     typename P::Sums none;
     mainloop<P>(s0, s1, d, K, acc, none);
 }
