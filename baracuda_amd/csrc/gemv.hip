@@ -167,6 +167,80 @@ __global__ __launch_bounds__(kDenseCols * kDenseSlices) void gemv_dense_m1_kerne
     }
 }
 
+// Vector path: a workgroup (16 waves) owns one 64-byte column segment (16
+// f32 or 32 f16/bf16 columns); a lane loads 16 bytes (one quad of the
+// segment) of a B row, four lanes cover the segment, so one wave instruction
+// reads 16 rows.  Wave w takes the K slice [w*per, (w+1)*per), its lanes the
+// rows k0 + r, k0 + r + 16, ... (r = lane / 4).  Partial sums are combined in
+// a fixed order -- a butterfly over the 16 row lanes, then the 16 waves in
+// LDS -- so results are bit-identical from launch to launch and independent
+// of the grid, as the reference's serial kernel's are; 4x / 8x the
+// workgroups of the scalar kernel at the same shape.  Workgroups sharing a
+// 128-byte line of B are placed on one XCD (consecutive segments per XCD).
+template <typename Tag>
+__global__ __launch_bounds__(1024) void gemv_dense_m1_vec_kernel(
+    int n, int k, float alpha, float beta, const typename Codec<Tag>::S *__restrict__ a,
+    int64_t stride_a, const typename Codec<Tag>::S *__restrict__ b, int64_t ldb, int64_t stride_b,
+    typename Codec<Tag>::S *__restrict__ d, int64_t stride_d) {
+    typedef Codec<Tag> C;
+    typedef typename C::S S;
+    constexpr int EPL = 16 / (int)sizeof(S);     // elements per 16-byte load
+    constexpr int COLS = 4 * EPL;                // columns per workgroup
+    constexpr int WAVES = 16;
+    __shared__ float part[WAVES][COLS];
+    const int slot = blockIdx.y;
+    const int nb = gridDim.x;
+    const int bx = blockIdx.x;
+    const int cb = nb % 8 == 0 ? (bx % 8) * (nb / 8) + bx / 8 : bx;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int q = lane & 3, r = lane >> 2;
+    const int col = cb * COLS + q * EPL;
+    const S *arow = a + (int64_t)slot * stride_a;
+    const S *bmat = b + (int64_t)slot * stride_b + col;
+    const int per = (k + WAVES - 1) / WAVES;
+    const int k0 = wave * per;
+    const int k1 = min(k, k0 + per);
+    float acc[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[e] = 0.0f;
+#pragma unroll 4
+    for (int kk = k0 + r; kk < k1; kk += 16) {
+        const v4i w = *reinterpret_cast<const v4i *>(bmat + (int64_t)kk * ldb);
+        const float av = C::ld(arow[kk]);
+        if constexpr (EPL == 4) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(av, __int_as_float(w[e]), acc[e]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t u = (uint32_t)w[e];
+                acc[2 * e] = __builtin_fmaf(av, C::ld((S)(u & 0xffffu)), acc[2 * e]);
+                acc[2 * e + 1] = __builtin_fmaf(av, C::ld((S)(u >> 16)), acc[2 * e + 1]);
+            }
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+#pragma unroll
+        for (int off = 4; off < 64; off <<= 1) acc[e] += __shfl_xor(acc[e], off, 64);
+    }
+    if (r == 0) {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) part[wave][q * EPL + e] = acc[e];
+    }
+    __syncthreads();
+    if (threadIdx.x < COLS) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) sum += part[w][threadIdx.x];
+        const int j = cb * COLS + threadIdx.x;
+        S *drow = d + (int64_t)slot * stride_d;
+        float out = alpha * sum;
+        if (beta != 0.0f) out += beta * C::ld(drow[j]);
+        drow[j] = C::st(out);
+    }
+}
+
 // gemv_dense.cu:101-122 gemv_validate, restated.
 int32_t gemv_validate(int32_t m, int32_t n, int32_t k, int32_t batch, int32_t layout, int64_t lda,
                       int64_t ldb, int64_t ldd, int64_t stride_d) {
@@ -190,6 +264,18 @@ int32_t launch_dense(int32_t m, int32_t n, int32_t k, int32_t batch, int32_t lay
     if (m == 0 || n == 0 || batch == 0) return kOk;
     if (!a || !b || !d) return kInvalid;
     typedef typename Codec<Tag>::S S;
+    // Vector path: whole 64-byte column segments and 16-byte aligned B rows
+    // (base, row pitch and batch stride).
+    constexpr int VCOLS = 64 / (int)sizeof(S);
+    const bool vec = n % VCOLS == 0 && ((int64_t)ldb * (int64_t)sizeof(S)) % 16 == 0 &&
+                     ((int64_t)stride_b * (int64_t)sizeof(S)) % 16 == 0 &&
+                     (reinterpret_cast<uintptr_t>(b) & 15u) == 0;
+    if (vec) {
+        hipLaunchKernelGGL((gemv_dense_m1_vec_kernel<Tag>), dim3(n / VCOLS, batch), dim3(1024), 0, stream,
+                           n, k, alpha, beta, (const S *)a, stride_a, (const S *)b, ldb, stride_b,
+                           (S *)d, stride_d);
+        return launch_status();
+    }
     dim3 grid((n + kDenseCols - 1) / kDenseCols, batch);
     hipLaunchKernelGGL((gemv_dense_m1_kernel<Tag>), grid, dim3(kDenseCols * kDenseSlices), 0, stream,
                        n, k, alpha, beta, (const S *)a, stride_a, (const S *)b, ldb, stride_b,

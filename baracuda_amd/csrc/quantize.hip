@@ -13,8 +13,9 @@
 //
 // MI355X layout: one workgroup (256 threads) per row (grid-strided), the row
 // is read once into registers with workgroup-coalesced loads (up to 64
-// elements per thread, i.e. D <= 16384), reduced with a wave butterfly + LDS,
-// quantized from registers: one HBM read of x, one write of q.  Longer rows
+// elements per thread, i.e. D <= 16384; bf16 rows as 16-byte chunks of 8),
+// reduced with a wave butterfly + LDS, quantized from registers: one HBM read
+// of x, one write of q (8-byte stores on the bf16 path).  Longer rows
 // take a two-pass loop over global memory.  Max is exact
 // in any order, so the result is bit-identical to the reference's.
 #include "bk_common.hpp"
@@ -99,6 +100,57 @@ __global__ __launch_bounds__(kQBlock) void quantize_per_token_kernel(
     }
 }
 
+// Vector path for 2-byte inputs (bf16): 16-byte loads of 8 elements, 8-byte
+// int8 stores; chunk c = tid + kQBlock * i, up to 8 chunks (64 values) per
+// thread held in registers (D <= 16384, D % 8 == 0, 16-byte aligned rows).
+template <typename S>
+__global__ __launch_bounds__(kQBlock) void quantize_per_token_bf16v_kernel(
+    const uint16_t *__restrict__ x, S *__restrict__ scale, int8_t *__restrict__ q, int N, int D,
+    int qmin, int qmax) {
+    constexpr int kChunks = kQMaxPerThread / 8;
+    __shared__ float red[kQBlock / 64];
+    const float fqmin = (float)qmin, fqmax = (float)qmax;
+    const int nch = D >> 3;
+    for (int n = blockIdx.x; n < N; n += gridDim.x) {
+        const v4i *row = reinterpret_cast<const v4i *>(x + (int64_t)n * D);
+        v4i w[kChunks];
+        float m = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kChunks; ++i) {
+            const int c = threadIdx.x + kQBlock * i;
+            w[i] = c < nch ? row[c] : v4i{0, 0, 0, 0};
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                const uint32_t u = (uint32_t)w[i][h];
+                m = fmaxf(m, fabsf(__uint_as_float(u << 16)));
+                m = fmaxf(m, fabsf(__uint_as_float(u & 0xffff0000u)));
+            }
+        }
+        const float max_abs = block_max(m, red);
+        const float s = max_abs > 0.0f ? max_abs / fqmax : 1.0f;
+        const float inv = s != 0.0f ? 1.0f / s : 0.0f;
+        if (threadIdx.x == 0) scale[n] = (S)s;
+        int8_t *qrow = q + (int64_t)n * D;
+#pragma unroll
+        for (int i = 0; i < kChunks; ++i) {
+            const int c = threadIdx.x + kQBlock * i;
+            if (c >= nch) break;
+            uint32_t lo = 0, hi = 0;
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                const uint32_t u = (uint32_t)w[i][h];
+                const uint32_t q0 = (uint8_t)quant1(__uint_as_float(u << 16), inv, fqmin, fqmax);
+                const uint32_t q1 = (uint8_t)quant1(__uint_as_float(u & 0xffff0000u), inv, fqmin, fqmax);
+                const uint32_t pair = q0 | (q1 << 8);
+                if (h < 2) lo |= pair << (16 * h);
+                else hi |= pair << (16 * (h - 2));
+            }
+            *reinterpret_cast<v2i *>(qrow + 8 * c) = v2i{(int)lo, (int)hi};
+        }
+        __syncthreads();   // `red` is reused by the next row
+    }
+}
+
 int32_t quant_check(int32_t N, int32_t D, int32_t qmin, int32_t qmax) {
     if (N < 0 || D < 0) return kInvalid;
     if (qmin > qmax) return kInvalid;
@@ -114,6 +166,16 @@ int32_t launch_quant(int32_t N, int32_t D, int32_t qmin, int32_t qmax, const voi
     if ((int64_t)N * D == 0) return kOk;
     if (!input || !scale || !output) return kInvalid;
     const int grid = N < 65535 ? N : 65535;
+    if constexpr (sizeof(T) == 2) {
+        const bool vec = D % 8 == 0 && D <= kQBlock * kQMaxPerThread &&
+                         (reinterpret_cast<uintptr_t>(input) & 15u) == 0 &&
+                         (reinterpret_cast<uintptr_t>(output) & 7u) == 0;
+        if (vec) {
+            hipLaunchKernelGGL((quantize_per_token_bf16v_kernel<S>), dim3(grid), dim3(kQBlock), 0, stream,
+                               (const uint16_t *)input, (S *)scale, (int8_t *)output, N, D, qmin, qmax);
+            return launch_status();
+        }
+    }
     hipLaunchKernelGGL((quantize_per_token_kernel<T, S>), dim3(grid), dim3(kQBlock), 0, stream,
                        (const T *)input, (S *)scale, (int8_t *)output, N, D, qmin, qmax);
     return launch_status();

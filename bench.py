@@ -159,7 +159,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",
-                    help="run only: w8a8|gemv|fp8|moe|int8epi|te|embedding|gather|copy (profiling; copy = 256 MiB "
+                    help="run only: w8a8|gemv|quant|fp8|moe|int8epi|te|embedding|gather|copy (profiling; copy = 256 MiB "
                          "device copy used to calibrate the HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -298,6 +298,42 @@ def main():
             extra["int8_s8out_4096_cubed"] = e
             del ua, ub, ud
             del ia, ib, ibr, idd
+        if only in ("", "gemv"):
+            # gemv_dense_m1 (reference ABI, RRR B[K,N]) at the reference's own skinny
+            # f32 contraction shape M=1, K=N=4096 (BASELINE adjacent figure).
+            log("bench: gemv_dense_m1 f32 / bf16 4096x4096")
+            gd = {}
+            for dt, name, es in ((torch.float32, "f32", 4), (torch.bfloat16, "bf16", 2)):
+                Kd = Nd = 4096
+                copies_d = 3 if es == 4 else 5   # > 256 MB touched per rotation
+                bmats = [torch.randn((Kd, Nd), device=dev).to(dt) for _ in range(copies_d)]
+                av = torch.randn(Kd, device=dev).to(dt)
+                dv = torch.empty(Nd, dtype=dt, device=dev)
+                dp = P.GemvDensePlan.select(P.GemvDenseDescriptor(n=Nd, k=Kd), dt)
+                itd = [0]
+
+                def gdense():
+                    dp.run(av, bmats[itd[0] % copies_d], dv, lda=Kd, stride_a=0, ldb=Nd, stride_b=0, ldd=Nd,
+                           stride_d=0, stream=stream)
+                    itd[0] += 1
+                dms = time_launches(gdense, 200, 20, stream, warm_ms=30.0)
+                nbd = Kd * Nd * es + Kd * es + Nd * es
+                gd[name] = {"us": round(dms * 1e3, 2), "GB_s": round(nbd / (dms * 1e-3) / 1e9, 1),
+                            "frac_hbm_peak": round(nbd / (dms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+                del bmats
+            extra["gemv_dense_m1_k4096_n4096"] = gd
+        if only in ("", "quant"):
+            log("bench: per-token int8 quantization bf16 4096x4096")
+            qx = torch.randn((4096, 4096), device=dev).to(torch.bfloat16)
+            qq = torch.empty((4096, 4096), dtype=torch.int8, device=dev)
+            qs = torch.empty(4096, dtype=torch.float32, device=dev)
+            qms = time_launches(lambda: P.dynamic_range_quantize_per_token_sym(qx, qs, qq, stream=stream),
+                                100, 10, stream, warm_ms=30.0)
+            qb = 4096 * 4096 * 3 + 4096 * 4
+            extra["quantize_per_token_bf16_4096x4096"] = {
+                "us": round(qms * 1e3, 2), "GB_s": round(qb / (qms * 1e-3) / 1e9, 1),
+                "frac_hbm_peak": round(qb / (qms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+            del qx, qq
         if only in ("", "te"):
             log("bench: fp8 fused cast+amax bf16 14336x4096 -> e4m3")
             tn = 14336 * 4096

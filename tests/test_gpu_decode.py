@@ -89,7 +89,8 @@ _TORCH = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
 
 
 @pytest.mark.parametrize("tag", ["f32", "f16", "bf16"])
-@pytest.mark.parametrize("case", [(4096, 4096, 1, False, 0.0), (37, 19, 3, True, 0.25), (300, 1000, 4, False, 0.5)])
+@pytest.mark.parametrize("case", [(4096, 4096, 1, False, 0.0), (37, 19, 3, True, 0.25), (300, 1000, 4, False, 0.5),
+                                  (512, 1000, 3, True, 0.25), (256, 64, 2, False, 0.5), (96, 7, 1, False, 0.0)])
 def test_gemv_dense_m1(gpu, tag, case):
     # gemv_dense_smoke.rs: f32 rel 1e-4, bf16 rel 1.6e-2 (f16 taken as 2e-3),
     # GQA broadcast (stride_b = 0), strided batch, beta, inter-slot gaps untouched.
@@ -118,6 +119,29 @@ def test_gemv_dense_m1(gpu, tag, case):
         assert np.allclose(got[sl], want[sl], rtol=rel, atol=rel * scale), gi
         gap = slice(gi * stride_d + n, (gi + 1) * stride_d)
         assert np.array_equal(got[gap], d0.double().numpy()[gap])
+
+
+@pytest.mark.parametrize("tag", ["f32", "bf16"])
+def test_gemv_dense_bit_stable_across_launches(gpu, tag):
+    # The reduction order is fixed: two launches (and a graph replay) agree bit for bit.
+    n, k = 4096, 4096
+    dt = _TORCH[tag]
+    a = torch.randn(k, device="cuda:0").to(dt)
+    b = torch.randn(k * n, device="cuda:0").to(dt)
+    plan = P.GemvDensePlan.select(P.GemvDenseDescriptor(n=n, k=k), dt)
+    outs = []
+    for _ in range(2):
+        d = torch.empty(n, dtype=dt, device="cuda:0")
+        plan.run(a, b, d, lda=k, stride_a=0, ldb=n, stride_b=0, ldd=n, stride_d=0)
+        outs.append(d)
+    dg = torch.empty(n, dtype=dt, device="cuda:0")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        plan.run(a, b, dg, lda=k, stride_a=0, ldb=n, stride_b=0, ldd=n, stride_d=0)
+    g.replay()
+    sync()
+    iv = torch.int32 if tag == "f32" else torch.int16
+    assert torch.equal(outs[0].view(iv), outs[1].view(iv)) and torch.equal(outs[0].view(iv), dg.view(iv))
 
 
 def test_gemv_dense_beta0_never_reads_d(gpu):
