@@ -29,6 +29,10 @@ using namespace mfma;
 constexpr int kMaxExperts = 1024;
 
 // expert_counts / expert_offsets from expert_ids (one workgroup, 1024 threads).
+// Up to 64 experts each wave counts 64 ids at a time with one ballot per
+// expert, lane e keeping expert e's running count, and adds its counts to
+// LDS once; more experts fall back to one LDS atomic per id.  Ids outside
+// [0, num_experts) are not counted.
 __global__ __launch_bounds__(1024) void moe_offsets_kernel(const int32_t *__restrict__ expert_ids,
                                                            int32_t size_m, int32_t num_experts,
                                                            int32_t *__restrict__ counts,
@@ -36,9 +40,23 @@ __global__ __launch_bounds__(1024) void moe_offsets_kernel(const int32_t *__rest
     __shared__ int32_t cnt[kMaxExperts];
     for (int e = threadIdx.x; e < num_experts; e += blockDim.x) cnt[e] = 0;
     __syncthreads();
-    for (int i = threadIdx.x; i < size_m; i += blockDim.x) {
-        const int e = expert_ids[i];
-        if (e >= 0 && e < num_experts) atomicAdd(&cnt[e], 1);
+    if (num_experts <= 64) {
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+        int mine = 0;   // count of expert `lane`
+        for (int base = wave * 64; base < size_m; base += waves * 64) {
+            const int i = base + lane;
+            const int e = i < size_m ? expert_ids[i] : -1;
+            for (int x = 0; x < num_experts; ++x) {
+                const int c = __popcll(__ballot(e == x));
+                if (lane == x) mine += c;
+            }
+        }
+        if (lane < num_experts && mine) atomicAdd(&cnt[lane], mine);
+    } else {
+        for (int i = threadIdx.x; i < size_m; i += blockDim.x) {
+            const int e = expert_ids[i];
+            if (e >= 0 && e < num_experts) atomicAdd(&cnt[e], 1);
+        }
     }
     __syncthreads();
     if (threadIdx.x == 0) {

@@ -83,3 +83,29 @@ def test_moe_config5_full_size_sampled(gpu):
     print("case: moe config5", flush=True)
     pairs = [0, 1, 2, 8191, 4095] + list(rng(51).integers(0, 8192, 27))
     _run(tokens=4096, E=8, topk=2, n=14336, k=4096, seed=5, pairs_check=pairs)
+
+
+@pytest.mark.parametrize("E", [1, 8, 63, 64, 65, 300])
+def test_expert_counting_any_order(gpu, E):
+    # Counts / offsets from unsorted expert ids: the ballot path (E <= 64) and
+    # the atomic path (E > 64) against the oracle's count + scan.  Ids outside
+    # [0, E) (undefined in the reference, which indexes counts with them) are
+    # skipped here; the oracle is fed the in-range ids.
+    size_m, n, k = 2000, 16, 32
+    g = rng(E)
+    expert_ids = g.integers(-2, E + 2, size_m).astype(np.int32)
+    sorted_ids = np.arange(size_m, dtype=np.int32)
+    x, w = int8_uniform(g, (size_m, k)), int8_uniform(g, (E, n, k))
+    sa = np.ones(size_m, dtype=np.float32)
+    sw = np.ones(E * n, dtype=np.float32)
+    out = torch.zeros((size_m, n), dtype=torch.bfloat16, device="cuda:0")
+    counts = torch.full((E,), -7, dtype=torch.int32, device="cuda:0")
+    offs = torch.full((E + 1,), -7, dtype=torch.int32, device="cuda:0")
+    P.MoeS8GroupedPlan.select(E, 1, size_m, n, k).run(dev(x), dev(w), dev(sorted_ids), dev(expert_ids), out,
+                                                      counts, offs, dev(sa), dev(sw))
+    sync()
+    valid = expert_ids[(expert_ids >= 0) & (expert_ids < E)]
+    c_ref, o_ref = O.moe_expert_offsets(valid, E)
+    assert np.array_equal(counts.cpu().numpy(), c_ref)
+    assert np.array_equal(offs.cpu().numpy(), o_ref)
+    assert np.array_equal(c_ref, np.bincount(valid, minlength=E))
