@@ -68,6 +68,7 @@ __device__ __forceinline__ float dot16_s8_bf16(const v4i w, const v4i xlo, const
 
 // Fast path: K % 1024 == 0, 16-byte aligned rows; one wave per workgroup
 // (finer dispatch than 4-wave groups: 11.9 vs 12.4 us at 14336 x 4096).
+// Each wave writes its two outputs with one 4-byte store.
 template <int ROWS>
 __global__ __launch_bounds__(64) void gemv_s8w_m1_kernel(
     int N, int K, const uint16_t *__restrict__ x, const int8_t *__restrict__ w, int64_t ldw,
@@ -93,10 +94,17 @@ __global__ __launch_bounds__(64) void gemv_s8w_m1_kernel(
 #pragma unroll
         for (int r = 0; r < ROWS; ++r) acc[r] = dot16_s8_bf16(wv[r], xlo, xhi, acc[r]);
     }
+    uint16_t o[ROWS];
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r) {
-        const float s = wave_sum_lane63(acc[r]);
-        if (lane == 63 && row0 + r < N) d[row0 + r] = f32_to_bf16_rne(s * scale[row0 + r]);
+    for (int r = 0; r < ROWS; ++r) o[r] = f32_to_bf16_rne(wave_sum_lane63(acc[r]) * scale[min(row0 + r, N - 1)]);
+    if (lane == 63) {
+        if (ROWS == 2 && row0 + 1 < N && (reinterpret_cast<uintptr_t>(d + row0) & 3u) == 0) {
+            *reinterpret_cast<uint32_t *>(d + row0) = (uint32_t)o[0] | ((uint32_t)o[ROWS - 1] << 16);
+        } else {
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r)
+                if (row0 + r < N) d[row0 + r] = o[r];
+        }
     }
 }
 
