@@ -148,3 +148,18 @@ def test_quantizer_feeds_fp8_gemm(gpu):
         (np.float32(ra.scale_inv_host()) * np.float32(rb.scale_inv_host()))
     got = d[:8].float().cpu().numpy()
     assert np.allclose(got, exact, rtol=2 ** -7, atol=1e-3 * np.abs(exact).max())
+
+
+def test_cast_amax_keeps_larger_slot_value(gpu):
+    # Workgroups whose max does not exceed the slot skip their atomic: a slot
+    # already above every |x| keeps its value; one below it is raised to
+    # exactly max|x|.
+    x = torch.randn(1 << 22, device="cuda:0").to(torch.bfloat16)
+    out = torch.empty(1 << 22, dtype=torch.uint8, device="cuda:0")
+    want = float(x.float().abs().max().item())
+    for start, expect in ((1000.0, 1000.0), (0.5, want), (want, want)):
+        r = _recipe("e4m3", hist=2)
+        r.amax_history.fill_(start)
+        P.Fp8CastPlan.select().run(x, out, r)
+        sync()
+        assert r.amax_history.cpu().numpy().tolist() == [expect, start]
