@@ -295,7 +295,8 @@ def _quant_gpu(x, dtype, qmin=-127, qmax=127):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.bfloat16])
-@pytest.mark.parametrize("shape", [(64, 4096), (7, 333), (3, 20000), (1, 1), (5, 16384), (9, 24)])
+@pytest.mark.parametrize("shape", [(64, 4096), (7, 333), (3, 20000), (1, 1), (5, 16384), (9, 24), (6, 8192),
+                                   (5, 8200), (13, 8)])
 def test_quantize_per_token_bit_exact(gpu, dtype, shape):
     print(f"case: quantize {dtype} {shape}", flush=True)
     g = rng(shape[0] * 31 + shape[1])
@@ -315,6 +316,14 @@ def test_quantize_many_rows_grid_stride(gpu):
         q, s, seen = _quant_gpu(x, dt, -128, 127)
         wq, ws = O.quantize_per_token_sym(seen, -128, 127)
         assert np.array_equal(q, wq) and np.array_equal(s.astype(np.float32), ws)
+
+
+def test_quantize_bf16_rows_grid_stride(gpu):
+    # bf16 16-byte-chunk path with N far above the 65535-workgroup grid.
+    x = rng(6).standard_normal((270001, 8)).astype(np.float32)
+    q, s, seen = _quant_gpu(x, torch.bfloat16)
+    wq, ws = O.quantize_per_token_sym(seen)
+    assert np.array_equal(q, wq) and np.array_equal(s.astype(np.float32), ws)
 
 
 def test_quantize_then_w8a8_matches_fp_matmul(gpu):
