@@ -305,7 +305,7 @@ def main():
             gd = {}
             for dt, name, es in ((torch.float32, "f32", 4), (torch.bfloat16, "bf16", 2)):
                 Kd = Nd = 4096
-                copies_d = 3 if es == 4 else 5   # > 256 MB touched per rotation
+                copies_d = 5 if es == 4 else 9   # 335 / 302 MB per rotation > 256 MB Infinity Cache
                 bmats = [torch.randn((Kd, Nd), device=dev).to(dt) for _ in range(copies_d)]
                 av = torch.randn(Kd, device=dev).to(dt)
                 dv = torch.empty(Nd, dtype=dt, device=dev)
@@ -319,34 +319,51 @@ def main():
                 dms = time_launches(gdense, 200, 20, stream, warm_ms=30.0)
                 nbd = Kd * Nd * es + Kd * es + Nd * es
                 gd[name] = {"us": round(dms * 1e3, 2), "GB_s": round(nbd / (dms * 1e-3) / 1e9, 1),
-                            "frac_hbm_peak": round(nbd / (dms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+                            "frac_hbm_peak": round(nbd / (dms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                            "copies_rotated": copies_d}
                 del bmats
             extra["gemv_dense_m1_k4096_n4096"] = gd
         if only in ("", "quant"):
             log("bench: per-token int8 quantization bf16 4096x4096")
-            qx = torch.randn((4096, 4096), device=dev).to(torch.bfloat16)
-            qq = torch.empty((4096, 4096), dtype=torch.int8, device=dev)
+            # 6 input/output pairs (302 MB per rotation > 256 MB Infinity Cache):
+            # every call reads and writes HBM.
+            qcop = 6
+            qxs = [torch.randn((4096, 4096), device=dev).to(torch.bfloat16) for _ in range(qcop)]
+            qqs = [torch.empty((4096, 4096), dtype=torch.int8, device=dev) for _ in range(qcop)]
             qs = torch.empty(4096, dtype=torch.float32, device=dev)
-            qms = time_launches(lambda: P.dynamic_range_quantize_per_token_sym(qx, qs, qq, stream=stream),
-                                100, 10, stream, warm_ms=30.0)
+            qit = [0]
+
+            def quant_step():
+                i = qit[0] % qcop
+                P.dynamic_range_quantize_per_token_sym(qxs[i], qs, qqs[i], stream=stream)
+                qit[0] += 1
+            qms = time_launches(quant_step, 120, 12, stream, warm_ms=30.0)
             qb = 4096 * 4096 * 3 + 4096 * 4
             extra["quantize_per_token_bf16_4096x4096"] = {
                 "us": round(qms * 1e3, 2), "GB_s": round(qb / (qms * 1e-3) / 1e9, 1),
-                "frac_hbm_peak": round(qb / (qms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
-            del qx, qq
+                "frac_hbm_peak": round(qb / (qms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4), "copies_rotated": qcop}
+            del qxs, qqs
         if only in ("", "te"):
             log("bench: fp8 fused cast+amax bf16 14336x4096 -> e4m3")
             tn = 14336 * 4096
-            tx = torch.randn(tn, device=dev).to(torch.bfloat16)
-            tq = torch.empty(tn, dtype=torch.uint8, device=dev)
+            # 2 input/output pairs (352 MB per rotation > 256 MB Infinity Cache).
+            tcop = 2
+            txs = [torch.randn(tn, device=dev).to(torch.bfloat16) for _ in range(tcop)]
+            tqs = [torch.empty(tn, dtype=torch.uint8, device=dev) for _ in range(tcop)]
             trec = P.Fp8Recipe(P.Fp8Format.E4M3, 16)
             tcast = P.Fp8CastPlan.select()
-            tms = time_launches(lambda: tcast.run(tx, tq, trec, stream=stream), 50, 10, stream, warm_ms=30.0)
+            tit = [0]
+
+            def cast_step():
+                i = tit[0] % tcop
+                tcast.run(txs[i], tqs[i], trec, stream=stream)
+                tit[0] += 1
+            tms = time_launches(cast_step, 50, 10, stream, warm_ms=30.0)
             tbytes = tn * 3
             extra["te_fp8_cast_amax_bf16_14336x4096"] = {
                 "us": round(tms * 1e3, 2), "GB_s": round(tbytes / (tms * 1e-3) / 1e9, 1),
-                "frac_hbm_peak": round(tbytes / (tms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
-            del tx, tq
+                "frac_hbm_peak": round(tbytes / (tms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4), "copies_rotated": tcop}
+            del txs, tqs
         if only in ("", "embedding"):
             log("bench: embedding V=32000 D=4096 N=1")
             e = {}
