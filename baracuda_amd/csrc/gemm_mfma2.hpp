@@ -79,6 +79,7 @@ template <class C>
 struct PolicyI8 {
     typedef C Cfg;
     static constexpr bool SUMS = false;   // u8 operand correction (PolicyU8RowB)
+    static constexpr bool FLIP = false;   // u8 operands flipped to u - 128 (PolicyU8RowB)
     struct Sums {};
     template <class F> __device__ static void fixup(F &, Sums &) {}
     __device__ static void stage_hook(const int8_t *, Sums &) {}
@@ -129,6 +130,7 @@ template <class C>
 struct PolicyI8x32 {
     typedef C Cfg;
     static constexpr bool SUMS = false;   // u8 operand correction (PolicyU8RowB)
+    static constexpr bool FLIP = false;   // u8 operands flipped to u - 128 (PolicyU8RowB)
     struct Sums {};
     template <class F> __device__ static void fixup(F &, Sums &) {}
     __device__ static void stage_hook(const int8_t *, Sums &) {}
@@ -169,6 +171,7 @@ template <class C, int FMT = 0>
 struct PolicyF8 {
     typedef C Cfg;
     static constexpr bool SUMS = false;   // u8 operand correction (PolicyU8RowB)
+    static constexpr bool FLIP = false;   // u8 operands flipped to u - 128 (PolicyU8RowB)
     struct Sums {};
     template <class F> __device__ static void fixup(F &, Sums &) {}
     __device__ static void stage_hook(const int8_t *, Sums &) {}
@@ -254,6 +257,7 @@ template <class C>
 struct PolicyU8RowB : PolicyI8RowB<C> {
     typedef PolicyI8<C> Base;
     static constexpr bool SUMS = true;
+    static constexpr bool FLIP = true;
     struct Sums {
         uint32_t ra;
         uint32_t cb[4];
@@ -514,14 +518,14 @@ __device__ __forceinline__ void stage_step(AccTile<P> &acc, Frags<P> &f0, Frags<
                                            bool has_next, int wave_m, int wave_n, int lane,
                                            typename P::Sums &sums) {
     typedef typename P::Cfg C;
-    static_assert(!P::SUMS || C::PIPE == 0, "operand sums are wired into PIPE 0 only");
+    static_assert((!P::SUMS && !P::FLIP) || C::PIPE == 0, "u8 operands are wired into PIPE 0 only");
     if (has_next) dma_stage<C>(nxt, d, next_k);
     if constexpr (C::PIPE == 0) {
         load_frags<P>(f0, cur, 0, wave_m, wave_n, lane);
-        if constexpr (P::SUMS) P::fixup(f0, sums);
+        if constexpr (P::FLIP) P::fixup(f0, sums);
         mma_block<P, 0, P::TJ>(acc, f0);
         load_frags<P>(f1, cur, 1, wave_m, wave_n, lane);
-        if constexpr (P::SUMS) P::fixup(f1, sums);
+        if constexpr (P::FLIP) P::fixup(f1, sums);
         mma_block<P, 0, P::TJ>(acc, f1);
         // `cur` stays valid until the barrier below; the fragments are dead here.
         if constexpr (P::SUMS) P::stage_hook(cur, sums);
@@ -606,7 +610,7 @@ __device__ __forceinline__ void mainloop(int8_t *s0, int8_t *s1, const D &d, int
 template <class P, class D>
 __device__ __forceinline__ void mainloop_p4(int8_t *s0, int8_t *s1, const D &d, int K, AccTile<P> &acc) {
     typedef typename P::Cfg C;
-    static_assert(!P::SUMS, "operand sums are wired into PIPE 0 only");
+    static_assert(!P::SUMS && !P::FLIP, "u8 operands are wired into PIPE 0 only");
     constexpr int TI = P::TI, TJ = P::TJ;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wave_m = wave / C::WAVES_N, wave_n = wave % C::WAVES_N;

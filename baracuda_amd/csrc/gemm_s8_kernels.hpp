@@ -306,6 +306,111 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_u8_rrr_dma_kernel(S8Args p
     M2::for_each_quad<P>(acc, [&](int ml, int nl, const v4i &v) { epi(ml, nl, v, m_base, n_base); });
 }
 
+// ---- u8 pre-pass (when the caller gives a workspace) ------------------------
+// Writes the operands flipped to u - 128 (so the GEMM is the plain s8 RRR
+// loop) and their exact int32 sums: rowsum[m] = sum_k A[m, k], colsum[n] =
+// sum_k B[k, n] (K < 2^23).  The A pass (one wave per row, udot4 over
+// 16-byte chunks) also zeroes colsum; the B pass adds K-slices of 4-column
+// groups with integer atomics (exact, so the order does not matter).
+__global__ __launch_bounds__(256) void u8_prep_a_kernel(const uint8_t *__restrict__ a, int64_t lda, int M, int K,
+                                                        int8_t *__restrict__ af, int *__restrict__ rowsum,
+                                                        int *__restrict__ colsum, int N) {
+    const int gid = blockIdx.x * 256 + threadIdx.x;
+    if (gid < N) colsum[gid] = 0;
+    const int lane = threadIdx.x & 63;
+    const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (m >= M) return;
+    const uint8_t *row = a + (int64_t)m * lda;
+    int8_t *frow = af + (int64_t)m * K;
+    uint32_t acc = 0;
+    for (int c = lane; c < (K >> 4); c += 64) {
+        const v4i w = *reinterpret_cast<const v4i *>(row + 16 * c);
+        acc = u8_sum16(w, acc);
+        *reinterpret_cast<v4i *>(frow + 16 * c) = u8_flip(w);
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) acc += (uint32_t)__shfl_xor((int)acc, off, 64);
+    if (lane == 0) rowsum[m] = (int)acc;
+}
+
+constexpr int kU8ColSlice = 256;   // K rows per B-pass workgroup (16 per thread row lane)
+
+// Workgroup: 256 columns x kU8ColSlice rows; thread (c, r) = (tid % 16,
+// tid / 16) takes the 16-byte column chunk c of rows r, r + 16, ...; the 16
+// row lanes are combined in LDS and each column gets one atomic.
+__global__ __launch_bounds__(256) void u8_prep_b_kernel(const uint8_t *__restrict__ b, int64_t ldb, int K, int N,
+                                                        int8_t *__restrict__ bf, int *__restrict__ colsum) {
+    __shared__ int part[16][257];
+    const int c = threadIdx.x & 15, r = threadIdx.x >> 4;
+    const int n = blockIdx.x * 256 + 16 * c;
+    const int k0 = blockIdx.y * kU8ColSlice, k1 = min(K, k0 + kU8ColSlice);
+    // Two 16-bit lanes per accumulator word: 16 rows of 255 fit easily.
+    uint32_t acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = 0;
+    if (n < N) {
+#pragma unroll 4
+        for (int k = k0 + r; k < k1; k += 16) {
+            const v4i w = *reinterpret_cast<const v4i *>(b + (int64_t)k * ldb + n);
+            *reinterpret_cast<v4i *>(bf + (int64_t)k * N + n) = u8_flip(w);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                acc[2 * q] += (uint32_t)w[q] & 0x00ff00ffu;
+                acc[2 * q + 1] += ((uint32_t)w[q] >> 8) & 0x00ff00ffu;
+            }
+        }
+    }
+    // column 16c + 4q + {0, 2} in acc[2q] lanes {lo, hi}; {1, 3} in acc[2q + 1]
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        part[r][16 * c + 4 * q] = (int)(acc[2 * q] & 0xffffu);
+        part[r][16 * c + 4 * q + 2] = (int)(acc[2 * q] >> 16);
+        part[r][16 * c + 4 * q + 1] = (int)(acc[2 * q + 1] & 0xffffu);
+        part[r][16 * c + 4 * q + 3] = (int)(acc[2 * q + 1] >> 16);
+    }
+    __syncthreads();
+    const int col = blockIdx.x * 256 + threadIdx.x;
+    if (col < N) {
+        int t = 0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) t += part[i][threadIdx.x];
+        atomicAdd(colsum + col, t);
+    }
+}
+
+// The LDS-DMA s8 RRR GEMM on the flipped operands (p.a / p.b point at them)
+// with the u8 epilogue over the pre-pass sums.
+template <bool VecOut, int ACT, typename BiasT>
+__global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_u8_rrr_ws_kernel(S8Args p, const int *__restrict__ rowsum,
+                                                                       const int *__restrict__ colsum) {
+    namespace M2 = mfma2;
+    typedef M2::PolicyI8RowB<DmaCfg> P;
+    __shared__ __attribute__((aligned(1024))) int8_t stage0[2 * M2::OPER];
+    __shared__ __attribute__((aligned(1024))) int8_t stage1[2 * M2::OPER];
+    const int tiles_m = p.M / M2::BM, tiles_n = p.N / M2::BN;
+    int tm, tn;
+    tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int m_base = tm * M2::BM, n_base = tn * M2::BN;
+    M2::DmaRowsRrr d;
+    d.a = M2::make_dma_interior<DmaCfg>(p.a, (uint32_t)(p.M * p.lda), (int)p.lda, m_base * (int)p.lda);
+    d.b = M2::make_dma_row_b<DmaCfg>(p.b, (uint32_t)(p.K * p.ldb), (int)p.ldb, n_base);
+    M2::AccTile<P> acc;
+    M2::mainloop<P>(stage0, stage1, d, p.K, acc);
+    // The tile's 256 row and 256 column sums into LDS (free after the loop).
+    static_assert(DmaCfg::NT == 512, "one sum per thread");
+    int *sc = reinterpret_cast<int *>(stage0);
+    sc[threadIdx.x] = threadIdx.x < 256 ? rowsum[m_base + threadIdx.x] : colsum[n_base + threadIdx.x - 256];
+    __syncthreads();
+    const U8Epilogue<VecOut, ACT, BiasT> epi{p, sc, sc + 256, 16384u * (uint32_t)p.K};
+    M2::for_each_quad<P>(acc, [&](int ml, int nl, const v4i &v) { epi(ml, nl, v, m_base, n_base); });
+}
+
+// Workspace of the pre-pass path: sums (256-byte aligned), then A and B flipped.
+inline size_t u8_ws_sums_bytes(int M, int N) { return ((size_t)(M + N) * 4 + 255) & ~(size_t)255; }
+inline size_t u8_rrr_workspace_bytes(int M, int N, int K) {
+    return u8_ws_sums_bytes(M, N) + (((size_t)M * K + 255) & ~(size_t)255) + (size_t)K * N;
+}
+
 template <bool Aligned, int ACT, typename BiasT>
 __global__ __launch_bounds__(NT, 1) void gemm_u8_rrr_kernel(S8Args p) {
     __shared__ __attribute__((aligned(16))) int8_t lds[4 * LDS_TILE];
@@ -334,10 +439,35 @@ __global__ __launch_bounds__(NT, 1) void gemm_u8_rrr_kernel(S8Args p) {
 }
 
 template <int ACT, typename BiasT>
-int32_t launch_u8_rrr(const S8Args &p, hipStream_t stream) {
+int32_t launch_u8_rrr(const S8Args &p, hipStream_t stream, void *workspace = nullptr, size_t workspace_bytes = 0) {
     const bool dma = p.K % mfma2::BK == 0 && p.M % mfma2::BM == 0 && p.N % mfma2::BN == 0 &&
                      p.lda % 16 == 0 && p.ldb % 16 == 0 && aligned16(p.a) && aligned16(p.b) &&
                      (int64_t)p.M * p.lda < (1ll << 31) && (int64_t)p.K * p.ldb < (1ll << 31);
+    if (dma && workspace && workspace_bytes >= u8_rrr_workspace_bytes(p.M, p.N, p.K) &&
+        (reinterpret_cast<uintptr_t>(workspace) & 255u) == 0 && (int64_t)p.K * p.N < (1ll << 31)) {
+        int *rowsum = static_cast<int *>(workspace), *colsum = rowsum + p.M;
+        int8_t *af = static_cast<int8_t *>(workspace) + u8_ws_sums_bytes(p.M, p.N);
+        int8_t *bf = af + (((size_t)p.M * p.K + 255) & ~(size_t)255);
+        const int agrid = max((p.M + 3) / 4, (p.N + 255) / 256);
+        hipLaunchKernelGGL(u8_prep_a_kernel, dim3(agrid), dim3(256), 0, stream, (const uint8_t *)p.a, p.lda, p.M,
+                           p.K, af, rowsum, colsum, p.N);
+        hipLaunchKernelGGL(u8_prep_b_kernel, dim3((p.N + 255) / 256, (p.K + kU8ColSlice - 1) / kU8ColSlice),
+                           dim3(256), 0, stream, (const uint8_t *)p.b, p.ldb, p.K, p.N, bf, colsum);
+        S8Args q = p;
+        q.a = af;
+        q.lda = p.K;
+        q.b = bf;
+        q.ldb = p.N;
+        const int tiles = (p.M / mfma2::BM) * (p.N / mfma2::BN);
+        const bool vec = p.ldd % 4 == 0 && (reinterpret_cast<uintptr_t>(p.d) % 4) == 0;
+        if (vec)
+            hipLaunchKernelGGL((gemm_u8_rrr_ws_kernel<true, ACT, BiasT>), dim3(tiles), dim3(DmaCfg::NT), 0,
+                               stream, q, (const int *)rowsum, (const int *)colsum);
+        else
+            hipLaunchKernelGGL((gemm_u8_rrr_ws_kernel<false, ACT, BiasT>), dim3(tiles), dim3(DmaCfg::NT), 0,
+                               stream, q, (const int *)rowsum, (const int *)colsum);
+        return launch_status();
+    }
     if (dma) {
         const int tiles = (p.M / mfma2::BM) * (p.N / mfma2::BN);
         const bool vec = p.ldd % 4 == 0 && (reinterpret_cast<uintptr_t>(p.d) % 4) == 0;

@@ -28,22 +28,25 @@ int32_t baracuda_kernels_gemm_u8_rrr_gfx950_can_implement(
     return check_u8_rrr(m, n, k, lda, ldb, c, ldc, ldd);
 }
 
+// Optional workspace (256-byte aligned): the operands flipped to u - 128 and
+// their (M + N) int32 sums.  Given it, whole-tile problems run a pre-pass and
+// then the plain s8 RRR loop; without it the flip and the sums are folded
+// into the GEMM loop (slower: the extra registers spill).
 size_t baracuda_kernels_gemm_u8_rrr_gfx950_workspace_size(int32_t m, int32_t n, int32_t k) {
-    (void)m; (void)n; (void)k;
-    return 0;
+    if (m <= 0 || n <= 0 || k <= 0 || m % 256 || n % 256 || k % 128) return 0;
+    return u8_rrr_workspace_bytes(m, n, k);
 }
 
 int32_t baracuda_kernels_gemm_u8_rrr_gfx950_run(
     int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,
     const void *c, int64_t ldc, void *d, int64_t ldd, float alpha, float beta,
     void *workspace, size_t workspace_bytes, void *stream) {
-    (void)workspace; (void)workspace_bytes;
     int32_t st = check_u8_rrr(m, n, k, lda, ldb, c, ldc, ldd);
     if (st != kOk) return st;
     if (!a || !b || !d) return kInvalid;
     S8Args p{m, n, k, (const int8_t *)a, lda, (const int8_t *)b, ldb, (const int8_t *)c, ldc, d, ldd,
              alpha, beta, nullptr, nullptr, nullptr};
-    return launch_u8_rrr<ACT_NONE, float>(p, (hipStream_t)stream);
+    return launch_u8_rrr<ACT_NONE, float>(p, (hipStream_t)stream, workspace, workspace_bytes);
 }
 
 #define BK_U8_RRR_BIAS(EPISFX, ACTV, BSFX, BTY)                                                      \
@@ -57,13 +60,12 @@ int32_t baracuda_kernels_gemm_u8_rrr_gfx950_run(
         int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,     \
         const void *c, int64_t ldc, void *d, int64_t ldd, const void *bias, float alpha, float beta, \
         void *workspace, size_t workspace_bytes, void *stream) {                                     \
-        (void)workspace; (void)workspace_bytes;                                                      \
         int32_t st = check_u8_rrr(m, n, k, lda, ldb, c, ldc, ldd);                                   \
         if (st != kOk) return st;                                                                    \
         if (!a || !b || !d || !bias) return kInvalid;                                                \
         S8Args p{m, n, k, (const int8_t *)a, lda, (const int8_t *)b, ldb, (const int8_t *)c, ldc, d, \
                  ldd, alpha, beta, nullptr, nullptr, bias};                                          \
-        return launch_u8_rrr<ACTV, BTY>(p, (hipStream_t)stream);                                     \
+        return launch_u8_rrr<ACTV, BTY>(p, (hipStream_t)stream, workspace, workspace_bytes);         \
     }
 
 BK_U8_RRR_BIAS(bias, ACT_BIAS, f32, float)

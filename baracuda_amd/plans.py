@@ -138,6 +138,10 @@ def _ptr(t: Optional[torch.Tensor]):
     return None if t is None else t.data_ptr()
 
 
+def _nbytes(t: Optional[torch.Tensor]) -> int:
+    return 0 if t is None else t.numel() * t.element_size()
+
+
 def _stream(stream) -> int:
     if stream is None:
         return torch.cuda.current_stream().cuda_stream
@@ -221,7 +225,9 @@ class IntGemmPlan:
         if d.element == ElementKind.U8:
             if d.epilogue == EpilogueKind.Identity:
                 return getattr(L, f"gemm_u8_rrr_gfx950_{suffix}")
-            return None if suffix == "workspace_size" else getattr(L, f"gemm_u8_rrr_gfx950_{epi}_{bt}_{suffix}")
+            if suffix == "workspace_size":   # one requirement for the whole u8 family
+                return getattr(L, "gemm_u8_rrr_gfx950_workspace_size")
+            return getattr(L, f"gemm_u8_rrr_gfx950_{epi}_{bt}_{suffix}")
         if d.layout == LayoutSku.Rcr:
             if d.epilogue == EpilogueKind.Identity:
                 return getattr(L, f"gemm_s8_rcr_gfx950_{suffix}")
@@ -267,7 +273,7 @@ class IntGemmPlan:
                     _ptr(c), _ld(c) if c is not None else 0, _ptr(d), _ld(d)]
             if desc.epilogue != EpilogueKind.Identity:
                 args.append(_ptr(bias))
-            st = self._symbol("run")(*args, alpha, beta, _ptr(workspace), 0, s)
+            st = self._symbol("run")(*args, alpha, beta, _ptr(workspace), _nbytes(workspace), s)
         elif desc.output == ElementKind.I32:
             st = L.gemm_s8_rcr_gfx950_i32_run(desc.m, desc.n, desc.k, _ptr(a), _ld(a), _ptr(b), _ld(b),
                                               _ptr(d), _ld(d), _ptr(workspace), 0, s)

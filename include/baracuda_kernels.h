@@ -12,8 +12,10 @@
  *     captured into a hipGraph;
  *   - `stream` is a hipStream_t passed as void* (NULL = default stream);
  *   - strides and leading dimensions are in elements;
- *   - workspace is accepted for signature parity and is never required
- *     (every _workspace_size returns 0).
+ *   - workspace is never required: every _workspace_size returns 0 except
+ *     the u8 RRR family's, whose optional workspace (when given at least
+ *     that size, 256-byte aligned) selects a faster pre-pass path; without
+ *     it every entry point runs as-is.
  *
  * Each declaration cites the reference entry point it replaces
  * (paths relative to the baracuda repository root).
@@ -191,7 +193,13 @@ BK_FP8_BIAS_DECL4(e5m2, rrr)
  * with C and D u8.  Replaces baracuda_kernels_gemm_u8_rrr_sm80_{run,workspace_size,
  * can_implement} and baracuda_kernels_gemm_u8_rrr_sm80_{bias,...}_{f32,i32}_*
  * (crates/baracuda-kernels-sys/kernels/gemm/gemm_u8_rrr_sm80{,_bias}.cu;
- *  crates/baracuda-kernels-sys/src/lib.rs:120-160, 462-). */
+ *  crates/baracuda-kernels-sys/src/lib.rs:120-160, 462-).
+ * Optional workspace (all u8 RRR SKUs; its size from
+ * baracuda_kernels_gemm_u8_rrr_gfx950_workspace_size, nonzero for whole
+ * 256x256 tiles and K % 128 == 0): M*K + K*N bytes of operands flipped to
+ * u - 128 plus (M + N) int32 operand sums, written by a pre-pass; contents on
+ * entry do not matter.  Without it the flip and the sums run inside the GEMM
+ * loop. */
 int32_t baracuda_kernels_gemm_u8_rrr_gfx950_run(
     int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,
     const void *c, int64_t ldc, void *d, int64_t ldd, float alpha, float beta,

@@ -121,6 +121,10 @@ def test_rrr_and_bias_can_implement():
     assert L.gemm_s8_rrr_gfx950_can_implement(4, 8, 16, None, 15, None, 8, None, 0, None, 8) == 2
     assert L.gemm_s8_rrr_gfx950_can_implement(0, 8, 16, None, 16, None, 8, None, 0, None, 8) == 2
     assert L.gemm_s8_rrr_gfx950_workspace_size(64, 64, 64) == 0
+    # the u8 RRR family's optional pre-pass workspace: whole tiles only
+    assert L.gemm_u8_rrr_gfx950_workspace_size(64, 64, 64) == 0
+    assert L.gemm_u8_rrr_gfx950_workspace_size(512, 256, 200) == 0
+    assert L.gemm_u8_rrr_gfx950_workspace_size(512, 768, 384) == (512 + 768) * 4 + 512 * 384 + 384 * 768
     for epi in ("bias", "bias_relu", "bias_gelu", "bias_silu"):
         for bt in ("f32", "i32"):
             assert getattr(L, f"gemm_s8_rrr_gfx950_{epi}_{bt}_can_implement")(

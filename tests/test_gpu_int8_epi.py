@@ -138,15 +138,20 @@ def test_rrr_large_k_sum_identity(gpu):
 
 
 # ---- U8 RRR (int8_rrr_smoke.rs run_u8_smoke: a = (7i)%16, b = (11i)%14) ------
-def _run_u8(epi, bias_kind, a, b, c=None, bias=None, alpha=0.125, beta=0.0):
+def _run_u8(epi, bias_kind, a, b, c=None, bias=None, alpha=0.125, beta=0.0, ws=False):
+    # ws: pass the optional workspace (pre-pass operand sums), filled with
+    # garbage first -- its contents must not matter.
     m, k = a.shape
     n = b.shape[1]
     plan = P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, layout=P.LayoutSku.Rrr, epilogue=epi,
                                                     bias_element=bias_kind, element=P.ElementKind.U8,
                                                     output=P.ElementKind.U8))
+    work = None
+    if ws and plan.workspace_size() > 0:
+        work = torch.full((plan.workspace_size(),), 0xAB, dtype=torch.uint8, device="cuda:0")
     d = torch.full((m, n), 99, dtype=torch.uint8, device="cuda:0")
     plan.run(dev(a), dev(b), d, c=None if c is None else dev(c), alpha=alpha, beta=beta,
-             bias=None if bias is None else dev(bias))
+             bias=None if bias is None else dev(bias), workspace=work)
     sync()
     return d.cpu().numpy()
 
@@ -168,27 +173,29 @@ def test_u8_reference_smoke_pattern(gpu, shape, epi, bias_kind):
     _check(got, want, epi)
 
 
+@pytest.mark.parametrize("ws", [False, True])
 @pytest.mark.parametrize("epi", EPIS)
 @pytest.mark.parametrize("shape", [(256, 256, 128), (512, 768, 384), (300, 520, 200), (130, 260, 1000)])
-def test_u8_full_range_with_c(gpu, shape, epi):
+def test_u8_full_range_with_c(gpu, shape, epi, ws):
     # Full-range bytes (the flipped sign bit matters) on the DMA and the
     # general path, including a K tail (200, 1000) whose zero padding the
     # correction accounts for.
     m, n, k = shape
-    print(f"case: u8 random {epi.value} {shape}", flush=True)
+    print(f"case: u8 random {epi.value} {shape} ws={ws}", flush=True)
     g = rng(m * 3 + n + k)
     a = g.integers(0, 256, (m, k), dtype=np.uint8)
     b = g.integers(0, 256, (k, n), dtype=np.uint8)
     c = g.integers(0, 256, (m, n), dtype=np.uint8)
     bias = (g.standard_normal(n) * 30).astype(np.float32)
     alpha = 1.0 / (64.0 * k)
-    got = _run_u8(epi, P.ElementKind.F32, a, b, c=c, bias=bias, alpha=alpha, beta=0.5)
+    got = _run_u8(epi, P.ElementKind.F32, a, b, c=c, bias=bias, alpha=alpha, beta=0.5, ws=ws)
     want = O.gemm_u8_epi(a, b, "rrr", alpha, 0.5, c, None if epi == P.EpilogueKind.Identity else bias,
                          ACT[epi])
     _check(got, want, epi)
 
 
-def test_u8_large_k_exact_accumulator(gpu):
+@pytest.mark.parametrize("ws", [False, True])
+def test_u8_large_k_exact_accumulator(gpu, ws):
     # alpha = 1 / 2^k-scale keeps the u8 output informative at K = 8192
     # (acc up to 255^2 * 8192 ~ 5.3e8 < 2^31): checks the 16384*K term.
     m, n, k = 256, 256, 8192
@@ -196,6 +203,20 @@ def test_u8_large_k_exact_accumulator(gpu):
     a = g.integers(0, 256, (m, k), dtype=np.uint8)
     b = g.integers(0, 256, (k, n), dtype=np.uint8)
     alpha = 255.0 / (255.0 * 255.0 * k)
-    got = _run_u8(P.EpilogueKind.Identity, P.ElementKind.F32, a, b, alpha=alpha)
+    got = _run_u8(P.EpilogueKind.Identity, P.ElementKind.F32, a, b, alpha=alpha, ws=ws)
     want = O.gemm_u8_epi(a, b, "rrr", alpha)
     assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("epi", EPIS)
+def test_u8_workspace_path_bit_identical(gpu, epi):
+    # The pre-pass sums and the in-loop sums are both exact: same bytes out.
+    m, n, k = 512, 768, 1024
+    g = rng(4242)
+    a = g.integers(0, 256, (m, k), dtype=np.uint8)
+    b = g.integers(0, 256, (k, n), dtype=np.uint8)
+    c = g.integers(0, 256, (m, n), dtype=np.uint8)
+    bias = (g.standard_normal(n) * 30).astype(np.float32)
+    kw = dict(c=c, bias=bias, alpha=1.0 / (64.0 * k), beta=0.5)
+    assert np.array_equal(_run_u8(epi, P.ElementKind.F32, a, b, ws=True, **kw),
+                          _run_u8(epi, P.ElementKind.F32, a, b, ws=False, **kw))
