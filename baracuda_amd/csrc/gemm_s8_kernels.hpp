@@ -36,6 +36,22 @@ struct S8Args {
 template <int EPI, bool VecOut, int ACT = ACT_NONE, typename BiasT = float>
 struct S8Epilogue {
     const S8Args &p;
+    // EPI_S8, whole group of 4 columns (N % 4 == 0): the 4 result bytes.
+    __device__ __forceinline__ uint32_t pack_s8(int m, int n0, const v4i &v) const {
+        int8_t o[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float z = p.alpha * (float)v[r];
+            if (p.beta != 0.0f && p.c != nullptr) z += p.beta * (float)p.c[(int64_t)m * p.ldc + n0 + r];
+            if constexpr (ACT != ACT_NONE) {
+                z += (float)static_cast<const BiasT *>(p.bias)[n0 + r];
+                z = activation<ACT>(z);
+            }
+            o[r] = sat_cast_s8(z);
+        }
+        return (uint32_t)(uint8_t)o[0] | ((uint32_t)(uint8_t)o[1] << 8) | ((uint32_t)(uint8_t)o[2] << 16) |
+               ((uint32_t)(uint8_t)o[3] << 24);
+    }
     __device__ __forceinline__ void operator()(int m, int n0, const v4i &v) const {
         if (m >= p.M || n0 >= p.N) return;
         // VecOut implies N % 4 == 0, so a group is then always complete.
@@ -156,6 +172,22 @@ int32_t launch_rrr(const S8Args &p, hipStream_t stream) {
 // LDS-DMA mainloop, 8 waves (2 x 4) of 128 x 64, v_mfma_i32_16x16x64_i8.
 typedef mfma2::Cfg<2, 4, 0> DmaCfg;
 
+// int8 outputs of a whole tile through LDS: each wave's 128 x 64 bytes are
+// staged (8 KiB per wave; LDS is free after the mainloop's last barrier) and
+// written as 16-byte row segments instead of 4-byte stores.
+template <class P, class Epi>
+__device__ __forceinline__ void store_s8_tile_staged(const mfma2::AccTile<P> &acc, int8_t *stage0, int8_t *stage1,
+                                                     const S8Args &p, int m_base, int n_base, const Epi &epi) {
+    const int wave = threadIdx.x >> 6;
+    const int wrow = (wave / DmaCfg::WAVES_N) * DmaCfg::WM;
+    const int wcol = (wave % DmaCfg::WAVES_N) * DmaCfg::WN;
+    int8_t *scratch = (wave < 4 ? stage0 : stage1) + (wave & 3) * (DmaCfg::WM * DmaCfg::WN);
+    mfma2::store_u8x4_staged<P>(
+        acc, scratch,
+        [&](int r, int c, const v4i &v) { return epi.pack_s8(m_base + wrow + r, n_base + wcol + c, v); },
+        [&](int r) { return static_cast<int8_t *>(p.d) + (int64_t)(m_base + wrow + r) * p.ldd + n_base + wcol; });
+}
+
 template <int EPI, bool VecOut, int ACT = ACT_NONE, typename BiasT = float>
 __global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_s8_rcr_dma_kernel(S8Args p) {
     namespace M2 = mfma2;
@@ -190,6 +222,12 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_s8_rcr_dma_kernel(S8Args p
         });
     } else {
         const S8Epilogue<EPI, VecOut, ACT, BiasT> epi{p};
+        if constexpr (EPI == EPI_S8 && VecOut) {
+            if (p.ldd % 16 == 0 && (reinterpret_cast<uintptr_t>(p.d) & 15u) == 0) {
+                store_s8_tile_staged<P>(acc, stage0, stage1, p, m_base, n_base, epi);
+                return;
+            }
+        }
         M2::for_each_quad<P>(acc, [&](int ml, int nl, const v4i &v) { epi(m_base + ml, n_base + nl, v); });
     }
 }
@@ -212,6 +250,12 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_s8_rrr_dma_kernel(S8Args p
     M2::AccTile<P> acc;
     M2::mainloop<P>(stage0, stage1, d, p.K, acc);
     const S8Epilogue<EPI_S8, VecOut, ACT, BiasT> epi{p};
+    if constexpr (VecOut) {
+        if (p.ldd % 16 == 0 && (reinterpret_cast<uintptr_t>(p.d) & 15u) == 0) {
+            store_s8_tile_staged<P>(acc, stage0, stage1, p, m_base, n_base, epi);
+            return;
+        }
+    }
     M2::for_each_quad<P>(acc, [&](int ml, int nl, const v4i &v) { epi(m_base + ml, n_base + nl, v); });
 }
 
@@ -229,6 +273,25 @@ struct U8Epilogue {
     const int *rs;        // [256] tile row sums of A
     const int *cs;        // [256] tile column sums of B
     uint32_t kcorr;       // 16384 * K_pad (mod 2^32), subtracted
+    // Whole group of 4 columns (N % 4 == 0): the 4 result bytes.
+    __device__ __forceinline__ uint32_t pack_u8(int ml, int nl, const v4i &v, int m_base, int n_base) const {
+        const int m = m_base + ml, n0 = n_base + nl;
+        const uint32_t rsum = (uint32_t)rs[ml];
+        const uint8_t *c = reinterpret_cast<const uint8_t *>(p.c);
+        uint32_t w = 0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t au = (uint32_t)v[r] + 128u * (rsum + (uint32_t)cs[nl + r]) - kcorr;
+            float z = p.alpha * (float)(int32_t)au;
+            if (p.beta != 0.0f && c != nullptr) z += p.beta * (float)c[(int64_t)m * p.ldc + n0 + r];
+            if constexpr (ACT != ACT_NONE) {
+                z += (float)static_cast<const BiasT *>(p.bias)[n0 + r];
+                z = activation<ACT>(z);
+            }
+            w |= (uint32_t)sat_cast_u8(z) << (8 * r);
+        }
+        return w;
+    }
     __device__ __forceinline__ void operator()(int ml, int nl, const v4i &v, int m_base,
                                                int n_base) const {
         const int m = m_base + ml, n0 = n_base + nl;
@@ -267,6 +330,28 @@ __device__ __forceinline__ void park_row_sums(uint32_t v, int *dst) {
     if ((lane & 1) == 0) dst[32 * wave + (lane >> 1)] = (int)v;
 }
 
+// u8 outputs of a whole tile: staged 16-byte row stores when D allows them.
+template <bool VecOut, class P, class Epi>
+__device__ __forceinline__ void store_u8_tile(const mfma2::AccTile<P> &acc, int8_t *stage0, int8_t *stage1,
+                                              const S8Args &p, int m_base, int n_base, const Epi &epi) {
+    if constexpr (VecOut) {
+        if (p.ldd % 16 == 0 && (reinterpret_cast<uintptr_t>(p.d) & 15u) == 0) {
+            const int wave = threadIdx.x >> 6;
+            const int wrow = (wave / DmaCfg::WAVES_N) * DmaCfg::WM;
+            const int wcol = (wave % DmaCfg::WAVES_N) * DmaCfg::WN;
+            int8_t *scratch = (wave < 4 ? stage0 : stage1) + (wave & 3) * (DmaCfg::WM * DmaCfg::WN);
+            mfma2::store_u8x4_staged<P>(
+                acc, scratch,
+                [&](int r, int c, const v4i &v) { return epi.pack_u8(wrow + r, wcol + c, v, m_base, n_base); },
+                [&](int r) {
+                    return static_cast<int8_t *>(p.d) + (int64_t)(m_base + wrow + r) * p.ldd + n_base + wcol;
+                });
+            return;
+        }
+    }
+    mfma2::for_each_quad<P>(acc, [&](int ml, int nl, const v4i &v) { epi(ml, nl, v, m_base, n_base); });
+}
+
 template <bool VecOut, int ACT, typename BiasT>
 __global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_u8_rrr_dma_kernel(S8Args p) {
     namespace M2 = mfma2;
@@ -286,9 +371,10 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_u8_rrr_dma_kernel(S8Args p
 #pragma unroll
     for (int q = 0; q < 4; ++q) sums.cb[q] = 0;
     M2::mainloop<P>(stage0, stage1, d, p.K, acc, sums);
-    // Park: row sums directly; column partials per wave in [8][256], then summed.
+    // Park: row sums directly; column partials per wave in [8][256], then
+    // summed; above the staged-store scratch of waves 4..7 (stage1's first 32 KiB).
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    int *sc = reinterpret_cast<int *>(stage0);           // rs[256] | cs[256] | part[8][256]
+    int *sc = reinterpret_cast<int *>(stage1 + 40 * 1024);   // rs[256] | cs[256] | part[8][256]
     park_row_sums(sums.ra, sc);
     // Lane i of group g holds column 16*(g + 4q) + i over this wave's 16 k-rows
     // in cb[q]: every column exactly once per wave.
@@ -303,7 +389,7 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_u8_rrr_dma_kernel(S8Args p
     }
     __syncthreads();
     const U8Epilogue<VecOut, ACT, BiasT> epi{p, sc, sc + 256, 16384u * (uint32_t)p.K};
-    M2::for_each_quad<P>(acc, [&](int ml, int nl, const v4i &v) { epi(ml, nl, v, m_base, n_base); });
+    store_u8_tile<VecOut, P>(acc, stage0, stage1, p, m_base, n_base, epi);
 }
 
 // ---- u8 pre-pass (when the caller gives a workspace) ------------------------
@@ -396,13 +482,14 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_u8_rrr_ws_kernel(S8Args p,
     d.b = M2::make_dma_row_b<DmaCfg>(p.b, (uint32_t)(p.K * p.ldb), (int)p.ldb, n_base);
     M2::AccTile<P> acc;
     M2::mainloop<P>(stage0, stage1, d, p.K, acc);
-    // The tile's 256 row and 256 column sums into LDS (free after the loop).
+    // The tile's 256 row and 256 column sums into LDS (free after the loop),
+    // above the staged-store scratch of waves 4..7.
     static_assert(DmaCfg::NT == 512, "one sum per thread");
-    int *sc = reinterpret_cast<int *>(stage0);
+    int *sc = reinterpret_cast<int *>(stage1 + 40 * 1024);
     sc[threadIdx.x] = threadIdx.x < 256 ? rowsum[m_base + threadIdx.x] : colsum[n_base + threadIdx.x - 256];
     __syncthreads();
     const U8Epilogue<VecOut, ACT, BiasT> epi{p, sc, sc + 256, 16384u * (uint32_t)p.K};
-    M2::for_each_quad<P>(acc, [&](int ml, int nl, const v4i &v) { epi(ml, nl, v, m_base, n_base); });
+    store_u8_tile<VecOut, P>(acc, stage0, stage1, p, m_base, n_base, epi);
 }
 
 // Workspace of the pre-pass path: sums (256-byte aligned), then A and B flipped.
