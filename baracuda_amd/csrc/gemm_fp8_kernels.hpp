@@ -41,6 +41,20 @@ struct F8Args {
 template <int FMT, int EPI, bool VecOut, int ACT>
 struct F8Epilogue {
     const F8Args &p;
+    // F8_OUT, whole group of 4 columns (N % 4 == 0): the 4 result bytes.
+    __device__ __forceinline__ uint32_t pack_fp8(int m, int n0, const v4f &v) const {
+        float z[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            z[r] = p.alpha * v[r];
+            if (p.beta != 0.0f && p.c != nullptr) z[r] += p.beta * fp8_to_f32<FMT>(p.c[(int64_t)m * p.ldc + n0 + r]);
+            if constexpr (ACT != ACT_NONE) {
+                z[r] += p.bias[n0 + r];
+                z[r] = activation<ACT>(z[r]);
+            }
+        }
+        return f32x4_to_fp8x4_satfinite<FMT>(z[0], z[1], z[2], z[3]);
+    }
     __device__ __forceinline__ void operator()(int m, int n0, const v4f &v) const {
         if (m >= p.M || n0 >= p.N) return;
         const int count = VecOut ? 4 : (p.N - n0 < 4 ? p.N - n0 : 4);
@@ -128,7 +142,39 @@ __global__ __launch_bounds__(F8DmaCfg::NT, 1) void gemm_fp8_dma_kernel(F8Args p)
         d.b = M2::make_dma_row_b<F8DmaCfg>(p.b, (uint32_t)(p.K * p.ldb), (int)p.ldb, n_base);
         M2::mainloop<P>(stage0, stage1, d, p.K, acc);
     }
+    if constexpr (EPI == F8_BF16) {
+        // bf16 rows staged per wave in LDS (free after the mainloop's last
+        // barrier), written as 16-byte units: D = bf16_rne(alpha * acc).
+        if (p.ldd % 8 == 0 && (reinterpret_cast<uintptr_t>(p.d) & 15u) == 0) {
+            const int wave = threadIdx.x >> 6;
+            const int wrow = m_base + (wave / F8DmaCfg::WAVES_N) * F8DmaCfg::WM;
+            const int wcol = n_base + (wave % F8DmaCfg::WAVES_N) * F8DmaCfg::WN;
+            int8_t *scratch = (wave < 4 ? stage0 : stage1) + (wave & 3) * (F8DmaCfg::WM * 128);
+            const float alpha = p.alpha;
+            M2::store_bf16x4_staged<P>(
+                acc, scratch,
+                [&](int, int, const v4f &v) {
+                    return v2i{(int)f32x2_to_bf16x2(alpha * v[0], alpha * v[1]),
+                               (int)f32x2_to_bf16x2(alpha * v[2], alpha * v[3])};
+                },
+                [&](int r) { return static_cast<uint16_t *>(p.d) + (int64_t)(wrow + r) * p.ldd + wcol; });
+            return;
+        }
+    }
     const F8Epilogue<FMT, EPI, true, ACT> epi{p};
+    if constexpr (EPI == F8_OUT) {
+        // fp8 bytes staged per wave, written as 16-byte row segments.
+        if (p.ldd % 16 == 0 && (reinterpret_cast<uintptr_t>(p.d) & 15u) == 0) {
+            const int wave = threadIdx.x >> 6;
+            const int wrow = m_base + (wave / F8DmaCfg::WAVES_N) * F8DmaCfg::WM;
+            const int wcol = n_base + (wave % F8DmaCfg::WAVES_N) * F8DmaCfg::WN;
+            int8_t *scratch = (wave < 4 ? stage0 : stage1) + (wave & 3) * (F8DmaCfg::WM * F8DmaCfg::WN);
+            M2::store_u8x4_staged<P>(
+                acc, scratch, [&](int r, int c, const v4f &v) { return epi.pack_fp8(wrow + r, wcol + c, v); },
+                [&](int r) { return static_cast<int8_t *>(p.d) + (int64_t)(wrow + r) * p.ldd + wcol; });
+            return;
+        }
+    }
     M2::for_each_quad<P>(acc, [&](int ml, int nl, const v4f &v) { epi(m_base + ml, n_base + nl, v); });
 }
 

@@ -744,8 +744,8 @@ __device__ __forceinline__ void store_w8a8_bf16_staged(const AccTile<P> &acc, in
     }
 }
 
-// 1-byte outputs of the int8 16x16 policy, staged in LDS so each 64-byte row
-// of the wave tile (WN = 64 columns) is written with 16-byte stores.
+// 1-byte outputs of any policy whose wave tile is WN = 64 columns, staged in
+// LDS so each 64-byte row of the wave tile is written with 16-byte stores.
 //   pack(r, c, quad)  4 output bytes of wave-tile row r, columns c..c+3
 //   row_dst(r)        destination of wave-tile row r at the wave's first column
 // `scratch`: WM * WN bytes private to this wave.  16-byte unit u of row r
@@ -761,7 +761,7 @@ __device__ __forceinline__ void store_u8x4_staged(const AccTile<P> &acc, int8_t 
     for (int i = 0; i < P::TI; ++i)
 #pragma unroll
         for (int j = 0; j < P::TJ; ++j)
-            P::visit(acc[i][j], i, j, lane, [&](int r, int c, const v4i &v) {
+            P::visit(acc[i][j], i, j, lane, [&](int r, int c, const auto &v) {
                 const int unit = (c >> 4) ^ ((r >> 2) & 3);
                 *reinterpret_cast<uint32_t *>(scratch + r * 64 + (unit << 4) + (c & 15)) = pack(r, c, v);
             });
@@ -773,6 +773,36 @@ __device__ __forceinline__ void store_u8x4_staged(const AccTile<P> &acc, int8_t 
         const int r = q * 16 + (lane >> 2), u = lane & 3;
         const v4i v = *reinterpret_cast<const v4i *>(scratch + r * 64 + ((u ^ ((r >> 2) & 3)) << 4));
         *reinterpret_cast<v4i *>(row_dst(r) + u * 16) = v;
+    }
+}
+
+// bf16 outputs of any policy whose wave tile is WN = 64 columns: each quad
+// (4 columns of one row) is packed to 4 bf16 by pack(r, c, quad) (8 bytes)
+// and staged in LDS; rows (128 bytes) are then written as 16-byte units.
+// `scratch`: WM * 128 bytes private to this wave; unit u of row r sits at
+// unit u ^ (r & 7).
+template <class P, class Pack, class RowDst>
+__device__ __forceinline__ void store_bf16x4_staged(const AccTile<P> &acc, int8_t *scratch, Pack &&pack,
+                                                    RowDst &&row_dst) {
+    typedef typename P::Cfg C;
+    static_assert(C::WN == 64, "staged bf16 store assumes 128-byte wave-tile rows");
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < P::TI; ++i)
+#pragma unroll
+        for (int j = 0; j < P::TJ; ++j)
+            P::visit(acc[i][j], i, j, lane, [&](int r, int c, const auto &v) {
+                const int unit = (c >> 3) ^ (r & 7);
+                *reinterpret_cast<v2i *>(scratch + r * 128 + (unit << 4) + ((c & 7) << 1)) = pack(r, c, v);
+            });
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int q = 0; q < C::WM / 8; ++q) {
+        const int r = q * 8 + (lane >> 3), u = lane & 7;
+        const v4i v = *reinterpret_cast<const v4i *>(scratch + r * 128 + ((u ^ (r & 7)) << 4));
+        *reinterpret_cast<v4i *>(row_dst(r) + u * 8) = v;
     }
 }
 
