@@ -776,9 +776,10 @@ __device__ __forceinline__ void store_u8x4_staged(const AccTile<P> &acc, int8_t 
     }
 }
 
-// bf16 outputs of any policy whose wave tile is WN = 64 columns: each quad
-// (4 columns of one row) is packed to 4 bf16 by pack(r, c, quad) (8 bytes)
-// and staged in LDS; rows (128 bytes) are then written as 16-byte units.
+// 16-bit outputs of any policy whose wave tile is WN = 64 columns: each quad
+// (4 columns of one row) is packed to 4 halves by pack(r, c, quad) (8 bytes)
+// and staged in LDS; rows (128 bytes) are then written as 16-byte units,
+// row_dst(r) giving each row's destination (nullptr: skip the row).
 // `scratch`: WM * 128 bytes private to this wave; unit u of row r sits at
 // unit u ^ (r & 7).
 template <class P, class Pack, class RowDst>
@@ -802,7 +803,8 @@ __device__ __forceinline__ void store_bf16x4_staged(const AccTile<P> &acc, int8_
     for (int q = 0; q < C::WM / 8; ++q) {
         const int r = q * 8 + (lane >> 3), u = lane & 7;
         const v4i v = *reinterpret_cast<const v4i *>(scratch + r * 128 + ((u ^ (r & 7)) << 4));
-        *reinterpret_cast<v4i *>(row_dst(r) + u * 8) = v;
+        uint16_t *dst = row_dst(r);   // nullptr: row not stored
+        if (dst != nullptr) *reinterpret_cast<v4i *>(dst + u * 8) = v;
     }
 }
 

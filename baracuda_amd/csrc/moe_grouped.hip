@@ -240,6 +240,31 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void moe_grouped_dma_kernel(MoeArgs 
     M2::AccTile<P> acc;
     M2::mainloop<P>(stage0, stage1, d, kb, acc);
     if constexpr (KIND != MOE_S8) {
+        if ((reinterpret_cast<uintptr_t>(p.out) & 15u) == 0) {
+            // Rows staged per wave in LDS and written as 16-byte units of the
+            // token's output row; padding rows of a partial tile are skipped.
+            const int wave = threadIdx.x >> 6;
+            const int wr = (wave / DmaCfg::WAVES_N) * DmaCfg::WM;
+            const int wc = n_base + (wave % DmaCfg::WAVES_N) * DmaCfg::WN;
+            int8_t *scratch = (wave < 4 ? stage0 : stage1) + (wave & 3) * (DmaCfg::WM * 128);
+            M2::store_bf16x4_staged<P>(
+                acc, scratch,
+                [&](int r, int, const v4f &v) {
+                    const float tw = p.topk_w ? p.topk_w[s_rows_tok[wr + r]] : 1.0f;
+                    uint16_t h[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const float y = p.topk_w ? v[q] * tw : v[q];
+                        h[q] = KIND == MOE_BF16 ? f32_to_bf16_rne(y) : f32_to_f16_rne(y);
+                    }
+                    return v2i{(int)((uint32_t)h[0] | ((uint32_t)h[1] << 16)),
+                               (int)((uint32_t)h[2] | ((uint32_t)h[3] << 16))};
+                },
+                [&](int r) -> uint16_t * {
+                    return wr + r < seg_rows ? p.out + (int64_t)s_rows_tok[wr + r] * p.N + wc : nullptr;
+                });
+            return;
+        }
         M2::for_each_quad<P>(acc, [&](int ml, int nl, const v4f &v) {
             moe_store_h<KIND>(p, s_rows_tok, seg_rows, ml, n_base + nl, v);
         });
