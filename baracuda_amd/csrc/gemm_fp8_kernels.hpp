@@ -113,7 +113,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_kernel(F8Args p) {
     for_each_fragment(acc, [&](int ml, int nl, const v4f &v) { epi(m_base + ml, n_base + nl, v); });
 }
 
-typedef mfma2::Cfg<2, 4, 0> F8DmaCfg;
+typedef mfma2::Cfg<2, 4> F8DmaCfg;
 
 template <int FMT, int LAYOUT>
 struct F8DmaPolicy { typedef mfma2::PolicyF8<F8DmaCfg, FMT> type; };

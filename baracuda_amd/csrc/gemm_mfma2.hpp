@@ -5,7 +5,7 @@
 // RCR "column-major [K,N]" operand).  Requirements checked by the launcher:
 // K % 128 == 0, lda % 16 == 0, ldb % 16 == 0, 16-byte aligned bases.
 //
-// Block tile 256(M) x 256(N); Cfg<WAVES_M, WAVES_N, PIPE> picks the wave
+// Block tile 256(M) x 256(N); Cfg<WAVES_M, WAVES_N> picks the wave
 // grid (the int8 and FP8 kernels use 2 x 4 wave64s, each owning a 128 x 64
 // output tile, two waves per SIMD).  K advances 128 bytes per stage, two
 // stages in flight.
@@ -18,13 +18,13 @@
 // is the XOR pattern measured bank-conflict free on gfx950 for every
 // ds_read_b128 fragment pattern used below (16-row int8 and 32-row fp8 frags).
 //
-// Per stage and wave: 2 sub-steps of 64 bytes of K.  Fragments of the next
-// sub-step are read from LDS while the MFMAs of the current one run (two
-// register sets F0/F1); the only barrier per stage sits in the middle of the
-// second sub-step's MFMAs, after which the next stage's first fragments are
-// requested.  The two stage buffers are distinct __shared__ arrays and the
-// loop is unrolled by two, so the DMA into one buffer is never mistaken for a
-// write to the buffer being read (no spurious vmcnt waits before ds_reads).
+// Per stage and wave: the DMA of the next stage is issued into the other
+// buffer, then 2 sub-steps of 64 bytes of K, each reading its fragments and
+// issuing its MFMAs (the two waves of a SIMD interleave), then a wait for
+// this wave's DMA and the stage's one barrier.  The two stage buffers are
+// distinct __shared__ arrays and the loop is unrolled by two, so the DMA
+// into one buffer is never mistaken for a write to the buffer being read
+// (no spurious vmcnt waits before ds_reads).
 //
 // Both operand fragments use the same lane -> (row, k) mapping, so every k is
 // paired with itself whatever the hardware's intra-instruction K order is:
@@ -42,17 +42,17 @@ constexpr int BK = 128;
 constexpr int OPER = BM * BK;        // 32 KiB per operand per stage
 
 // Block configuration: WAVES_M x WAVES_N wave64s, each owning a
-// (256 / WAVES_M) x (256 / WAVES_N) output tile.  PIPE 0: per sub-step,
-// read its fragments then issue its MFMAs (latency hidden by the other wave
-// of the SIMD); PIPE 1: two fragment register sets, the next sub-step's
-// fragments are read while the current sub-step's MFMAs run.
+// (256 / WAVES_M) x (256 / WAVES_N) output tile.  Per sub-step a wave reads
+// its fragments, then issues its MFMAs; the latency is hidden by the other
+// wave of the SIMD.  (Measured slower and removed: double-buffered
+// fragments, a mid-stage barrier, pinned read/MFMA interleaving, a
+// ping-pong of the two waves of a SIMD, one wave per SIMD.)
 // TB: square block tile edge (256 by default; the A and B stage regions are
 // TB x BK bytes each, B at stage + OPER).
-template <int WAVES_M_, int WAVES_N_, int PIPE_, int TB_ = 256>
+template <int WAVES_M_, int WAVES_N_, int TB_ = 256>
 struct Cfg {
     static constexpr int WAVES_M = WAVES_M_;
     static constexpr int WAVES_N = WAVES_N_;
-    static constexpr int PIPE = PIPE_;
     static constexpr int TB = TB_;
     static constexpr int OPER = TB * BK;                    // bytes per operand per stage
     static constexpr int WAVES = WAVES_M * WAVES_N;
@@ -510,64 +510,23 @@ __device__ __forceinline__ void dma_stage(int8_t *stage, const D &d, int kbyte) 
 }
 
 // One stage: compute from `cur`, stream the next stage into `nxt` (if any).
-// PIPE 1: F0 already holds `cur`'s sub-step 0 fragments on entry and holds
-// `nxt`'s on exit.
 template <class P, class D>
 __device__ __forceinline__ void stage_step(AccTile<P> &acc, Frags<P> &f0, Frags<P> &f1,
                                            const int8_t *cur, int8_t *nxt, const D &d, int next_k,
                                            bool has_next, int wave_m, int wave_n, int lane,
                                            typename P::Sums &sums) {
     typedef typename P::Cfg C;
-    static_assert((!P::SUMS && !P::FLIP) || C::PIPE == 0, "u8 operands are wired into PIPE 0 only");
     if (has_next) dma_stage<C>(nxt, d, next_k);
-    if constexpr (C::PIPE == 0) {
-        load_frags<P>(f0, cur, 0, wave_m, wave_n, lane);
-        if constexpr (P::FLIP) P::fixup(f0, sums);
-        mma_block<P, 0, P::TJ>(acc, f0);
-        load_frags<P>(f1, cur, 1, wave_m, wave_n, lane);
-        if constexpr (P::FLIP) P::fixup(f1, sums);
-        mma_block<P, 0, P::TJ>(acc, f1);
-        // `cur` stays valid until the barrier below; the fragments are dead here.
-        if constexpr (P::SUMS) P::stage_hook(cur, sums);
-        wait_dma();        // this wave's DMA into `nxt` has landed
-        __syncthreads();   // ... and every wave's; every wave is done reading `cur`
-    } else if constexpr (C::PIPE >= 2) {
-        // Per sub-step: B fragments and A fragment 0 first, then each row i of
-        // MFMAs overlaps the read of A fragment i+1 (scheduler pinned).
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            Frags<P> &f = s ? f1 : f0;
-#pragma unroll
-            for (int t = 0; t < P::TJ; ++t) f.b[t] = P::load_b(cur + C::OPER, wave_n * C::WN, t, s, lane);
-            f.a[0] = P::load(cur, wave_m * C::WM, 0, s, lane);
-            if constexpr (C::PIPE == 3) __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-            for (int i = 0; i < P::TI; ++i) {
-                if (i + 1 < P::TI) f.a[i + 1] = P::load(cur, wave_m * C::WM, i + 1, s, lane);
-#pragma unroll
-                for (int h = 0; h < P::H; ++h)
-#pragma unroll
-                    for (int j = 0; j < P::TJ; ++j) P::mma(acc[i][j], f.b[j], f.a[i], h);
-            }
-            if constexpr (C::PIPE == 3) __builtin_amdgcn_s_setprio(0);
-            __builtin_amdgcn_sched_group_barrier(0x100, P::TJ + 1, 0);
-#pragma unroll
-            for (int i = 0; i < P::TI; ++i) {
-                if (i + 1 < P::TI) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x008, P::TJ * P::H, 0);
-            }
-        }
-        wait_dma();
-        __syncthreads();
-    } else {
-        load_frags<P>(f1, cur, 1, wave_m, wave_n, lane);
-        mma_block<P, 0, P::TJ>(acc, f0);
-        mma_block<P, 0, P::TJ / 2>(acc, f1);
-        wait_dma();
-        __syncthreads();
-        if (has_next) load_frags<P>(f0, nxt, 0, wave_m, wave_n, lane);
-        mma_block<P, P::TJ / 2, P::TJ>(acc, f1);
-    }
+    load_frags<P>(f0, cur, 0, wave_m, wave_n, lane);
+    if constexpr (P::FLIP) P::fixup(f0, sums);
+    mma_block<P, 0, P::TJ>(acc, f0);
+    load_frags<P>(f1, cur, 1, wave_m, wave_n, lane);
+    if constexpr (P::FLIP) P::fixup(f1, sums);
+    mma_block<P, 0, P::TJ>(acc, f1);
+    // `cur` stays valid until the barrier below; the fragments are dead here.
+    if constexpr (P::SUMS) P::stage_hook(cur, sums);
+    wait_dma();        // this wave's DMA into `nxt` has landed
+    __syncthreads();   // ... and every wave's; every wave is done reading `cur`
 }
 
 // Full K loop for one 256x256 tile.  s0 / s1 are the two stage buffers
@@ -588,7 +547,6 @@ __device__ __forceinline__ void mainloop(int8_t *s0, int8_t *s1, const D &d, int
     dma_stage<C>(s0, d, 0);
     wait_dma();
     __syncthreads();
-    if constexpr (C::PIPE == 1) load_frags<P>(f0, s0, 0, wave_m, wave_n, lane);
     int kt = 0;
     for (; kt + 2 <= KT; kt += 2) {
         stage_step<P>(acc, f0, f1, s0, s1, d, (kt + 1) * BK, true, wave_m, wave_n, lane, sums);
@@ -597,98 +555,9 @@ __device__ __forceinline__ void mainloop(int8_t *s0, int8_t *s1, const D &d, int
     if (kt < KT) stage_step<P>(acc, f0, f1, s0, s1, d, 0, false, wave_m, wave_n, lane, sums);
 }
 
-// PIPE 4: one barrier per stage, placed halfway through the second
-// sub-step's MFMA rows, so the post-barrier fragment reads of the next stage
-// overlap MFMAs instead of idling the MFMA pipe.  Per stage k (buffer cur):
-//   sub-step 0: A rows streamed one ahead of the MFMA rows (B already loaded)
-//   sub-step 1: B + A rows streamed; after half of the rows every remaining
-//               A fragment of `cur` is read, then wait for this wave's DMA
-//               of stage k+1, barrier (every wave is done with `cur` and
-//               stage k+1 has landed), DMA stage k+2 into `cur`, read stage
-//               k+1's sub-step-0 B fragments, finish the MFMA rows.
-// Register peak: accumulators + one B set + half the A rows + the next B set.
-template <class P, class D>
-__device__ __forceinline__ void mainloop_p4(int8_t *s0, int8_t *s1, const D &d, int K, AccTile<P> &acc) {
-    typedef typename P::Cfg C;
-    static_assert(!P::SUMS && !P::FLIP, "u8 operands are wired into PIPE 0 only");
-    constexpr int TI = P::TI, TJ = P::TJ;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wave_m = wave / C::WAVES_N, wave_n = wave % C::WAVES_N;
-    const int row_a = wave_m * C::WM, row_b = wave_n * C::WN;
-#pragma unroll
-    for (int i = 0; i < TI; ++i)
-#pragma unroll
-        for (int j = 0; j < TJ; ++j) acc[i][j] = P::zero();
-    const int KT = K / BK;
-    dma_stage<C>(s0, d, 0);
-    if (KT > 1) dma_stage<C>(s1, d, BK);
-    if (KT > 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * C::DMA_PER_WAVE) : "memory");
-    else wait_dma();
-    __syncthreads();
-    typename P::Frag bnext[TJ];
-#pragma unroll
-    for (int t = 0; t < TJ; ++t) bnext[t] = P::load_b(s0 + C::OPER, row_b, t, 0, lane);
-    auto stage = [&](int8_t *cur, int8_t *nxt, int kt) {
-        // sub-step 0
-        {
-            typename P::Frag a0 = P::load(cur, row_a, 0, 0, lane);
-#pragma unroll
-            for (int i = 0; i < TI; ++i) {
-                typename P::Frag a1;
-                if (i + 1 < TI) a1 = P::load(cur, row_a, i + 1, 0, lane);
-#pragma unroll
-                for (int h = 0; h < P::H; ++h)
-#pragma unroll
-                    for (int j = 0; j < TJ; ++j) P::mma(acc[i][j], bnext[j], a0, h);
-                if (i + 1 < TI) a0 = a1;
-            }
-        }
-        // sub-step 1
-        typename P::Frag b1[TJ];
-#pragma unroll
-        for (int t = 0; t < TJ; ++t) b1[t] = P::load_b(cur + C::OPER, row_b, t, 1, lane);
-        typename P::Frag a[TI];
-        a[0] = P::load(cur, row_a, 0, 1, lane);
-#pragma unroll
-        for (int i = 0; i < TI / 2; ++i) {
-            a[i + 1] = P::load(cur, row_a, i + 1, 1, lane);
-#pragma unroll
-            for (int h = 0; h < P::H; ++h)
-#pragma unroll
-                for (int j = 0; j < TJ; ++j) P::mma(acc[i][j], b1[j], a[i], h);
-        }
-#pragma unroll
-        for (int i = TI / 2 + 1; i < TI; ++i) a[i] = P::load(cur, row_a, i, 1, lane);
-        wait_dma();        // this wave's DMA of stage kt+1 has landed
-        __syncthreads();   // ... and every wave's; every wave has read all of `cur`
-        if (kt + 2 < KT) dma_stage<C>(cur, d, (kt + 2) * BK);
-        if (kt + 1 < KT) {
-#pragma unroll
-            for (int t = 0; t < TJ; ++t) bnext[t] = P::load_b(nxt + C::OPER, row_b, t, 0, lane);
-        }
-#pragma unroll
-        for (int i = TI / 2; i < TI; ++i)
-#pragma unroll
-            for (int h = 0; h < P::H; ++h)
-#pragma unroll
-                for (int j = 0; j < TJ; ++j) P::mma(acc[i][j], b1[j], a[i], h);
-    };
-    int kt = 0;
-    for (; kt + 2 <= KT; kt += 2) {
-        stage(s0, s1, kt);
-        stage(s1, s0, kt + 1);
-    }
-    if (kt < KT) stage(s0, s1, kt);
-    __syncthreads();   // LDS free for the caller's epilogue
-}
-
 template <class P, class D>
 __device__ __forceinline__ void mainloop(int8_t *s0, int8_t *s1, const D &d, int K, AccTile<P> &acc) {
     static_assert(!P::SUMS, "this policy needs its operand sums");
-    if constexpr (P::Cfg::PIPE == 4) {
-        mainloop_p4<P>(s0, s1, d, K, acc);
-        return;
-    }
     typename P::Sums none;
     mainloop<P>(s0, s1, d, K, acc, none);
 }

@@ -170,7 +170,7 @@ int32_t launch_rrr(const S8Args &p, hipStream_t stream) {
 
 // Fast path: M, N multiples of 256, K % 128 == 0, 16-byte aligned rows ->
 // LDS-DMA mainloop, 8 waves (2 x 4) of 128 x 64, v_mfma_i32_16x16x64_i8.
-typedef mfma2::Cfg<2, 4, 0> DmaCfg;
+typedef mfma2::Cfg<2, 4> DmaCfg;
 
 // int8 outputs of a whole tile through LDS: each wave's 128 x 64 bytes are
 // staged (8 KiB per wave; LDS is free after the mainloop's last barrier) and

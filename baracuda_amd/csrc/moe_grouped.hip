@@ -193,7 +193,7 @@ __global__ __launch_bounds__(NT, 1) void moe_grouped_kernel(MoeArgs p) {
 // Fast path: K % 128 == 0, N % 256 == 0, 16-byte aligned operands.  A rows
 // are gathered per tile row (token rows of the expert's segment), B is the
 // expert's weight slab.
-typedef mfma2::Cfg<2, 4, 0> DmaCfg;
+typedef mfma2::Cfg<2, 4> DmaCfg;
 
 // Workgroup id -> (slot, n-tile).  Workgroups are dispatched round-robin
 // over the 8 XCDs; the id is regrouped so each XCD owns a contiguous range of
