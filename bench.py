@@ -61,6 +61,32 @@ def time_launches(fn, steps, warmup, stream, warm_ms=0.0):
     return start.elapsed_time(end) / steps
 
 
+def graph_us(fn, per_graph=100, replays=20):
+    """Device time per call of a capture-safe launch: `per_graph` calls
+    captured into one HIP graph, replayed; no host launch gaps."""
+    import torch
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()                                  # warm the path outside capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        for _ in range(per_graph):
+            fn()
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    st.record()
+    for _ in range(replays):
+        g.replay()
+    en.record()
+    torch.cuda.synchronize()
+    return st.elapsed_time(en) * 1e3 / (replays * per_graph)
+
+
 def cpu_cores():
     try:
         n = len(os.sched_getaffinity(0))
@@ -380,7 +406,7 @@ def main():
                 eo = torch.empty((1, D), dtype=dt, device=dev)
                 ep = P.EmbeddingPlan.select(P.EmbeddingDescriptor(V, D, 1, None, P._EMBED_KIND[dt]))
                 ems = time_launches(lambda: ep.run(ew, eidx, eo, stream=stream), 200, 20, stream, warm_ms=30.0)
-                e[name] = {"us": round(ems * 1e3, 2)}
+                e[name] = {"us": round(ems * 1e3, 2), "graph_replay_us": round(graph_us(lambda: ep.run(ew, eidx, eo)), 2)}
                 del ew
             extra["embedding_v32000_d4096_n1"] = e
         if only in ("", "gather"):
@@ -392,8 +418,10 @@ def main():
                 idx = torch.randint(0, V, (nr,), dtype=torch.int32, device=dev).view(torch.uint32)
                 dst = torch.empty((nr, H), dtype=torch.bfloat16, device=dev)
                 gms = time_launches(lambda: P.gather_rows(dst, table, idx, stream=stream), 200, 20, stream, warm_ms=30.0)
+                gg = graph_us(lambda: P.gather_rows(dst, table, idx))
                 nb = 2 * nr * H * 2 + 4 * nr
-                g[f"n{nr}"] = {"us": round(gms * 1e3, 2), "GB_s": round(nb / (gms * 1e-3) / 1e9, 1)}
+                g[f"n{nr}"] = {"us": round(gms * 1e3, 2), "GB_s": round(nb / (gms * 1e-3) / 1e9, 1),
+                               "graph_replay_us": round(gg, 2)}
             extra["gather_rows_bf16_128256x4096"] = g
             del table
 
