@@ -190,12 +190,15 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(see DESIGN.md for how the path would shard). Run with --gpus 1.", file=sys.stderr)
+              "Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
     import torch
 
+    from baracuda_amd.build import LIB, build as build_lib
+    if not LIB.exists():          # load what is built; build only when nothing is
+        build_lib(verbose=True)
     from baracuda_amd import plans as P
     from oracle.inputs import w8a8
 

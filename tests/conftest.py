@@ -10,6 +10,11 @@ sys.path.insert(0, str(ROOT))
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
+    # Load what is built; build only when nothing is (hipcc cross-compiles
+    # gfx950 without a GPU).
+    from baracuda_amd.build import LIB, build
+    if not LIB.exists():
+        build(verbose=True)
 
 
 @pytest.fixture(scope="session")
