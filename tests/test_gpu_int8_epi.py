@@ -156,10 +156,11 @@ def _run_u8(epi, bias_kind, a, b, c=None, bias=None, alpha=0.125, beta=0.0, ws=F
     return d.cpu().numpy()
 
 
+@pytest.mark.parametrize("ws", [False, True])
 @pytest.mark.parametrize("bias_kind", [P.ElementKind.F32, P.ElementKind.I32])
 @pytest.mark.parametrize("epi", EPIS)
 @pytest.mark.parametrize("shape", REF_SHAPES + [(256, 256, 128), (512, 512, 256)])
-def test_u8_reference_smoke_pattern(gpu, shape, epi, bias_kind):
+def test_u8_reference_smoke_pattern(gpu, shape, epi, bias_kind, ws):
     if epi == P.EpilogueKind.Identity and bias_kind == P.ElementKind.I32:
         pytest.skip("Identity has no bias")
     m, n, k = shape
@@ -167,7 +168,7 @@ def test_u8_reference_smoke_pattern(gpu, shape, epi, bias_kind):
     a = ((np.arange(m * k) * 7) % 16).astype(np.uint8).reshape(m, k)
     b = ((np.arange(k * n) * 11) % 14).astype(np.uint8).reshape(k, n)
     bias = _bias(n, bias_kind)
-    got = _run_u8(epi, bias_kind, a, b, bias=bias)
+    got = _run_u8(epi, bias_kind, a, b, bias=bias, ws=ws)
     want = O.gemm_u8_epi(a, b, "rrr", 0.125, 0.0, None, None if epi == P.EpilogueKind.Identity else bias,
                          ACT[epi])
     _check(got, want, epi)
