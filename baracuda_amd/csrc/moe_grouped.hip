@@ -43,13 +43,22 @@ __global__ __launch_bounds__(1024) void moe_offsets_kernel(const int32_t *__rest
     if (num_experts <= 64) {
         const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
         int mine = 0;   // count of expert `lane`
-        for (int base = wave * 64; base < size_m; base += waves * 64) {
-            const int i = base + lane;
-            const int e = i < size_m ? expert_ids[i] : -1;
-            for (int x = 0; x < num_experts; ++x) {
-                const int c = __popcll(__ballot(e == x));
-                if (lane == x) mine += c;
+        // Each wave takes 8 ids per lane per pass, all loads issued before the
+        // first ballot so one memory round trip covers 512 ids.
+        constexpr int V = 8;
+        for (int base = wave * 64 * V; base < size_m; base += waves * 64 * V) {
+            int e[V];
+#pragma unroll
+            for (int v = 0; v < V; ++v) {
+                const int i = base + v * 64 + lane;
+                e[v] = i < size_m ? expert_ids[i] : -1;
             }
+#pragma unroll
+            for (int v = 0; v < V; ++v)
+                for (int x = 0; x < num_experts; ++x) {
+                    const int c = __popcll(__ballot(e[v] == x));
+                    if (lane == x) mine += c;
+                }
         }
         if (lane < num_experts && mine) atomicAdd(&cnt[lane], mine);
     } else {
