@@ -373,10 +373,18 @@ def main():
                 P.dynamic_range_quantize_per_token_sym(qxs[i], qs, qqs[i], stream=stream)
                 qit[0] += 1
             qms = time_launches(quant_step, 120, 12, stream, warm_ms=30.0)
+
+            def quant_cur():   # on the capturing stream, same rotation
+                i = qit[0] % qcop
+                P.dynamic_range_quantize_per_token_sym(qxs[i], qs, qqs[i])
+                qit[0] += 1
+            qg = graph_us(quant_cur, per_graph=96)
             qb = 4096 * 4096 * 3 + 4096 * 4
             extra["quantize_per_token_bf16_4096x4096"] = {
                 "us": round(qms * 1e3, 2), "GB_s": round(qb / (qms * 1e-3) / 1e9, 1),
-                "frac_hbm_peak": round(qb / (qms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4), "copies_rotated": qcop}
+                "frac_hbm_peak": round(qb / (qms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4), "copies_rotated": qcop,
+                "graph_replay_us": round(qg, 2),
+                "graph_replay_frac_hbm_peak": round(qb / (qg * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)}
             del qxs, qqs
         if only in ("", "te"):
             log("bench: fp8 fused cast+amax bf16 14336x4096 -> e4m3")

@@ -296,7 +296,7 @@ def _quant_gpu(x, dtype, qmin=-127, qmax=127):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.bfloat16])
 @pytest.mark.parametrize("shape", [(64, 4096), (7, 333), (3, 20000), (1, 1), (5, 16384), (9, 24), (6, 8192),
-                                   (5, 8200), (13, 8)])
+                                   (5, 8200), (13, 8), (4, 2048), (4, 2056), (4, 4104)])
 def test_quantize_per_token_bit_exact(gpu, dtype, shape):
     print(f"case: quantize {dtype} {shape}", flush=True)
     g = rng(shape[0] * 31 + shape[1])
