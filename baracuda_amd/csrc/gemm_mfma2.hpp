@@ -609,7 +609,9 @@ __device__ __forceinline__ void store_w8a8_bf16_staged(const AccTile<P> &acc, in
         uint16_t *dst = row_dst(row);
         if (dst == nullptr) continue;
         const v4i v = *reinterpret_cast<const v4i *>(scratch + row * 128 + ((u ^ (row & 7)) << 4));
-        *reinterpret_cast<v4i *>(dst + u * 8) = v;
+        // Non-temporal: the 32 MiB output of a 4096^2 tile grid streams past
+        // the caches instead of evicting the operands still being read.
+        __builtin_nontemporal_store(v, reinterpret_cast<v4i *>(dst + u * 8));
     }
 }
 
@@ -641,7 +643,7 @@ __device__ __forceinline__ void store_u8x4_staged(const AccTile<P> &acc, int8_t 
     for (int q = 0; q < C::WM / 16; ++q) {
         const int r = q * 16 + (lane >> 2), u = lane & 3;
         const v4i v = *reinterpret_cast<const v4i *>(scratch + r * 64 + ((u ^ ((r >> 2) & 3)) << 4));
-        *reinterpret_cast<v4i *>(row_dst(r) + u * 16) = v;
+        __builtin_nontemporal_store(v, reinterpret_cast<v4i *>(row_dst(r) + u * 16));
     }
 }
 
@@ -673,7 +675,7 @@ __device__ __forceinline__ void store_bf16x4_staged(const AccTile<P> &acc, int8_
         const int r = q * 8 + (lane >> 3), u = lane & 7;
         const v4i v = *reinterpret_cast<const v4i *>(scratch + r * 128 + ((u ^ (r & 7)) << 4));
         uint16_t *dst = row_dst(r);   // nullptr: row not stored
-        if (dst != nullptr) *reinterpret_cast<v4i *>(dst + u * 8) = v;
+        if (dst != nullptr) __builtin_nontemporal_store(v, reinterpret_cast<v4i *>(dst + u * 8));
     }
 }
 
