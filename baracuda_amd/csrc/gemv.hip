@@ -69,7 +69,7 @@ __device__ __forceinline__ float dot16_s8_bf16(const v4i w, const v4i xlo, const
 // Fast path: K % 1024 == 0, 16-byte aligned rows; one wave per workgroup
 // (finer dispatch than 4-wave groups: 11.9 vs 12.4 us at 14336 x 4096).
 // Each wave writes its two outputs with one 4-byte store.
-template <int ROWS>
+template <int ROWS, int B>
 __global__ __launch_bounds__(64) void gemv_s8w_m1_kernel(
     int N, int K, const uint16_t *__restrict__ x, const int8_t *__restrict__ w, int64_t ldw,
     const float *__restrict__ scale, uint16_t *__restrict__ d) {
@@ -81,22 +81,41 @@ __global__ __launch_bounds__(64) void gemv_s8w_m1_kernel(
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) wr[r] = w + (int64_t)min(row0 + r, N - 1) * ldw + lane * 16;
     const v4i *xv = reinterpret_cast<const v4i *>(x) + lane * 2;
+    // The row scales are fetched up front: loaded after the reduction, their
+    // latency would add to every wave's tail.
+    float sc[ROWS];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) sc[r] = scale[min(row0 + r, N - 1)];
     float acc[ROWS];
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) acc[r] = 0.0f;
-#pragma unroll 4
-    for (int c = 0; c < chunks; ++c) {
-        v4i wv[ROWS];
+    // Batches of B K-chunks (B divides the chunk count): every load of a
+    // batch is issued before its first dot product, so a wave keeps B KiB of
+    // each row in flight (one batch of 4 covers K = 4096).
+    for (int c0 = 0; c0 < chunks; c0 += B) {
+        v4i wv[B][ROWS], xlo[B], xhi[B];
 #pragma unroll
-        for (int r = 0; r < ROWS; ++r)
-            wv[r] = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(wr[r] + (int64_t)c * 1024));
-        const v4i xlo = xv[c * 128], xhi = xv[c * 128 + 1];
+        for (int u = 0; u < B; ++u)
 #pragma unroll
-        for (int r = 0; r < ROWS; ++r) acc[r] = dot16_s8_bf16(wv[r], xlo, xhi, acc[r]);
+            for (int r = 0; r < ROWS; ++r)
+                wv[u][r] = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(wr[r] + (int64_t)(c0 + u) * 1024));
+        // Keep the weight loads ahead of everything else: the scheduler would
+        // otherwise interleave them with the dot products one load at a time.
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+            xlo[u] = xv[(c0 + u) * 128];
+            xhi[u] = xv[(c0 + u) * 128 + 1];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < B; ++u)
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) acc[r] = dot16_s8_bf16(wv[u][r], xlo[u], xhi[u], acc[r]);
     }
     uint16_t o[ROWS];
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r) o[r] = f32_to_bf16_rne(wave_sum_lane63(acc[r]) * scale[min(row0 + r, N - 1)]);
+    for (int r = 0; r < ROWS; ++r) o[r] = f32_to_bf16_rne(wave_sum_lane63(acc[r]) * sc[r]);
     if (lane == 63) {
         if (ROWS == 2 && row0 + 1 < N && (reinterpret_cast<uintptr_t>(d + row0) & 3u) == 0) {
             *reinterpret_cast<uint32_t *>(d + row0) = (uint32_t)o[0] | ((uint32_t)o[ROWS - 1] << 16);
@@ -338,9 +357,16 @@ int32_t baracuda_kernels_gemv_s8w_m1_bf16_gfx950_run(int32_t n, int32_t k, const
                       (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
     if (fast) {
         const int waves = (n + kGemvRows - 1) / kGemvRows;
-        hipLaunchKernelGGL((gemv_s8w_m1_kernel<kGemvRows>), dim3(waves), dim3(64), 0, stream, n, k,
-                           (const uint16_t *)x,
-                           (const int8_t *)w, ldw, (const float *)scale, (uint16_t *)d);
+        const int chunks = k / 1024;
+        if (chunks % 4 == 0)
+            hipLaunchKernelGGL((gemv_s8w_m1_kernel<kGemvRows, 4>), dim3(waves), dim3(64), 0, stream, n, k,
+                               (const uint16_t *)x, (const int8_t *)w, ldw, (const float *)scale, (uint16_t *)d);
+        else if (chunks % 2 == 0)
+            hipLaunchKernelGGL((gemv_s8w_m1_kernel<kGemvRows, 2>), dim3(waves), dim3(64), 0, stream, n, k,
+                               (const uint16_t *)x, (const int8_t *)w, ldw, (const float *)scale, (uint16_t *)d);
+        else
+            hipLaunchKernelGGL((gemv_s8w_m1_kernel<kGemvRows, 1>), dim3(waves), dim3(64), 0, stream, n, k,
+                               (const uint16_t *)x, (const int8_t *)w, ldw, (const float *)scale, (uint16_t *)d);
     } else {
         hipLaunchKernelGGL(gemv_s8w_m1_generic_kernel, dim3((n + kGemvWaves - 1) / kGemvWaves),
                            dim3(64 * kGemvWaves), 0, stream, n, k, (const uint16_t *)x,

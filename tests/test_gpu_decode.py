@@ -42,7 +42,8 @@ def _gemv_run(w, scale, xb):
     return host_bits16(d)
 
 
-@pytest.mark.parametrize("shape", [(14336, 4096), (4096, 14336), (1, 1024), (77, 3000), (1000, 17)])
+@pytest.mark.parametrize("shape", [(14336, 4096), (4096, 14336), (1, 1024), (77, 3000), (1000, 17), (5, 5120),
+                                   (3, 12288)])
 def test_gemv_s8w(gpu, shape):
     print(f"case: gemv_s8w {shape}", flush=True)
     w, scale, xb = _gemv_inputs(*shape)
