@@ -2,7 +2,9 @@
 
 Headline (BASELINE.json metric, config 2): W8A8 int8 GEMM, M=N=K=4096, RCR,
 per-token x per-channel dequant to bf16, TOPS and fraction of the int8 MFMA
-peak.  A "step" is one GEMM launch over the resident inputs.  The same JSON
+peak.  A "step" is one GEMM launch over inputs resident in HBM; the timed
+launches rotate over 8 operand/output sets (537 MB, over twice the 256 MB
+Infinity Cache), so every launch reads its operands from HBM.  The same JSON
 line carries the roofline of the dominant kernel, the CPU baseline (the
 oracle's restatement of the reference CPU path on a bounded row sample) and
 secondary figures (m=1 GEMV HBM GB/s, FP8 GEMM, grouped MoE, gather_rows).
