@@ -147,7 +147,7 @@ __global__ __launch_bounds__(kQBlock) void quantize_per_token_bf16v_kernel(
                 if (h < 2) lo |= pair << (16 * h);
                 else hi |= pair << (16 * (h - 2));
             }
-            *reinterpret_cast<v2i *>(qrow + 8 * c) = v2i{(int)lo, (int)hi};
+            __builtin_nontemporal_store(v2i{(int)lo, (int)hi}, reinterpret_cast<v2i *>(qrow + 8 * c));
         }
         __syncthreads();   // `red` is reused by the next row
     }

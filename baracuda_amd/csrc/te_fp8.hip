@@ -55,12 +55,12 @@ template <> __device__ inline void te_st<BF16>(BF16 *p, float v) { p->bits = f32
 template <typename T>
 __device__ inline void te_ld8(const T *p, float (&v)[8]) {
     if constexpr (sizeof(T) == 4) {
-        const v4f a = *reinterpret_cast<const v4f *>(p);
-        const v4f b = *reinterpret_cast<const v4f *>(p + 4);
+        const v4f a = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(p));
+        const v4f b = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(p + 4));
 #pragma unroll
         for (int i = 0; i < 4; ++i) { v[i] = a[i]; v[4 + i] = b[i]; }
     } else {
-        const v4i w = *reinterpret_cast<const v4i *>(p);
+        const v4i w = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(p));
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t u = (uint32_t)w[i];
@@ -119,7 +119,7 @@ __global__ __launch_bounds__(kTeBlock) void te_cast_amax_kernel(const T *__restr
                 }
                 const uint32_t lo = f32x4_to_fp8x4_satfinite<FMT>(y[0], y[1], y[2], y[3]);
                 const uint32_t hi = f32x4_to_fp8x4_satfinite<FMT>(y[4], y[5], y[6], y[7]);
-                *reinterpret_cast<v2i *>(out + 8 * u) = v2i{(int)lo, (int)hi};
+                __builtin_nontemporal_store(v2i{(int)lo, (int)hi}, reinterpret_cast<v2i *>(out + 8 * u));
             }
         }
         const int64_t t0 = units << 3;
