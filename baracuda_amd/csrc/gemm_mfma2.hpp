@@ -423,9 +423,13 @@ __device__ __forceinline__ DmaOperand<true> make_dma_gathered(const int8_t *base
 // inline asm so the compiler's wait-count pass does not treat consecutive
 // DMAs into one buffer as dependent (it would wait vmcnt(0) before each);
 // completion is awaited explicitly by wait_dma() before the stage barrier.
+// The M0 value is the low 32 bits of the generic address: in the LDS
+// aperture those are the LDS byte offset, and taking them directly avoids
+// the null-pointer select of an address-space cast, so the whole destination
+// computation stays in scalar registers (callers pass a wave-uniform
+// pointer built from a readfirstlane wave index).
 __device__ __forceinline__ void dma16(const v4i &rsrc, int voff, int soff, const int8_t *lds_dst) {
-    const uint32_t lds = __builtin_amdgcn_readfirstlane(
-        (uint32_t)reinterpret_cast<uintptr_t>((lds_void *)lds_dst));
+    const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)reinterpret_cast<uintptr_t>(lds_dst));
     asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                  :
                  : "s"(lds), "v"(voff), "s"(rsrc), "s"(soff)
@@ -437,7 +441,7 @@ __device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" :
 template <class C>
 __device__ __forceinline__ void dma_operand(int8_t *dst, const DmaOperand<false> &d, int kbyte) {
     constexpr int ROWS_PER_WAVE = C::ROWS_PER_WAVE;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 #pragma unroll
     for (int i = 0; i < C::DMA_PER_WAVE; ++i) {
         const int soff = __builtin_amdgcn_readfirstlane(kbyte + i * d.row_stride);
@@ -448,7 +452,7 @@ __device__ __forceinline__ void dma_operand(int8_t *dst, const DmaOperand<false>
 template <class C>
 __device__ __forceinline__ void dma_operand(int8_t *dst, const DmaOperand<true> &d, int kbyte) {
     constexpr int ROWS_PER_WAVE = C::ROWS_PER_WAVE;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int soff = __builtin_amdgcn_readfirstlane(kbyte);
 #pragma unroll
     for (int i = 0; i < C::DMA_PER_WAVE; ++i) dma16(d.rsrc, d.off[i], soff, dst + (wave * ROWS_PER_WAVE + i * 8) * BK);
@@ -484,7 +488,7 @@ __device__ __forceinline__ DmaOperandRowB make_dma_row_b(const int8_t *base, uin
 
 template <class C>
 __device__ __forceinline__ void dma_operand(int8_t *dst, const DmaOperandRowB &d, int kbyte) {
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int soff = __builtin_amdgcn_readfirstlane((kbyte + 4 * i) * d.ld);
@@ -520,6 +524,9 @@ __device__ __forceinline__ void stage_step(AccTile<P> &acc, Frags<P> &f0, Frags<
     load_frags<P>(f0, cur, 0, wave_m, wave_n, lane);
     if constexpr (P::FLIP) P::fixup(f0, sums);
     mma_block<P, 0, P::TJ>(acc, f0);
+    // u8: the flip's temporaries leave no room for both fragment sets, so the
+    // second sub-step's reads are not hoisted over the first's MFMAs.
+    if constexpr (P::FLIP) __builtin_amdgcn_sched_barrier(0);
     load_frags<P>(f1, cur, 1, wave_m, wave_n, lane);
     if constexpr (P::FLIP) P::fixup(f1, sums);
     mma_block<P, 0, P::TJ>(acc, f1);
