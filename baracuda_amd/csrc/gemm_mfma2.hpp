@@ -569,6 +569,30 @@ __device__ __forceinline__ void mainloop(int8_t *s0, int8_t *s1, const D &d, int
     mainloop<P>(s0, s1, d, K, acc, none);
 }
 
+// The DMA and barrier sequence of mainloop() without fragment reads or
+// MFMAs, for a wave whose output rows are all padding: it still moves its
+// share of every stage and meets every barrier of the waves that compute.
+template <class C, class D>
+__device__ __forceinline__ void mainloop_dma_only(int8_t *s0, int8_t *s1, const D &d, int K) {
+    const int KT = K / BK;
+    dma_stage<C>(s0, d, 0);
+    wait_dma();
+    __syncthreads();
+    int kt = 0;
+    for (; kt + 2 <= KT; kt += 2) {
+        dma_stage<C>(s1, d, (kt + 1) * BK);
+        wait_dma();
+        __syncthreads();
+        if (kt + 2 < KT) dma_stage<C>(s0, d, (kt + 2) * BK);
+        wait_dma();
+        __syncthreads();
+    }
+    if (kt < KT) {
+        wait_dma();
+        __syncthreads();
+    }
+}
+
 // W8A8 bf16 epilogue for the int8 16x16 policy, staged through LDS so each
 // output row segment of the wave tile (WN bf16 = 128 bytes for WN = 64) is
 // written with full-line 16-byte stores.

@@ -246,6 +246,12 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void moe_grouped_dma_kernel(MoeArgs 
                                         [&](int r) { return (s_rows_tok[r] / in_div) * kb; });
     d.b = M2::make_dma_interior<DmaCfg>(p.w + (int64_t)e * p.N * kb, (uint32_t)((int64_t)p.N * kb),
                                         kb, n_base * kb);
+    // A wave whose 128 tile rows are all padding (the expert's last tile
+    // holds at most 128 rows) only moves its share of each stage.
+    if ((int)((threadIdx.x >> 6) / DmaCfg::WAVES_N) * DmaCfg::WM >= seg_rows) {
+        M2::mainloop_dma_only<DmaCfg>(stage0, stage1, d, kb);
+        return;
+    }
     M2::AccTile<P> acc;
     M2::mainloop<P>(stage0, stage1, d, kb, acc);
     if constexpr (KIND != MOE_S8) {
