@@ -349,7 +349,7 @@ def main():
             del ia, ib, ibr, idd
         if only in ("", "gemv"):
             # gemv_dense_m1 (reference ABI, RRR B[K,N]) at the reference's own skinny
-            # f32 contraction shape M=1, K=N=4096 (BASELINE adjacent figure).
+            # f32 contraction shape M=1, K=N=4096 (a figure adjacent to the BASELINE.json metric).
             log("bench: gemv_dense_m1 f32 / bf16 4096x4096")
             gd = {}
             for dt, name, es in ((torch.float32, "f32", 4), (torch.bfloat16, "bf16", 2)):
@@ -486,10 +486,10 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
-        "data": "synthetic (seeded PCG64 int8 U[-127,127], scales U per BASELINE config 2); "
+        "data": "synthetic (seeded PCG64 int8 U[-127,127], scales U per BASELINE.json config 2); "
                 "8 operand/output sets rotated so every launch reads HBM",
         "config": {"workload": "W8A8 int8 GEMM M=N=K=4096, RCR, per-token x per-channel f32 scales, "
-                               "int32 acc, bf16 out (BASELINE config 2)",
+                               "int32 acc, bf16 out (BASELINE.json config 2)",
                    "m": M, "n": N, "k": K, "layout": "rcr", "out": "bf16", "operand_sets_rotated": HEAD_SETS},
         "roofline": None if not ms else {
             "bound": "mfma", "achieved": round(tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",

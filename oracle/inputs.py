@@ -1,4 +1,4 @@
-"""Seeded synthetic inputs for the BASELINE configurations (test infrastructure).
+"""Seeded synthetic inputs for the BASELINE.json configurations (test infrastructure).
 
 One generator for every consumer (tests, smoke, bench's CPU leg):
 numpy PCG64 seeded with the config index (1-5) unless a test passes its own.

@@ -193,7 +193,7 @@ def test_gather_rows_oob_and_ragged(gpu, dt):
 
 
 def test_gather_rows_config4_bf16_table(gpu):
-    # BASELINE config 4b: bf16 [128256, 4096] ~ N(0, 0.02), n in {1, 8, 64}.
+    # BASELINE.json config 4b: bf16 [128256, 4096] ~ N(0, 0.02), n in {1, 8, 64}.
     V, H = 128256, 4096
     gen = torch.Generator(device="cuda:0").manual_seed(4)
     table = (torch.randn((V, H), generator=gen, device="cuda:0") * 0.02).to(torch.bfloat16)

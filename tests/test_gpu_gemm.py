@@ -150,7 +150,7 @@ def test_w8a8_bf16_bit_exact(gpu, shape):
 
 
 def test_w8a8_config2_full_size_sampled_rows(gpu):
-    # BASELINE config 2: 4096^3; every row sampled below is compared bit-exact,
+    # BASELINE.json config 2: 4096^3; every row sampled below is compared bit-exact,
     # plus size-independent checks on the whole output.
     print("case: w8a8 4096^3", flush=True)
     a, w, sa, sw = w8a8(4096, 4096, 4096, seed=2)
@@ -192,7 +192,7 @@ def test_int8_determinism_replays(gpu):
 
 # ---- FP8 ---------------------------------------------------------------------
 def _fp8_inputs(m, n, k, seed=3):
-    # BASELINE config 3 recipe: N(0,1), scale absmax -> 448, cast to e4m3.
+    # BASELINE.json config 3 recipe: N(0,1), scale absmax -> 448, cast to e4m3.
     g = rng(seed)
     xa = g.standard_normal((m, k)).astype(np.float32)
     xb = g.standard_normal((n, k)).astype(np.float32)

@@ -79,7 +79,7 @@ def test_moe_oracle_grouped_agrees(gpu):
 
 
 def test_moe_config5_full_size_sampled(gpu):
-    # BASELINE config 5: 8 experts, hidden 4096, ffn 14336, 4096 tokens top-2 Zipf(1.1).
+    # BASELINE.json config 5: 8 experts, hidden 4096, ffn 14336, 4096 tokens top-2 Zipf(1.1).
     print("case: moe config5", flush=True)
     pairs = [0, 1, 2, 8191, 4095] + list(rng(51).integers(0, 8192, 27))
     _run(tokens=4096, E=8, topk=2, n=14336, k=4096, seed=5, pairs_check=pairs)
