@@ -30,7 +30,7 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E, GB/s
 # HBM bytes per launch measured with rocprofv3 PMC (FETCH_SIZE x2.00 and
 # WRITE_SIZE x1.00, scales calibrated on a plain device copy); the runs and
 # raw readings are in profiles/path_kernels_hbm_traffic.md.
-TRAFFIC_W8A8_4096 = 49278.5 * 1024 * 2 + 32904.0 * 1024   # FETCH_SIZE x2 + WRITE_SIZE (KiB), profiles/path_kernels_hbm_traffic.md
+TRAFFIC_W8A8_4096 = 49278.5 * 1024 * 2 + 32914.9 * 1024   # FETCH_SIZE x2 + WRITE_SIZE (KiB), profiles/path_kernels_hbm_traffic.md
 TRAFFIC_GEMV_14336x4096 = 29180.5 * 1024 * 2.0 + 224.0 * 1024 * 1.0
 
 
