@@ -11,8 +11,8 @@ from tests.gpu_util import dev, host_bits16, sync
 pytestmark = pytest.mark.gpu
 
 
-def _run(tokens, E, topk, n, k, seed, topk_w=False, pairs_check=None):
-    sorted_ids, expert_ids = moe_routing(tokens, E, topk, seed=seed)
+def _run(tokens, E, topk, n, k, seed, topk_w=False, pairs_check=None, routing=None):
+    sorted_ids, expert_ids = routing if routing is not None else moe_routing(tokens, E, topk, seed=seed)
     size_m = tokens * topk
     g = rng(seed + 100)
     x, w = int8_uniform(g, (tokens, k)), int8_uniform(g, (E, n, k))
@@ -109,3 +109,20 @@ def test_expert_counting_any_order(gpu, E):
     assert np.array_equal(counts.cpu().numpy(), c_ref)
     assert np.array_equal(offs.cpu().numpy(), o_ref)
     assert np.array_equal(c_ref, np.bincount(valid, minlength=E))
+
+
+def _block_routing(counts, seed):
+    # top-1 routing with exact per-expert row counts, tokens shuffled
+    tokens = sum(counts)
+    pair_expert = np.repeat(np.arange(len(counts), dtype=np.int32), counts)
+    rng(seed).shuffle(pair_expert)
+    order = np.argsort(pair_expert, kind="stable").astype(np.int32)
+    return tokens, (order, pair_expert[order].astype(np.int32))
+
+
+def test_moe_dma_partial_tile_boundaries(gpu):
+    # Last tiles of 1, 128 and 129 rows (the first two leave the second half
+    # of the wave grid with padding rows only), a full tile, an empty expert.
+    print("case: moe partial tile boundaries", flush=True)
+    tokens, routing = _block_routing([257, 128, 0, 129, 256], seed=12)
+    _run(tokens=tokens, E=5, topk=1, n=512, k=256, seed=12, routing=routing)

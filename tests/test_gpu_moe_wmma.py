@@ -97,3 +97,19 @@ def test_random_routing(gpu, shape, t, topk_w):
     tw = g.uniform(0.1, 1.0, size_m).astype(np.float32) if topk_w else None
     got, exact, absx = _run(t, x, w, sid, eid, topk, tw, size_m, is_prefill=tokens > 256)
     _check(got, exact, absx, t)
+
+
+@pytest.mark.parametrize("t", ["bf16", "f16"])
+def test_partial_tile_boundaries(gpu, t):
+    # LDS-DMA path with last tiles of 1, 128 and 129 rows and an empty expert.
+    counts = [257, 128, 0, 129]
+    tokens = sum(counts)
+    pair_expert = np.repeat(np.arange(len(counts), dtype=np.int32), counts)
+    rng(13).shuffle(pair_expert)
+    sid = np.argsort(pair_expert, kind="stable").astype(np.int32)
+    eid = pair_expert[sid].astype(np.int32)
+    g = rng(14)
+    x = g.standard_normal((tokens, 256)).astype(np.float32)
+    w = (g.standard_normal((len(counts), 256, 256)) * 0.1).astype(np.float32)
+    got, exact, absx = _run(t, x, w, sid, eid, 1, None, tokens, is_prefill=True)
+    _check(got, exact, absx, t)
