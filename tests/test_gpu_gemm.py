@@ -94,6 +94,43 @@ def test_i32_extreme_values_no_overflow(gpu):
     assert np.all(got == 128 * 127 * k)
 
 
+@pytest.mark.parametrize("pads", [(128, 64), (16, 16), (0, 4096)])
+def test_w8a8_dma_path_strided_operands(gpu, pads):
+    # Whole 256x256 tiles with lda = K + pad_a, ldb = K + pad_b (16-byte
+    # multiples): the LDS-DMA path with row pitches other than K.
+    m, n, k = 512, 512, 384
+    pa, pb = pads
+    print(f"case: w8a8 dma strided lda={k + pa} ldb={k + pb}", flush=True)
+    g = rng(31 + pa + pb)
+    af = int8_uniform(g, (m, k + pa))
+    bf = int8_uniform(g, (n, k + pb))
+    sa = g.uniform(0.005, 0.02, m).astype(np.float32)
+    sw = g.uniform(0.001, 0.01, n).astype(np.float32)
+    d = torch.empty((m, n), dtype=torch.bfloat16, device="cuda:0")
+    P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, output=P.ElementKind.Bf16)).run(
+        dev(af)[:, :k], dev(bf)[:, :k], d, scale_a=dev(sa), scale_b=dev(sw))
+    sync()
+    want = O.gemm_w8a8_bf16(np.ascontiguousarray(af[:, :k]), np.ascontiguousarray(bf[:, :k]), sa, sw, nthreads=8)
+    assert np.array_equal(host_bits16(d), want)
+
+
+def test_fp8_dma_path_strided_operands_match_contiguous(gpu):
+    # The same operands once contiguous and once with lda = K + 128, ldb =
+    # K + 256: the LDS-DMA kernel runs the same MFMA sequence, so the bf16
+    # outputs are bit-identical.
+    m, n, k = 512, 768, 512
+    g = rng(41)
+    af = torch.from_numpy(O.f32_to_fp8(g.standard_normal((m, k + 128)).astype(np.float32), "e4m3")).to("cuda:0")
+    bf = torch.from_numpy(O.f32_to_fp8(g.standard_normal((n, k + 256)).astype(np.float32), "e4m3")).to("cuda:0")
+    plan = P.Fp8GemmPlan.select(P.Fp8GemmDescriptor(m, n, k, output=P.ElementKind.Bf16))
+    d1 = torch.empty((m, n), dtype=torch.bfloat16, device="cuda:0")
+    d2 = torch.empty((m, n), dtype=torch.bfloat16, device="cuda:0")
+    plan.run(af[:, :k], bf[:, :k], d1, scale_a=0.5, scale_b=0.25)
+    plan.run(af[:, :k].contiguous(), bf[:, :k].contiguous(), d2, scale_a=0.5, scale_b=0.25)
+    sync()
+    assert torch.equal(d1.view(torch.int16), d2.view(torch.int16))
+
+
 def test_i32_strided_leading_dims(gpu):
     g = rng(9)
     m, n, k, lda, ldb, ldd = 200, 136, 96, 112, 128, 160
