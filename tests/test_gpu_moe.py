@@ -126,3 +126,10 @@ def test_moe_dma_partial_tile_boundaries(gpu):
     print("case: moe partial tile boundaries", flush=True)
     tokens, routing = _block_routing([257, 128, 0, 129, 256], seed=12)
     _run(tokens=tokens, E=5, topk=1, n=512, k=256, seed=12, routing=routing)
+
+
+def test_moe_dma_path_many_experts(gpu):
+    # 80 experts (the LDS-counter path of the offsets kernel) on the LDS-DMA
+    # GEMM: mostly single partial tiles, some experts empty.
+    print("case: moe 80 experts", flush=True)
+    _run(tokens=600, E=80, topk=2, n=256, k=256, seed=21)
