@@ -405,3 +405,25 @@ def test_quantized_linear_plan_two_pass(gpu, dtype):
         assert np.array_equal(out.cpu().numpy(), want)
     else:
         assert np.array_equal(host_bits16(out), O.f32_to_bf16_bits_fast(want))
+
+
+def test_i32_operand_beyond_2gib(gpu):
+    # A is 16384 x 131200 int8 (2.0 GiB): past the 32-bit buffer offsets of
+    # the LDS-DMA path, so the general kernel (64-bit row addressing) runs.
+    # Sampled rows are compared exactly against an int64 dot product.
+    m, n, k = 16384, 256, 131200
+    print(f"case: i32 beyond 2 GiB {m}x{n}x{k}", flush=True)
+    gen = torch.Generator(device="cuda:0").manual_seed(77)
+    a = torch.randint(-127, 128, (m, k), dtype=torch.int8, device="cuda:0", generator=gen)
+    b = torch.randint(-127, 128, (n, k), dtype=torch.int8, device="cuda:0", generator=gen)
+    assert m * k >= 2 ** 31
+    d = torch.empty((m, n), dtype=torch.int32, device="cuda:0")
+    P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, output=P.ElementKind.I32)).run(a, b, d)
+    sync()
+    rows = [0, 1, 8191, 16383] + list(rng(78).integers(0, m, 4))
+    bh = b.cpu().numpy().astype(np.int64)
+    got = d[rows].cpu().numpy()
+    for i, r in enumerate(rows):
+        want = bh @ a[r].cpu().numpy().astype(np.int64)
+        assert np.array_equal(got[i], want.astype(np.int32)), r
+    del a
