@@ -209,3 +209,23 @@ def test_gather_rows_config4_bf16_table(gpu):
         # oracle on the gathered rows only (remapped indices 0..n-1), bit-exact
         want = O.gather_rows(rows, np.arange(n, dtype=np.uint32))
         assert np.array_equal(dest.cpu().view(torch.int16).numpy(), want)
+
+
+def test_gemv_s8w_weights_beyond_2gib(gpu):
+    # W is 262144 x 8192 int8 (2 GiB): 64-bit row addressing; sampled rows
+    # within 1 bf16 ulp of the exact f64 value.
+    n, k = 262144, 8192
+    print(f"case: gemv_s8w beyond 2 GiB {n}x{k}", flush=True)
+    gen = torch.Generator(device="cuda:0").manual_seed(91)
+    w = torch.randint(-127, 128, (n, k), dtype=torch.int8, device="cuda:0", generator=gen)
+    scale = (torch.rand(n, device="cuda:0", generator=gen) * 0.009 + 0.001)
+    x = torch.randn(k, device="cuda:0", generator=gen).to(torch.bfloat16)
+    d = torch.empty(n, dtype=torch.bfloat16, device="cuda:0")
+    P.GemvS8wPlan.select(n, k).run(x, w, scale, d)
+    sync()
+    rows = [0, 1, 131071, 262143] + list(rng(92).integers(0, n, 4))
+    xb = x.cpu().view(torch.int16).numpy().view(np.uint16)
+    got = host_bits16(d)[rows]
+    wr = w[rows].cpu().numpy()
+    _gemv_check(got, wr, scale[rows].cpu().numpy(), xb)
+    del w
