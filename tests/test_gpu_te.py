@@ -163,3 +163,22 @@ def test_cast_amax_keeps_larger_slot_value(gpu):
         P.Fp8CastPlan.select().run(x, out, r)
         sync()
         assert r.amax_history.cpu().numpy().tolist() == [expect, start]
+
+
+def test_cast_amax_beyond_2g_elements(gpu):
+    # 2^31 + 24 bf16 elements (4 GiB in, 2 GiB out): 64-bit element indices
+    # and the numel % 8 tail; sampled spans bit-exact, amax = max|x| exactly.
+    n = (1 << 31) + 24
+    print(f"case: te cast beyond 2^31 elements n={n}", flush=True)
+    gen = torch.Generator(device="cuda:0").manual_seed(95)
+    x = torch.empty(n, dtype=torch.bfloat16, device="cuda:0")
+    x.normal_(generator=gen)
+    out = torch.empty(n, dtype=torch.uint8, device="cuda:0")
+    r = _recipe("e4m3", hist=2, scale=2.5)
+    P.Fp8CastPlan.select().run(x, out, r)
+    sync()
+    for s0 in (0, (1 << 30) + 8, n - 4096):
+        bits, _ = O.te_cast_amax(x[s0:s0 + 4096].float().cpu().numpy(), 2.5, "e4m3")
+        assert np.array_equal(out[s0:s0 + 4096].cpu().numpy(), bits), s0
+    assert r.amax_history.cpu().numpy()[0] == float(x.abs().max().float().item())
+    del x, out
