@@ -101,7 +101,7 @@ __global__ __launch_bounds__(kQBlock) void quantize_per_token_kernel(
 }
 
 // Vector path for 2-byte inputs (bf16): 16-byte non-temporal loads of 8
-// elements, 8-byte int8 stores; chunk c = tid + kQBlock * i, kChunks chunks
+// elements, 8-byte non-temporal int8 stores; chunk c = tid + kQBlock * i, kChunks chunks
 // (8 * kChunks values) per thread held in registers (D <= 2048 * kChunks,
 // D % 8 == 0, 16-byte aligned rows).  The launcher picks the smallest of
 // 1, 2, 4, 8 chunks that holds the row: fewer registers keep more rows in
