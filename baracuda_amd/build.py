@@ -8,6 +8,7 @@ the source tree).  ``python -m baracuda_amd.build`` runs it.
 from __future__ import annotations
 
 import concurrent.futures as cf
+import hashlib
 import os
 import shutil
 import subprocess
@@ -19,6 +20,8 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libbaracuda_kernels.so"
+# Digest of the sources and flags the library was built from, written beside it.
+STAMP = PKG / "libbaracuda_kernels.so.srchash"
 
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -42,9 +45,35 @@ def _compile(src: Path) -> Path:
     return obj
 
 
+def source_digest() -> str:
+    """SHA-256 over every kernel source, public header and the build flags."""
+    h = hashlib.sha256()
+    h.update(" ".join(HIP_FLAGS[:-2]).encode())
+    files = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.hpp")) + sorted((ROOT / "include").glob("*.h"))
+    for f in files:
+        h.update(f.name.encode())
+        h.update(f.read_bytes())
+    return h.hexdigest()
+
+
+def is_stale() -> bool:
+    """True when the library is missing or was built from other sources."""
+    if not LIB.exists() or not STAMP.exists():
+        return True
+    return STAMP.read_text().strip() != source_digest()
+
+
+def ensure_built(verbose: bool = False) -> Path:
+    """Build only when the library is missing or stale (source digest differs)."""
+    if is_stale():
+        build(verbose=verbose)
+    return LIB
+
+
 def build(verbose: bool = False) -> Path:
     """Compile every kernel source and link the shared library; returns its path."""
     BUILD.mkdir(exist_ok=True)
+    digest = source_digest()
     sources = sorted(CSRC.glob("*.hip"))
     with cf.ThreadPoolExecutor(max_workers=min(8, len(sources))) as ex:
         objs = list(ex.map(_compile, sources))
@@ -54,6 +83,7 @@ def build(verbose: bool = False) -> Path:
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
     os.replace(tmp, LIB)
+    STAMP.write_text(digest + "\n")
     if verbose:
         print(f"built {LIB} from {len(sources)} sources")
     return LIB

@@ -153,6 +153,14 @@ def _need(cond: bool, msg: str) -> None:
         raise InvalidProblem(msg)
 
 
+def _vec(t: Optional[torch.Tensor], n: int, dtype, what: str) -> None:
+    """A dense 1-D vector of exactly n elements: the kernels index it as
+    contiguous memory, so a strided view would be read (or written) wrongly."""
+    _need(t is not None, f"{what} is required")
+    _need(t.dim() == 1 and t.is_contiguous() and t.numel() == n and t.dtype == dtype,
+          f"{what} must be a contiguous 1-D {dtype} vector of {n} elements")
+
+
 def _ld(t: torch.Tensor) -> int:
     _need(t.dim() == 2 and t.stride(1) == 1, "operand must be a 2-D row-major view")
     return t.stride(0)
@@ -259,8 +267,8 @@ class IntGemmPlan:
         if desc.epilogue != EpilogueKind.Identity:
             bdt = torch.float32 if desc.bias_element == ElementKind.F32 else torch.int32
             _need(bias is not None, "Bias* epilogue needs a bias vector")
-            _need(bias.numel() >= desc.n and bias.dtype == bdt and bias.is_contiguous(),
-                  "bias must be a contiguous [N] vector of the descriptor's bias element")
+            _need(bias.dim() == 1 and bias.numel() >= desc.n and bias.dtype == bdt and bias.is_contiguous(),
+                  "bias must be a contiguous 1-D [N] vector of the descriptor's bias element")
 
     def run(self, a, b, d, c=None, alpha=1.0, beta=0.0, scale_a=None, scale_b=None,
             bias=None, workspace=None, stream=None) -> None:
@@ -278,9 +286,8 @@ class IntGemmPlan:
             st = L.gemm_s8_rcr_gfx950_i32_run(desc.m, desc.n, desc.k, _ptr(a), _ld(a), _ptr(b), _ld(b),
                                               _ptr(d), _ld(d), _ptr(workspace), 0, s)
         else:
-            _need(scale_a is not None and scale_b is not None, "W8A8 needs scale_a and scale_b")
-            _need(scale_a.numel() == desc.m and scale_b.numel() == desc.n and
-                  scale_a.dtype == torch.float32 and scale_b.dtype == torch.float32, "scale shape/dtype")
+            _vec(scale_a, desc.m, torch.float32, "W8A8 scale_a")
+            _vec(scale_b, desc.n, torch.float32, "W8A8 scale_b")
             st = L.gemm_w8a8_rcr_gfx950_bf16_run(desc.m, desc.n, desc.k, _ptr(a), _ld(a), _ptr(b), _ld(b),
                                                  _ptr(scale_a), _ptr(scale_b), _ptr(d), _ld(d),
                                                  _ptr(workspace), 0, s)
@@ -437,9 +444,9 @@ class GemvS8wPlan:
 
     def run(self, x, w, scale, d, stream=None) -> None:
         _need(w.dtype == torch.int8 and tuple(w.shape) == (self.n, self.k), "W must be int8 [N, K]")
-        _need(x.dtype == torch.bfloat16 and x.numel() == self.k, "x must be bf16 [K]")
-        _need(scale.dtype == torch.float32 and scale.numel() == self.n, "scale must be f32 [N]")
-        _need(d.dtype == torch.bfloat16 and d.numel() == self.n, "d must be bf16 [N]")
+        _vec(x, self.k, torch.bfloat16, "GEMV x")
+        _vec(scale, self.n, torch.float32, "GEMV scale")
+        _vec(d, self.n, torch.bfloat16, "GEMV d")
         ldw = _ld(w) if self.k > 0 else 1
         st = lib().gemv_s8w_m1_bf16_gfx950_run(self.n, self.k, _ptr(x), _ptr(w), ldw, _ptr(scale),
                                                _ptr(d), None, 0, _stream(stream))
@@ -559,7 +566,16 @@ class MoeS8GroupedPlan:
             scale_a, scale_w, topk_weights=None, stream=None) -> None:
         _need(x.dtype == torch.int8 and w.dtype == torch.int8 and out.dtype == torch.bfloat16, "dtypes")
         _need(w.numel() == self.E * self.n * self.k and x.shape[-1] == self.k, "shapes")
+        _need(x.is_contiguous() and w.is_contiguous() and out.is_contiguous(), "x, w, out contiguous")
         _need(out.numel() >= self.size_m * self.n, "out too small")
+        _vec(sorted_token_ids, self.size_m, torch.int32, "sorted_token_ids")
+        _vec(expert_ids, self.size_m, torch.int32, "expert_ids")
+        _vec(expert_counts, self.E, torch.int32, "expert_counts")
+        _vec(expert_offsets, self.E + 1, torch.int32, "expert_offsets")
+        _vec(scale_a, x.numel() // self.k, torch.float32, "scale_a")
+        _vec(scale_w, self.E * self.n, torch.float32, "scale_w")
+        if topk_weights is not None:
+            _vec(topk_weights, self.size_m, torch.float32, "topk_weights")
         st = lib().moe_s8_grouped_bf16_gfx950_run(
             _ptr(x), _ptr(w), _ptr(sorted_token_ids), _ptr(expert_ids), _ptr(topk_weights), _ptr(out),
             _ptr(expert_counts), _ptr(expert_offsets), self.E, self.topk, self.size_m, self.n, self.k,
@@ -573,7 +589,9 @@ def dynamic_range_quantize_per_token_sym(x, scale, q, qmin=-127, qmax=127, strea
     scale = max|x|/qmax (1 for an all-zero row), q = clamp(rne(x/scale))."""
     _need(x.dim() == 2 and x.is_contiguous() and q.is_contiguous(), "x, q contiguous [N, D]")
     n, d = x.shape
-    _need(tuple(q.shape) == (n, d) and q.dtype == torch.int8 and scale.numel() == n, "q [N,D] int8, scale [N]")
+    _need(tuple(q.shape) == (n, d) and q.dtype == torch.int8, "q must be int8 [N, D]")
+    _need(scale.dim() == 1 and scale.is_contiguous() and scale.numel() == n,
+          "scale must be a contiguous 1-D [N] vector")
     L = lib()
     if x.dtype == torch.float32:
         _need(scale.dtype == torch.float32, "f32 input takes an f32 scale")

@@ -27,6 +27,10 @@ METRIC = "int8/fp8 GEMM TOPS (% MFMA peak) at 4096³; m=1 GEMV HBM GB/s (% peak)
 PEAK_INT8_TOPS = 5000.0     # MI355X dense int8 MFMA, TOP/s
 PEAK_FP8_TFLOPS = 5000.0    # MI355X dense fp8 MFMA, TFLOP/s
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E, GB/s
+# Dense int8 / fp8 MFMA work per clock of the whole chip: 256 CUs x 8192
+# ops/clk (5.03 POP/s at the 2.4 GHz peak engine clock).
+OPS_PER_CLK = 256 * 8192
+HEAD_WARM_MS = 300.0        # wall time the headline kernel runs before its timed launches
 # HBM bytes per launch measured with rocprofv3 PMC (FETCH_SIZE x2.00 and
 # WRITE_SIZE x1.00, scales calibrated on a plain device copy); the runs and
 # raw readings are in profiles/path_kernels_hbm_traffic.md.
@@ -90,11 +94,95 @@ def graph_us(fn, per_graph=100, replays=20):
 
 
 def cpu_cores():
+    """Host threads for the CPU baseline: every core this process may run on,
+    bounded by OMP_NUM_THREADS when the host sets it (the GPU box allots 16
+    cores to a one-GPU job and exports OMP_NUM_THREADS=16; threads beyond a
+    job's share only time-slice)."""
     try:
         n = len(os.sched_getaffinity(0))
     except AttributeError:
         n = os.cpu_count() or 1
-    return max(1, min(n, 16))
+    try:
+        n = min(n, int(os.environ["OMP_NUM_THREADS"]))
+    except (KeyError, ValueError):
+        pass
+    return max(1, n)
+
+
+class ClockSampler:
+    """Samples the GPU's graphics clock (amdsmi gpu_metrics, per-XCD
+    current_gfxclks) from a background thread while the GPU is busy, so the
+    MFMA peak can be restated at the clock the timed kernel actually ran at.
+    Fails soft: every figure is None when amdsmi is unavailable."""
+
+    def __init__(self, period_s=0.004):
+        import threading
+        self.period_s = period_s
+        self.samples = []
+        self.error = None
+        self._stop = threading.Event()
+        self._thr = threading.Thread(target=self._loop, daemon=True)
+        self._h = None
+
+    def _handle(self):
+        import amdsmi
+        import torch
+        amdsmi.amdsmi_init()
+        hs = amdsmi.amdsmi_get_processor_handles()
+        bus = getattr(torch.cuda.get_device_properties(0), "pci_bus_id", None)
+        for h in hs:
+            bdf = amdsmi.amdsmi_get_gpu_device_bdf(h)     # "dddd:bb:dd.f"
+            if bus is not None and int(bdf.split(":")[1], 16) == int(bus):
+                return h
+        return hs[0] if len(hs) == 1 else None
+
+    def _read(self):
+        import amdsmi
+        m = amdsmi.amdsmi_get_gpu_metrics_info(self._h)
+        xs = [v for v in (m.get("current_gfxclks") or []) if isinstance(v, int) and 0 < v < 10000]
+        if xs:
+            return sum(xs) / len(xs)
+        v = m.get("current_gfxclk")
+        return float(v) if isinstance(v, int) and 0 < v < 10000 else None
+
+    def _loop(self):
+        while not self._stop.is_set():
+            try:
+                v = self._read()
+                if v is not None:
+                    self.samples.append(v)
+            except Exception as e:   # noqa: BLE001 -- telemetry only
+                self.error = repr(e)
+                return
+            time.sleep(self.period_s)
+
+    def __enter__(self):
+        try:
+            self._h = self._handle()
+            if self._h is None:
+                self.error = "no amdsmi handle for cuda:0"
+            else:
+                self._thr.start()
+        except Exception as e:   # noqa: BLE001
+            self.error = repr(e)
+        return self
+
+    def __exit__(self, *exc):
+        self._stop.set()
+        if self._thr.is_alive():
+            self._thr.join()
+        return False
+
+    def summary(self):
+        """Mean / min / max MHz over the busy samples (the upper half of the
+        sample range, so idle gaps between host syncs do not count)."""
+        if not self.samples:
+            return {"mhz_mean": None, "samples": 0, "source": "amdsmi current_gfxclks", "error": self.error}
+        xs = sorted(self.samples)
+        busy = xs[len(xs) // 2:]
+        return {"mhz_mean": round(sum(busy) / len(busy), 1), "mhz_min": busy[0], "mhz_max": busy[-1],
+                "samples": len(busy), "source": "amdsmi current_gfxclks (mean over XCDs), sampled while the "
+                                                 "headline kernel ran"}
 
 
 def cpu_baseline_w8a8(a, w, sa, sw, budget_s=15.0):
@@ -202,9 +290,8 @@ def main():
     import numpy as np
     import torch
 
-    from baracuda_amd.build import LIB, build as build_lib
-    if not LIB.exists():          # load what is built; build only when nothing is
-        build_lib(verbose=True)
+    from baracuda_amd.build import ensure_built
+    ensure_built(verbose=True)    # rebuilds when the sources differ from what was built
     from baracuda_amd import plans as P
     from oracle.inputs import w8a8
 
@@ -455,17 +542,24 @@ def main():
             del table
 
     ms = None
+    sclk = {}
     if only in ("", "w8a8"):
         log("bench: w8a8 4096^3")
         torch.cuda.synchronize()
         # The same kernel with one operand set reused every launch (operands
         # and output stay in the Infinity Cache), timed first so that the
         # headline's rotated launches are the last ones a profiler sees.
-        ms_res = time_launches(run_resident, args.steps, args.warmup, stream)
+        ms_res = time_launches(run_resident, args.steps, args.warmup, stream, warm_ms=100.0)
         extra["w8a8_4096_cubed_resident_operands"] = {
             "us": round(ms_res * 1e3, 2), "TOPS": round(ops / (ms_res * 1e-3) / 1e12, 1),
             "note": "one operand set reused every launch; the headline value rotates 8 sets"}
-        ms = time_launches(run, args.steps, 40, stream)
+        # Headline: the kernel itself runs for HEAD_WARM_MS of wall time right
+        # before its timed launches, whatever --warmup is (the clocks settle
+        # under sustained MFMA load; a count-only warm-up of a few launches
+        # times the ramp), while the graphics clock is sampled.
+        with ClockSampler() as clk:
+            ms = time_launches(run, args.steps, args.warmup, stream, warm_ms=HEAD_WARM_MS)
+        sclk = clk.summary()
     tops = ops / (ms * 1e-3) / 1e12 if ms else None
 
     cpu = None
@@ -496,9 +590,15 @@ def main():
                                "int32 acc, bf16 out (BASELINE.json config 2)",
                    "m": M, "n": N, "k": K, "layout": "rcr", "out": "bf16", "operand_sets_rotated": HEAD_SETS},
         "roofline": None if not ms else {
-            "bound": "mfma", "achieved": round(tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
+            "bound": "mfma", "achieved": round(tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
             "frac": round(tops / PEAK_INT8_TOPS, 4), "traffic": int(TRAFFIC_W8A8_4096),
-            "kernel": "gemm_s8_rcr_dma_kernel<EPI_W8A8_BF16, vec> (int8 tera-ops per second)"},
+            "kernel": "gemm_s8_rcr_dma_kernel<EPI_W8A8_BF16, vec> (int8 tera-ops per second)",
+            "sclk": sclk,
+            "peak_at_measured_sclk": (round(OPS_PER_CLK * sclk["mhz_mean"] * 1e6 / 1e12, 1)
+                                      if sclk.get("mhz_mean") else None),
+            "frac_at_measured_sclk": (round(tops / (OPS_PER_CLK * sclk["mhz_mean"] * 1e6 / 1e12), 4)
+                                      if sclk.get("mhz_mean") else None),
+            "warmup_ms": HEAD_WARM_MS},
         "cpu_baseline": cpu,
         "cpu_baseline_extra": cpu_extra,
         "extra": extra,

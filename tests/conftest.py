@@ -10,11 +10,10 @@ sys.path.insert(0, str(ROOT))
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
-    # Load what is built; build only when nothing is (hipcc cross-compiles
-    # gfx950 without a GPU).
-    from baracuda_amd.build import LIB, build
-    if not LIB.exists():
-        build(verbose=True)
+    # Load what is built; rebuild when it is missing or its recorded source
+    # digest differs from the sources (hipcc cross-compiles gfx950 without a GPU).
+    from baracuda_amd.build import ensure_built
+    ensure_built(verbose=True)
 
 
 @pytest.fixture(scope="session")

@@ -212,9 +212,11 @@ def test_gather_rows_config4_bf16_table(gpu):
 
 
 def test_gemv_s8w_weights_beyond_2gib(gpu):
-    # W is 262144 x 8192 int8 (2 GiB): 64-bit row addressing; sampled rows
+    # W is 262152 x 8192 int8 (2 GiB + 64 KiB): byte offsets past 2^31 need
+    # 64-bit row addressing; sampled rows (the last 8 lie wholly past 2^31)
     # within 1 bf16 ulp of the exact f64 value.
-    n, k = 262144, 8192
+    n, k = 262152, 8192
+    assert (n - 1) * k > 2 ** 31
     print(f"case: gemv_s8w beyond 2 GiB {n}x{k}", flush=True)
     gen = torch.Generator(device="cuda:0").manual_seed(91)
     w = torch.randint(-127, 128, (n, k), dtype=torch.int8, device="cuda:0", generator=gen)
@@ -223,7 +225,7 @@ def test_gemv_s8w_weights_beyond_2gib(gpu):
     d = torch.empty(n, dtype=torch.bfloat16, device="cuda:0")
     P.GemvS8wPlan.select(n, k).run(x, w, scale, d)
     sync()
-    rows = [0, 1, 131071, 262143] + list(rng(92).integers(0, n, 4))
+    rows = [0, 1, 131071, 262143, 262144, 262148, n - 1] + list(rng(92).integers(0, n, 4))
     xb = x.cpu().view(torch.int16).numpy().view(np.uint16)
     got = host_bits16(d)[rows]
     wr = w[rows].cpu().numpy()

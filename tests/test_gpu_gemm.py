@@ -430,17 +430,21 @@ def test_i32_operand_beyond_2gib(gpu):
 
 
 def test_quantize_bf16_input_beyond_2gib(gpu):
-    # 65536 x 16384 bf16 (2 GiB of input, 1 GiB of int8 output): 64-bit row
-    # offsets in the 16-byte-chunk path; sampled rows bit-exact.
-    n, dd = 65536, 16384
-    print(f"case: quantize beyond 2 GiB {n}x{dd}", flush=True)
+    # 131080 x 16384 bf16: 2^31 + 131072 elements (4 GiB of input, 2 GiB of
+    # int8 output), so element indices and byte offsets pass 2^31: 64-bit row
+    # offsets in the 16-byte-chunk path; sampled rows (the last lie wholly
+    # past element 2^31) bit-exact.
+    n, dd = 131080, 16384
+    assert n * dd > 2 ** 31 and 131072 * dd == 2 ** 31
+    print(f"case: quantize beyond 2^31 elements {n}x{dd}", flush=True)
     gen = torch.Generator(device="cuda:0").manual_seed(93)
-    x = torch.randn((n, dd), device="cuda:0", generator=gen, dtype=torch.float32).to(torch.bfloat16)
+    x = torch.empty((n, dd), device="cuda:0", dtype=torch.bfloat16)
+    x.normal_(generator=gen)
     q = torch.empty((n, dd), dtype=torch.int8, device="cuda:0")
     scale = torch.empty(n, dtype=torch.float32, device="cuda:0")
     P.dynamic_range_quantize_per_token_sym(x, scale, q)
     sync()
-    rows = [0, 1, 32767, 65535] + list(rng(94).integers(0, n, 4))
+    rows = [0, 1, 65535, 131071, 131072, 131075, n - 1] + list(rng(94).integers(0, n, 4))
     seen = x[rows].float().cpu().numpy()
     wq, ws = O.quantize_per_token_sym(seen)
     assert np.array_equal(q[rows].cpu().numpy(), wq)

@@ -166,9 +166,11 @@ def test_cast_amax_keeps_larger_slot_value(gpu):
 
 
 def test_cast_amax_beyond_2g_elements(gpu):
-    # 2^31 + 24 bf16 elements (4 GiB in, 2 GiB out): 64-bit element indices
-    # and the numel % 8 tail; sampled spans bit-exact, amax = max|x| exactly.
-    n = (1 << 31) + 24
+    # 2^31 + 29 bf16 elements (4 GiB in, 2 GiB out): 64-bit element indices
+    # and, since n % 8 == 5, the scalar tail past element 2^31; sampled spans
+    # (the last one ends at the final element) bit-exact, amax = max|x| exactly.
+    n = (1 << 31) + 29
+    assert n % 8 != 0
     print(f"case: te cast beyond 2^31 elements n={n}", flush=True)
     gen = torch.Generator(device="cuda:0").manual_seed(95)
     x = torch.empty(n, dtype=torch.bfloat16, device="cuda:0")
@@ -177,8 +179,9 @@ def test_cast_amax_beyond_2g_elements(gpu):
     r = _recipe("e4m3", hist=2, scale=2.5)
     P.Fp8CastPlan.select().run(x, out, r)
     sync()
-    for s0 in (0, (1 << 30) + 8, n - 4096):
-        bits, _ = O.te_cast_amax(x[s0:s0 + 4096].float().cpu().numpy(), 2.5, "e4m3")
-        assert np.array_equal(out[s0:s0 + 4096].cpu().numpy(), bits), s0
+    for s0 in (0, (1 << 30) + 8, (1 << 31) - 3, n - 4096, n - 13):
+        e0 = min(s0 + 4096, n)
+        bits, _ = O.te_cast_amax(x[s0:e0].float().cpu().numpy(), 2.5, "e4m3")
+        assert np.array_equal(out[s0:e0].cpu().numpy(), bits), s0
     assert r.amax_history.cpu().numpy()[0] == float(x.abs().max().float().item())
     del x, out
