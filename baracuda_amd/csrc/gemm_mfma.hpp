@@ -194,9 +194,12 @@ __device__ __forceinline__ void compute_stage(const int8_t *la, const int8_t *lb
 
 // Full K loop for one 256x256 output tile.  `lds` must hold 2 * 2 * LDS_TILE
 // bytes.  Ends with a barrier so the caller may reuse LDS.
+// U8 needs `sums` (zeroed here): raw-byte sums of A rows and B rows (= output
+// columns), gathered by compute_stage.
 template <Elem E, bool Checked>
 __device__ __forceinline__ void mainloop(int8_t *lds, const RowSet &as, const RowSet &bs, int K,
-                                         typename AccT<E>::type (&acc)[TM][TN]) {
+                                         typename AccT<E>::type (&acc)[TM][TN],
+                                         U8Sums *sums = nullptr) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -209,6 +212,7 @@ __device__ __forceinline__ void mainloop(int8_t *lds, const RowSet &as, const Ro
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = typename AccT<E>::type{0, 0, 0, 0};
 
+    if constexpr (E == Elem::U8) sums->ra = sums->cb = 0;
     const int KT = (K + BK - 1) / BK;
     v4i ra[LOADS], rb[LOADS];
     load_stage<Checked>(ra, rb, as, bs, 0, K, unit);
@@ -220,7 +224,7 @@ __device__ __forceinline__ void mainloop(int8_t *lds, const RowSet &as, const Ro
         int8_t *nxt = lds + ((kt + 1) & 1) * 2 * LDS_TILE;
         const bool more = kt + 1 < KT;
         if (more) load_stage<Checked>(ra, rb, as, bs, (kt + 1) * BK, K, unit);
-        compute_stage<E>(cur, cur + LDS_TILE, acc, wave_m, wave_n, lane);
+        compute_stage<E>(cur, cur + LDS_TILE, acc, wave_m, wave_n, lane, sums);
         if (more) store_stage(nxt, nxt + LDS_TILE, ra, rb, tid);
         __syncthreads();
     }

@@ -293,6 +293,40 @@ struct PolicyU8RowB : PolicyI8RowB<C> {
     }
 };
 
+// u8 x u8 RCR through the signed MFMA: both operands are K-contiguous rows,
+// so both get PolicyU8RowB's treatment of A -- fragments flipped to u - 128
+// before the MFMA, and once per stage each wave sums the raw bytes of rows
+// 32*wave .. +31 of the landed A and B tiles (two lanes per row,
+// ds_read_b128).  The B row sums are the output-column sums of the
+// correction sum(u_a*u_b) = acc_s + 128*(rowsum + colsum) - 16384*K.
+template <class C>
+struct PolicyU8 : PolicyI8<C> {
+    typedef PolicyI8<C> Base;
+    static constexpr bool SUMS = true;
+    static constexpr bool FLIP = true;
+    struct Sums {
+        uint32_t ra, rb;
+    };
+    template <class F>
+    __device__ static void fixup(F &f, Sums &) {
+#pragma unroll
+        for (int t = 0; t < Base::TI; ++t) f.a[t] = u8_flip(f.a[t]);
+#pragma unroll
+        for (int t = 0; t < Base::TJ; ++t) f.b[t] = u8_flip(f.b[t]);
+    }
+    __device__ static void stage_hook(const int8_t *stage, Sums &s) {
+        static_assert(C::WAVES == 8 && C::TB == 256, "slices assume 8 waves over 256 rows");
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        const int row = 32 * wave + (lane >> 1);
+        const int u0 = (lane & 1) * 4;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            s.ra = u8_sum16(*reinterpret_cast<const v4i *>(stage + lds_off(row, u0 + u)), s.ra);
+            s.rb = u8_sum16(*reinterpret_cast<const v4i *>(stage + C::OPER + lds_off(row, u0 + u)), s.rb);
+        }
+    }
+};
+
 // fp8 row-major B for the 32x32x64 policy: lane l needs the 32 k-bytes
 // 64s + 32*(l/32) .. +31 of column n0 + l%32.  16-lane group g covers columns
 // 16*(g%2) .. +15 and the k half g/2; four transposing reads of 8 k-rows each.

@@ -576,6 +576,92 @@ int32_t launch_u8_rrr(const S8Args &p, hipStream_t stream, void *workspace = nul
     return launch_status();
 }
 
+// ---- u8 x u8 RCR (B [N, K]) ---------------------------------------------------
+// Same correction as the RRR kernels; both operands are K-contiguous rows, so
+// the column sums are B row sums, gathered exactly like the A row sums.
+template <bool VecOut, int ACT, typename BiasT>
+__global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_u8_rcr_dma_kernel(S8Args p) {
+    namespace M2 = mfma2;
+    typedef M2::PolicyU8<DmaCfg> P;
+    __shared__ __attribute__((aligned(1024))) int8_t stage0[2 * M2::OPER];
+    __shared__ __attribute__((aligned(1024))) int8_t stage1[2 * M2::OPER];
+    const int tiles_m = p.M / M2::BM, tiles_n = p.N / M2::BN;
+    int tm, tn;
+    tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int m_base = tm * M2::BM, n_base = tn * M2::BN;
+    M2::DmaRows<false, false> d;
+    d.a = M2::make_dma_interior<DmaCfg>(p.a, (uint32_t)(p.M * p.lda), (int)p.lda, m_base * (int)p.lda);
+    d.b = M2::make_dma_interior<DmaCfg>(p.b, (uint32_t)(p.N * p.ldb), (int)p.ldb, n_base * (int)p.ldb);
+    M2::AccTile<P> acc;
+    typename P::Sums sums;
+    sums.ra = sums.rb = 0;
+    M2::mainloop<P>(stage0, stage1, d, p.K, acc, sums);
+    // Row sums of A and of B into LDS (free after the loop's last barrier),
+    // above the staged-store scratch of waves 4..7 (stage1's first 32 KiB).
+    int *sc = reinterpret_cast<int *>(stage1 + 40 * 1024);   // rs[256] | cs[256]
+    park_row_sums(sums.ra, sc);
+    park_row_sums(sums.rb, sc + 256);
+    __syncthreads();
+    const U8Epilogue<VecOut, ACT, BiasT> epi{p, sc, sc + 256, 16384u * (uint32_t)p.K};
+    store_u8_tile<VecOut, P>(acc, stage0, stage1, p, m_base, n_base, epi);
+}
+
+// General u8 RCR path: register-staged mainloop, clamped rows, byte-exact K
+// tail (zero-padded k: 0 in the raw sums, (-128)^2 in acc_s, K_pad corrects).
+template <bool Aligned, int ACT, typename BiasT>
+__global__ __launch_bounds__(NT, 1) void gemm_u8_rcr_kernel(S8Args p) {
+    __shared__ __attribute__((aligned(16))) int8_t lds[4 * LDS_TILE];
+    const int tiles_m = (p.M + BM - 1) / BM;
+    const int tiles_n = (p.N + BN - 1) / BN;
+    int tm, tn;
+    tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int m_base = tm * BM, n_base = tn * BN;
+    const int tid = threadIdx.x;
+    RowSet as, bs;
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+        const int r = i * LOAD_ROWS + (tid >> 3);
+        as.ptr[i] = p.a + (int64_t)min(m_base + r, p.M - 1) * p.lda;
+        bs.ptr[i] = p.b + (int64_t)min(n_base + r, p.N - 1) * p.ldb;
+    }
+    v4i acc[TM][TN];
+    U8Sums sums;
+    mainloop<Elem::U8, !Aligned>(lds, as, bs, p.K, acc, &sums);
+    int *sc = reinterpret_cast<int *>(lds);
+    park_row_sums(sums.ra, sc);
+    park_row_sums(sums.cb, sc + 256);
+    __syncthreads();
+    const uint32_t kpad = (uint32_t)((p.K + BK - 1) / BK) * (uint32_t)BK;
+    const U8Epilogue<false, ACT, BiasT> epi{p, sc, sc + 256, 16384u * kpad};
+    for_each_fragment(acc, [&](int ml, int nl, const v4i &v) { epi(ml, nl, v, m_base, n_base); });
+}
+
+template <int ACT, typename BiasT>
+int32_t launch_u8_rcr(const S8Args &p, hipStream_t stream) {
+    const bool dma = p.K % mfma2::BK == 0 && p.M % mfma2::BM == 0 && p.N % mfma2::BN == 0 &&
+                     p.lda % 16 == 0 && p.ldb % 16 == 0 && aligned16(p.a) && aligned16(p.b) &&
+                     (int64_t)p.M * p.lda < (1ll << 31) && (int64_t)p.N * p.ldb < (1ll << 31);
+    if (dma) {
+        const int tiles = (p.M / mfma2::BM) * (p.N / mfma2::BN);
+        const bool vec = p.ldd % 4 == 0 && (reinterpret_cast<uintptr_t>(p.d) % 4) == 0;
+        if (vec)
+            hipLaunchKernelGGL((gemm_u8_rcr_dma_kernel<true, ACT, BiasT>), dim3(tiles), dim3(DmaCfg::NT), 0,
+                               stream, p);
+        else
+            hipLaunchKernelGGL((gemm_u8_rcr_dma_kernel<false, ACT, BiasT>), dim3(tiles), dim3(DmaCfg::NT), 0,
+                               stream, p);
+        return launch_status();
+    }
+    const int tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
+    const bool aligned = p.K % BK == 0 && p.lda % 16 == 0 && p.ldb % 16 == 0 && aligned16(p.a) &&
+                         aligned16(p.b);
+    if (aligned)
+        hipLaunchKernelGGL((gemm_u8_rcr_kernel<true, ACT, BiasT>), dim3(tiles), dim3(NT), 0, stream, p);
+    else
+        hipLaunchKernelGGL((gemm_u8_rcr_kernel<false, ACT, BiasT>), dim3(tiles), dim3(NT), 0, stream, p);
+    return launch_status();
+}
+
 template <int EPI, bool VecOut, int ACT, typename BiasT>
 void launch_kernel(const S8Args &p, bool fast_k, hipStream_t stream) {
     if (fast_k) {

@@ -77,6 +77,14 @@ for _e in ("bias", "bias_relu", "bias_gelu", "bias_silu"):
         _sig(f"baracuda_kernels_gemm_s8_rrr_gfx950_{_e}_{_b}_run", i32, *_RCR_RUN, vp, f32, f32, vp, sz, vp)
         _sig(f"baracuda_kernels_gemm_s8_rrr_gfx950_{_e}_{_b}_can_implement", i32, *_RCR_RUN)
 _sig("baracuda_kernels_gemm_s8_rrr_gfx950_run", i32, *_RCR_RUN, f32, f32, vp, sz, vp)
+_sig("baracuda_kernels_gemm_u8_rcr_gfx950_run", i32, *_RCR_RUN, f32, f32, vp, sz, vp)
+_sig("baracuda_kernels_gemm_u8_rcr_gfx950_workspace_size", sz, i32, i32, i32)
+_sig("baracuda_kernels_gemm_u8_rcr_gfx950_can_implement", i32, *_RCR_RUN)
+for _e in ("bias", "bias_relu", "bias_gelu", "bias_silu"):
+    for _b in ("f32", "i32"):
+        _sig(f"baracuda_kernels_gemm_{_e}_{_b}bias_u8_rcr_gfx950_run", i32, *_RCR_RUN, vp, f32, f32, vp, sz, vp)
+        _sig(f"baracuda_kernels_gemm_{_e}_{_b}bias_u8_rcr_gfx950_workspace_size", sz, i32, i32, i32)
+        _sig(f"baracuda_kernels_gemm_{_e}_{_b}bias_u8_rcr_gfx950_can_implement", i32, *_RCR_RUN, vp)
 _sig("baracuda_kernels_gemm_u8_rrr_gfx950_run", i32, *_RCR_RUN, f32, f32, vp, sz, vp)
 _sig("baracuda_kernels_gemm_u8_rrr_gfx950_workspace_size", sz, i32, i32, i32)
 _sig("baracuda_kernels_gemm_u8_rrr_gfx950_can_implement", i32, *_RCR_RUN)

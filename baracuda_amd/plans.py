@@ -183,7 +183,7 @@ class IntGemmPlan:
     """int_gemm.rs IntGemmPlan: select / can_implement / workspace_size / sku / run.
 
     RCR (int_gemm.rs:73-85, CUTLASS arm) and RRR (:86-124, bespoke arm) for S8
-    operands.  S8 output: D = sat_s8(rne(act(alpha*acc + beta*C + bias[n]))) for
+    and U8 operands (U8 takes a U8 output, sat_u8).  S8 output: D = sat_s8(rne(act(alpha*acc + beta*C + bias[n]))) for
     the Identity and Bias / BiasRelu / BiasGelu / BiasSilu epilogues, bias f32
     or i32 [N].  RCR additionally offers I32 (raw accumulator) and Bf16 (W8A8
     per-token x per-channel dequant, needs scale_a / scale_b) with Identity."""
@@ -196,9 +196,11 @@ class IntGemmPlan:
         if desc.m <= 0 or desc.n <= 0 or desc.k <= 0:
             raise InvalidProblem("int GEMM problem must have positive M, N, K")
         if desc.element == ElementKind.U8:
-            # int_gemm.rs:93-101: U8 is a bespoke RRR SKU with a u8 output.
-            if desc.layout != LayoutSku.Rrr or desc.output != ElementKind.U8:
-                raise Unsupported("U8 int GEMM is RRR with a U8 output")
+            # U8 operands take a U8 output in both layouts: RCR is the CUTLASS
+            # arm (plan.rs:2273-2346, 2570-2915), RRR the bespoke one
+            # (int_gemm.rs:93-101).
+            if desc.output != ElementKind.U8:
+                raise Unsupported("U8 int GEMM has a U8 output")
             has_bias = desc.epilogue != EpilogueKind.Identity
             if has_bias and desc.bias_element not in (ElementKind.F32, ElementKind.I32):
                 raise Unsupported(f"bias element {desc.bias_element}")
@@ -230,6 +232,10 @@ class IntGemmPlan:
         if d.output == ElementKind.Bf16:
             return getattr(L, f"gemm_w8a8_rcr_gfx950_bf16_{suffix}")
         epi, bt = d.epilogue.value, d.bias_element.value
+        if d.element == ElementKind.U8 and d.layout == LayoutSku.Rcr:
+            if d.epilogue == EpilogueKind.Identity:
+                return getattr(L, f"gemm_u8_rcr_gfx950_{suffix}")
+            return getattr(L, f"gemm_{epi}_{bt}bias_u8_rcr_gfx950_{suffix}")
         if d.element == ElementKind.U8:
             if d.epilogue == EpilogueKind.Identity:
                 return getattr(L, f"gemm_u8_rrr_gfx950_{suffix}")

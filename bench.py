@@ -435,6 +435,13 @@ def main():
                                     "with_workspace_us": round(uwms * 1e3, 2),
                                     "with_workspace_TOPS": round(ops / (uwms * 1e-3) / 1e12, 1)}
             del uws
+            ubc = torch.randint(0, 256, (N, K), dtype=torch.uint8, device=dev)
+            upc = P.IntGemmPlan.select(P.IntGemmDescriptor(M, N, K, layout=P.LayoutSku.Rcr,
+                                                           element=P.ElementKind.U8, output=P.ElementKind.U8))
+            ucms = time_launches(lambda: upc.run(ua, ubc, ud, alpha=1.0 / 65536, stream=stream), 20, 5, stream,
+                                 warm_ms=30.0)
+            e["rcr_u8_identity"] = {"us": round(ucms * 1e3, 2), "TOPS": round(ops / (ucms * 1e-3) / 1e12, 1)}
+            del ubc
             extra["int8_s8out_4096_cubed"] = e
             del ua, ub, ud
             del ia, ib, ibr, idd

@@ -109,6 +109,43 @@ BK_S8_RCR_BIAS_DECL(bias_gelu, i32bias)
 BK_S8_RCR_BIAS_DECL(bias_silu, i32bias)
 #undef BK_S8_RCR_BIAS_DECL
 
+/* ======================= u8 GEMM, RCR layout ============================
+ * u8 x u8, A row-major [M,K], B [N,K] (column-major [K,N]), int32 accumulator,
+ * D = sat_u8(rne(act(alpha*acc + beta*C [+ bias[n]]))) with C and D u8.
+ * Replaces baracuda_kernels_gemm_u8_rcr_sm80_{run,workspace_size,can_implement}
+ * (crates/baracuda-cutlass-kernels-sys/kernels/gemm_u8_rcr_sm80.cu; re-exported at
+ *  crates/baracuda-kernels-sys/src/cutlass_reexport.rs:669-676) and
+ * baracuda_kernels_gemm_{bias,bias_relu,bias_gelu,bias_silu}_{f32bias,i32bias}_u8_rcr_sm80_*
+ * (gemm_u8_rcr_sm80_bias.cu; cutlass_reexport.rs:1062-1096, 1141-1176).
+ * Workspace 0. */
+int32_t baracuda_kernels_gemm_u8_rcr_gfx950_run(
+    int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,
+    const void *c, int64_t ldc, void *d, int64_t ldd, float alpha, float beta,
+    void *workspace, size_t workspace_bytes, void *stream);
+size_t baracuda_kernels_gemm_u8_rcr_gfx950_workspace_size(int32_t m, int32_t n, int32_t k);
+int32_t baracuda_kernels_gemm_u8_rcr_gfx950_can_implement(
+    int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,
+    const void *c, int64_t ldc, void *d, int64_t ldd);
+#define BK_U8_RCR_BIAS_DECL(EPI, BIAS)                                                          \
+    int32_t baracuda_kernels_gemm_##EPI##_##BIAS##_u8_rcr_gfx950_run(                           \
+        int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb, \
+        const void *c, int64_t ldc, void *d, int64_t ldd, const void *bias, float alpha,         \
+        float beta, void *workspace, size_t workspace_bytes, void *stream);                      \
+    size_t baracuda_kernels_gemm_##EPI##_##BIAS##_u8_rcr_gfx950_workspace_size(int32_t m,       \
+                                                                             int32_t n, int32_t k); \
+    int32_t baracuda_kernels_gemm_##EPI##_##BIAS##_u8_rcr_gfx950_can_implement(                 \
+        int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb, \
+        const void *c, int64_t ldc, void *d, int64_t ldd, const void *bias);
+BK_U8_RCR_BIAS_DECL(bias, f32bias)
+BK_U8_RCR_BIAS_DECL(bias_relu, f32bias)
+BK_U8_RCR_BIAS_DECL(bias_gelu, f32bias)
+BK_U8_RCR_BIAS_DECL(bias_silu, f32bias)
+BK_U8_RCR_BIAS_DECL(bias, i32bias)
+BK_U8_RCR_BIAS_DECL(bias_relu, i32bias)
+BK_U8_RCR_BIAS_DECL(bias_gelu, i32bias)
+BK_U8_RCR_BIAS_DECL(bias_silu, i32bias)
+#undef BK_U8_RCR_BIAS_DECL
+
 /* ======================= int8 GEMM, RRR layout ===========================
  * A row-major [M,K] (lda), B row-major [K,N] (ldb), D row-major [M,N].
  * Replaces baracuda_kernels_gemm_s8_rrr_sm80_{run,workspace_size,can_implement}

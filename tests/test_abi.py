@@ -38,6 +38,9 @@ def _declared():
     for epi, bias in re.findall(r"BK_S8_RCR_BIAS_DECL\((\w+), (\w+)\)", text):
         for suf in ("run", "workspace_size", "can_implement"):
             names.add(f"baracuda_kernels_gemm_{epi}_{bias}_s8_rcr_gfx950_{suf}")
+    for epi, bias in re.findall(r"BK_U8_RCR_BIAS_DECL\((\w+), (\w+)\)", text):
+        for suf in ("run", "workspace_size", "can_implement"):
+            names.add(f"baracuda_kernels_gemm_{epi}_{bias}_u8_rcr_gfx950_{suf}")
     for epi, bias in re.findall(r"BK_U8_RRR_BIAS_DECL\((\w+), (\w+)\)", text):
         for suf in ("run", "can_implement"):
             names.add(f"baracuda_kernels_gemm_u8_rrr_gfx950_{epi}_{bias}_{suf}")

@@ -1,5 +1,5 @@
-"""GPU parity of the int8 RRR GEMM and the bias / activation epilogue family
-(RCR and RRR) against the CPU oracle.
+"""GPU parity of the int8 RRR GEMM, the u8 RRR and RCR GEMMs and the bias /
+activation epilogue family (RCR and RRR) against the CPU oracle.
 
 Inputs follow the reference smoke test (crates/baracuda-kernels/tests/
 int8_rrr_smoke.rs): a = ((7i)%15)-7, b = ((11i)%13)-6, alpha = 0.125, bias
@@ -137,13 +137,17 @@ def test_rrr_large_k_sum_identity(gpu):
     assert np.array_equal(got[rows], O.gemm_s8_epi(a[rows], b, "rrr", 1.0 / 4096))
 
 
-# ---- U8 RRR (int8_rrr_smoke.rs run_u8_smoke: a = (7i)%16, b = (11i)%14) ------
-def _run_u8(epi, bias_kind, a, b, c=None, bias=None, alpha=0.125, beta=0.0, ws=False):
-    # ws: pass the optional workspace (pre-pass operand sums), filled with
-    # garbage first -- its contents must not matter.
+# ---- U8 RRR and RCR (int8_rrr_smoke.rs / int8_smoke.rs run_u8_smoke:
+# a = (7i)%16, b = (11i)%14) ---------------------------------------------------
+RRR, RCR = P.LayoutSku.Rrr, P.LayoutSku.Rcr
+
+
+def _run_u8(epi, bias_kind, a, b, c=None, bias=None, alpha=0.125, beta=0.0, ws=False, layout=RRR):
+    # ws: pass the optional workspace (pre-pass operand sums, RRR only),
+    # filled with garbage first -- its contents must not matter.
     m, k = a.shape
-    n = b.shape[1]
-    plan = P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, layout=P.LayoutSku.Rrr, epilogue=epi,
+    n = b.shape[1] if layout == RRR else b.shape[0]
+    plan = P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, layout=layout, epilogue=epi,
                                                     bias_element=bias_kind, element=P.ElementKind.U8,
                                                     output=P.ElementKind.U8))
     work = None
@@ -156,56 +160,97 @@ def _run_u8(epi, bias_kind, a, b, c=None, bias=None, alpha=0.125, beta=0.0, ws=F
     return d.cpu().numpy()
 
 
-@pytest.mark.parametrize("ws", [False, True])
+# (layout, ws): the u8 workspace pre-pass exists for RRR only.
+U8_PATHS = [(RRR, False), (RRR, True), (RCR, False)]
+_LNAME = {RRR: "rrr", RCR: "rcr"}
+
+
+def _u8_b(g_or_pattern, k, n, layout):
+    """B of a u8 test: [K, N] for RRR, [N, K] for RCR."""
+    return g_or_pattern.reshape(k, n) if layout == RRR else g_or_pattern.reshape(n, k)
+
+
+@pytest.mark.parametrize("layout,ws", U8_PATHS)
 @pytest.mark.parametrize("bias_kind", [P.ElementKind.F32, P.ElementKind.I32])
 @pytest.mark.parametrize("epi", EPIS)
 @pytest.mark.parametrize("shape", REF_SHAPES + [(256, 256, 128), (512, 512, 256)])
-def test_u8_reference_smoke_pattern(gpu, shape, epi, bias_kind, ws):
+def test_u8_reference_smoke_pattern(gpu, shape, epi, bias_kind, layout, ws):
     if epi == P.EpilogueKind.Identity and bias_kind == P.ElementKind.I32:
         pytest.skip("Identity has no bias")
     m, n, k = shape
-    print(f"case: u8 rrr {epi.value} {bias_kind.value} {shape}", flush=True)
+    print(f"case: u8 {_LNAME[layout]} {epi.value} {bias_kind.value} {shape} ws={ws}", flush=True)
     a = ((np.arange(m * k) * 7) % 16).astype(np.uint8).reshape(m, k)
-    b = ((np.arange(k * n) * 11) % 14).astype(np.uint8).reshape(k, n)
+    b = _u8_b(((np.arange(k * n) * 11) % 14).astype(np.uint8), k, n, layout)
     bias = _bias(n, bias_kind)
-    got = _run_u8(epi, bias_kind, a, b, bias=bias, ws=ws)
-    want = O.gemm_u8_epi(a, b, "rrr", 0.125, 0.0, None, None if epi == P.EpilogueKind.Identity else bias,
-                         ACT[epi])
+    got = _run_u8(epi, bias_kind, a, b, bias=bias, ws=ws, layout=layout)
+    want = O.gemm_u8_epi(a, b, _LNAME[layout], 0.125, 0.0, None,
+                         None if epi == P.EpilogueKind.Identity else bias, ACT[epi])
     _check(got, want, epi)
 
 
-@pytest.mark.parametrize("ws", [False, True])
+@pytest.mark.parametrize("layout,ws", U8_PATHS)
 @pytest.mark.parametrize("epi", EPIS)
 @pytest.mark.parametrize("shape", [(256, 256, 128), (512, 768, 384), (300, 520, 200), (130, 260, 1000)])
-def test_u8_full_range_with_c(gpu, shape, epi, ws):
+def test_u8_full_range_with_c(gpu, shape, epi, layout, ws):
     # Full-range bytes (the flipped sign bit matters) on the DMA and the
     # general path, including a K tail (200, 1000) whose zero padding the
     # correction accounts for.
     m, n, k = shape
-    print(f"case: u8 random {epi.value} {shape} ws={ws}", flush=True)
+    print(f"case: u8 {_LNAME[layout]} random {epi.value} {shape} ws={ws}", flush=True)
     g = rng(m * 3 + n + k)
     a = g.integers(0, 256, (m, k), dtype=np.uint8)
-    b = g.integers(0, 256, (k, n), dtype=np.uint8)
+    b = _u8_b(g.integers(0, 256, k * n, dtype=np.uint8), k, n, layout)
     c = g.integers(0, 256, (m, n), dtype=np.uint8)
     bias = (g.standard_normal(n) * 30).astype(np.float32)
     alpha = 1.0 / (64.0 * k)
-    got = _run_u8(epi, P.ElementKind.F32, a, b, c=c, bias=bias, alpha=alpha, beta=0.5, ws=ws)
-    want = O.gemm_u8_epi(a, b, "rrr", alpha, 0.5, c, None if epi == P.EpilogueKind.Identity else bias,
-                         ACT[epi])
+    got = _run_u8(epi, P.ElementKind.F32, a, b, c=c, bias=bias, alpha=alpha, beta=0.5, ws=ws, layout=layout)
+    want = O.gemm_u8_epi(a, b, _LNAME[layout], alpha, 0.5, c,
+                         None if epi == P.EpilogueKind.Identity else bias, ACT[epi])
     _check(got, want, epi)
 
 
-@pytest.mark.parametrize("ws", [False, True])
-def test_u8_large_k_exact_accumulator(gpu, ws):
+@pytest.mark.parametrize("layout,ws", U8_PATHS)
+def test_u8_large_k_exact_accumulator(gpu, layout, ws):
     # alpha = 1 / 2^k-scale keeps the u8 output informative at K = 8192
     # (acc up to 255^2 * 8192 ~ 5.3e8 < 2^31): checks the 16384*K term.
     m, n, k = 256, 256, 8192
     g = rng(99)
     a = g.integers(0, 256, (m, k), dtype=np.uint8)
-    b = g.integers(0, 256, (k, n), dtype=np.uint8)
+    b = _u8_b(g.integers(0, 256, k * n, dtype=np.uint8), k, n, layout)
     alpha = 255.0 / (255.0 * 255.0 * k)
-    got = _run_u8(P.EpilogueKind.Identity, P.ElementKind.F32, a, b, alpha=alpha, ws=ws)
-    want = O.gemm_u8_epi(a, b, "rrr", alpha)
+    got = _run_u8(P.EpilogueKind.Identity, P.ElementKind.F32, a, b, alpha=alpha, ws=ws, layout=layout)
+    want = O.gemm_u8_epi(a, b, _LNAME[layout], alpha)
+    assert np.array_equal(got, want)
+
+
+def test_u8_rcr_strided_unaligned_and_full_result(gpu):
+    # RCR u8 on padded leading dimensions with a B base offset by 1 byte (the
+    # general kernel's byte-granular path), BiasRelu with an i32 bias; then
+    # a 1024 x 1024 x 2048 Identity result checked in full against torch's
+    # int64 matmul (alpha 1/2^20 keeps the u8 output informative).
+    m, n, k = 130, 260, 96
+    g = rng(15)
+    a_full = g.integers(0, 256, (m, k + 16), dtype=np.uint8)
+    b_full = g.integers(0, 256, (n, k + 9), dtype=np.uint8)
+    a_t, b_t = dev(a_full)[:, :k], dev(b_full)[:, 1:k + 1]
+    d_full = torch.zeros((m, n + 4), dtype=torch.uint8, device="cuda:0")
+    d = d_full[:, :n]
+    bias = _bias(n, P.ElementKind.I32)
+    plan = P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, layout=RCR, epilogue=P.EpilogueKind.BiasRelu,
+                                                    bias_element=P.ElementKind.I32, element=P.ElementKind.U8,
+                                                    output=P.ElementKind.U8))
+    plan.run(a_t, b_t, d, alpha=1.0 / 2048, bias=dev(bias))
+    sync()
+    want = O.gemm_u8_epi(a_full[:, :k], b_full[:, 1:k + 1], "rcr", 1.0 / 2048, bias=bias, act="relu")
+    assert np.array_equal(d.cpu().numpy(), want)
+    assert np.all(d_full[:, n:].cpu().numpy() == 0)   # padding untouched
+    m = n = 1024
+    k = 2048
+    a = g.integers(0, 256, (m, k), dtype=np.uint8)
+    b = g.integers(0, 256, (n, k), dtype=np.uint8)
+    got = _run_u8(P.EpilogueKind.Identity, P.ElementKind.F32, a, b, alpha=1.0 / (1 << 20), layout=RCR)
+    acc = (torch.from_numpy(a).to(torch.int64) @ torch.from_numpy(b).to(torch.int64).T).numpy()
+    want = np.clip(np.rint(np.float32(1.0 / (1 << 20)) * acc.astype(np.float32)), 0, 255).astype(np.uint8)
     assert np.array_equal(got, want)
 
 
