@@ -9,6 +9,7 @@
 //   (plain)   D = sat_s8(rne(alpha*acc + beta*C))              gemm_s8_rcr_sm80 semantics
 //   w8a8 bf16 D = bf16_rne((sa[m]*sw[n]) * (float)acc)          new SKU
 //   w8a8 f32  D = (sa[m]*sw[n]) * (float)acc                    quantized_linear_w8a8_f32
+//   w8a8 f64  D = (double)(((float)sa[m]*(float)sw[n]) * (float)acc)  quantized_linear_w8a8_f64
 //
 // The accumulator wraps modulo 2^32 where the reference's mma.sync
 // saturates; the two agree whenever |acc| < 2^31, which holds for int8
@@ -127,6 +128,33 @@ int32_t baracuda_kernels_quantized_linear_w8a8_f32_gfx950_run(
     S8Args p{M, C_out, K, (const int8_t *)act_q, K, (const int8_t *)weight_q, K, nullptr, 0,
              output, C_out, 1.0f, 0.0f, (const float *)scale_a, (const float *)scale_w, nullptr};
     return launch<EPI_W8A8_F32>(p, (hipStream_t)stream);
+}
+
+// ---- quantized_linear_w8a8 f64 (compose.cu:27-28, same ABI) ----------------
+// f64 scales and output; the reference kernel narrows the scales to f32
+// (qc_load_as_f32), forms y = sa*sw*(float)acc in f32 and widens y to f64
+// (baracuda_quantize_compose.cuh:265-274, qc_store_from_f32<double>).
+int32_t baracuda_kernels_quantized_linear_w8a8_f64_gfx950_can_implement(
+    int32_t M, int32_t C_out, int32_t K, const void *weight_q, const void *act_q,
+    const void *scale_a, const void *scale_w, const void *output) {
+    (void)weight_q; (void)act_q; (void)scale_a; (void)scale_w; (void)output;
+    if (M < 0 || C_out < 0 || K < 0) return kInvalid;
+    return kOk;
+}
+
+int32_t baracuda_kernels_quantized_linear_w8a8_f64_gfx950_run(
+    int32_t M, int32_t C_out, int32_t K, const void *weight_q, const void *act_q,
+    const void *scale_a, const void *scale_w, void *output,
+    void *workspace, size_t workspace_bytes, void *stream) {
+    (void)workspace; (void)workspace_bytes;
+    if (M < 0 || C_out < 0 || K < 0) return kInvalid;
+    if ((int64_t)M * C_out == 0) return kOk;
+    if (!weight_q || !act_q || !scale_a || !scale_w || !output) return kInvalid;
+    // The scale pointers travel in S8Args' f32 slots and are read as f64 by
+    // the EPI_W8A8_F64 epilogue; K == 0 runs the same tile pass with acc = 0.
+    S8Args p{M, C_out, K, (const int8_t *)act_q, K, (const int8_t *)weight_q, K, nullptr, 0,
+             output, C_out, 1.0f, 0.0f, (const float *)scale_a, (const float *)scale_w, nullptr};
+    return launch<EPI_W8A8_F64>(p, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -5,6 +5,9 @@
 //   EPI_S8         D = sat_s8(rne(act(alpha*acc + beta*C [+ bias[n]])))
 //   EPI_W8A8_BF16  D = bf16_rne((sa[m]*sw[n]) * (float)acc)
 //   EPI_W8A8_F32   D = (sa[m]*sw[n]) * (float)acc
+//   EPI_W8A8_F64   D = (double)(((float)sa[m]*(float)sw[n]) * (float)acc), sa / sw f64
+//                  (quantized_linear_w8a8_f64: the reference narrows the f64
+//                  scales to f32, computes in f32 and widens the result)
 // The accumulator wraps modulo 2^32 where the reference's mma.sync
 // saturates; the two agree whenever |acc| < 2^31, which holds for int8
 // operands in [-127,127] whenever K < 133143.
@@ -19,7 +22,7 @@ namespace {
 
 using namespace mfma;
 
-enum Epi : int { EPI_I32 = 0, EPI_S8 = 1, EPI_W8A8_BF16 = 2, EPI_W8A8_F32 = 3 };
+enum Epi : int { EPI_I32 = 0, EPI_S8 = 1, EPI_W8A8_BF16 = 2, EPI_W8A8_F32 = 3, EPI_W8A8_F64 = 4 };
 
 struct S8Args {
     int M, N, K;
@@ -84,6 +87,14 @@ struct S8Epilogue {
             } else {
                 for (int r = 0; r < count; ++r) d[r] = o[r];
             }
+        } else if constexpr (EPI == EPI_W8A8_F64) {
+            const double *sa64 = reinterpret_cast<const double *>(p.sa);
+            const double *sw64 = reinterpret_cast<const double *>(p.sw);
+            const float sam = (float)sa64[m];
+            double *d = static_cast<double *>(p.d) + (int64_t)m * p.ldd + n0;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                if (r < count) d[r] = (double)((sam * (float)sw64[n0 + r]) * (float)v[r]);
         } else {
             // W8A8 dequant: y = (sa[m] * sw[n]) * (float)acc, products in f32.
             const float sam = p.sa[m];
@@ -675,7 +686,7 @@ void launch_kernel(const S8Args &p, bool fast_k, hipStream_t stream) {
 
 template <int EPI, int ACT = ACT_NONE, typename BiasT = float>
 int32_t launch(const S8Args &p, hipStream_t stream) {
-    const int out_elem = (EPI == EPI_I32 || EPI == EPI_W8A8_F32) ? 4 : (EPI == EPI_S8 ? 1 : 2);
+    const int out_elem = (EPI == EPI_I32 || EPI == EPI_W8A8_F32) ? 4 : EPI == EPI_W8A8_F64 ? 8 : (EPI == EPI_S8 ? 1 : 2);
     // The DMA path needs whole 256x256 tiles, whole K stages and 16-byte rows.
     const bool fast_k = p.K > 0 && p.K % BK == 0 && p.lda % 16 == 0 && p.ldb % 16 == 0 &&
                         aligned16(p.a) && aligned16(p.b) &&

@@ -32,6 +32,8 @@ _sig("baracuda_kernels_gemm_w8a8_rcr_gfx950_bf16_workspace_size", sz, i32, i32, 
 _sig("baracuda_kernels_gemm_w8a8_rcr_gfx950_bf16_can_implement", i32, i32, i32, i32, vp, i64, vp, i64, vp, vp, vp, i64)
 _sig("baracuda_kernels_quantized_linear_w8a8_f32_gfx950_run", i32, i32, i32, i32, vp, vp, vp, vp, vp, vp, sz, vp)
 _sig("baracuda_kernels_quantized_linear_w8a8_f32_gfx950_can_implement", i32, i32, i32, i32, vp, vp, vp, vp, vp)
+_sig("baracuda_kernels_quantized_linear_w8a8_f64_gfx950_run", i32, i32, i32, i32, vp, vp, vp, vp, vp, vp, sz, vp)
+_sig("baracuda_kernels_quantized_linear_w8a8_f64_gfx950_can_implement", i32, i32, i32, i32, vp, vp, vp, vp, vp)
 _sig("baracuda_kernels_gemm_fp8_e4m3_rcr_gfx950_run", i32, i32, i32, i32, vp, i64, vp, i64, vp, i64, vp, i64, f32, f32, vp, sz, vp)
 _sig("baracuda_kernels_gemm_fp8_e4m3_rcr_gfx950_workspace_size", sz, i32, i32, i32)
 _sig("baracuda_kernels_gemm_fp8_e4m3_rcr_gfx950_can_implement", i32, *_RCR_CAN)

@@ -626,8 +626,9 @@ class QuantizedLinearDescriptor:
 class QuantizedLinearPlan:
     """quantized_linear.rs QuantizedLinearPlan (:142-386): two launches on one
     stream -- per-token activation quantization into caller scratch, then the
-    W8A8 GEMM with the (sa*sw)*acc dequant epilogue.  f32 activation -> f32
-    output (the reference's SKU); bf16 activation -> bf16 output (gfx950)."""
+    W8A8 GEMM with the (sa*sw)*acc dequant epilogue.  f32 / f64 activation ->
+    f32 / f64 output with scales of the same type (the reference's SKUs);
+    bf16 activation -> bf16 output, f32 scales (gfx950)."""
 
     def __init__(self, desc: QuantizedLinearDescriptor):
         self.desc = desc
@@ -657,6 +658,13 @@ class QuantizedLinearPlan:
         if activation.dtype == torch.float32:
             _need(output.dtype == torch.float32 and weight_scale.dtype == torch.float32, "f32 output/scales")
             st = L.quantized_linear_w8a8_f32_gfx950_run(d.m, d.c_out, d.k, _ptr(weight_q), _ptr(act_q_scratch),
+                                                         _ptr(act_scale_scratch), _ptr(weight_scale),
+                                                         _ptr(output), None, 0, s)
+        elif activation.dtype == torch.float64:
+            # quantized_linear.rs:166-171 f64 arm: f64 activation, scales and output.
+            _need(output.dtype == torch.float64 and weight_scale.dtype == torch.float64 and
+                  act_scale_scratch.dtype == torch.float64, "f64 output / scales")
+            st = L.quantized_linear_w8a8_f64_gfx950_run(d.m, d.c_out, d.k, _ptr(weight_q), _ptr(act_q_scratch),
                                                          _ptr(act_scale_scratch), _ptr(weight_scale),
                                                          _ptr(output), None, 0, s)
         elif activation.dtype == torch.bfloat16:

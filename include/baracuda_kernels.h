@@ -83,6 +83,19 @@ int32_t baracuda_kernels_quantized_linear_w8a8_f32_gfx950_can_implement(
     int32_t M, int32_t C_out, int32_t K, const void *weight_q, const void *act_q,
     const void *scale_a, const void *scale_w, const void *output);
 
+/* Replaces baracuda_kernels_quantized_linear_w8a8_f64_{run,can_implement}
+ * (crates/baracuda-kernels-sys/kernels/quantize/compose.cu:27-28, macro at
+ * baracuda_quantize_compose.cuh:340-370): f64 scale_a [M], scale_w [C_out] and
+ * output [M,C_out]; output = (double)(((float)scale_a[m]*(float)scale_w[c]) * (float)acc),
+ * the reference's f32 evaluation with narrowed scales. */
+int32_t baracuda_kernels_quantized_linear_w8a8_f64_gfx950_run(
+    int32_t M, int32_t C_out, int32_t K, const void *weight_q, const void *act_q,
+    const void *scale_a, const void *scale_w, void *output,
+    void *workspace, size_t workspace_bytes, void *stream);
+int32_t baracuda_kernels_quantized_linear_w8a8_f64_gfx950_can_implement(
+    int32_t M, int32_t C_out, int32_t K, const void *weight_q, const void *act_q,
+    const void *scale_a, const void *scale_w, const void *output);
+
 /* int8 RCR with the bias / activation epilogue family.  Same ABI as
  * baracuda_kernels_gemm_{bias,bias_relu,bias_gelu,bias_silu}_{f32bias,i32bias}_s8_rcr_sm80_*
  * (crates/baracuda-cutlass-kernels-sys/kernels/gemm_s8_rcr_sm80_bias.cu:225-275,

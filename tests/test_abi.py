@@ -113,6 +113,9 @@ def test_gemm_invalid_problems_rejected_before_launch():
     assert L.gemm_fp8_e4m3_rcr_gfx950_bf16_workspace_size(16, 16, 16) == 0
     assert L.quantized_linear_w8a8_f32_gfx950_can_implement(-1, 2, 2, None, None, None, None, None) == 2
     assert L.quantized_linear_w8a8_f32_gfx950_run(0, 2, 2, None, None, None, None, None, None, 0, None) == 0
+    assert L.quantized_linear_w8a8_f64_gfx950_can_implement(-1, 2, 2, None, None, None, None, None) == 2
+    assert L.quantized_linear_w8a8_f64_gfx950_run(0, 2, 2, None, None, None, None, None, None, 0, None) == 0
+    assert L.quantized_linear_w8a8_f64_gfx950_run(2, 2, 2, None, None, None, None, None, None, 0, None) == 2
 
 
 

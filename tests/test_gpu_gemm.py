@@ -221,6 +221,30 @@ def test_quantized_linear_w8a8_f32(gpu):
     assert np.array_equal(out.cpu().numpy(), want)
 
 
+def test_quantized_linear_w8a8_f64(gpu):
+    # compose.cu:27-28 f64 SKU: f64 scales narrowed to f32, y = sa*sw*acc in
+    # f32, widened to f64.  The f64 scales carry bits below f32 precision so
+    # a kernel that multiplied in f64 would differ.
+    a, w, _, _ = w8a8(130, 70, 200, seed=18)
+    g = rng(19)
+    sa = g.uniform(0.005, 0.02, 130)            # f64, not f32-representable
+    sw = g.uniform(0.001, 0.01, 70)
+    out = torch.empty((130, 70), dtype=torch.float64, device="cuda:0")
+    from baracuda_amd.ffi import lib
+    tw, ta, tsa, tsw = dev(w), dev(a), dev(sa), dev(sw)
+    st = lib().quantized_linear_w8a8_f64_gfx950_run(130, 70, 200, tw.data_ptr(), ta.data_ptr(),
+                                                    tsa.data_ptr(), tsw.data_ptr(), out.data_ptr(),
+                                                    None, 0, torch.cuda.current_stream().cuda_stream)
+    assert st == 0
+    sync()
+    acc = O.gemm_s8_rcr_i32(a, w).astype(np.float32)
+    want = ((sa.astype(np.float32)[:, None] * sw.astype(np.float32)[None, :]) * acc).astype(np.float64)
+    got = out.cpu().numpy()
+    assert np.array_equal(got, want)
+    f64_product = (sa[:, None] * sw[None, :]) * acc.astype(np.float64)
+    assert not np.array_equal(got, f64_product)     # the f32 evaluation is what is matched
+
+
 def test_int8_determinism_replays(gpu):
     a, w, sa, sw = w8a8(1024, 768, 1024, seed=4)
     outs = [_w8a8(a, w, sa, sw) for _ in range(3)]
@@ -280,17 +304,48 @@ def test_fp8_e4m3_out_reference_pattern(gpu):
 
 
 def test_fp8_bf16_config3_sampled(gpu):
+    # BASELINE.json config 3 at full size.  Per element, 32 sampled rows (4 in
+    # each of the 8 tile-rows of 256, at varying offsets; every row crosses
+    # all 56 tile-columns, so both rounds of the 448-tile grid) against the
+    # f64 oracle within 1 bf16 ulp + 1e-4 * sum|a*b|.  Over the whole
+    # 2048 x 14336 output:
+    #   - the f32-out SKU against hipBLASLt (torch._scaled_mm, an independent
+    #     library on the same operands) within 1e-3 rel + 1e-4 * sum|a*b|;
+    #   - the bf16-out SKU equals bf16_rne(alpha * f32-out) bit for bit (both
+    #     SKUs share the mainloop, so this pins the bf16 epilogue everywhere);
+    #   - every row sum of the f32 output against the exact f64
+    #     sum_k dec(a[m,k]) * sum_n dec(b[n,k]), within the summed per-element bound.
     print("case: fp8 bf16 2048x14336x4096", flush=True)
-    a, b, sa, sb = _fp8_inputs(2048, 14336, 4096)
+    m, n, k = 2048, 14336, 4096
+    a, b, sa, sb = _fp8_inputs(m, n, k)
     d = _fp8_run(a, b, P.ElementKind.Bf16, scale_a=sa, scale_b=sb)
     got = O.bf16_bits_to_f32(host_bits16(d))
     alpha = float(np.float32(sa) * np.float32(sb))
-    for r in [0, 777, 2047]:
+    fa = O.e4m3_to_f32(a).astype(np.float64)
+    fb = O.e4m3_to_f32(b).astype(np.float64)
+    abs_b = np.abs(fb)
+    rows = sorted({t * 256 + off for t in range(8) for off in (0, 37 + 19 * t, 128 + 7 * t, 255)})
+    assert len(rows) == 32
+    for r in rows:
         exact = O.gemm_fp8_e4m3_f64(a, b, rows=(r, r + 1), nthreads=8)[0] * alpha
         err = np.abs(got[r].astype(np.float64) - exact)
-        ta = np.abs(O.e4m3_to_f32(a[r]).astype(np.float64))
-        absum = np.abs(O.e4m3_to_f32(b).astype(np.float64)) @ ta * alpha
+        absum = abs_b @ np.abs(fa[r]) * alpha
         assert np.all(err <= bf16_ulp(exact) + 1e-4 * absum), (r, err.max())
+    del d, got
+    f32 = _fp8_run(a, b, P.ElementKind.F32, alpha=1.0)
+    one = torch.tensor(1.0, device="cuda:0")
+    ref = torch._scaled_mm(dev(a).view(torch.float8_e4m3fn), dev(b).view(torch.float8_e4m3fn).t(),
+                           scale_a=one, scale_b=one, out_dtype=torch.float32)
+    ours = f32.cpu().numpy()
+    ref = ref.cpu().numpy().astype(np.float64)
+    absum = torch.from_numpy(np.abs(fa)).cuda() @ torch.from_numpy(abs_b).cuda().T   # f64 on the GPU
+    absum = absum.cpu().numpy()
+    assert np.all(np.abs(ours.astype(np.float64) - ref) <= 1e-3 * np.abs(ref) + 1e-4 * absum)
+    bf = host_bits16(_fp8_run(a, b, P.ElementKind.Bf16, scale_a=sa, scale_b=sb))
+    assert np.array_equal(bf, O.f32_to_bf16_bits_fast(np.float32(alpha) * ours))
+    row_exact = fa @ fb.sum(0)                       # sum_n sum_k a b, exact in f64
+    row_tol = (1e-3 * np.abs(ref) + 1e-4 * absum).sum(1)
+    assert np.all(np.abs(ours.astype(np.float64).sum(1) - row_exact) <= row_tol)
 
 
 @pytest.mark.parametrize("shape", [(256, 128, 64), (512, 512, 1024), (256, 512, 384)])
@@ -382,7 +437,7 @@ def test_quantize_then_w8a8_matches_fp_matmul(gpu):
     assert err.max() <= 0.02 * np.abs(ref).max()
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.bfloat16])
 def test_quantized_linear_plan_two_pass(gpu, dtype):
     # QuantizedLinearPlan::run = quantize (pass 1) + W8A8 GEMM (pass 2); the
     # output equals the oracle chain on the same activation.
@@ -393,16 +448,21 @@ def test_quantized_linear_plan_two_pass(gpu, dtype):
     ta = torch.from_numpy(a).to(dtype).cuda()
     out = torch.empty((m, c_out), dtype=dtype, device="cuda:0")
     aq = torch.empty((m, k), dtype=torch.int8, device="cuda:0")
-    sa = torch.empty(m, dtype=torch.float32, device="cuda:0")
+    sdt = torch.float64 if dtype == torch.float64 else torch.float32
+    sa = torch.empty(m, dtype=sdt, device="cuda:0")
     plan = P.QuantizedLinearPlan.select(P.QuantizedLinearDescriptor(m, c_out, k))
-    plan.run(ta, dev(wq), dev(ws), out, aq, sa)
+    plan.run(ta, dev(wq), dev(ws).to(sdt), out, aq, sa)
     sync()
+    # f64 activations are read through an f32 narrowing (the reference's
+    # qc_load_as_f32), so the oracle chain runs on the f32 values throughout.
     qa, sa_ref = O.quantize_per_token_sym(ta.float().cpu().numpy())
     assert np.array_equal(aq.cpu().numpy(), qa) and np.array_equal(sa.cpu().numpy(), sa_ref)
     acc = O.gemm_s8_rcr_i32(qa, wq).astype(np.float32)
     want = (sa_ref[:, None] * ws[None, :]).astype(np.float32) * acc
     if dtype == torch.float32:
         assert np.array_equal(out.cpu().numpy(), want)
+    elif dtype == torch.float64:
+        assert np.array_equal(out.cpu().numpy(), want.astype(np.float64))
     else:
         assert np.array_equal(host_bits16(out), O.f32_to_bf16_bits_fast(want))
 
