@@ -536,13 +536,23 @@ __global__ __launch_bounds__(NT, 1) void gemm_u8_rrr_kernel(S8Args p) {
     for_each_fragment(acc, [&](int ml, int nl, const v4i &v) { epi(ml, nl, v, m_base, n_base); });
 }
 
+// Whole-tile problems the LDS-DMA u8 RRR kernels take.
+inline bool u8_rrr_dma_eligible(const S8Args &p) {
+    return p.K % mfma2::BK == 0 && p.M % mfma2::BM == 0 && p.N % mfma2::BN == 0 && p.lda % 16 == 0 &&
+           p.ldb % 16 == 0 && aligned16(p.a) && aligned16(p.b) && (int64_t)p.M * p.lda < (1ll << 31) &&
+           (int64_t)p.K * p.ldb < (1ll << 31);
+}
+
+// ... of which those whose operands the pre-pass can rewrite into a workspace.
+inline bool u8_rrr_prepass_eligible(const S8Args &p) {
+    return u8_rrr_dma_eligible(p) && (int64_t)p.K * p.N < (1ll << 31);
+}
+
 template <int ACT, typename BiasT>
 int32_t launch_u8_rrr(const S8Args &p, hipStream_t stream, void *workspace = nullptr, size_t workspace_bytes = 0) {
-    const bool dma = p.K % mfma2::BK == 0 && p.M % mfma2::BM == 0 && p.N % mfma2::BN == 0 &&
-                     p.lda % 16 == 0 && p.ldb % 16 == 0 && aligned16(p.a) && aligned16(p.b) &&
-                     (int64_t)p.M * p.lda < (1ll << 31) && (int64_t)p.K * p.ldb < (1ll << 31);
-    if (dma && workspace && workspace_bytes >= u8_rrr_workspace_bytes(p.M, p.N, p.K) &&
-        (reinterpret_cast<uintptr_t>(workspace) & 255u) == 0 && (int64_t)p.K * p.N < (1ll << 31)) {
+    const bool dma = u8_rrr_dma_eligible(p);
+    if (u8_rrr_prepass_eligible(p) && workspace && workspace_bytes >= u8_rrr_workspace_bytes(p.M, p.N, p.K) &&
+        (reinterpret_cast<uintptr_t>(workspace) & 255u) == 0) {
         int *rowsum = static_cast<int *>(workspace), *colsum = rowsum + p.M;
         int8_t *af = static_cast<int8_t *>(workspace) + u8_ws_sums_bytes(p.M, p.N);
         int8_t *bf = af + (((size_t)p.M * p.K + 255) & ~(size_t)255);

@@ -90,6 +90,7 @@ for _e in ("bias", "bias_relu", "bias_gelu", "bias_silu"):
 _sig("baracuda_kernels_gemm_u8_rrr_gfx950_run", i32, *_RCR_RUN, f32, f32, vp, sz, vp)
 _sig("baracuda_kernels_gemm_u8_rrr_gfx950_workspace_size", sz, i32, i32, i32)
 _sig("baracuda_kernels_gemm_u8_rrr_gfx950_can_implement", i32, *_RCR_RUN)
+_sig("baracuda_kernels_gemm_u8_rrr_gfx950_noalloc_run", i32, *_RCR_RUN, f32, f32, vp)
 for _e in ("bias", "bias_relu", "bias_gelu", "bias_silu"):
     for _b in ("f32", "i32"):
         _sig(f"baracuda_kernels_gemm_u8_rrr_gfx950_{_e}_{_b}_run", i32, *_RCR_RUN, vp, f32, f32, vp, sz, vp)

@@ -258,6 +258,23 @@ size_t baracuda_kernels_gemm_u8_rrr_gfx950_workspace_size(int32_t m, int32_t n, 
 int32_t baracuda_kernels_gemm_u8_rrr_gfx950_can_implement(
     int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,
     const void *c, int64_t ldc, void *d, int64_t ldd);
+/* Allocation-free variant of baracuda_kernels_gemm_u8_rrr_gfx950_run (no
+ * counterpart in the reference): for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc), which therefore cannot hand in the optional workspace.
+ * Whole-tile problems (M, N % 256 == 0, K % 128 == 0, 16-byte aligned
+ * operands) use a fixed device array of BARACUDA_U8_RRR_NOALLOC_SCRATCH_BYTES
+ * bytes held by each GPU the library runs on until the process ends; a
+ * problem whose pre-pass needs more (workspace_size(m, n, k) bytes) returns
+ * 4.  Other shapes run the in-loop path.  Calls no hipMalloc,
+ * hipFree or allocating routine; every call on one GPU shares that GPU's
+ * array, so calls that overlap on one GPU (different streams, or host
+ * threads) race -- serialise them.  Results are identical to
+ * baracuda_kernels_gemm_u8_rrr_gfx950_run. */
+#define BARACUDA_U8_RRR_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int32_t baracuda_kernels_gemm_u8_rrr_gfx950_noalloc_run(
+    int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,
+    const void *c, int64_t ldc, void *d, int64_t ldd, float alpha, float beta, void *stream);
 #define BK_U8_RRR_BIAS_DECL(EPI, BIAS)                                                          \
     int32_t baracuda_kernels_gemm_u8_rrr_gfx950_##EPI##_##BIAS##_run(                           \
         int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb, \
