@@ -120,16 +120,21 @@ struct F8DmaPolicy { typedef mfma2::PolicyF8<F8DmaCfg, FMT> type; };
 template <int FMT>
 struct F8DmaPolicy<FMT, F8_RRR> { typedef mfma2::PolicyF8RowB<F8DmaCfg, FMT> type; };
 
-// Fast path: whole 256x256 tiles, K % 128 == 0, 16-byte rows, vector stores.
+// Fast path: 256x256 tiles (edge tiles included), K % 128 == 0, 16-byte rows,
+// N % 4 == 0, vector stores.
 template <int FMT, int LAYOUT, int EPI, int ACT>
 __global__ __launch_bounds__(F8DmaCfg::NT, 1) void gemm_fp8_dma_kernel(F8Args p) {
     namespace M2 = mfma2;
     typedef typename F8DmaPolicy<FMT, LAYOUT>::type P;
     __shared__ __attribute__((aligned(1024))) int8_t stage0[2 * M2::OPER];
     __shared__ __attribute__((aligned(1024))) int8_t stage1[2 * M2::OPER];
+    // Edge tiles (M or N not a multiple of 256): rows past M / N load as
+    // zeros (past the buffer resources' byte counts; RRR B columns past N
+    // read the next k-row, reaching only output columns that are not stored).
     int tm, tn;
-    tile_coords(blockIdx.x, p.M / M2::BM, p.N / M2::BN, tm, tn);
+    tile_coords(blockIdx.x, (p.M + M2::BM - 1) / M2::BM, (p.N + M2::BN - 1) / M2::BN, tm, tn);
     const int m_base = tm * M2::BM, n_base = tn * M2::BN;
+    const bool full = m_base + M2::BM <= p.M && n_base + M2::BN <= p.N;
     M2::AccTile<P> acc;
     if constexpr (LAYOUT == F8_RCR) {
         M2::DmaRows<false, false> d;
@@ -145,7 +150,7 @@ __global__ __launch_bounds__(F8DmaCfg::NT, 1) void gemm_fp8_dma_kernel(F8Args p)
     if constexpr (EPI == F8_BF16) {
         // bf16 rows staged per wave in LDS (free after the mainloop's last
         // barrier), written as 16-byte units: D = bf16_rne(alpha * acc).
-        if (p.ldd % 8 == 0 && (reinterpret_cast<uintptr_t>(p.d) & 15u) == 0) {
+        if (p.ldd % 8 == 0 && (reinterpret_cast<uintptr_t>(p.d) & 15u) == 0 && (full || p.N % 8 == 0)) {
             const int wave = threadIdx.x >> 6;
             const int wrow = m_base + (wave / F8DmaCfg::WAVES_N) * F8DmaCfg::WM;
             const int wcol = n_base + (wave % F8DmaCfg::WAVES_N) * F8DmaCfg::WN;
@@ -157,21 +162,32 @@ __global__ __launch_bounds__(F8DmaCfg::NT, 1) void gemm_fp8_dma_kernel(F8Args p)
                     return v2i{(int)f32x2_to_bf16x2(alpha * v[0], alpha * v[1]),
                                (int)f32x2_to_bf16x2(alpha * v[2], alpha * v[3])};
                 },
-                [&](int r) { return static_cast<uint16_t *>(p.d) + (int64_t)(wrow + r) * p.ldd + wcol; });
+                [&](int r) {
+                    return wrow + r < p.M ? static_cast<uint16_t *>(p.d) + (int64_t)(wrow + r) * p.ldd + wcol
+                                          : nullptr;
+                },
+                min(F8DmaCfg::WN, p.N - wcol));
             return;
         }
     }
     const F8Epilogue<FMT, EPI, true, ACT> epi{p};
     if constexpr (EPI == F8_OUT) {
         // fp8 bytes staged per wave, written as 16-byte row segments.
-        if (p.ldd % 16 == 0 && (reinterpret_cast<uintptr_t>(p.d) & 15u) == 0) {
+        if (p.ldd % 16 == 0 && (reinterpret_cast<uintptr_t>(p.d) & 15u) == 0 && (full || p.N % 16 == 0)) {
             const int wave = threadIdx.x >> 6;
             const int wrow = m_base + (wave / F8DmaCfg::WAVES_N) * F8DmaCfg::WM;
             const int wcol = n_base + (wave % F8DmaCfg::WAVES_N) * F8DmaCfg::WN;
             int8_t *scratch = (wave < 4 ? stage0 : stage1) + (wave & 3) * (F8DmaCfg::WM * F8DmaCfg::WN);
             M2::store_u8x4_staged<P>(
-                acc, scratch, [&](int r, int c, const v4f &v) { return epi.pack_fp8(wrow + r, wcol + c, v); },
-                [&](int r) { return static_cast<int8_t *>(p.d) + (int64_t)(wrow + r) * p.ldd + wcol; });
+                acc, scratch,
+                [&](int r, int c, const v4f &v) {
+                    return (wrow + r < p.M && wcol + c < p.N) ? epi.pack_fp8(wrow + r, wcol + c, v) : 0u;
+                },
+                [&](int r) {
+                    return wrow + r < p.M ? static_cast<int8_t *>(p.d) + (int64_t)(wrow + r) * p.ldd + wcol
+                                          : nullptr;
+                },
+                min(F8DmaCfg::WN, p.N - wcol));
             return;
         }
     }
@@ -182,12 +198,17 @@ template <int FMT, int LAYOUT, int EPI, int ACT>
 int32_t launch_fp8(const F8Args &p, hipStream_t stream) {
     const int out_elem = EPI == F8_F32 ? 4 : (EPI == F8_BF16 ? 2 : 1);
     const int64_t b_rows = LAYOUT == F8_RCR ? p.N : p.K;
+    // Edge tiles load zeros past the operands, so the byte offsets of the
+    // extents padded to whole tiles must stay below 2^31; the vector epilogue
+    // needs whole 4-column groups (N % 4 == 0).
+    const int64_t pad_m = (int64_t)((p.M + mfma2::BM - 1) / mfma2::BM) * mfma2::BM;
+    const int64_t pad_b = LAYOUT == F8_RCR ? (int64_t)((p.N + mfma2::BN - 1) / mfma2::BN) * mfma2::BN * p.ldb
+                                           : b_rows * p.ldb + mfma2::BN;
     const bool fast = p.K % mfma2::BK == 0 && p.lda % 16 == 0 && p.ldb % 16 == 0 && aligned16(p.a) &&
-                      aligned16(p.b) && p.M % mfma2::BM == 0 && p.N % mfma2::BN == 0 &&
-                      (int64_t)p.M * p.lda < (1ll << 31) && b_rows * p.ldb < (1ll << 31) &&
+                      aligned16(p.b) && p.N % 4 == 0 && pad_m * p.lda < (1ll << 31) && pad_b < (1ll << 31) &&
                       p.ldd % 4 == 0 && (reinterpret_cast<uintptr_t>(p.d) % (4 * out_elem)) == 0;
     if (fast) {
-        const int tiles = (p.M / mfma2::BM) * (p.N / mfma2::BN);
+        const int tiles = (int)(pad_m / mfma2::BM) * ((p.N + mfma2::BN - 1) / mfma2::BN);
         hipLaunchKernelGGL((gemm_fp8_dma_kernel<FMT, LAYOUT, EPI, ACT>), dim3(tiles), dim3(F8DmaCfg::NT),
                            0, stream, p);
     } else {

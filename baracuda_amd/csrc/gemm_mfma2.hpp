@@ -639,11 +639,14 @@ __device__ __forceinline__ void mainloop_dma_only(int8_t *s0, int8_t *s1, const 
 // `scratch` holds WM*WN*2 bytes private to this wave; LDS must be free (the
 // mainloop ends with a barrier).  Products are rounded in the order
 // ((sam * sw) * acc) [* post], then packed with v_cvt_pk_bf16_f32.
+//   ncols    valid columns of the wave tile (a multiple of 8; units at or
+//            past it are not stored: the N edge of a partial tile)
 template <class P, bool HasPost, class RowDst>
 __device__ __forceinline__ void store_w8a8_bf16_staged(const AccTile<P> &acc, int8_t *scratch,
                                                        const float (&sam)[P::TI],
                                                        const float (&post)[P::TI],
-                                                       const v4f (&swv)[P::TJ], RowDst &&row_dst) {
+                                                       const v4f (&swv)[P::TJ], RowDst &&row_dst,
+                                                       int ncols = P::Cfg::WN) {
     typedef typename P::Cfg C;
     static_assert(C::WN * 2 == 128, "staged store assumes 128-byte wave-tile rows");
     const int lane = threadIdx.x & 63;
@@ -672,7 +675,7 @@ __device__ __forceinline__ void store_w8a8_bf16_staged(const AccTile<P> &acc, in
     for (int q = 0; q < C::WM / 8; ++q) {
         const int row = q * 8 + (lane >> 3), u = lane & 7;
         uint16_t *dst = row_dst(row);
-        if (dst == nullptr) continue;
+        if (dst == nullptr || u * 8 >= ncols) continue;
         const v4i v = *reinterpret_cast<const v4i *>(scratch + row * 128 + ((u ^ (row & 7)) << 4));
         // Non-temporal: the 32 MiB output of a 4096^2 tile grid streams past
         // the caches instead of evicting the operands still being read.
@@ -684,12 +687,14 @@ __device__ __forceinline__ void store_w8a8_bf16_staged(const AccTile<P> &acc, in
 // LDS so each 64-byte row of the wave tile is written with 16-byte stores.
 //   pack(r, c, quad)  4 output bytes of wave-tile row r, columns c..c+3
 //   row_dst(r)        destination of wave-tile row r at the wave's first column
+//                     (nullptr: row not stored)
+//   ncols             valid columns of the wave tile (a multiple of 16 bytes)
 // `scratch`: WM * WN bytes private to this wave.  16-byte unit u of row r
 // sits at unit u ^ ((r >> 2) & 3), so the 16 rows of one 4-byte write
 // instruction fall in distinct banks.
 template <class P, class Pack, class RowDst>
 __device__ __forceinline__ void store_u8x4_staged(const AccTile<P> &acc, int8_t *scratch, Pack &&pack,
-                                                  RowDst &&row_dst) {
+                                                  RowDst &&row_dst, int ncols = P::Cfg::WN) {
     typedef typename P::Cfg C;
     static_assert(C::WN == 64, "staged byte store assumes 64-byte wave-tile rows");
     const int lane = threadIdx.x & 63;
@@ -708,7 +713,8 @@ __device__ __forceinline__ void store_u8x4_staged(const AccTile<P> &acc, int8_t 
     for (int q = 0; q < C::WM / 16; ++q) {
         const int r = q * 16 + (lane >> 2), u = lane & 3;
         const v4i v = *reinterpret_cast<const v4i *>(scratch + r * 64 + ((u ^ ((r >> 2) & 3)) << 4));
-        __builtin_nontemporal_store(v, reinterpret_cast<v4i *>(row_dst(r) + u * 16));
+        auto *dst = row_dst(r);
+        if (dst != nullptr && u * 16 < ncols) __builtin_nontemporal_store(v, reinterpret_cast<v4i *>(dst + u * 16));
     }
 }
 
@@ -718,9 +724,11 @@ __device__ __forceinline__ void store_u8x4_staged(const AccTile<P> &acc, int8_t 
 // row_dst(r) giving each row's destination (nullptr: skip the row).
 // `scratch`: WM * 128 bytes private to this wave; unit u of row r sits at
 // unit u ^ (r & 7).
+// ncols: valid columns of the wave tile (a multiple of 8), units past it are
+// not stored.
 template <class P, class Pack, class RowDst>
 __device__ __forceinline__ void store_bf16x4_staged(const AccTile<P> &acc, int8_t *scratch, Pack &&pack,
-                                                    RowDst &&row_dst) {
+                                                    RowDst &&row_dst, int ncols = P::Cfg::WN) {
     typedef typename P::Cfg C;
     static_assert(C::WN == 64, "staged bf16 store assumes 128-byte wave-tile rows");
     const int lane = threadIdx.x & 63;
@@ -740,7 +748,7 @@ __device__ __forceinline__ void store_bf16x4_staged(const AccTile<P> &acc, int8_
         const int r = q * 8 + (lane >> 3), u = lane & 7;
         const v4i v = *reinterpret_cast<const v4i *>(scratch + r * 128 + ((u ^ (r & 7)) << 4));
         uint16_t *dst = row_dst(r);   // nullptr: row not stored
-        if (dst != nullptr) __builtin_nontemporal_store(v, reinterpret_cast<v4i *>(dst + u * 8));
+        if (dst != nullptr && u * 8 < ncols) __builtin_nontemporal_store(v, reinterpret_cast<v4i *>(dst + u * 8));
     }
 }
 

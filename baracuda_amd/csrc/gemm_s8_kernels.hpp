@@ -179,13 +179,22 @@ int32_t launch_rrr(const S8Args &p, hipStream_t stream) {
     return launch_status();
 }
 
-// Fast path: M, N multiples of 256, K % 128 == 0, 16-byte aligned rows ->
+// Rows of an operand padded to whole 256-row tiles, times its row pitch,
+// fit the 32-bit buffer offsets of the LDS-DMA path.
+inline bool dma_extent_ok(int rows, int64_t ld) {
+    return ((int64_t)(rows + 255) / 256) * 256 * ld < (1ll << 31);
+}
+
+// Fast path: 256x256 tiles (edge tiles read zeros past M / N), K % 128 == 0,
+// 16-byte aligned rows ->
 // LDS-DMA mainloop, 8 waves (2 x 4) of 128 x 64, v_mfma_i32_16x16x64_i8.
 typedef mfma2::Cfg<2, 4> DmaCfg;
 
 // int8 outputs of a whole tile through LDS: each wave's 128 x 64 bytes are
 // staged (8 KiB per wave; LDS is free after the mainloop's last barrier) and
 // written as 16-byte row segments instead of 4-byte stores.
+// Partial tiles (the M / N edge, N % 16 == 0): rows past M and 16-byte
+// units past N are neither computed nor stored.
 template <class P, class Epi>
 __device__ __forceinline__ void store_s8_tile_staged(const mfma2::AccTile<P> &acc, int8_t *stage0, int8_t *stage1,
                                                      const S8Args &p, int m_base, int n_base, const Epi &epi) {
@@ -193,10 +202,19 @@ __device__ __forceinline__ void store_s8_tile_staged(const mfma2::AccTile<P> &ac
     const int wrow = (wave / DmaCfg::WAVES_N) * DmaCfg::WM;
     const int wcol = (wave % DmaCfg::WAVES_N) * DmaCfg::WN;
     int8_t *scratch = (wave < 4 ? stage0 : stage1) + (wave & 3) * (DmaCfg::WM * DmaCfg::WN);
+    const int ncols = min(DmaCfg::WN, p.N - (n_base + wcol));
     mfma2::store_u8x4_staged<P>(
         acc, scratch,
-        [&](int r, int c, const v4i &v) { return epi.pack_s8(m_base + wrow + r, n_base + wcol + c, v); },
-        [&](int r) { return static_cast<int8_t *>(p.d) + (int64_t)(m_base + wrow + r) * p.ldd + n_base + wcol; });
+        [&](int r, int c, const v4i &v) {
+            const int m = m_base + wrow + r, n = n_base + wcol + c;
+            return (m < p.M && n < p.N) ? epi.pack_s8(m, n, v) : 0u;
+        },
+        [&](int r) {
+            return m_base + wrow + r < p.M
+                       ? static_cast<int8_t *>(p.d) + (int64_t)(m_base + wrow + r) * p.ldd + n_base + wcol
+                       : nullptr;
+        },
+        ncols);
 }
 
 template <int EPI, bool VecOut, int ACT = ACT_NONE, typename BiasT = float>
@@ -205,7 +223,9 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_s8_rcr_dma_kernel(S8Args p
     typedef M2::PolicyI8<DmaCfg> P;
     __shared__ __attribute__((aligned(1024))) int8_t stage0[2 * M2::OPER];
     __shared__ __attribute__((aligned(1024))) int8_t stage1[2 * M2::OPER];
-    const int tiles_m = p.M / M2::BM, tiles_n = p.N / M2::BN;
+    // Edge tiles (M or N not a multiple of 256): operand rows past M / N
+    // lie past the buffer resources' byte counts and load as zeros.
+    const int tiles_m = (p.M + M2::BM - 1) / M2::BM, tiles_n = (p.N + M2::BN - 1) / M2::BN;
     int tm, tn;
     tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
     const int m_base = tm * M2::BM, n_base = tn * M2::BN;
@@ -214,27 +234,38 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_s8_rcr_dma_kernel(S8Args p
     d.b = M2::make_dma_interior<DmaCfg>(p.b, (uint32_t)(p.N * p.ldb), (int)p.ldb, n_base * (int)p.ldb);
     M2::AccTile<P> acc;
     M2::mainloop<P>(stage0, stage1, d, p.K, acc);
+    const bool full = m_base + M2::BM <= p.M && n_base + M2::BN <= p.N;
     if constexpr (EPI == EPI_W8A8_BF16 && VecOut) {
-        // Whole tiles: scales fetched once per lane, output staged in LDS
-        // (free after the mainloop's last barrier) and written as full rows.
-        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-        const int wrow = m_base + (wave / DmaCfg::WAVES_N) * DmaCfg::WM;
-        const int wcol = n_base + (wave % DmaCfg::WAVES_N) * DmaCfg::WN;
-        float sam[P::TI], none[P::TI];
-        v4f swv[P::TJ];
+        if (full || p.N % 8 == 0) {
+            // Scales fetched once per lane, output staged in LDS (free after the
+            // mainloop's last barrier) and written as full rows; in an edge tile
+            // (N % 8 == 0 there) rows past M and 8-column units past N are skipped.
+            const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+            const int wrow = m_base + (wave / DmaCfg::WAVES_N) * DmaCfg::WM;
+            const int wcol = n_base + (wave % DmaCfg::WAVES_N) * DmaCfg::WN;
+            float sam[P::TI], none[P::TI];
+            v4f swv[P::TJ];
 #pragma unroll
-        for (int i = 0; i < P::TI; ++i) sam[i] = p.sa[wrow + i * 16 + (lane & 15)];
+            for (int i = 0; i < P::TI; ++i) sam[i] = p.sa[min(wrow + i * 16 + (lane & 15), p.M - 1)];
 #pragma unroll
-        for (int j = 0; j < P::TJ; ++j)
-            swv[j] = *reinterpret_cast<const v4f *>(p.sw + wcol + j * 16 + (lane >> 4) * 4);
-        int8_t *scratch = (wave < 4 ? stage0 : stage1) + (wave & 3) * (DmaCfg::WM * DmaCfg::WN * 2);
-        M2::store_w8a8_bf16_staged<P, false>(acc, scratch, sam, none, swv, [&](int r) {
-            return static_cast<uint16_t *>(p.d) + (int64_t)(wrow + r) * p.ldd + wcol;
-        });
-    } else {
+            for (int j = 0; j < P::TJ; ++j) {
+                const int col = wcol + j * 16 + (lane >> 4) * 4;
+                swv[j] = col < p.N ? *reinterpret_cast<const v4f *>(p.sw + col) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+            int8_t *scratch = (wave < 4 ? stage0 : stage1) + (wave & 3) * (DmaCfg::WM * DmaCfg::WN * 2);
+            M2::store_w8a8_bf16_staged<P, false>(
+                acc, scratch, sam, none, swv,
+                [&](int r) {
+                    return wrow + r < p.M ? static_cast<uint16_t *>(p.d) + (int64_t)(wrow + r) * p.ldd + wcol : nullptr;
+                },
+                min(DmaCfg::WN, p.N - wcol));
+            return;
+        }
+    }
+    {
         const S8Epilogue<EPI, VecOut, ACT, BiasT> epi{p};
         if constexpr (EPI == EPI_S8 && VecOut) {
-            if (p.ldd % 16 == 0 && (reinterpret_cast<uintptr_t>(p.d) & 15u) == 0) {
+            if (p.ldd % 16 == 0 && (reinterpret_cast<uintptr_t>(p.d) & 15u) == 0 && (full || p.N % 16 == 0)) {
                 store_s8_tile_staged<P>(acc, stage0, stage1, p, m_base, n_base, epi);
                 return;
             }
@@ -251,7 +282,10 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_s8_rrr_dma_kernel(S8Args p
     typedef M2::PolicyI8RowB<DmaCfg> P;
     __shared__ __attribute__((aligned(1024))) int8_t stage0[2 * M2::OPER];
     __shared__ __attribute__((aligned(1024))) int8_t stage1[2 * M2::OPER];
-    const int tiles_m = p.M / M2::BM, tiles_n = p.N / M2::BN;
+    // Edge tiles: A rows past M load as zeros (past the buffer's byte count);
+    // B columns past N read bytes of the next k-row (or zeros after the
+    // last), which only reach output columns that are not stored.
+    const int tiles_m = (p.M + M2::BM - 1) / M2::BM, tiles_n = (p.N + M2::BN - 1) / M2::BN;
     int tm, tn;
     tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
     const int m_base = tm * M2::BM, n_base = tn * M2::BN;
@@ -261,8 +295,9 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_s8_rrr_dma_kernel(S8Args p
     M2::AccTile<P> acc;
     M2::mainloop<P>(stage0, stage1, d, p.K, acc);
     const S8Epilogue<EPI_S8, VecOut, ACT, BiasT> epi{p};
+    const bool full = m_base + M2::BM <= p.M && n_base + M2::BN <= p.N;
     if constexpr (VecOut) {
-        if (p.ldd % 16 == 0 && (reinterpret_cast<uintptr_t>(p.d) & 15u) == 0) {
+        if (p.ldd % 16 == 0 && (reinterpret_cast<uintptr_t>(p.d) & 15u) == 0 && (full || p.N % 16 == 0)) {
             store_s8_tile_staged<P>(acc, stage0, stage1, p, m_base, n_base, epi);
             return;
         }
@@ -698,10 +733,12 @@ template <int EPI, int ACT = ACT_NONE, typename BiasT = float>
 int32_t launch(const S8Args &p, hipStream_t stream) {
     const int out_elem = (EPI == EPI_I32 || EPI == EPI_W8A8_F32) ? 4 : EPI == EPI_W8A8_F64 ? 8 : (EPI == EPI_S8 ? 1 : 2);
     // The DMA path needs whole 256x256 tiles, whole K stages and 16-byte rows.
+    // The DMA path needs whole K stages and 16-byte rows; edge tiles read
+    // zeros past the operands, so the byte offsets of the padded extents
+    // must stay below 2^31.
     const bool fast_k = p.K > 0 && p.K % BK == 0 && p.lda % 16 == 0 && p.ldb % 16 == 0 &&
-                        aligned16(p.a) && aligned16(p.b) &&
-                        (int64_t)p.M * p.lda < (1ll << 31) && (int64_t)p.N * p.ldb < (1ll << 31) &&
-                        p.M % mfma2::BM == 0 && p.N % mfma2::BN == 0;
+                        aligned16(p.a) && aligned16(p.b) && dma_extent_ok(p.M, p.lda) &&
+                        dma_extent_ok(p.N, p.ldb);
     // 4-wide vector stores need every 4-column group of D (and sw) aligned;
     // the LDS-staged W8A8 bf16 store writes 16-byte units (8 columns).
     bool vec = ((p.ldd * out_elem) % (4 * out_elem)) == 0 &&
@@ -719,12 +756,11 @@ int32_t launch(const S8Args &p, hipStream_t stream) {
 // kernel.
 template <int ACT, typename BiasT>
 int32_t launch_rrr_dma(const S8Args &p, hipStream_t stream) {
-    const bool fits = p.K % mfma2::BK == 0 && p.M % mfma2::BM == 0 && p.N % mfma2::BN == 0 &&
-                      p.lda % 16 == 0 && p.ldb % 16 == 0 && aligned16(p.a) && aligned16(p.b) &&
-                      (int64_t)p.M * p.lda < (1ll << 31) && (int64_t)p.K * p.ldb < (1ll << 31);
+    const bool fits = p.K % mfma2::BK == 0 && p.lda % 16 == 0 && p.ldb % 16 == 0 && aligned16(p.a) &&
+                      aligned16(p.b) && dma_extent_ok(p.M, p.lda) && (int64_t)p.K * p.ldb + mfma2::BN < (1ll << 31);
     if (!fits) return kUnsupported;
-    const int tiles = (p.M / mfma2::BM) * (p.N / mfma2::BN);
-    const bool vec = p.ldd % 4 == 0 && (reinterpret_cast<uintptr_t>(p.d) % 4) == 0;
+    const int tiles = ((p.M + mfma2::BM - 1) / mfma2::BM) * ((p.N + mfma2::BN - 1) / mfma2::BN);
+    const bool vec = p.N % 4 == 0 && p.ldd % 4 == 0 && (reinterpret_cast<uintptr_t>(p.d) % 4) == 0;
     if (vec)
         hipLaunchKernelGGL((gemm_s8_rrr_dma_kernel<true, ACT, BiasT>), dim3(tiles), dim3(DmaCfg::NT), 0, stream, p);
     else

@@ -279,7 +279,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",
-                    help="run only: w8a8|gemv|quant|fp8|moe|int8epi|te|embedding|gather|copy (profiling; copy = 256 MiB "
+                    help="run only: w8a8|w8a8x|gemv|quant|fp8|moe|int8epi|te|embedding|gather|copy (profiling; copy = 256 MiB "
                          "device copy used to calibrate the HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -547,6 +547,41 @@ def main():
                                "graph_replay_us": round(gg, 2)}
             extra["gather_rows_bf16_128256x4096"] = g
             del table
+
+        if only in ("", "w8a8x"):
+            log("bench: w8a8 off-grid M and constant operands")
+            # Token counts off the 256-row tile grid (edge tiles on the LDS-DMA
+            # path) at the config-2 width; 4 rotated operand sets.
+            og = {}
+            for mm in (4000, 4097):
+                sets = [(torch.randint(-127, 128, (mm, K), dtype=torch.int8, device=dev),
+                         torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev),
+                         torch.rand(mm, device=dev) * 0.015 + 0.005, torch.rand(N, device=dev) * 0.009 + 0.001,
+                         torch.empty((mm, N), dtype=torch.bfloat16, device=dev)) for _ in range(4)]
+                op = P.IntGemmPlan.select(P.IntGemmDescriptor(mm, N, K, output=P.ElementKind.Bf16))
+                oi = [0]
+
+                def off_run():
+                    xa, xw, xsa, xsw, xo = sets[oi[0] % 4]
+                    op.run(xa, xw, xo, scale_a=xsa, scale_b=xsw, stream=stream)
+                    oi[0] += 1
+                oms = time_launches(off_run, 100, 10, stream, warm_ms=50.0)
+                og[f"m{mm}"] = {"us": round(oms * 1e3, 2),
+                                "useful_TOPS": round(2.0 * mm * N * K / (oms * 1e-3) / 1e12, 1),
+                                "tiles": -(-mm // 256) * (N // 256)}
+                del sets
+            extra["w8a8_off_grid_n4096_k4096"] = og
+            # The headline kernel on constant operands (every byte 1): the same
+            # instructions and traffic, no data-dependent switching activity.
+            ca = torch.ones((M, K), dtype=torch.int8, device=dev)
+            cw = torch.ones((N, K), dtype=torch.int8, device=dev)
+            co = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+            cms = time_launches(lambda: plan.run(ca, cw, co, scale_a=dsa, scale_b=dsw, stream=stream),
+                                100, 10, stream, warm_ms=50.0)
+            extra["w8a8_4096_cubed_constant_operands"] = {
+                "us": round(cms * 1e3, 2), "TOPS": round(ops / (cms * 1e-3) / 1e12, 1),
+                "note": "A = W = all ones, one resident set: compare with w8a8_4096_cubed_resident_operands"}
+            del ca, cw, co
 
     ms = None
     sclk = {}

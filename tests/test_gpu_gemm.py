@@ -69,6 +69,49 @@ def test_w8a8_dma_path_shapes(gpu, shape):
     assert np.array_equal(_w8a8(a, w, sa, sw), O.gemm_w8a8_bf16(a, w, sa, sw, nthreads=8))
 
 
+# Edge tiles on the LDS-DMA path (K % 128 == 0, M or N not a multiple of
+# 256): operand rows past M / N load as zeros, stores past them are masked.
+# N % 8 == 4 and N % 4 != 0 take the per-quad epilogue inside the same kernel.
+EDGE_SHAPES = [(300, 520, 384), (1, 256, 4096), (257, 264, 128), (100, 68, 256), (70, 70, 128),
+               (513, 300, 1152), (4000, 512, 256)]
+
+
+@pytest.mark.parametrize("shape", EDGE_SHAPES)
+def test_edge_tiles_dma_path(gpu, shape):
+    m, n, k = shape
+    print(f"case: edge dma {shape}", flush=True)
+    g = rng(m + 5 * n + 11 * k)
+    a, b = int8_uniform(g, (m, k)), int8_uniform(g, (n, k))
+    assert np.array_equal(_i32(a, b), O.gemm_s8_rcr_i32(a, b, nthreads=8))
+    c = int8_uniform(g, (m, n))
+    d = torch.full((m, n), 99, dtype=torch.int8, device="cuda:0")
+    P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k)).run(dev(a), dev(b), d, c=dev(c), alpha=0.002, beta=0.75)
+    sync()
+    assert np.array_equal(d.cpu().numpy(), O.gemm_s8_rcr_s8(a, b, 0.002, 0.75, c))
+    a8, w8, sa, sw = w8a8(m, n, k, seed=m + n)
+    assert np.array_equal(_w8a8(a8, w8, sa, sw), O.gemm_w8a8_bf16(a8, w8, sa, sw, nthreads=8))
+
+
+def test_w8a8_m4000_and_m4097_sampled_rows(gpu):
+    # Off-grid token counts at the config-2 width: the last tile row is partial
+    # (160 of 256 rows at M = 4000, 1 row at M = 4097); rows on both sides of
+    # every tile-row boundary and the edge rows are compared bit-exact, plus
+    # the exact int32 column-sum identity over the whole output.
+    for m in (4000, 4097):
+        print(f"case: w8a8 M={m} N=K=4096", flush=True)
+        a, w, sa, sw = w8a8(m, 4096, 4096, seed=m)
+        got = _w8a8(a, w, sa, sw)
+        rows = [0, 255, 256, 3839, 3840, 3841, m - 2, m - 1] + list(rng(m).integers(0, m, 8))
+        for r in rows:
+            want = O.gemm_w8a8_bf16(a, w, sa, sw, rows=(int(r), int(r) + 1), nthreads=8)
+            assert np.array_equal(got[r], want[0]), (m, r)
+        d = torch.empty((m, 4096), dtype=torch.int32, device="cuda:0")
+        P.IntGemmPlan.select(P.IntGemmDescriptor(m, 4096, 4096, output=P.ElementKind.I32)).run(dev(a), dev(w), d)
+        sync()
+        colsum = d.to(torch.int64).sum(0).cpu().numpy()
+        assert np.array_equal(colsum, w.astype(np.int64) @ a.astype(np.int64).sum(0))
+
+
 @pytest.mark.parametrize("pad", [8, 4])
 def test_w8a8_dma_path_strided_output(gpu, pad):
     # ldd = N + pad: pad 8 keeps the LDS-staged 16-byte stores, pad 4 takes
@@ -289,6 +332,20 @@ def test_fp8_f32_accumulator(gpu, shape):
     a, b, _, _ = _fp8_inputs(*shape)
     got = _fp8_run(a, b, P.ElementKind.F32, alpha=1.0).cpu().numpy()
     _fp8_check_acc(got, a, b)
+
+
+@pytest.mark.parametrize("shape", [(300, 520, 384), (1, 256, 4096), (257, 264, 128), (100, 68, 256)])
+def test_fp8_edge_tiles_dma_path(gpu, shape):
+    # f32 accumulators and bf16 outputs of edge tiles on the LDS-DMA path
+    print(f"case: fp8 edge {shape}", flush=True)
+    a, b, sa, sb = _fp8_inputs(*shape, seed=shape[0])
+    got = _fp8_run(a, b, P.ElementKind.F32, alpha=1.0).cpu().numpy()
+    exact = _fp8_check_acc(got, a, b)
+    gotb = _fp8_run(a, b, P.ElementKind.Bf16, scale_a=sa, scale_b=sb).float().cpu().numpy().astype(np.float64)
+    ta, tb = np.abs(O.e4m3_to_f32(a).astype(np.float64)), np.abs(O.e4m3_to_f32(b).astype(np.float64))
+    want = exact * (np.float64(np.float32(sa) * np.float32(sb)))
+    tol = bf16_ulp(want) + 1e-4 * (ta @ tb.T) * float(np.float32(sa) * np.float32(sb))
+    assert np.all(np.abs(gotb - want) <= tol)
 
 
 def test_fp8_e4m3_out_reference_pattern(gpu):

@@ -68,6 +68,23 @@ def _check(got, want, epi):
         assert diff.max() <= 1 and (diff != 0).mean() < 0.01
 
 
+@pytest.mark.parametrize("epi", [P.EpilogueKind.Identity, P.EpilogueKind.BiasRelu])
+@pytest.mark.parametrize("layout", [P.LayoutSku.Rrr, P.LayoutSku.Rcr])
+@pytest.mark.parametrize("shape", [(300, 528, 384), (1, 256, 4096), (257, 272, 128), (100, 68, 256)])
+def test_edge_tiles_dma_path_with_c(gpu, shape, layout, epi):
+    # K % 128 == 0 with M / N off the 256 grid: the LDS-DMA kernels with
+    # zero-filled rows past M (and RRR B columns past N) and masked stores.
+    m, n, k = shape
+    print(f"case: edge {layout.value} {epi.value} {shape}", flush=True)
+    g = rng(m + 5 * n + 7 * k)
+    a = int8_uniform(g, (m, k))
+    b = int8_uniform(g, (k, n) if layout == P.LayoutSku.Rrr else (n, k))
+    c = int8_uniform(g, (m, n))
+    bias = (g.standard_normal(n) * 8).astype(np.float32)
+    got = _run(layout, epi, P.ElementKind.F32, a, b, c=c, bias=bias, alpha=1.0 / 256, beta=0.75)
+    _check(got, _want(layout, epi, a, b, c, bias, 1.0 / 256, 0.75), epi)
+
+
 @pytest.mark.parametrize("bias_kind", [P.ElementKind.F32, P.ElementKind.I32])
 @pytest.mark.parametrize("epi", EPIS)
 @pytest.mark.parametrize("layout", [P.LayoutSku.Rrr, P.LayoutSku.Rcr])
