@@ -94,19 +94,23 @@ __global__ __launch_bounds__(64) void gemv_s8w_m1_kernel(
     // each row in flight (one batch of 4 covers K = 4096).
     for (int c0 = 0; c0 < chunks; c0 += B) {
         v4i wv[B][ROWS], xlo[B], xhi[B];
-#pragma unroll
-        for (int u = 0; u < B; ++u)
-#pragma unroll
-            for (int r = 0; r < ROWS; ++r)
-                wv[u][r] = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(wr[r] + (int64_t)(c0 + u) * 1024));
-        // Keep the weight loads ahead of everything else: the scheduler would
-        // otherwise interleave them with the dot products one load at a time.
-        __builtin_amdgcn_sched_barrier(0);
+        // The batch's x values (L2 hits) are requested before its weights:
+        // loads complete in issue order, so x issued last would hold back
+        // the first dot product until every weight load had landed
+        // (11.27 -> 11.11 us at 14336 x 4096).
 #pragma unroll
         for (int u = 0; u < B; ++u) {
             xlo[u] = xv[(c0 + u) * 128];
             xhi[u] = xv[(c0 + u) * 128 + 1];
         }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < B; ++u)
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r)
+                wv[u][r] = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(wr[r] + (int64_t)(c0 + u) * 1024));
+        // Keep the weight loads ahead of the dot products: the scheduler would
+        // otherwise interleave them one load at a time.
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int u = 0; u < B; ++u)

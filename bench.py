@@ -349,10 +349,18 @@ def main():
                 gp.run(x, ws[it[0] % copies], scale, d, stream=stream)
                 it[0] += 1
             gms = time_launches(gemv, 200, 20, stream, warm_ms=30.0)
+
+            def gemv_cur():   # on the capturing stream, same rotation
+                gp.run(x, ws[it[0] % copies], scale, d)
+                it[0] += 1
+            ggs = graph_us(gemv_cur, per_graph=100)
             nbytes = n * k + 2 * k + 4 * n + 2 * n
             gbs = nbytes / (gms * 1e-3) / 1e9
             extra["gemv_s8w_m1_14336x4096"] = {"us": round(gms * 1e3, 3), "GB_s": round(gbs, 1),
                                                "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),
+                                               "graph_replay_us": round(ggs, 3),
+                                               "graph_replay_frac_hbm_peak": round(
+                                                   nbytes / (ggs * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
                                                "bytes_per_call": nbytes, "weight_copies_rotated": copies,
                                                "hbm_traffic_pmc": int(TRAFFIC_GEMV_14336x4096)}
             del ws
