@@ -287,6 +287,128 @@ __global__ __launch_bounds__(1024) void gemv_dense_m1_vec_kernel(
     }
 }
 
+// Split-K path (optional caller workspace, large problems): B read in long
+// contiguous row spans instead of 64-byte column segments.  The column-
+// segment pattern of the kernel above is bound by its access pattern -- a
+// read-only probe of it moves the 32 MiB of a bf16 K = N = 4096 B in 16 us,
+// the same bytes read contiguously take 6 us.
+//   pass 1: workgroup (slice s, column group g): 256 threads x 16 bytes of
+//           columns over the kSplitRows (32) rows of slice s; partial[s][col] =
+//           sum over the slice's k (ascending) of a[k] * B[k, col]
+//   pass 2: total = sum over s of partial[s][col] (16 ascending runs of
+//           slices, added in run order); D = alpha * total (+ beta * D)
+// Both orders are fixed, so results are bit-identical from launch to launch
+// (they differ from the no-workspace kernel's order, within the same
+// tolerance against the f64 reference).
+constexpr int kSplitRows = 32;
+constexpr int kSplitThreads = 256;
+
+template <typename Tag>
+__global__ __launch_bounds__(kSplitThreads) void gemv_dense_split_partial_kernel(
+    int n, int k, const typename Codec<Tag>::S *__restrict__ a, int64_t stride_a,
+    const typename Codec<Tag>::S *__restrict__ b, int64_t ldb, int64_t stride_b, float *__restrict__ part) {
+    typedef Codec<Tag> C;
+    typedef typename C::S S;
+    constexpr int EPL = 16 / (int)sizeof(S);
+    const int slices = (k + kSplitRows - 1) / kSplitRows;
+    const int s = blockIdx.x, slot = blockIdx.z;
+    const int col = (blockIdx.y * kSplitThreads + threadIdx.x) * EPL;
+    if (col >= n) return;
+    const S *arow = a + (int64_t)slot * stride_a;
+    const S *bcol = b + (int64_t)slot * stride_b + col;
+    const int k0 = s * kSplitRows, k1 = min(k, k0 + kSplitRows);
+    float acc[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[e] = 0.0f;
+    auto fma_row = [&](const v4i &w, float av) {
+        if constexpr (EPL == 4) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(av, __int_as_float(w[e]), acc[e]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t u = (uint32_t)w[e];
+                acc[2 * e] = __builtin_fmaf(av, C::ld((S)(u & 0xffffu)), acc[2 * e]);
+                acc[2 * e + 1] = __builtin_fmaf(av, C::ld((S)(u >> 16)), acc[2 * e + 1]);
+            }
+        }
+    };
+    if (k1 - k0 == kSplitRows) {
+        // whole slice (uniform branch): every row load issued before the first FMA
+        v4i w[kSplitRows];
+        float av[kSplitRows];
+#pragma unroll
+        for (int r = 0; r < kSplitRows; ++r)
+            w[r] = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(bcol + (int64_t)(k0 + r) * ldb));
+#pragma unroll
+        for (int r = 0; r < kSplitRows; ++r) av[r] = C::ld(arow[k0 + r]);
+#pragma unroll
+        for (int r = 0; r < kSplitRows; ++r) fma_row(w[r], av[r]);
+    } else {
+        for (int kk = k0; kk < k1; ++kk)
+            fma_row(__builtin_nontemporal_load(reinterpret_cast<const v4i *>(bcol + (int64_t)kk * ldb)),
+                    C::ld(arow[kk]));
+    }
+    float *dst = part + ((int64_t)slot * slices + s) * n + col;
+#pragma unroll
+    for (int e = 0; e < EPL; e += 4)
+        *reinterpret_cast<v4f *>(dst + e) = v4f{acc[e], acc[e + 1], acc[e + 2], acc[e + 3]};
+}
+
+// Pass 2: workgroup of 16 waves per 64 columns; wave w sums the slices
+// [w*per, (w+1)*per) of its lane's column in ascending order, then the 16
+// wave sums are added in wave order.
+template <typename Tag>
+__global__ __launch_bounds__(1024) void gemv_dense_split_reduce_kernel(
+    int n, int k, float alpha, float beta, const float *__restrict__ part, typename Codec<Tag>::S *__restrict__ d,
+    int64_t stride_d) {
+    typedef Codec<Tag> C;
+    __shared__ float ws[16][64];
+    const int slices = (k + kSplitRows - 1) / kSplitRows;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int j = blockIdx.x * 64 + lane, slot = blockIdx.y;
+    const int per = (slices + 15) / 16;
+    const int q0 = wave * per, q1 = min(slices, q0 + per);
+    float s = 0.0f;
+    if (j < n) {
+        const float *p = part + (int64_t)slot * slices * n + j;
+        int q = q0;
+        for (; q + 16 <= q1; q += 16) {
+            float v[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) v[u] = p[(int64_t)(q + u) * n];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) s += v[u];
+        }
+        for (; q < q1; ++q) s += p[(int64_t)q * n];
+    }
+    ws[wave][lane] = s;
+    __syncthreads();
+    if (wave == 0 && j < n) {
+        float t = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 16; ++w) t += ws[w][lane];
+        typename C::S *drow = d + (int64_t)slot * stride_d;
+        float out = alpha * t;
+        if (beta != 0.0f) out += beta * C::ld(drow[j]);
+        drow[j] = C::st(out);
+    }
+}
+
+// Workspace of the split-K path (0: the shape does not take it).  Taken for
+// K >= 256 and N * K >= 2^20 elements with N a multiple of the 16-byte
+// element count; the run also needs 16-byte aligned B rows.
+template <typename Tag>
+size_t dense_split_workspace(int32_t m, int32_t n, int32_t k, int32_t batch, int32_t layout) {
+    typedef typename Codec<Tag>::S S;
+    constexpr int EPL = 16 / (int)sizeof(S);
+    if (m != 1 || layout != 0 || n <= 0 || k < 256 || batch <= 0 || n % EPL != 0 ||
+        (int64_t)n * k < (1ll << 20))
+        return 0;
+    const int64_t slices = (k + kSplitRows - 1) / kSplitRows;
+    return (size_t)batch * (size_t)slices * (size_t)n * sizeof(float);
+}
+
 // gemv_dense.cu:101-122 gemv_validate, restated.
 int32_t gemv_validate(int32_t m, int32_t n, int32_t k, int32_t batch, int32_t layout, int64_t lda,
                       int64_t ldb, int64_t ldd, int64_t stride_d) {
@@ -304,7 +426,7 @@ template <typename Tag>
 int32_t launch_dense(int32_t m, int32_t n, int32_t k, int32_t batch, int32_t layout, float alpha,
                      float beta, const void *a, int64_t lda, int64_t stride_a, const void *b,
                      int64_t ldb, int64_t stride_b, void *d, int64_t ldd, int64_t stride_d,
-                     hipStream_t stream) {
+                     void *workspace, size_t workspace_bytes, hipStream_t stream) {
     const int32_t st = gemv_validate(m, n, k, batch, layout, lda, ldb, ldd, stride_d);
     if (st != kOk) return st;
     if (m == 0 || n == 0 || batch == 0) return kOk;
@@ -316,6 +438,20 @@ int32_t launch_dense(int32_t m, int32_t n, int32_t k, int32_t batch, int32_t lay
     const bool vec = n % VCOLS == 0 && ((int64_t)ldb * (int64_t)sizeof(S)) % 16 == 0 &&
                      ((int64_t)stride_b * (int64_t)sizeof(S)) % 16 == 0 &&
                      (reinterpret_cast<uintptr_t>(b) & 15u) == 0;
+    const size_t split_ws = dense_split_workspace<Tag>(m, n, k, batch, layout);
+    if (split_ws != 0 && workspace != nullptr && workspace_bytes >= split_ws &&
+        (reinterpret_cast<uintptr_t>(workspace) & 15u) == 0 &&
+        ((int64_t)ldb * (int64_t)sizeof(S)) % 16 == 0 && ((int64_t)stride_b * (int64_t)sizeof(S)) % 16 == 0 &&
+        (reinterpret_cast<uintptr_t>(b) & 15u) == 0) {
+        constexpr int EPL = 16 / (int)sizeof(S);
+        const int slices = (k + kSplitRows - 1) / kSplitRows;
+        const int groups = (n / EPL + kSplitThreads - 1) / kSplitThreads;
+        hipLaunchKernelGGL((gemv_dense_split_partial_kernel<Tag>), dim3(slices, groups, batch), dim3(kSplitThreads),
+                           0, stream, n, k, (const S *)a, stride_a, (const S *)b, ldb, stride_b, (float *)workspace);
+        hipLaunchKernelGGL((gemv_dense_split_reduce_kernel<Tag>), dim3((n + 63) / 64, batch), dim3(1024), 0, stream,
+                           n, k, alpha, beta, (const float *)workspace, (S *)d, stride_d);
+        return launch_status();
+    }
     if (vec) {
         hipLaunchKernelGGL((gemv_dense_m1_vec_kernel<Tag>), dim3(n / VCOLS, batch), dim3(1024), 0, stream,
                            n, k, alpha, beta, (const S *)a, stride_a, (const S *)b, ldb, stride_b,
@@ -386,9 +522,9 @@ int32_t baracuda_kernels_gemv_s8w_m1_bf16_gfx950_run(int32_t n, int32_t k, const
         const void *a, int64_t lda, int64_t stride_a, const void *b, int64_t ldb,                 \
         int64_t stride_b, void *d, int64_t ldd, int64_t stride_d, void *workspace,                \
         size_t workspace_bytes, void *stream) {                                                   \
-        (void)workspace; (void)workspace_bytes;                                                   \
         return launch_dense<TY>(m, n, k, batch, layout, alpha, beta, a, lda, stride_a, b, ldb,    \
-                                stride_b, d, ldd, stride_d, (hipStream_t)stream);                 \
+                                stride_b, d, ldd, stride_d, workspace, workspace_bytes,           \
+                                (hipStream_t)stream);                                             \
     }                                                                                             \
     int32_t baracuda_kernels_gemv_dense_m1_##TAG##_can_implement(                                 \
         int32_t m, int32_t n, int32_t k, int32_t batch, int32_t layout, int64_t lda, int64_t ldb, \
@@ -398,8 +534,7 @@ int32_t baracuda_kernels_gemv_s8w_m1_bf16_gfx950_run(int32_t n, int32_t k, const
     }                                                                                             \
     size_t baracuda_kernels_gemv_dense_m1_##TAG##_workspace_size(int32_t m, int32_t n, int32_t k, \
                                                                  int32_t batch, int32_t layout) { \
-        (void)m; (void)n; (void)k; (void)batch; (void)layout;                                     \
-        return 0;                                                                                 \
+        return dense_split_workspace<TY>(m, n, k, batch, layout);                                 \
     }
 
 BK_GEMV_DENSE(f32, float)

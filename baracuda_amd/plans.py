@@ -432,7 +432,7 @@ class GemvDensePlan:
             _need(t.dtype == self.dtype, "dtype mismatch")
         st = self._fn("run")(desc.m, desc.n, desc.k, desc.batch, desc.layout, alpha, beta,
                              _ptr(a), lda, stride_a, _ptr(b), ldb, stride_b, _ptr(d), ldd, stride_d,
-                             _ptr(workspace), 0, _stream(stream))
+                             _ptr(workspace), _nbytes(workspace), _stream(stream))
         check(st, "GemvDensePlan::run")
 
 

@@ -472,11 +472,21 @@ def main():
                            stride_d=0, stream=stream)
                     itd[0] += 1
                 dms = time_launches(gdense, 200, 20, stream, warm_ms=30.0)
+                # the same call with the optional workspace (split-K path)
+                dws = torch.empty(dp.workspace_size(), dtype=torch.uint8, device=dev)
+
+                def gdense_ws():
+                    dp.run(av, bmats[itd[0] % copies_d], dv, lda=Kd, stride_a=0, ldb=Nd, stride_b=0, ldd=Nd,
+                           stride_d=0, workspace=dws, stream=stream)
+                    itd[0] += 1
+                wms = time_launches(gdense_ws, 200, 20, stream, warm_ms=30.0)
                 nbd = Kd * Nd * es + Kd * es + Nd * es
                 gd[name] = {"us": round(dms * 1e3, 2), "GB_s": round(nbd / (dms * 1e-3) / 1e9, 1),
                             "frac_hbm_peak": round(nbd / (dms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-                            "copies_rotated": copies_d}
-                del bmats
+                            "with_workspace_us": round(wms * 1e3, 2),
+                            "with_workspace_frac_hbm_peak": round(nbd / (wms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                            "workspace_bytes": dp.workspace_size(), "copies_rotated": copies_d}
+                del bmats, dws
             extra["gemv_dense_m1_k4096_n4096"] = gd
         if only in ("", "quant"):
             log("bench: per-token int8 quantization bf16 4096x4096")

@@ -122,6 +122,69 @@ def test_gemv_dense_m1(gpu, tag, case):
         assert np.array_equal(got[gap], d0.double().numpy()[gap])
 
 
+@pytest.mark.parametrize("tag", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("case", [(4096, 4096, 1, False, 0.0), (512, 4096, 3, True, 0.25), (2048, 1000, 2, False, 0.5),
+                                  (8192, 257, 1, False, 0.0)])
+def test_gemv_dense_m1_split_workspace(gpu, tag, case):
+    # The optional-workspace split-K path (contiguous B row spans, fixed-order
+    # partial sums): same tolerances against the f64 reference, strided batch,
+    # broadcast B, beta, gaps between batch slots untouched.
+    n, k, batch, bcast, beta = case
+    print(f"case: gemv_dense split {tag} {case}", flush=True)
+    g = rng(7 * n + k + batch)
+    dt = _TORCH[tag]
+    stride_a, stride_d, ldb = k + 3, n + 5, n
+    stride_b = 0 if bcast else k * ldb
+    a = torch.from_numpy(g.standard_normal(batch * stride_a).astype(np.float32)).to(dt)
+    b = torch.from_numpy(g.standard_normal(max(1, (1 if bcast else batch)) * k * ldb).astype(np.float32) / 8).to(dt)
+    d0 = torch.from_numpy(g.standard_normal(batch * stride_d).astype(np.float32)).to(dt)
+    d = d0.clone().cuda()
+    plan = P.GemvDensePlan.select(P.GemvDenseDescriptor(n=n, k=k, batch=batch), dt)
+    wsb = plan.workspace_size()
+    assert wsb == batch * ((k + 31) // 32) * n * 4
+    ws = torch.full((wsb // 4,), float("nan"), dtype=torch.float32, device="cuda:0")
+    plan.run(a.cuda(), b.cuda(), d, lda=k, stride_a=stride_a, ldb=ldb, stride_b=stride_b, ldd=n,
+             stride_d=stride_d, alpha=0.75, beta=beta, workspace=ws)
+    sync()
+    want = O.gemv_dense_m1_f64(a.double().numpy(), b.double().numpy(), d0.double().numpy(), n, k, batch,
+                               stride_a, ldb, stride_b, stride_d, 0.75, beta)
+    got = d.cpu().double().numpy()
+    rel = {"f32": 1e-4, "f16": 2e-3, "bf16": 1.6e-2}[tag]
+    for gi in range(batch):
+        sl = slice(gi * stride_d, gi * stride_d + n)
+        scale = np.abs(want[sl]).max()
+        assert np.allclose(got[sl], want[sl], rtol=rel, atol=rel * scale), gi
+        gap = slice(gi * stride_d + n, (gi + 1) * stride_d)
+        assert np.array_equal(got[gap], d0.double().numpy()[gap])
+
+
+@pytest.mark.parametrize("tag", ["f32", "bf16"])
+def test_gemv_dense_split_bit_stable_and_capturable(gpu, tag):
+    # Fixed partial and reduction orders: launches and graph replays agree bit for bit.
+    n, k = 4096, 4096
+    dt = _TORCH[tag]
+    a = torch.randn(k, device="cuda:0").to(dt)
+    b = torch.randn(k * n, device="cuda:0").to(dt)
+    plan = P.GemvDensePlan.select(P.GemvDenseDescriptor(n=n, k=k), dt)
+    ws = torch.empty(plan.workspace_size(), dtype=torch.uint8, device="cuda:0")
+    run = lambda d: plan.run(a, b, d, lda=k, stride_a=0, ldb=n, stride_b=0, ldd=n, stride_d=0, workspace=ws)  # noqa: E731
+    outs = []
+    for _ in range(2):
+        d = torch.empty(n, dtype=dt, device="cuda:0")
+        run(d)
+        outs.append(d)
+    dg = torch.empty(n, dtype=dt, device="cuda:0")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        run(dg)
+    iv = torch.int32 if tag == "f32" else torch.int16
+    for _ in range(3):
+        dg.fill_(0)
+        g.replay()
+        sync()
+        assert torch.equal(outs[0].view(iv), outs[1].view(iv)) and torch.equal(outs[0].view(iv), dg.view(iv))
+
+
 @pytest.mark.parametrize("tag", ["f32", "bf16"])
 def test_gemv_dense_bit_stable_across_launches(gpu, tag):
     # The reduction order is fixed: two launches (and a graph replay) agree bit for bit.
