@@ -279,7 +279,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",
-                    help="run only: w8a8|w8a8x|gemv|quant|fp8|moe|int8epi|te|embedding|gather|copy (profiling; copy = 256 MiB "
+                    help="run only: w8a8|w8a8x|w8a8c|gemv|quant|fp8|moe|int8epi|te|embedding|gather|copy (profiling; copy = 256 MiB "
                          "device copy used to calibrate the HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -589,6 +589,12 @@ def main():
                                 "tiles": -(-mm // 256) * (N // 256)}
                 del sets
             extra["w8a8_off_grid_n4096_k4096"] = og
+        if only in ("", "w8a8c"):
+            log("bench: w8a8 random vs constant operands (resident)")
+            if only == "w8a8c":   # the random-operand phase this mode profiles against
+                rms = time_launches(run_resident, 100, 10, stream, warm_ms=50.0)
+                extra["w8a8_4096_cubed_resident_operands"] = {
+                    "us": round(rms * 1e3, 2), "TOPS": round(ops / (rms * 1e-3) / 1e12, 1)}
             # The headline kernel on constant operands (every byte 1): the same
             # instructions and traffic, no data-dependent switching activity.
             ca = torch.ones((M, K), dtype=torch.int8, device=dev)
