@@ -396,9 +396,15 @@ def main():
             mms = time_launches(lambda: mp.run(mx, mw, dsid, deid, mo, cnt, off, msa, msw, stream=stream),
                                 10, 3, stream, warm_ms=30.0)
             mt = 2.0 * tokens * topk * n * k / (mms * 1e-3) / 1e12
+            rows_e = np.bincount(eid, minlength=E)
+            tiles_m = int(sum(-(-int(r) // 256) for r in rows_e))
             extra["moe_s8_grouped_e8_top2_4096x14336x4096"] = {
                 "us": round(mms * 1e3, 1), "TOPS": round(mt, 1), "frac_int8_peak": round(mt / PEAK_INT8_TOPS, 4),
-                "expert_rows": np.bincount(eid, minlength=E).tolist()}
+                "expert_rows": rows_e.tolist(),
+                # 256 x 256 tiles over the ragged experts: computed rows vs routed rows
+                "tiles": tiles_m * (n // 256), "tile_rounds_on_256_cus": round(tiles_m * (n // 256) / 256, 2),
+                "padded_rows": tiles_m * 256, "routed_rows": int(rows_e.sum()),
+                "padding_frac": round(1 - rows_e.sum() / (tiles_m * 256), 4)}
             del mx, mw, mo
             log("bench: moe grouped bf16 (moe_wmma ABI)")
             bx = torch.randn((tokens, k), device=dev).to(torch.bfloat16)
@@ -515,7 +521,30 @@ def main():
                 "frac_hbm_peak": round(qb / (qms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4), "copies_rotated": qcop,
                 "graph_replay_us": round(qg, 2),
                 "graph_replay_frac_hbm_peak": round(qb / (qg * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)}
-            del qxs, qqs
+            # QuantizedLinearPlan end to end (bf16 activations): per-token
+            # quantization into the int8 scratch, then the W8A8 GEMM, two
+            # launches on one stream; activations rotate over the same sets.
+            lw = torch.randint(-127, 128, (4096, 4096), dtype=torch.int8, device=dev)
+            lsw = torch.rand(4096, device=dev) * 0.009 + 0.001
+            lo = torch.empty((4096, 4096), dtype=torch.bfloat16, device=dev)
+            lplan = P.QuantizedLinearPlan.select(P.QuantizedLinearDescriptor(4096, 4096, 4096))
+
+            def qlin_step():
+                i = qit[0] % qcop
+                lplan.run(qxs[i], lw, lsw, lo, qqs[i], qs, stream=stream)
+                qit[0] += 1
+            lms = time_launches(qlin_step, 60, 6, stream, warm_ms=50.0)
+
+            def qlin_cur():
+                i = qit[0] % qcop
+                lplan.run(qxs[i], lw, lsw, lo, qqs[i], qs)
+                qit[0] += 1
+            lg = graph_us(qlin_cur, per_graph=24, replays=10)
+            extra["quantized_linear_bf16_4096_cubed"] = {
+                "us": round(lms * 1e3, 2), "TOPS": round(2.0 * 4096 ** 3 / (lms * 1e-3) / 1e12, 1),
+                "graph_replay_us": round(lg, 2),
+                "note": "quantize + W8A8 GEMM (two launches); activations rotate over the quantizer's sets"}
+            del qxs, qqs, lw, lo
         if only in ("", "te"):
             log("bench: fp8 fused cast+amax bf16 14336x4096 -> e4m3")
             tn = 14336 * 4096
