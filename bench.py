@@ -49,6 +49,8 @@ def time_launches(fn, steps, warmup, stream, warm_ms=0.0):
     until that much wall time has passed (the clocks ramp under sustained
     load: a 60 us kernel timed after 10 launches reads ~15% slow)."""
     import torch
+    fn()                       # first call outside the warm-up clock: it may
+    torch.cuda.synchronize()   # load the kernel's code object (milliseconds)
     t0 = time.perf_counter()
     n = 0
     while n < warmup or (warm_ms > 0 and (time.perf_counter() - t0) * 1e3 < warm_ms):
