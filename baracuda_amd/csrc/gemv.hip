@@ -397,13 +397,14 @@ __global__ __launch_bounds__(1024) void gemv_dense_split_reduce_kernel(
 
 // Workspace of the split-K path (0: the shape does not take it).  Taken for
 // K >= 256 and N * K >= 2^20 elements with N a multiple of the 16-byte
-// element count; the run also needs 16-byte aligned B rows.
+// element count (and grid y / z extents within 65535); the run also needs
+// 16-byte aligned B rows.
 template <typename Tag>
 size_t dense_split_workspace(int32_t m, int32_t n, int32_t k, int32_t batch, int32_t layout) {
     typedef typename Codec<Tag>::S S;
     constexpr int EPL = 16 / (int)sizeof(S);
-    if (m != 1 || layout != 0 || n <= 0 || k < 256 || batch <= 0 || n % EPL != 0 ||
-        (int64_t)n * k < (1ll << 20))
+    if (m != 1 || layout != 0 || n <= 0 || k < 256 || batch <= 0 || batch > 65535 || n % EPL != 0 ||
+        (int64_t)n * k < (1ll << 20) || (n / EPL + kSplitThreads - 1) / kSplitThreads > 65535)
         return 0;
     const int64_t slices = (k + kSplitRows - 1) / kSplitRows;
     return (size_t)batch * (size_t)slices * (size_t)n * sizeof(float);
