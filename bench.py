@@ -233,6 +233,16 @@ def cpu_baselines_extra(budget_s=4.0):
     dt = time.perf_counter() - t0
     out["config1_int8_256_cubed_serial"] = {"s": round(dt, 4), "GOPS": round(2 * 256 ** 3 / dt / 1e9, 2),
                                             "threads": 1}
+    # config 2 serial, faithful to the oracle's loop: 64 sampled rows of
+    # 4096^3, the whole problem extrapolated
+    sa_, sw_ = np.full(64, 0.01, np.float32), np.full(4096, 0.005, np.float32)
+    a64, w2 = int8_uniform(g, (64, 4096)), int8_uniform(g, (4096, 4096))
+    t0 = time.perf_counter()
+    O.gemm_w8a8_bf16(a64, w2, sa_, sw_, nthreads=1)
+    dt = time.perf_counter() - t0
+    out["w8a8_4096_cubed_serial_64_rows"] = {"s": round(dt, 3), "extrapolated_full_s": round(dt * 64, 1),
+                                             "TOPS": round(2.0 * 64 * 4096 * 4096 / dt / 1e12, 6), "threads": 1}
+    del a64, w2
     n, k = 14336, 4096
     w = int8_uniform(g, (n, k))
     x = (g.standard_normal(k).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
