@@ -135,7 +135,13 @@ def check(status: int, what: str) -> None:
 
 
 def _ptr(t: Optional[torch.Tensor]):
-    return None if t is None else t.data_ptr()
+    """Device address of a GPU tensor; a host tensor is rejected here rather
+    than handed to a kernel, which would fault on the host address."""
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise InvalidProblem("operand tensors must be on the GPU")
+    return t.data_ptr()
 
 
 def _nbytes(t: Optional[torch.Tensor]) -> int:

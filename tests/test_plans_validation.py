@@ -84,3 +84,19 @@ def test_moe_strided_routing_rejected():
             plan.run(x, w, out=out, stream=0, **kw)
     with pytest.raises(P.InvalidProblem):
         plan.run(x, w, out=out, topk_weights=_strided(tokens * topk, torch.float32), stream=0, **good)
+
+
+def test_host_tensors_rejected_before_launch():
+    # Valid shapes and dtypes, but host memory: rejected before any kernel
+    # would dereference a host address.
+    m = n = k = 256
+    plan = P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, output=P.ElementKind.I32))
+    a = torch.zeros((m, k), dtype=torch.int8)
+    b = torch.zeros((n, k), dtype=torch.int8)
+    d = torch.empty((m, n), dtype=torch.int32)
+    with pytest.raises(P.InvalidProblem, match="GPU"):
+        plan.run(a, b, d, stream=0)
+    gp = P.GemvDensePlan.select(P.GemvDenseDescriptor(n=64, k=64), torch.float32)
+    with pytest.raises(P.InvalidProblem, match="GPU"):
+        gp.run(torch.ones(64), torch.ones(64 * 64), torch.empty(64), lda=64, stride_a=0, ldb=64, stride_b=0,
+               ldd=64, stride_d=0, stream=0)
