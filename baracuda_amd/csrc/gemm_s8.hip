@@ -29,20 +29,18 @@ int32_t baracuda_kernels_gemm_s8_rcr_gfx950_i32_can_implement(
 }
 
 size_t baracuda_kernels_gemm_s8_rcr_gfx950_i32_workspace_size(int32_t m, int32_t n, int32_t k) {
-    (void)m; (void)n; (void)k;
-    return 0;
+    return tail_split_workspace(m, n, k);
 }
 
 int32_t baracuda_kernels_gemm_s8_rcr_gfx950_i32_run(
     int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,
     void *d, int64_t ldd, void *workspace, size_t workspace_bytes, void *stream) {
-    (void)workspace; (void)workspace_bytes;
     int32_t st = check_rcr(m, n, k, lda, ldb, ldd);
     if (st != kOk) return st;
     if (!a || !b || !d) return kInvalid;
     S8Args p{m, n, k, (const int8_t *)a, lda, (const int8_t *)b, ldb, nullptr, 0, d, ldd,
              1.0f, 0.0f, nullptr, nullptr, nullptr};
-    return launch<EPI_I32>(p, (hipStream_t)stream);
+    return launch<EPI_I32>(p, (hipStream_t)stream, workspace, workspace_bytes);
 }
 
 // ---- int8 RCR, int8 output: D = sat_s8(alpha*acc + beta*C) ------------------
@@ -58,21 +56,19 @@ int32_t baracuda_kernels_gemm_s8_rcr_gfx950_can_implement(
 }
 
 size_t baracuda_kernels_gemm_s8_rcr_gfx950_workspace_size(int32_t m, int32_t n, int32_t k) {
-    (void)m; (void)n; (void)k;
-    return 0;
+    return tail_split_workspace(m, n, k);
 }
 
 int32_t baracuda_kernels_gemm_s8_rcr_gfx950_run(
     int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,
     const void *c, int64_t ldc, void *d, int64_t ldd, float alpha, float beta,
     void *workspace, size_t workspace_bytes, void *stream) {
-    (void)workspace; (void)workspace_bytes;
     int32_t st = baracuda_kernels_gemm_s8_rcr_gfx950_can_implement(m, n, k, a, lda, b, ldb, c, ldc, d, ldd);
     if (st != kOk) return st;
     if (!a || !b || !d) return kInvalid;
     S8Args p{m, n, k, (const int8_t *)a, lda, (const int8_t *)b, ldb, (const int8_t *)c, ldc, d, ldd,
              alpha, beta, nullptr, nullptr, nullptr};
-    return launch<EPI_S8>(p, (hipStream_t)stream);
+    return launch<EPI_S8>(p, (hipStream_t)stream, workspace, workspace_bytes);
 }
 
 // ---- W8A8: D = bf16((scale_a[m] * scale_b[n]) * acc) (new SKU) -----------
@@ -84,21 +80,19 @@ int32_t baracuda_kernels_gemm_w8a8_rcr_gfx950_bf16_can_implement(
 }
 
 size_t baracuda_kernels_gemm_w8a8_rcr_gfx950_bf16_workspace_size(int32_t m, int32_t n, int32_t k) {
-    (void)m; (void)n; (void)k;
-    return 0;
+    return tail_split_workspace(m, n, k);
 }
 
 int32_t baracuda_kernels_gemm_w8a8_rcr_gfx950_bf16_run(
     int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,
     const float *scale_a, const float *scale_b, void *d, int64_t ldd,
     void *workspace, size_t workspace_bytes, void *stream) {
-    (void)workspace; (void)workspace_bytes;
     int32_t st = check_rcr(m, n, k, lda, ldb, ldd);
     if (st != kOk) return st;
     if (!a || !b || !d || !scale_a || !scale_b) return kInvalid;
     S8Args p{m, n, k, (const int8_t *)a, lda, (const int8_t *)b, ldb, nullptr, 0, d, ldd,
              1.0f, 0.0f, scale_a, scale_b, nullptr};
-    return launch<EPI_W8A8_BF16>(p, (hipStream_t)stream);
+    return launch<EPI_W8A8_BF16>(p, (hipStream_t)stream, workspace, workspace_bytes);
 }
 
 // ---- quantized_linear_w8a8 f32 (baracuda_quantize_compose.cuh:340-370 ABI) --

@@ -34,21 +34,19 @@ extern "C" {
     }                                                                                                \
     size_t baracuda_kernels_gemm_##EPISFX##_##BSFX##_s8_rcr_gfx950_workspace_size(int32_t m,         \
                                                                                 int32_t n, int32_t k) { \
-        (void)m; (void)n; (void)k;                                                                   \
-        return 0;                                                                                    \
+        return tail_split_workspace(m, n, k);                                                        \
     }                                                                                                \
     int32_t baracuda_kernels_gemm_##EPISFX##_##BSFX##_s8_rcr_gfx950_run(                            \
         int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,     \
         const void *c, int64_t ldc, void *d, int64_t ldd, const void *bias, float alpha, float beta, \
         void *workspace, size_t workspace_bytes, void *stream) {                                     \
-        (void)workspace; (void)workspace_bytes;                                                      \
         int32_t st = bk_rcr_can(m, n, k, a, lda, b, ldb, c,   \
                                                                       ldc, d, ldd);                  \
         if (st != kOk) return st;                                                                    \
         if (!a || !b || !d || !bias) return kInvalid;                                                \
         S8Args p{m, n, k, (const int8_t *)a, lda, (const int8_t *)b, ldb, (const int8_t *)c, ldc, d, \
                  ldd, alpha, beta, nullptr, nullptr, bias};                                          \
-        return launch<EPI_S8, ACTV, BTY>(p, (hipStream_t)stream);                                    \
+        return launch<EPI_S8, ACTV, BTY>(p, (hipStream_t)stream, workspace, workspace_bytes);        \
     }
 
 BK_S8_RCR_BIAS(bias, ACT_BIAS, f32bias, float)

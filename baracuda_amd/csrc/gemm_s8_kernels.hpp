@@ -13,6 +13,8 @@
 // operands in [-127,127] whenever K < 133143.
 #pragma once
 
+#include <algorithm>
+
 #include "gemm_mfma.hpp"
 #include "gemm_mfma2.hpp"
 #include "act.hpp"
@@ -179,6 +181,39 @@ int32_t launch_rrr(const S8Args &p, hipStream_t stream) {
     return launch_status();
 }
 
+// ---- split-K of a partial last round of tiles (optional workspace) ----------
+// T tiles on 256 CUs leave a last round of T % 256 tiles.  When that round is
+// at most half full and consists of whole tile rows, its tiles are split
+// along K into `split` chunks (>= 2 stages each) run in the same launch as
+// the full rounds; each chunk stores its int32 accumulators in its own
+// workspace slot, and a second kernel adds a tile's slots in chunk order and
+// applies the epilogue.  Integer sums are exact in any order, so the output
+// is bit-identical to the unsplit kernel's.
+struct TailSplit {
+    int full_tiles;   // tiles of the full rounds (whole tile rows), plain path
+    int tail_tiles;   // tiles of the last round, split
+    int split;        // K chunks per tail tile (1: no split)
+};
+
+inline TailSplit tail_split_plan(int M, int N, int K) {
+    TailSplit t{0, 0, 1};
+    if (M <= 0 || N <= 0 || K <= 0 || K % 128 != 0) return t;
+    const int tiles_m = (M + 255) / 256, tiles_n = (N + 255) / 256;
+    const int64_t T = (int64_t)tiles_m * tiles_n;
+    const int64_t full = T / 256 * 256;
+    const int64_t tail = T - full;
+    if (tail == 0 || tail > 128 || full % tiles_n != 0) return t;
+    const int split = std::min((int)(256 / tail), K / 128 / 2);
+    if (split < 2) return t;
+    return TailSplit{(int)full, (int)tail, split};
+}
+
+// int32 slot of every (tail tile, chunk): 256 x 256 accumulators.
+inline size_t tail_split_workspace(int M, int N, int K) {
+    const TailSplit t = tail_split_plan(M, N, K);
+    return t.split > 1 ? (size_t)t.tail_tiles * t.split * 65536u * sizeof(int32_t) : 0;
+}
+
 // Rows of an operand padded to whole 256-row tiles, times its row pitch,
 // fit the 32-bit buffer offsets of the LDS-DMA path.
 inline bool dma_extent_ok(int rows, int64_t ld) {
@@ -217,23 +252,46 @@ __device__ __forceinline__ void store_s8_tile_staged(const mfma2::AccTile<P> &ac
         ncols);
 }
 
+// `ts`: workgroups below ts.full_tiles (all of them when ts.split == 1) run
+// whole tiles; the rest run K chunks of the tail tiles (tail_split_plan) and
+// store their accumulators in `slots`.
 template <int EPI, bool VecOut, int ACT = ACT_NONE, typename BiasT = float>
-__global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_s8_rcr_dma_kernel(S8Args p) {
+__global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_s8_rcr_dma_kernel(S8Args p, TailSplit ts,
+                                                                         int32_t *__restrict__ slots) {
     namespace M2 = mfma2;
     typedef M2::PolicyI8<DmaCfg> P;
     __shared__ __attribute__((aligned(1024))) int8_t stage0[2 * M2::OPER];
     __shared__ __attribute__((aligned(1024))) int8_t stage1[2 * M2::OPER];
     // Edge tiles (M or N not a multiple of 256): operand rows past M / N
     // lie past the buffer resources' byte counts and load as zeros.
-    const int tiles_m = (p.M + M2::BM - 1) / M2::BM, tiles_n = (p.N + M2::BN - 1) / M2::BN;
-    int tm, tn;
-    tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int tiles_n = (p.N + M2::BN - 1) / M2::BN;
+    int tm, tn, k0 = 0, klen = p.K, chunk = -1;
+    if (ts.split > 1 && (int)blockIdx.x >= ts.full_tiles) {
+        const int u = blockIdx.x - ts.full_tiles, ti = u / ts.split;
+        chunk = u % ts.split;
+        tm = ts.full_tiles / tiles_n + ti / tiles_n;
+        tn = ti % tiles_n;
+        const int kt = p.K / M2::BK;
+        k0 = chunk * kt / ts.split * M2::BK;
+        klen = (chunk + 1) * kt / ts.split * M2::BK - k0;
+    } else {
+        const int tiles_m = ts.split > 1 ? ts.full_tiles / tiles_n : (p.M + M2::BM - 1) / M2::BM;
+        tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    }
     const int m_base = tm * M2::BM, n_base = tn * M2::BN;
     M2::DmaRows<false, false> d;
-    d.a = M2::make_dma_interior<DmaCfg>(p.a, (uint32_t)(p.M * p.lda), (int)p.lda, m_base * (int)p.lda);
-    d.b = M2::make_dma_interior<DmaCfg>(p.b, (uint32_t)(p.N * p.ldb), (int)p.ldb, n_base * (int)p.ldb);
+    d.a = M2::make_dma_interior<DmaCfg>(p.a, (uint32_t)(p.M * p.lda), (int)p.lda, m_base * (int)p.lda + k0);
+    d.b = M2::make_dma_interior<DmaCfg>(p.b, (uint32_t)(p.N * p.ldb), (int)p.ldb, n_base * (int)p.ldb + k0);
     M2::AccTile<P> acc;
-    M2::mainloop<P>(stage0, stage1, d, p.K, acc);
+    M2::mainloop<P>(stage0, stage1, d, klen, acc);
+    if (chunk >= 0) {
+        // this chunk's int32 accumulators -> its slot (rows / columns in range)
+        int32_t *slot = slots + ((int64_t)(blockIdx.x - ts.full_tiles)) * 65536;
+        M2::for_each_quad<P>(acc, [&](int ml, int nl, const v4i &v) {
+            if (m_base + ml < p.M && n_base + nl < p.N) *reinterpret_cast<v4i *>(slot + ml * 256 + nl) = v;
+        });
+        return;
+    }
     const bool full = m_base + M2::BM <= p.M && n_base + M2::BN <= p.N;
     if constexpr (EPI == EPI_W8A8_BF16 && VecOut) {
         if (full || p.N % 8 == 0) {
@@ -272,6 +330,29 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_s8_rcr_dma_kernel(S8Args p
         }
         M2::for_each_quad<P>(acc, [&](int ml, int nl, const v4i &v) { epi(m_base + ml, n_base + nl, v); });
     }
+}
+
+// Tail tiles of a split launch: a tile's K-chunk slots added in chunk order
+// (int32, exact), then the epilogue of the unsplit kernel's general path.
+// Workgroup (tail tile, 4 rows) x 64 column quads.
+template <int EPI, bool VecOut, int ACT = ACT_NONE, typename BiasT = float>
+__global__ __launch_bounds__(256) void gemm_s8_tail_reduce_kernel(S8Args p, TailSplit ts,
+                                                                   const int32_t *__restrict__ slots) {
+    const int tiles_n = (p.N + 255) / 256;
+    const int ti = blockIdx.x;
+    const int tm = ts.full_tiles / tiles_n + ti / tiles_n, tn = ti % tiles_n;
+    const int row = blockIdx.y * 4 + (threadIdx.x >> 6), q = threadIdx.x & 63;
+    const int m = tm * 256 + row, n0 = tn * 256 + 4 * q;
+    if (m >= p.M || n0 >= p.N) return;
+    const int32_t *s = slots + (int64_t)ti * ts.split * 65536 + row * 256 + 4 * q;
+    v4i acc = *reinterpret_cast<const v4i *>(s);
+    for (int c = 1; c < ts.split; ++c) {
+        const v4i v = *reinterpret_cast<const v4i *>(s + (int64_t)c * 65536);
+        acc = v4i{(int)((uint32_t)acc[0] + (uint32_t)v[0]), (int)((uint32_t)acc[1] + (uint32_t)v[1]),
+                  (int)((uint32_t)acc[2] + (uint32_t)v[2]), (int)((uint32_t)acc[3] + (uint32_t)v[3])};
+    }
+    const S8Epilogue<EPI, VecOut, ACT, BiasT> epi{p};
+    epi(m, n0, acc);
 }
 
 // RRR fast path: A through the interior DMA, row-major B through the
@@ -719,18 +800,34 @@ int32_t launch_u8_rcr(const S8Args &p, hipStream_t stream) {
 }
 
 template <int EPI, bool VecOut, int ACT, typename BiasT>
-void launch_kernel(const S8Args &p, bool fast_k, hipStream_t stream) {
+void launch_kernel(const S8Args &p, bool fast_k, hipStream_t stream, void *workspace, size_t workspace_bytes) {
     if (fast_k) {
         const int tiles = ((p.M + mfma2::BM - 1) / mfma2::BM) * ((p.N + mfma2::BN - 1) / mfma2::BN);
-        hipLaunchKernelGGL((gemm_s8_rcr_dma_kernel<EPI, VecOut, ACT, BiasT>), dim3(tiles), dim3(DmaCfg::NT), 0, stream, p);
+        TailSplit ts = tail_split_plan(p.M, p.N, p.K);
+        const size_t need = tail_split_workspace(p.M, p.N, p.K);
+        if (ts.split > 1 && workspace != nullptr && workspace_bytes >= need &&
+            (reinterpret_cast<uintptr_t>(workspace) & 15u) == 0) {
+            int32_t *slots = static_cast<int32_t *>(workspace);
+            hipLaunchKernelGGL((gemm_s8_rcr_dma_kernel<EPI, VecOut, ACT, BiasT>),
+                               dim3(ts.full_tiles + ts.tail_tiles * ts.split), dim3(DmaCfg::NT), 0, stream, p, ts,
+                               slots);
+            hipLaunchKernelGGL((gemm_s8_tail_reduce_kernel<EPI, VecOut, ACT, BiasT>), dim3(ts.tail_tiles, 64),
+                               dim3(256), 0, stream, p, ts, (const int32_t *)slots);
+            return;
+        }
+        hipLaunchKernelGGL((gemm_s8_rcr_dma_kernel<EPI, VecOut, ACT, BiasT>), dim3(tiles), dim3(DmaCfg::NT), 0, stream, p,
+                           TailSplit{0, 0, 1}, (int32_t *)nullptr);
     } else {
         const int tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
         hipLaunchKernelGGL((gemm_s8_rcr_kernel<EPI, VecOut, ACT, BiasT>), dim3(tiles), dim3(NT), 0, stream, p);
     }
 }
 
+// workspace (optional): tail_split_workspace(M, N, K) bytes, 16-byte aligned,
+// contents on entry do not matter; given it, a partial last round of tiles
+// runs split along K (tail_split_plan).
 template <int EPI, int ACT = ACT_NONE, typename BiasT = float>
-int32_t launch(const S8Args &p, hipStream_t stream) {
+int32_t launch(const S8Args &p, hipStream_t stream, void *workspace = nullptr, size_t workspace_bytes = 0) {
     const int out_elem = (EPI == EPI_I32 || EPI == EPI_W8A8_F32) ? 4 : EPI == EPI_W8A8_F64 ? 8 : (EPI == EPI_S8 ? 1 : 2);
     // The DMA path needs whole 256x256 tiles, whole K stages and 16-byte rows.
     // The DMA path needs whole K stages and 16-byte rows; edge tiles read
@@ -745,8 +842,8 @@ int32_t launch(const S8Args &p, hipStream_t stream) {
                (reinterpret_cast<uintptr_t>(p.d) % (4 * out_elem)) == 0 &&
                (p.sw == nullptr || aligned16(p.sw)) && (p.N % 4 == 0);
     if (EPI == EPI_W8A8_BF16) vec = vec && p.ldd % 8 == 0 && aligned16(p.d);
-    if (vec) launch_kernel<EPI, true, ACT, BiasT>(p, fast_k, stream);
-    else launch_kernel<EPI, false, ACT, BiasT>(p, fast_k, stream);
+    if (vec) launch_kernel<EPI, true, ACT, BiasT>(p, fast_k, stream, workspace, workspace_bytes);
+    else launch_kernel<EPI, false, ACT, BiasT>(p, fast_k, stream, workspace, workspace_bytes);
     return launch_status();
 }
 

@@ -296,13 +296,13 @@ class IntGemmPlan:
             st = self._symbol("run")(*args, alpha, beta, _ptr(workspace), _nbytes(workspace), s)
         elif desc.output == ElementKind.I32:
             st = L.gemm_s8_rcr_gfx950_i32_run(desc.m, desc.n, desc.k, _ptr(a), _ld(a), _ptr(b), _ld(b),
-                                              _ptr(d), _ld(d), _ptr(workspace), 0, s)
+                                              _ptr(d), _ld(d), _ptr(workspace), _nbytes(workspace), s)
         else:
             _vec(scale_a, desc.m, torch.float32, "W8A8 scale_a")
             _vec(scale_b, desc.n, torch.float32, "W8A8 scale_b")
             st = L.gemm_w8a8_rcr_gfx950_bf16_run(desc.m, desc.n, desc.k, _ptr(a), _ld(a), _ptr(b), _ld(b),
                                                  _ptr(scale_a), _ptr(scale_b), _ptr(d), _ld(d),
-                                                 _ptr(workspace), 0, s)
+                                                 _ptr(workspace), _nbytes(workspace), s)
         check(st, "IntGemmPlan::run")
 
 

@@ -642,6 +642,19 @@ def main():
                 og[f"m{mm}"] = {"us": round(oms * 1e3, 2),
                                 "useful_TOPS": round(2.0 * mm * N * K / (oms * 1e-3) / 1e12, 1),
                                 "tiles": -(-mm // 256) * (N // 256)}
+                if op.workspace_size() > 0:
+                    # the optional workspace: the partial last round split along K
+                    ows = torch.empty(op.workspace_size(), dtype=torch.uint8, device=dev)
+
+                    def off_run_ws():
+                        xa, xw, xsa, xsw, xo = sets[oi[0] % 4]
+                        op.run(xa, xw, xo, scale_a=xsa, scale_b=xsw, workspace=ows, stream=stream)
+                        oi[0] += 1
+                    wms = time_launches(off_run_ws, 100, 10, stream, warm_ms=50.0)
+                    og[f"m{mm}"].update({"with_workspace_us": round(wms * 1e3, 2),
+                                         "with_workspace_useful_TOPS": round(2.0 * mm * N * K / (wms * 1e-3) / 1e12, 1),
+                                         "workspace_bytes": op.workspace_size()})
+                    del ows
                 del sets
             extra["w8a8_off_grid_n4096_k4096"] = og
         if only in ("", "w8a8c"):

@@ -13,9 +13,14 @@
  *   - `stream` is a hipStream_t passed as void* (NULL = default stream);
  *   - strides and leading dimensions are in elements;
  *   - workspace is never required: every _workspace_size returns 0 except
- *     the u8 RRR family's and gemv_dense_m1's (large shapes), whose optional
- *     workspace (when given at least that size, 256- / 16-byte aligned)
- *     selects a faster path; without it every entry point runs as-is.
+ *     the u8 RRR family's, gemv_dense_m1's (large shapes) and the int8 RCR
+ *     SKUs' (s8 / i32 / W8A8 bf16 out and the bias family, when the last
+ *     round of 256 x 256 tiles on the 256 CUs is at most half full), whose
+ *     optional workspace (when given at least that size, 256- / 16-byte
+ *     aligned; contents on entry do not matter) selects a faster path: the
+ *     u8 pre-pass, the dense GEMV's split-K, the int8 tail round split along
+ *     K (two launches, bit-identical output).  Without it every entry point
+ *     runs as-is.
  *
  * Each declaration cites the reference entry point it replaces
  * (paths relative to the baracuda repository root).

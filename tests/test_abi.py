@@ -250,3 +250,15 @@ def test_plan_select_and_sku():
         P.GemvDensePlan.select(P.GemvDenseDescriptor(n=4, k=4, m=2), __import__("torch").float32)
     with pytest.raises(P.Unsupported):
         P.MoeS8GroupedPlan.select(2048, 2, 16, 16, 16)
+
+
+def test_tail_split_workspace_sizes():
+    # the optional split-K workspace of a partial last round: whole rounds, a
+    # last round more than half full, or K too short take none
+    assert P.IntGemmPlan.select(P.IntGemmDescriptor(4097, 4096, 4096, output=P.ElementKind.Bf16)
+                                ).workspace_size() == 16 * 16 * 65536 * 4
+    assert P.IntGemmPlan.select(P.IntGemmDescriptor(512, 512, 8192, output=P.ElementKind.I32)
+                                ).workspace_size() == 4 * 32 * 65536 * 4
+    # whole rounds, or a last round more than half full, or K too short: no workspace
+    for m, n, k in ((4096, 4096, 4096), (4352, 2048, 4096), (256, 256, 128), (4000, 4096, 4096)):
+        assert P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, output=P.ElementKind.Bf16)).workspace_size() == 0

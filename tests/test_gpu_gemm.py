@@ -112,6 +112,61 @@ def test_w8a8_m4000_and_m4097_sampled_rows(gpu):
         assert np.array_equal(colsum, w.astype(np.int64) @ a.astype(np.int64).sum(0))
 
 
+def _ws(plan):
+    n = plan.workspace_size()
+    return torch.full((max(n, 1),), 0x5A, dtype=torch.uint8, device="cuda:0") if n else None
+
+
+def test_tail_split_w8a8_m4097_bit_identical(gpu):
+    # M = 4097 at the config-2 width: 272 tiles, the 17th tile row (one valid
+    # row) runs split along K through the optional workspace; the output
+    # equals the unsplit launch's and the oracle's.
+    m, n, k = 4097, 4096, 4096
+    print("case: tail split w8a8 M=4097", flush=True)
+    a, w, sa, sw = w8a8(m, n, k, seed=41)
+    plan = P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, output=P.ElementKind.Bf16))
+    ws = _ws(plan)
+    assert ws is not None and plan.workspace_size() == 16 * 16 * 65536 * 4
+    outs = []
+    for work in (None, ws):
+        d = torch.empty((m, n), dtype=torch.bfloat16, device="cuda:0")
+        plan.run(dev(a), dev(w), d, scale_a=dev(sa), scale_b=dev(sw), workspace=work)
+        sync()
+        outs.append(host_bits16(d))
+    assert np.array_equal(outs[0], outs[1])
+    for r in (0, 4095, 4096):
+        assert np.array_equal(outs[1][r], O.gemm_w8a8_bf16(a, w, sa, sw, rows=(r, r + 1), nthreads=8)[0]), r
+
+
+@pytest.mark.parametrize("shape", [(512, 512, 8192), (300, 520, 1024), (1, 256, 4096), (1024, 768, 2048)])
+def test_tail_split_small_grids(gpu, shape):
+    # Grids below one round (T < 256 tiles) split every tile along K: int32
+    # accumulators exact, s8 with C / beta and a bias epilogue equal the oracle.
+    m, n, k = shape
+    print(f"case: tail split {shape}", flush=True)
+    g = rng(m + 3 * n + k)
+    a, b = int8_uniform(g, (m, k)), int8_uniform(g, (n, k))
+    pi = P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, output=P.ElementKind.I32))
+    assert pi.workspace_size() > 0
+    d = torch.full((m, n), -7, dtype=torch.int32, device="cuda:0")
+    pi.run(dev(a), dev(b), d, workspace=_ws(pi))
+    sync()
+    assert np.array_equal(d.cpu().numpy(), O.gemm_s8_rcr_i32(a, b, nthreads=8))
+    c = int8_uniform(g, (m, n))
+    ps = P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k))
+    d8 = torch.full((m, n), 99, dtype=torch.int8, device="cuda:0")
+    ps.run(dev(a), dev(b), d8, c=dev(c), alpha=0.002, beta=0.75, workspace=_ws(ps))
+    sync()
+    assert np.array_equal(d8.cpu().numpy(), O.gemm_s8_rcr_s8(a, b, 0.002, 0.75, c))
+    bias = (g.standard_normal(n) * 8).astype(np.float32)
+    pb = P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, epilogue=P.EpilogueKind.BiasRelu,
+                                                  bias_element=P.ElementKind.F32))
+    db = torch.full((m, n), 99, dtype=torch.int8, device="cuda:0")
+    pb.run(dev(a), dev(b), db, c=dev(c), alpha=1.0 / 256, beta=0.75, bias=dev(bias), workspace=_ws(pb))
+    sync()
+    assert np.array_equal(db.cpu().numpy(), O.gemm_s8_epi(a, b, "rcr", 1.0 / 256, 0.75, c, bias, "relu"))
+
+
 @pytest.mark.parametrize("pad", [8, 4])
 def test_w8a8_dma_path_strided_output(gpu, pad):
     # ldd = N + pad: pad 8 keeps the LDS-staged 16-byte stores, pad 4 takes
