@@ -99,13 +99,17 @@ struct MoeArgs {
     int E, topk, size_m, N, K;  // K in elements
 };
 
-// Ragged tile list: slot -> (expert, first pair of the tile, rows in it).
-// The E+1 offsets are loaded in one parallel step into LDS, then every thread
-// walks them from LDS (workgroup-uniform result); false past the last tile.
-__device__ __forceinline__ bool moe_tile(const MoeArgs &p, int32_t *s_off, int slot, int &e,
-                                         int &seg0, int &rows_out) {
+// The E+1 offsets, clamped to size_m, loaded in one parallel step into LDS.
+__device__ __forceinline__ void moe_load_offsets(const MoeArgs &p, int32_t *s_off) {
     for (int i = threadIdx.x; i <= p.E; i += blockDim.x) s_off[i] = min(p.offsets[i], p.size_m);
     __syncthreads();
+}
+
+// Ragged tile list: slot -> (expert, first pair of the tile, rows in it),
+// walked by every thread from the offsets in LDS (workgroup-uniform result);
+// false past the last tile.
+__device__ __forceinline__ bool moe_find(const MoeArgs &p, const int32_t *s_off, int slot, int &e,
+                                         int &seg0, int &rows_out) {
     for (e = 0; e < p.E; ++e) {
         const int o0 = s_off[e], o1 = s_off[e + 1];
         const int rows = o1 > o0 ? o1 - o0 : 0;
@@ -118,6 +122,12 @@ __device__ __forceinline__ bool moe_tile(const MoeArgs &p, int32_t *s_off, int s
         slot -= tiles;
     }
     return false;
+}
+
+__device__ __forceinline__ bool moe_tile(const MoeArgs &p, int32_t *s_off, int slot, int &e,
+                                         int &seg0, int &rows_out) {
+    moe_load_offsets(p, s_off);
+    return moe_find(p, s_off, slot, e, seg0, rows_out);
 }
 
 // W8A8 epilogue of one group of 4 columns of tile row ml.
@@ -204,17 +214,31 @@ __global__ __launch_bounds__(NT, 1) void moe_grouped_kernel(MoeArgs p) {
 // expert's weight slab.
 typedef mfma2::Cfg<2, 4> DmaCfg;
 
-// Workgroup id -> (slot, n-tile).  Workgroups are dispatched round-robin
-// over the 8 XCDs; the id is regrouped so each XCD owns a contiguous range of
-// n-tiles with every expert's m-tiles for them (slot fastest), so an expert's
-// weight panel is fetched into one XCD's L2 only.  Ids past the work exit.
-__device__ __forceinline__ bool moe_dma_coords(int pid, int total_padded, int slots, int n_tiles,
-                                               int &slot, int &ntile) {
+// Workgroup id -> tile of the compact ragged list.  The list holds
+// T = S * n_tiles tiles (S = sum_e ceil(cnt_e / 256) m-tiles, from the
+// offsets in LDS), tile r = (n-tile r / S, slot r % S).  Workgroups are
+// dispatched round-robin over the 8 XCDs; the id is regrouped so each XCD
+// owns a contiguous range of the list (slot fastest), so an expert's weight
+// panel is fetched into one XCD's L2 only.  Ids past the list exit (the
+// grid is sized for the largest possible S).  Against a regroup over that
+// largest grid, whose surplus slots exit inside every XCD's range: 567
+// against 577 us on config 5 (five alternating pairs).
+__device__ __forceinline__ bool moe_dma_coords(const MoeArgs &p, const int32_t *s_off, int pid,
+                                               int n_tiles, int &slot, int &ntile) {
     constexpr int XCDS = 8;
-    const int t = (pid % XCDS) * (total_padded / XCDS) + pid / XCDS;
-    slot = t % slots;
-    ntile = t / slots;
-    return ntile < n_tiles;
+    int S = 0;
+    for (int e = 0; e < p.E; ++e) {
+        const int rows = s_off[e + 1] > s_off[e] ? s_off[e + 1] - s_off[e] : 0;
+        S += (rows + 255) / 256;
+    }
+    const int T = S * n_tiles;
+    const int padded = (T + XCDS - 1) / XCDS * XCDS;
+    if (pid >= padded) return false;
+    const int r = (pid % XCDS) * (padded / XCDS) + pid / XCDS;
+    if (r >= T) return false;
+    slot = r % S;
+    ntile = r / S;
+    return true;
 }
 
 template <int KIND> struct MoePolicy { typedef mfma2::PolicyI8<DmaCfg> type; };
@@ -222,7 +246,7 @@ template <> struct MoePolicy<MOE_BF16> { typedef mfma2::PolicyH16<DmaCfg, true> 
 template <> struct MoePolicy<MOE_F16> { typedef mfma2::PolicyH16<DmaCfg, false> type; };
 
 template <int KIND>
-__global__ __launch_bounds__(DmaCfg::NT, 1) void moe_grouped_dma_kernel(MoeArgs p, int slots) {
+__global__ __launch_bounds__(DmaCfg::NT, 1) void moe_grouped_dma_kernel(MoeArgs p) {
     namespace M2 = mfma2;
     typedef typename MoePolicy<KIND>::type P;
     constexpr int ES = MoeElem<KIND>::SIZE;
@@ -230,10 +254,10 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void moe_grouped_dma_kernel(MoeArgs 
     __shared__ __attribute__((aligned(1024))) int8_t stage1[2 * M2::OPER];
     __shared__ int32_t s_rows_tok[M2::BM];
     __shared__ int32_t s_off[kMaxExperts + 1];
-    int slot, ntile;
-    if (!moe_dma_coords(blockIdx.x, gridDim.x, slots, p.N / M2::BN, slot, ntile)) return;
-    int e, seg0, seg_rows;
-    if (!moe_tile(p, s_off, slot, e, seg0, seg_rows)) return;   // whole workgroup exits
+    moe_load_offsets(p, s_off);
+    int slot, ntile, e, seg0, seg_rows;
+    if (!moe_dma_coords(p, s_off, blockIdx.x, p.N / M2::BN, slot, ntile)) return;   // whole workgroup exits
+    if (!moe_find(p, s_off, slot, e, seg0, seg_rows)) return;
     const int n_base = ntile * M2::BN;
     for (int r = threadIdx.x; r < M2::BM; r += DmaCfg::NT)
         s_rows_tok[r] = p.sorted_ids[seg0 + min(r, seg_rows - 1)];
@@ -332,7 +356,7 @@ int32_t launch_moe(const MoeArgs &p, const int32_t *expert_ids, int32_t *expert_
     if (fast) {
         const int work = slots * (p.N / mfma2::BN);
         const int padded = (work + 7) / 8 * 8;   // whole XCD groups
-        hipLaunchKernelGGL((moe_grouped_dma_kernel<KIND>), dim3(padded), dim3(DmaCfg::NT), 0, stream, p, slots);
+        hipLaunchKernelGGL((moe_grouped_dma_kernel<KIND>), dim3(padded), dim3(DmaCfg::NT), 0, stream, p);
     } else {
         dim3 grid(slots, (p.N + BN - 1) / BN);
         hipLaunchKernelGGL((moe_grouped_kernel<KIND>), grid, dim3(NT), 0, stream, p);

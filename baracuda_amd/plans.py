@@ -574,8 +574,13 @@ class MoeS8GroupedPlan:
               "MoeS8GroupedPlan::select")
         return cls(num_experts, topk, size_m, size_n, size_k)
 
+    def workspace_size(self) -> int:
+        """Optional workspace: the K split of a partial last round of tiles
+        (bit-identical output with or without it)."""
+        return int(lib().moe_s8_grouped_bf16_gfx950_workspace_size(self.E, self.topk, self.size_m, self.n, self.k))
+
     def run(self, x, w, sorted_token_ids, expert_ids, out, expert_counts, expert_offsets,
-            scale_a, scale_w, topk_weights=None, stream=None) -> None:
+            scale_a, scale_w, topk_weights=None, workspace=None, stream=None) -> None:
         _need(x.dtype == torch.int8 and w.dtype == torch.int8 and out.dtype == torch.bfloat16, "dtypes")
         _need(w.numel() == self.E * self.n * self.k and x.shape[-1] == self.k, "shapes")
         _need(x.is_contiguous() and w.is_contiguous() and out.is_contiguous(), "x, w, out contiguous")
@@ -591,7 +596,7 @@ class MoeS8GroupedPlan:
         st = lib().moe_s8_grouped_bf16_gfx950_run(
             _ptr(x), _ptr(w), _ptr(sorted_token_ids), _ptr(expert_ids), _ptr(topk_weights), _ptr(out),
             _ptr(expert_counts), _ptr(expert_offsets), self.E, self.topk, self.size_m, self.n, self.k,
-            _ptr(scale_a), _ptr(scale_w), None, 0, _stream(stream))
+            _ptr(scale_a), _ptr(scale_w), _ptr(workspace), _nbytes(workspace), _stream(stream))
         check(st, "MoeS8GroupedPlan::run")
 
 

@@ -11,7 +11,7 @@ from tests.gpu_util import dev, host_bits16, sync
 pytestmark = pytest.mark.gpu
 
 
-def _run(tokens, E, topk, n, k, seed, topk_w=False, pairs_check=None, routing=None):
+def _run(tokens, E, topk, n, k, seed, topk_w=False, pairs_check=None, routing=None, ws_bytes=None):
     sorted_ids, expert_ids = routing if routing is not None else moe_routing(tokens, E, topk, seed=seed)
     size_m = tokens * topk
     g = rng(seed + 100)
@@ -26,8 +26,12 @@ def _run(tokens, E, topk, n, k, seed, topk_w=False, pairs_check=None, routing=No
     counts = torch.zeros(E, dtype=torch.int32, device="cuda:0")
     offs = torch.zeros(E + 1, dtype=torch.int32, device="cuda:0")
     plan = P.MoeS8GroupedPlan.select(E, topk, size_m, n, k)
+    ws = None
+    if ws_bytes is not None:
+        # contents on entry must not matter
+        ws = torch.full(((ws_bytes or plan.workspace_size()) // 4,), -123456, dtype=torch.int32, device="cuda:0")
     plan.run(dev(xin), dev(w), dev(sorted_ids), dev(expert_ids), out, counts, offs, dev(sa_in), dev(sw),
-             topk_weights=dev(tw) if tw is not None else None)
+             topk_weights=dev(tw) if tw is not None else None, workspace=ws)
     sync()
     c_ref, o_ref = O.moe_expert_offsets(expert_ids, E)
     assert np.array_equal(counts.cpu().numpy(), c_ref)
@@ -133,3 +137,20 @@ def test_moe_dma_path_many_experts(gpu):
     # GEMM: mostly single partial tiles, some experts empty.
     print("case: moe 80 experts", flush=True)
     _run(tokens=600, E=80, topk=2, n=256, k=256, seed=21)
+
+
+def test_moe_dma_tile_list_not_multiple_of_8(gpu):
+    # 43 m-tiles x 3 n-tiles = 129 tiles: the XCD regroup pads the list to
+    # 136 and the surplus ids exit; sampled pairs over every expert.
+    print("case: moe tile list 129", flush=True)
+    counts = [256] * 40 + [200, 3, 129]
+    tokens, routing = _block_routing(counts, seed=16)
+    _run(tokens=tokens, E=len(counts), topk=1, n=768, k=256, seed=16, routing=routing,
+         pairs_check=list(range(0, tokens, 37)) + [tokens - 1])
+
+
+def test_moe_workspace_is_ignored(gpu):
+    # workspace_size() is 0; a workspace passed anyway changes nothing
+    print("case: moe workspace ignored", flush=True)
+    assert P.MoeS8GroupedPlan.select(8, 2, 1400, 512, 384).workspace_size() == 0
+    _run(tokens=700, E=8, topk=2, n=512, k=384, seed=9, ws_bytes=1 << 20)
