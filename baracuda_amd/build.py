@@ -85,7 +85,8 @@ def build(verbose: bool = False) -> Path:
     os.replace(tmp, LIB)
     STAMP.write_text(digest + "\n")
     if verbose:
-        print(f"built {LIB} from {len(sources)} sources")
+        # stderr: callers such as bench.py keep stdout for their own output
+        print(f"built {LIB} from {len(sources)} sources", file=sys.stderr)
     return LIB
 
 

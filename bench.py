@@ -381,28 +381,38 @@ def main():
             m, n, k = 2048, 14336, 4096
             # 5 operand/output sets (629 MB per rotation > 2 x the 256 MB
             # Infinity Cache): every call reads its operands from HBM.
+            # BASELINE.json config 3 inputs: N(0,1), scaled so the absmax maps
+            # to 448, cast to e4m3 (RNE); per-tensor scales absmax / 448.
+            fgen = torch.Generator(device=dev)
+            fgen.manual_seed(3)
+
+            def e4m3_operand(rows):
+                x = torch.randn((rows, k), generator=fgen, device=dev)
+                s_x = float(x.abs().max()) / 448.0
+                q = (x / s_x).to(torch.float8_e4m3fn).view(torch.uint8)
+                del x
+                return q, s_x
             fsets = []
             for _ in range(5):
-                fa = torch.randint(0, 256, (m, k), dtype=torch.uint8, device=dev)
-                fb = torch.randint(0, 256, (n, k), dtype=torch.uint8, device=dev)
-                fa[(fa & 0x7F) == 0x7F] = 0   # no NaN codes
-                fb[(fb & 0x7F) == 0x7F] = 0
-                fsets.append((fa, fb, torch.empty((m, n), dtype=torch.bfloat16, device=dev)))
+                fa, s_fa = e4m3_operand(m)
+                fb, s_fb = e4m3_operand(n)
+                fsets.append((fa, fb, torch.empty((m, n), dtype=torch.bfloat16, device=dev), s_fa, s_fb))
             fp = P.Fp8GemmPlan.select(P.Fp8GemmDescriptor(m, n, k, output=P.ElementKind.Bf16))
             fit = [0]
 
             def fp8_step():
-                xa, xb, xd = fsets[fit[0] % 5]
-                fp.run(xa, xb, xd, scale_a=0.01, scale_b=0.02, stream=stream)
+                xa, xb, xd, s_xa, s_xb = fsets[fit[0] % 5]
+                fp.run(xa, xb, xd, scale_a=s_xa, scale_b=s_xb, stream=stream)
                 fit[0] += 1
             fms = time_launches(fp8_step, 40, 5, stream, warm_ms=30.0)
-            ra, rb, rd = fsets[0]
-            frs = time_launches(lambda: fp.run(ra, rb, rd, scale_a=0.01, scale_b=0.02, stream=stream), 40, 5,
+            ra, rb, rd, s_ra, s_rb = fsets[0]
+            frs = time_launches(lambda: fp.run(ra, rb, rd, scale_a=s_ra, scale_b=s_rb, stream=stream), 40, 5,
                                 stream, warm_ms=30.0)
             tf = 2.0 * m * n * k / (fms * 1e-3) / 1e12
             extra["fp8_e4m3_gemm_2048x14336x4096"] = {"us": round(fms * 1e3, 2), "TFLOPS": round(tf, 1),
                                                       "frac_fp8_peak": round(tf / PEAK_FP8_TFLOPS, 4),
                                                       "operand_sets_rotated": 5,
+                                                      "data": "N(0,1), absmax -> 448, e4m3 RNE; scales absmax/448",
                                                       "resident_operands_us": round(frs * 1e3, 2)}
             del fsets, fa, fb, ra, rb, rd
         if only in ("", "moe"):
