@@ -103,3 +103,38 @@ def test_fp8_sweep(gpu, shape):
     ta, tb = np.abs(O.e4m3_to_f32(a).astype(np.float64)), np.abs(O.e4m3_to_f32(b).astype(np.float64))
     err = np.abs(d.cpu().numpy().astype(np.float64) - exact)
     assert np.all(err <= 1e-3 * np.abs(exact) + 1e-4 * (ta @ tb.T)), err.max()
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_int8_rrr_bias_relu_sweep(gpu, shape):
+    # RRR (B [K, N] row-major) s8 out, BiasRelu with an f32 bias and C:
+    # bit-exact against the oracle.
+    m, n, k = shape
+    print(f"case: sweep rrr bias_relu {shape}", flush=True)
+    g = rng(3 * m + n + 17 * k)
+    a, b, c = int8_uniform(g, (m, k)), int8_uniform(g, (k, n)), int8_uniform(g, (m, n))
+    bias = (g.standard_normal(n) * 6).astype(np.float32)
+    plan = P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, layout=P.LayoutSku.Rrr,
+                                                    epilogue=P.EpilogueKind.BiasRelu,
+                                                    bias_element=P.ElementKind.F32))
+    d = torch.full((m, n), 99, dtype=torch.int8, device="cuda:0")
+    plan.run(dev(a), dev(b), d, c=dev(c), alpha=0.004, beta=0.25, bias=dev(bias))
+    sync()
+    assert np.array_equal(d.cpu().numpy(), O.gemm_s8_epi(a, b, "rrr", 0.004, 0.25, c, bias, "relu"))
+
+
+@pytest.mark.parametrize("use_ws", [False, True])
+@pytest.mark.parametrize("shape", SHAPES[::3])
+def test_u8_rrr_sweep(gpu, shape, use_ws):
+    m, n, k = shape
+    print(f"case: sweep u8 rrr {shape} ws={use_ws}", flush=True)
+    g = rng(m + 11 * n + 5 * k)
+    a = g.integers(0, 256, (m, k)).astype(np.uint8)
+    b = g.integers(0, 256, (k, n)).astype(np.uint8)
+    plan = P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, layout=P.LayoutSku.Rrr, element=P.ElementKind.U8,
+                                                    output=P.ElementKind.U8))
+    d = torch.full((m, n), 99, dtype=torch.uint8, device="cuda:0")
+    alpha = 1.0 / (128.0 * k)
+    plan.run(dev(a), dev(b), d, alpha=alpha, workspace=_ws(plan, use_ws))
+    sync()
+    assert np.array_equal(d.cpu().numpy(), O.gemm_u8_epi(a, b, "rrr", alpha))
