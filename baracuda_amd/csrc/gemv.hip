@@ -293,14 +293,21 @@ __global__ __launch_bounds__(1024) void gemv_dense_m1_vec_kernel(
 // read-only probe of it moves the 32 MiB of a bf16 K = N = 4096 B in 16 us,
 // the same bytes read contiguously take 6 us.
 //   pass 1: workgroup (slice s, column group g): 256 threads x 16 bytes of
-//           columns over the kSplitRows (32) rows of slice s; partial[s][col] =
+//           columns over the split_rows<Tag>() rows of slice s (16 for 16-bit
+//           elements, 8 for f32); partial[s][col] =
 //           sum over the slice's k (ascending) of a[k] * B[k, col]
 //   pass 2: total = sum over s of partial[s][col] (16 ascending runs of
 //           slices, added in run order); D = alpha * total (+ beta * D)
 // Both orders are fixed, so results are bit-identical from launch to launch
 // (they differ from the no-workspace kernel's order, within the same
 // tolerance against the f64 reference).
-constexpr int kSplitRows = 32;
+// Rows per slice: more, shorter slices put more workgroups and more loads in
+// flight at once; the partials grow in proportion.  K = N = 4096 with B
+// rotated through HBM, one box, with workspace: bf16 8 / 12 / 16 / 24 / 32
+// rows 13.6 / 14.8 / 11.0 / 17.0 / 12.1 us, f32 17.9 / 19.9 / 18.7 / 22.0 /
+// 19.2 us (slice counts that are not powers of two leave ragged grids).
+template <typename Tag>
+constexpr int split_rows() { return sizeof(typename Codec<Tag>::S) == 4 ? 8 : 16; }
 constexpr int kSplitThreads = 256;
 
 template <typename Tag>
@@ -310,6 +317,7 @@ __global__ __launch_bounds__(kSplitThreads) void gemv_dense_split_partial_kernel
     typedef Codec<Tag> C;
     typedef typename C::S S;
     constexpr int EPL = 16 / (int)sizeof(S);
+    constexpr int kSplitRows = split_rows<Tag>();
     const int slices = (k + kSplitRows - 1) / kSplitRows;
     const int s = blockIdx.x, slot = blockIdx.z;
     const int col = (blockIdx.y * kSplitThreads + threadIdx.x) * EPL;
@@ -364,6 +372,7 @@ __global__ __launch_bounds__(1024) void gemv_dense_split_reduce_kernel(
     int64_t stride_d) {
     typedef Codec<Tag> C;
     __shared__ float ws[16][64];
+    constexpr int kSplitRows = split_rows<Tag>();
     const int slices = (k + kSplitRows - 1) / kSplitRows;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int j = blockIdx.x * 64 + lane, slot = blockIdx.y;
@@ -406,7 +415,7 @@ size_t dense_split_workspace(int32_t m, int32_t n, int32_t k, int32_t batch, int
     if (m != 1 || layout != 0 || n <= 0 || k < 256 || batch <= 0 || batch > 65535 || n % EPL != 0 ||
         (int64_t)n * k < (1ll << 20) || (n / EPL + kSplitThreads - 1) / kSplitThreads > 65535)
         return 0;
-    const int64_t slices = (k + kSplitRows - 1) / kSplitRows;
+    const int64_t slices = (k + split_rows<Tag>() - 1) / split_rows<Tag>();
     return (size_t)batch * (size_t)slices * (size_t)n * sizeof(float);
 }
 
@@ -445,7 +454,7 @@ int32_t launch_dense(int32_t m, int32_t n, int32_t k, int32_t batch, int32_t lay
         ((int64_t)ldb * (int64_t)sizeof(S)) % 16 == 0 && ((int64_t)stride_b * (int64_t)sizeof(S)) % 16 == 0 &&
         (reinterpret_cast<uintptr_t>(b) & 15u) == 0) {
         constexpr int EPL = 16 / (int)sizeof(S);
-        const int slices = (k + kSplitRows - 1) / kSplitRows;
+        const int slices = (k + split_rows<Tag>() - 1) / split_rows<Tag>();
         const int groups = (n / EPL + kSplitThreads - 1) / kSplitThreads;
         hipLaunchKernelGGL((gemv_dense_split_partial_kernel<Tag>), dim3(slices, groups, batch), dim3(kSplitThreads),
                            0, stream, n, k, (const S *)a, stride_a, (const S *)b, ldb, stride_b, (float *)workspace);

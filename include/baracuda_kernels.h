@@ -441,11 +441,12 @@ int32_t baracuda_kernels_gemm_fp8_e4m3_rcr_gfx950_f32_can_implement(
  * (crates/baracuda-kernels-sys/kernels/gemm/gemv_dense.cu:235-342), same ABI:
  * D[g,0,:] = alpha*A[g,0,:]·B[g] + beta*D[g,0,:], RRR (layout 0), f32 accumulate,
  * stride_b == 0 broadcasts B, beta == 0 never reads D.  The reference's
- * _workspace_size returns 0; here it returns batch * ceil(K/32) * N * 4
- * bytes for K >= 256, N * K >= 2^20 and N a multiple of 16 bytes of
- * elements (0 otherwise): given that workspace (16-byte aligned), _run reads
- * B in contiguous row spans and sums per-32-row partials in a fixed order
- * (split-K, two launches); given none it runs the column-segment kernel. */
+ * _workspace_size returns 0; here it returns batch * ceil(K/R) * N * 4
+ * bytes (R = 16 rows for f16 / bf16, 8 for f32) for K >= 256, N * K >= 2^20
+ * and N a multiple of 16 bytes of elements (0 otherwise): given that
+ * workspace (16-byte aligned), _run reads B in contiguous row spans and sums
+ * per-R-row partials in a fixed order (split-K, two launches); given none it
+ * runs the column-segment kernel. */
 #define BK_GEMV_DENSE_DECL(TAG)                                                                  \
     int32_t baracuda_kernels_gemv_dense_m1_##TAG##_run(                                          \
         int32_t m, int32_t n, int32_t k, int32_t batch, int32_t layout, float alpha, float beta, \
