@@ -216,13 +216,20 @@ typedef mfma2::Cfg<2, 4> DmaCfg;
 
 // Workgroup id -> tile of the compact ragged list.  The list holds
 // T = S * n_tiles tiles (S = sum_e ceil(cnt_e / 256) m-tiles, from the
-// offsets in LDS), tile r = (n-tile r / S, slot r % S).  Workgroups are
-// dispatched round-robin over the 8 XCDs; the id is regrouped so each XCD
-// owns a contiguous range of the list (slot fastest), so an expert's weight
-// panel is fetched into one XCD's L2 only.  Ids past the list exit (the
-// grid is sized for the largest possible S).  Against a regroup over that
-// largest grid, whose surplus slots exit inside every XCD's range: 567
-// against 577 us on config 5 (five alternating pairs).
+// offsets in LDS), in blocks of kMoeNBlock n-tiles: block b holds every
+// (slot, n-tile) pair of its n-tiles, n-tile fastest, so that the tiles an
+// XCD runs together share A panels (4 n-tiles per slot) as well as the
+// expert's weight panels (consecutive slots of one expert).  Workgroups
+// are dispatched round-robin over the 8 XCDs; the id is regrouped so each
+// XCD owns a contiguous range of the list.  Ids past the list exit (the
+// grid is sized for the largest possible S).  Config 5, one box, four
+// alternating passes: blocks of 1 / 2 / 3 / 4 / 8 / 16 n-tiles 536–539 /
+// 528–542 / 520–528 / 512–526 / 517–525 / 529–539 µs (1 is the plain
+// slot-fastest order); against a regroup over the largest grid, whose
+// surplus slots exited inside every XCD's range, the compact list alone
+// measured 567 against 577 µs.
+constexpr int kMoeNBlock = 4;
+
 __device__ __forceinline__ bool moe_dma_coords(const MoeArgs &p, const int32_t *s_off, int pid,
                                                int n_tiles, int &slot, int &ntile) {
     constexpr int XCDS = 8;
@@ -236,8 +243,11 @@ __device__ __forceinline__ bool moe_dma_coords(const MoeArgs &p, const int32_t *
     if (pid >= padded) return false;
     const int r = (pid % XCDS) * (padded / XCDS) + pid / XCDS;
     if (r >= T) return false;
-    slot = r % S;
-    ntile = r / S;
+    const int b = r / (S * kMoeNBlock);
+    const int bw = min(kMoeNBlock, n_tiles - b * kMoeNBlock);   // the last block may be narrower
+    const int i = r - b * S * kMoeNBlock;
+    slot = i / bw;
+    ntile = b * kMoeNBlock + i % bw;
     return true;
 }
 

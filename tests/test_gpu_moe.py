@@ -154,3 +154,11 @@ def test_moe_workspace_is_ignored(gpu):
     print("case: moe workspace ignored", flush=True)
     assert P.MoeS8GroupedPlan.select(8, 2, 1400, 512, 384).workspace_size() == 0
     _run(tokens=700, E=8, topk=2, n=512, k=384, seed=9, ws_bytes=1 << 20)
+
+
+@pytest.mark.parametrize("n", [1280, 2304])
+def test_moe_dma_ragged_n_blocks(gpu, n):
+    # n-tiles in blocks of 4 with a narrower last block (5 = 4 + 1, 9 = 4 + 4 + 1)
+    print(f"case: moe n blocks n={n}", flush=True)
+    tokens, routing = _block_routing([300, 0, 41, 513, 256], seed=n)
+    _run(tokens=tokens, E=5, topk=1, n=n, k=384, seed=n, routing=routing)
