@@ -162,3 +162,22 @@ def test_moe_dma_ragged_n_blocks(gpu, n):
     print(f"case: moe n blocks n={n}", flush=True)
     tokens, routing = _block_routing([300, 0, 41, 513, 256], seed=n)
     _run(tokens=tokens, E=5, topk=1, n=n, k=384, seed=n, routing=routing)
+
+
+def test_moe_dma_no_valid_rows(gpu):
+    # every expert id out of range: no tiles (S = 0) on the LDS-DMA path;
+    # counts / offsets zero and the output untouched
+    print("case: moe dma no valid rows", flush=True)
+    E, size_m, n, k = 4, 300, 256, 128
+    g = rng(99)
+    x, w = int8_uniform(g, (size_m, k)), int8_uniform(g, (E, n, k))
+    out = torch.full((size_m, n), 3.0, dtype=torch.bfloat16, device="cuda:0")
+    counts = torch.full((E,), -1, dtype=torch.int32, device="cuda:0")
+    offs = torch.full((E + 1,), -1, dtype=torch.int32, device="cuda:0")
+    ids = np.full(size_m, E + 3, dtype=np.int32)
+    P.MoeS8GroupedPlan.select(E, 1, size_m, n, k).run(
+        dev(x), dev(w), dev(np.arange(size_m, dtype=np.int32)), dev(ids), out, counts, offs,
+        dev(np.ones(size_m, np.float32)), dev(np.ones(E * n, np.float32)))
+    sync()
+    assert torch.all(counts == 0) and torch.all(offs == 0)
+    assert torch.all(out == 3.0)
