@@ -246,12 +246,15 @@ def cpu_baselines_extra(budget_s=4.0):
     n, k = 14336, 4096
     w = int8_uniform(g, (n, k))
     x = (g.standard_normal(k).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
-    reps, t0 = 0, time.perf_counter()
-    while reps < 3 or time.perf_counter() - t0 < 0.5:
-        O.gemv_s8w_m1_f64(x, w, nthreads=cores)
-        reps += 1
-    dt = (time.perf_counter() - t0) / reps
-    out["gemv_s8w_m1_14336x4096"] = {"us": round(dt * 1e6, 1), "GB_s": round((n * k + 2 * k + 6 * n) / dt / 1e9, 2)}
+    gv = {}
+    for th in sorted({1, cores}):
+        reps, t0 = 0, time.perf_counter()
+        while reps < 3 or time.perf_counter() - t0 < 0.5:
+            O.gemv_s8w_m1_f64(x, w, nthreads=th)
+            reps += 1
+        dt = (time.perf_counter() - t0) / reps
+        gv[f"threads_{th}"] = {"us": round(dt * 1e6, 1), "GB_s": round((n * k + 2 * k + 6 * n) / dt / 1e9, 2)}
+    out["gemv_s8w_m1_14336x4096"] = gv
     del w
     m, n, k = 2048, 14336, 4096
     fa = g.integers(0, 126, (m, k), dtype=np.uint8)
@@ -264,7 +267,7 @@ def cpu_baselines_extra(budget_s=4.0):
     O.gemm_fp8_e4m3_f64(fa, fb, rows=(0, rows), nthreads=cores)
     dt = time.perf_counter() - t0
     out["fp8_e4m3_2048x14336x4096"] = {"TFLOPS": round(2.0 * rows * n * k / dt / 1e12, 6),
-                                       "sample_rows": rows, "s": round(dt, 2)}
+                                       "sample_rows": rows, "s": round(dt, 2), "threads": cores}
     del fa, fb
     V, H = 128256, 4096
     table = np.zeros((V, H), dtype=np.uint16)   # pages touched only where gathered
@@ -276,7 +279,7 @@ def cpu_baselines_extra(budget_s=4.0):
             O.gather_rows(table, idx)
             reps += 1
         dt = (time.perf_counter() - t0) / reps
-        gr[f"n{nr}"] = {"us": round(dt * 1e6, 2)}
+        gr[f"n{nr}"] = {"us": round(dt * 1e6, 2), "threads": 1}
     out["gather_rows_bf16_128256x4096"] = gr
     out["note"] = ("W8A8 is the headline cpu_baseline; the grouped MoE config is not sampled "
                    "(its 470 MB expert slab dominates host set-up time)")
