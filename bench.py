@@ -31,6 +31,7 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E, GB/s
 # ops/clk (5.03 POP/s at the 2.4 GHz peak engine clock).
 OPS_PER_CLK = 256 * 8192
 HEAD_WARM_MS = 300.0        # wall time the headline kernel runs before its timed launches
+CLOCK_LOAD_S = 2.0          # the headline kernel in a loop while clock / power are sampled
 # HBM bytes per launch measured with rocprofv3 PMC (FETCH_SIZE x2.00 and
 # WRITE_SIZE x1.00, scales calibrated on a plain device copy); the runs and
 # raw readings are in profiles/path_kernels_hbm_traffic.md.
@@ -113,14 +114,17 @@ def cpu_cores():
 
 class ClockSampler:
     """Samples the GPU's graphics clock (amdsmi gpu_metrics, per-XCD
-    current_gfxclks) from a background thread while the GPU is busy, so the
-    MFMA peak can be restated at the clock the timed kernel actually ran at.
-    Fails soft: every figure is None when amdsmi is unavailable."""
+    current_gfxclks) and socket power from a background thread while a kernel
+    runs in a loop, so the MFMA peak can be restated at the clock the kernel
+    actually ran at.  The firmware refreshes the metrics table only every
+    ~0.5 s, so a reading is used only after the table has changed at least
+    once since sampling began (earlier readings describe the time before the
+    load).  Fails soft: every figure is None when amdsmi is unavailable."""
 
-    def __init__(self, period_s=0.004):
+    def __init__(self, period_s=0.02):
         import threading
         self.period_s = period_s
-        self.samples = []
+        self.samples = []   # (mhz mean over XCDs, socket power W)
         self.error = None
         self._stop = threading.Event()
         self._thr = threading.Thread(target=self._loop, daemon=True)
@@ -143,16 +147,19 @@ class ClockSampler:
         m = amdsmi.amdsmi_get_gpu_metrics_info(self._h)
         xs = [v for v in (m.get("current_gfxclks") or []) if isinstance(v, int) and 0 < v < 10000]
         if xs:
-            return sum(xs) / len(xs)
-        v = m.get("current_gfxclk")
-        return float(v) if isinstance(v, int) and 0 < v < 10000 else None
+            mhz = sum(xs) / len(xs)
+        else:
+            v = m.get("current_gfxclk")
+            mhz = float(v) if isinstance(v, int) and 0 < v < 10000 else None
+        pw = m.get("current_socket_power")
+        return mhz, (float(pw) if isinstance(pw, int) and 0 < pw < 100000 else None)
 
     def _loop(self):
         while not self._stop.is_set():
             try:
-                v = self._read()
-                if v is not None:
-                    self.samples.append(v)
+                mhz, pw = self._read()
+                if mhz is not None:
+                    self.samples.append((mhz, pw))
             except Exception as e:   # noqa: BLE001 -- telemetry only
                 self.error = repr(e)
                 return
@@ -176,15 +183,32 @@ class ClockSampler:
         return False
 
     def summary(self):
-        """Mean / min / max MHz over the busy samples (the upper half of the
-        sample range, so idle gaps between host syncs do not count)."""
-        if not self.samples:
-            return {"mhz_mean": None, "samples": 0, "source": "amdsmi current_gfxclks", "error": self.error}
-        xs = sorted(self.samples)
-        busy = xs[len(xs) // 2:]
-        return {"mhz_mean": round(sum(busy) / len(busy), 1), "mhz_min": busy[0], "mhz_max": busy[-1],
-                "samples": len(busy), "source": "amdsmi current_gfxclks (mean over XCDs), sampled while the "
-                                                 "headline kernel ran"}
+        """Mean clock (MHz, over XCDs) and socket power (W) over the readings
+        taken after the first refresh of the metrics table."""
+        src = ("amdsmi gpu_metrics current_gfxclks (mean over XCDs) and current_socket_power, read while "
+               "the headline kernel ran in a loop, after the first refresh of the table (~0.5 s period)")
+        first = next((i for i in range(1, len(self.samples)) if self.samples[i] != self.samples[0]), None)
+        if first is None:
+            return {"mhz_mean": None, "samples": len(self.samples), "source": src,
+                    "error": self.error or "metrics table did not refresh during the sample"}
+        live = self.samples[first:]
+        mh = [x for x, _ in live]
+        pw = [p for _, p in live if p is not None]
+        return {"mhz_mean": round(sum(mh) / len(mh), 1), "mhz_min": min(mh), "mhz_max": max(mh),
+                "socket_power_w_mean": round(sum(pw) / len(pw), 1) if pw else None,
+                "samples": len(live), "source": src}
+
+
+def clock_under_load(fn, seconds=None):
+    """Clock / power summary (ClockSampler) while fn runs in a loop."""
+    import torch
+    with ClockSampler() as clk:
+        t_end = time.perf_counter() + (CLOCK_LOAD_S if seconds is None else seconds)
+        while time.perf_counter() < t_end:
+            for _ in range(64):
+                fn()
+            torch.cuda.synchronize()
+    return clk.summary()
 
 
 def cpu_baseline_w8a8(a, w, sa, sw, budget_s=15.0):
@@ -681,11 +705,14 @@ def main():
             ca = torch.ones((M, K), dtype=torch.int8, device=dev)
             cw = torch.ones((N, K), dtype=torch.int8, device=dev)
             co = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
-            cms = time_launches(lambda: plan.run(ca, cw, co, scale_a=dsa, scale_b=dsw, stream=stream),
-                                100, 10, stream, warm_ms=50.0)
+            run_const = lambda: plan.run(ca, cw, co, scale_a=dsa, scale_b=dsw, stream=stream)  # noqa: E731
+            cms = time_launches(run_const, 100, 10, stream, warm_ms=50.0)
+            csclk = clock_under_load(run_const)
             extra["w8a8_4096_cubed_constant_operands"] = {
                 "us": round(cms * 1e3, 2), "TOPS": round(ops / (cms * 1e-3) / 1e12, 1),
-                "note": "A = W = all ones, one resident set: compare with w8a8_4096_cubed_resident_operands"}
+                "sclk_mhz": csclk.get("mhz_mean"), "socket_power_w": csclk.get("socket_power_w_mean"),
+                "note": "A = W = all ones, one resident set: compare with w8a8_4096_cubed_resident_operands "
+                        "and with roofline.sclk (random operands)"}
             del ca, cw, co
 
     ms = None
@@ -704,9 +731,11 @@ def main():
         # before its timed launches, whatever --warmup is (the clocks settle
         # under sustained MFMA load; a count-only warm-up of a few launches
         # times the ramp), while the graphics clock is sampled.
-        with ClockSampler() as clk:
-            ms = time_launches(run, args.steps, args.warmup, stream, warm_ms=HEAD_WARM_MS)
-        sclk = clk.summary()
+        ms = time_launches(run, args.steps, args.warmup, stream, warm_ms=HEAD_WARM_MS)
+        # Clock and power under the same load, read after the timed launches
+        # (the metrics table refreshes too slowly to cover them): the
+        # headline kernel keeps running for CLOCK_LOAD_S while it is sampled.
+        sclk = clock_under_load(run)
     tops = ops / (ms * 1e-3) / 1e12 if ms else None
 
     cpu = None
