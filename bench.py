@@ -186,7 +186,7 @@ class ClockSampler:
         """Mean clock (MHz, over XCDs) and socket power (W) over the readings
         taken after the first refresh of the metrics table."""
         src = ("amdsmi gpu_metrics current_gfxclks (mean over XCDs) and current_socket_power, read while "
-               "the headline kernel ran in a loop, after the first refresh of the table (~0.5 s period)")
+               "the kernel ran in a loop, after the first refresh of the table (~0.5 s period)")
         first = next((i for i in range(1, len(self.samples)) if self.samples[i] != self.samples[0]), None)
         if first is None:
             return {"mhz_mean": None, "samples": len(self.samples), "source": src,
@@ -727,15 +727,15 @@ def main():
         extra["w8a8_4096_cubed_resident_operands"] = {
             "us": round(ms_res * 1e3, 2), "TOPS": round(ops / (ms_res * 1e-3) / 1e12, 1),
             "note": "one operand set reused every launch; the headline value rotates 8 sets"}
-        # Headline: the kernel itself runs for HEAD_WARM_MS of wall time right
-        # before its timed launches, whatever --warmup is (the clocks settle
-        # under sustained MFMA load; a count-only warm-up of a few launches
-        # times the ramp), while the graphics clock is sampled.
-        ms = time_launches(run, args.steps, args.warmup, stream, warm_ms=HEAD_WARM_MS)
-        # Clock and power under the same load, read after the timed launches
-        # (the metrics table refreshes too slowly to cover them): the
-        # headline kernel keeps running for CLOCK_LOAD_S while it is sampled.
+        # Headline: the kernel first runs in a loop for CLOCK_LOAD_S while
+        # the graphics clock and socket power are read (the metrics table
+        # refreshes too slowly to cover the timed launches themselves), then
+        # for HEAD_WARM_MS more of wall time right before its timed launches,
+        # whatever --warmup is (the clocks settle under sustained MFMA load;
+        # a count-only warm-up of a few launches times the ramp).  The timed
+        # launches are the last ones of the kernel a profiler sees.
         sclk = clock_under_load(run)
+        ms = time_launches(run, args.steps, args.warmup, stream, warm_ms=HEAD_WARM_MS)
     tops = ops / (ms * 1e-3) / 1e12 if ms else None
 
     cpu = None
