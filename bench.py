@@ -436,11 +436,14 @@ def main():
             frs = time_launches(lambda: fp.run(ra, rb, rd, scale_a=s_ra, scale_b=s_rb, stream=stream), 40, 5,
                                 stream, warm_ms=30.0)
             tf = 2.0 * m * n * k / (fms * 1e-3) / 1e12
+            fclk = clock_under_load(fp8_step)
             extra["fp8_e4m3_gemm_2048x14336x4096"] = {"us": round(fms * 1e3, 2), "TFLOPS": round(tf, 1),
                                                       "frac_fp8_peak": round(tf / PEAK_FP8_TFLOPS, 4),
                                                       "operand_sets_rotated": 5,
                                                       "data": "N(0,1), absmax -> 448, e4m3 RNE; scales absmax/448",
-                                                      "resident_operands_us": round(frs * 1e3, 2)}
+                                                      "resident_operands_us": round(frs * 1e3, 2),
+                                                      "sclk_mhz": fclk.get("mhz_mean"),
+                                                      "socket_power_w": fclk.get("socket_power_w_mean")}
             del fsets, fa, fb, ra, rb, rd
         if only in ("", "moe"):
             log("bench: moe grouped int8")
@@ -456,9 +459,10 @@ def main():
             off = torch.empty(E + 1, dtype=torch.int32, device=dev)
             dsid, deid = torch.from_numpy(sid).to(dev), torch.from_numpy(eid).to(dev)
             mp = P.MoeS8GroupedPlan.select(E, topk, tokens * topk, n, k)
-            mms = time_launches(lambda: mp.run(mx, mw, dsid, deid, mo, cnt, off, msa, msw, stream=stream),
-                                10, 3, stream, warm_ms=30.0)
+            moe_step = lambda: mp.run(mx, mw, dsid, deid, mo, cnt, off, msa, msw, stream=stream)  # noqa: E731
+            mms = time_launches(moe_step, 10, 3, stream, warm_ms=30.0)
             mt = 2.0 * tokens * topk * n * k / (mms * 1e-3) / 1e12
+            mclk = clock_under_load(moe_step)
             rows_e = np.bincount(eid, minlength=E)
             tiles_m = int(sum(-(-int(r) // 256) for r in rows_e))
             extra["moe_s8_grouped_e8_top2_4096x14336x4096"] = {
@@ -467,7 +471,8 @@ def main():
                 # 256 x 256 tiles over the ragged experts: computed rows vs routed rows
                 "tiles": tiles_m * (n // 256), "tile_rounds_on_256_cus": round(tiles_m * (n // 256) / 256, 2),
                 "padded_rows": tiles_m * 256, "routed_rows": int(rows_e.sum()),
-                "padding_frac": round(1 - rows_e.sum() / (tiles_m * 256), 4)}
+                "padding_frac": round(1 - rows_e.sum() / (tiles_m * 256), 4),
+                "sclk_mhz": mclk.get("mhz_mean"), "socket_power_w": mclk.get("socket_power_w_mean")}
             del mx, mw, mo
             log("bench: moe grouped bf16 (moe_wmma ABI)")
             bx = torch.randn((tokens, k), device=dev).to(torch.bfloat16)
