@@ -15,6 +15,8 @@
 // reads); everything else the register-staged mainloop (16x16x128).
 #pragma once
 
+#include <type_traits>
+
 #include "gemm_mfma.hpp"
 #include "gemm_mfma2.hpp"
 #include "act.hpp"
@@ -42,12 +44,14 @@ template <int FMT, int EPI, bool VecOut, int ACT>
 struct F8Epilogue {
     const F8Args &p;
     // F8_OUT, whole group of 4 columns (N % 4 == 0): the 4 result bytes.
+    // HasC: beta != 0 and C given (decided once per tile by the caller).
+    template <bool HasC>
     __device__ __forceinline__ uint32_t pack_fp8(int m, int n0, const v4f &v) const {
         float z[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             z[r] = p.alpha * v[r];
-            if (p.beta != 0.0f && p.c != nullptr) z[r] += p.beta * fp8_to_f32<FMT>(p.c[(int64_t)m * p.ldc + n0 + r]);
+            if constexpr (HasC) z[r] += p.beta * fp8_to_f32<FMT>(p.c[(int64_t)m * p.ldc + n0 + r]);
             if constexpr (ACT != ACT_NONE) {
                 z[r] += p.bias[n0 + r];
                 z[r] = activation<ACT>(z[r]);
@@ -178,16 +182,34 @@ __global__ __launch_bounds__(F8DmaCfg::NT, 1) void gemm_fp8_dma_kernel(F8Args p)
             const int wrow = m_base + (wave / F8DmaCfg::WAVES_N) * F8DmaCfg::WM;
             const int wcol = n_base + (wave % F8DmaCfg::WAVES_N) * F8DmaCfg::WN;
             int8_t *scratch = (wave < 4 ? stage0 : stage1) + (wave & 3) * (F8DmaCfg::WM * F8DmaCfg::WN);
-            M2::store_u8x4_staged<P>(
-                acc, scratch,
-                [&](int r, int c, const v4f &v) {
-                    return (wrow + r < p.M && wcol + c < p.N) ? epi.pack_fp8(wrow + r, wcol + c, v) : 0u;
-                },
-                [&](int r) {
-                    return wrow + r < p.M ? static_cast<int8_t *>(p.d) + (int64_t)(wrow + r) * p.ldd + wcol
-                                          : nullptr;
-                },
-                min(F8DmaCfg::WN, p.N - wcol));
+            // The C term and the M / N bounds decided once per tile, not per element.
+            auto staged = [&](auto has_c, auto whole) {
+                M2::store_u8x4_staged<P>(
+                    acc, scratch,
+                    [&](int r, int c, const v4f &v) {
+                        if constexpr (decltype(whole)::value)
+                            return epi.template pack_fp8<decltype(has_c)::value>(wrow + r, wcol + c, v);
+                        else
+                            return (wrow + r < p.M && wcol + c < p.N)
+                                       ? epi.template pack_fp8<decltype(has_c)::value>(wrow + r, wcol + c, v)
+                                       : 0u;
+                    },
+                    [&](int r) {
+                        return wrow + r < p.M ? static_cast<int8_t *>(p.d) + (int64_t)(wrow + r) * p.ldd + wcol
+                                              : nullptr;
+                    },
+                    min(F8DmaCfg::WN, p.N - wcol));
+            };
+            using T_ = std::true_type;
+            using F_ = std::false_type;
+            const bool has_c = p.beta != 0.0f && p.c != nullptr;
+            if (has_c) {
+                if (full) staged(T_{}, T_{});
+                else staged(T_{}, F_{});
+            } else {
+                if (full) staged(F_{}, T_{});
+                else staged(F_{}, F_{});
+            }
             return;
         }
     }

@@ -14,6 +14,7 @@
 #pragma once
 
 #include <algorithm>
+#include <type_traits>
 
 #include "gemm_mfma.hpp"
 #include "gemm_mfma2.hpp"
@@ -42,12 +43,14 @@ template <int EPI, bool VecOut, int ACT = ACT_NONE, typename BiasT = float>
 struct S8Epilogue {
     const S8Args &p;
     // EPI_S8, whole group of 4 columns (N % 4 == 0): the 4 result bytes.
+    // HasC: beta != 0 and C given (decided once per tile by the caller).
+    template <bool HasC>
     __device__ __forceinline__ uint32_t pack_s8(int m, int n0, const v4i &v) const {
         int8_t o[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             float z = p.alpha * (float)v[r];
-            if (p.beta != 0.0f && p.c != nullptr) z += p.beta * (float)p.c[(int64_t)m * p.ldc + n0 + r];
+            if constexpr (HasC) z += p.beta * (float)p.c[(int64_t)m * p.ldc + n0 + r];
             if constexpr (ACT != ACT_NONE) {
                 z += (float)static_cast<const BiasT *>(p.bias)[n0 + r];
                 z = activation<ACT>(z);
@@ -230,9 +233,9 @@ typedef mfma2::Cfg<2, 4> DmaCfg;
 // written as 16-byte row segments instead of 4-byte stores.
 // Partial tiles (the M / N edge, N % 16 == 0): rows past M and 16-byte
 // units past N are neither computed nor stored.
-template <class P, class Epi>
-__device__ __forceinline__ void store_s8_tile_staged(const mfma2::AccTile<P> &acc, int8_t *stage0, int8_t *stage1,
-                                                     const S8Args &p, int m_base, int n_base, const Epi &epi) {
+template <class P, bool HasC, bool Full, class Epi>
+__device__ __forceinline__ void store_s8_tile_staged_as(const mfma2::AccTile<P> &acc, int8_t *stage0, int8_t *stage1,
+                                                        const S8Args &p, int m_base, int n_base, const Epi &epi) {
     const int wave = threadIdx.x >> 6;
     const int wrow = (wave / DmaCfg::WAVES_N) * DmaCfg::WM;
     const int wcol = (wave % DmaCfg::WAVES_N) * DmaCfg::WN;
@@ -242,7 +245,8 @@ __device__ __forceinline__ void store_s8_tile_staged(const mfma2::AccTile<P> &ac
         acc, scratch,
         [&](int r, int c, const v4i &v) {
             const int m = m_base + wrow + r, n = n_base + wcol + c;
-            return (m < p.M && n < p.N) ? epi.pack_s8(m, n, v) : 0u;
+            if constexpr (Full) return epi.template pack_s8<HasC>(m, n, v);
+            else return (m < p.M && n < p.N) ? epi.template pack_s8<HasC>(m, n, v) : 0u;
         },
         [&](int r) {
             return m_base + wrow + r < p.M
@@ -250,6 +254,22 @@ __device__ __forceinline__ void store_s8_tile_staged(const mfma2::AccTile<P> &ac
                        : nullptr;
         },
         ncols);
+}
+
+// The C term and the M / N bounds decided once per tile (full: whole tile
+// in range), not per element.
+template <class P, class Epi>
+__device__ __forceinline__ void store_s8_tile_staged(const mfma2::AccTile<P> &acc, int8_t *stage0, int8_t *stage1,
+                                                     const S8Args &p, int m_base, int n_base, const Epi &epi) {
+    const bool has_c = p.beta != 0.0f && p.c != nullptr;
+    const bool full = m_base + mfma2::BM <= p.M && n_base + mfma2::BN <= p.N;
+    if (has_c) {
+        if (full) store_s8_tile_staged_as<P, true, true>(acc, stage0, stage1, p, m_base, n_base, epi);
+        else store_s8_tile_staged_as<P, true, false>(acc, stage0, stage1, p, m_base, n_base, epi);
+    } else {
+        if (full) store_s8_tile_staged_as<P, false, true>(acc, stage0, stage1, p, m_base, n_base, epi);
+        else store_s8_tile_staged_as<P, false, false>(acc, stage0, stage1, p, m_base, n_base, epi);
+    }
 }
 
 // `ts`: workgroups below ts.full_tiles (all of them when ts.split == 1) run
@@ -401,6 +421,8 @@ struct U8Epilogue {
     const int *cs;        // [256] tile column sums of B
     uint32_t kcorr;       // 16384 * K_pad (mod 2^32), subtracted
     // Whole group of 4 columns (N % 4 == 0): the 4 result bytes.
+    // HasC: beta != 0 and C given (decided once per tile by the caller).
+    template <bool HasC>
     __device__ __forceinline__ uint32_t pack_u8(int ml, int nl, const v4i &v, int m_base, int n_base) const {
         const int m = m_base + ml, n0 = n_base + nl;
         const uint32_t rsum = (uint32_t)rs[ml];
@@ -410,7 +432,7 @@ struct U8Epilogue {
         for (int r = 0; r < 4; ++r) {
             const uint32_t au = (uint32_t)v[r] + 128u * (rsum + (uint32_t)cs[nl + r]) - kcorr;
             float z = p.alpha * (float)(int32_t)au;
-            if (p.beta != 0.0f && c != nullptr) z += p.beta * (float)c[(int64_t)m * p.ldc + n0 + r];
+            if constexpr (HasC) z += p.beta * (float)c[(int64_t)m * p.ldc + n0 + r];
             if constexpr (ACT != ACT_NONE) {
                 z += (float)static_cast<const BiasT *>(p.bias)[n0 + r];
                 z = activation<ACT>(z);
@@ -467,12 +489,19 @@ __device__ __forceinline__ void store_u8_tile(const mfma2::AccTile<P> &acc, int8
             const int wrow = (wave / DmaCfg::WAVES_N) * DmaCfg::WM;
             const int wcol = (wave % DmaCfg::WAVES_N) * DmaCfg::WN;
             int8_t *scratch = (wave < 4 ? stage0 : stage1) + (wave & 3) * (DmaCfg::WM * DmaCfg::WN);
-            mfma2::store_u8x4_staged<P>(
-                acc, scratch,
-                [&](int r, int c, const v4i &v) { return epi.pack_u8(wrow + r, wcol + c, v, m_base, n_base); },
-                [&](int r) {
-                    return static_cast<int8_t *>(p.d) + (int64_t)(m_base + wrow + r) * p.ldd + n_base + wcol;
-                });
+            auto staged = [&](auto has_c) {
+                mfma2::store_u8x4_staged<P>(
+                    acc, scratch,
+                    [&](int r, int c, const v4i &v) {
+                        return epi.template pack_u8<decltype(has_c)::value>(wrow + r, wcol + c, v, m_base, n_base);
+                    },
+                    [&](int r) {
+                        return static_cast<int8_t *>(p.d) + (int64_t)(m_base + wrow + r) * p.ldd + n_base + wcol;
+                    });
+            };
+            // the C term decided once per tile, not per element
+            if (p.beta != 0.0f && p.c != nullptr) staged(std::true_type{});
+            else staged(std::false_type{});
             return;
         }
     }

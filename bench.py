@@ -504,6 +504,13 @@ def main():
                 it_ = ops / (ims * 1e-3) / 1e12
                 e[name] = {"us": round(ims * 1e3, 2), "TOPS": round(it_, 1),
                            "frac_int8_peak": round(it_ / PEAK_INT8_TOPS, 4)}
+                if name == "rcr_identity":
+                    # D = sat(rne(alpha * acc + beta * C)): the reference SKU's full epilogue
+                    icc = torch.randint(-127, 128, (M, N), dtype=torch.int8, device=dev)
+                    cms_ = time_launches(lambda: ip.run(ia, bmat, idd, c=icc, alpha=1.0 / 4096, beta=0.5,
+                                                        stream=stream), 40, 5, stream, warm_ms=30.0)
+                    e[name]["with_c_beta_us"] = round(cms_ * 1e3, 2)
+                    del icc
             ua = torch.randint(0, 256, (M, K), dtype=torch.uint8, device=dev)
             ub = torch.randint(0, 256, (K, N), dtype=torch.uint8, device=dev)
             ud = torch.empty((M, N), dtype=torch.uint8, device=dev)
