@@ -198,18 +198,18 @@ __device__ __forceinline__ uint32_t u8_sum16(const v4i &f, uint32_t acc) {
     return acc;
 }
 
+
+// Round half to even to int32, then clamp (the reference's
+// __float2int_rn + max / min, baracuda_dtype.cuh:23-36): rint, v_cvt_i32_f32
+// (saturating; NaN converts to 0) and one v_med3_i32.
 __device__ __forceinline__ uint8_t sat_cast_u8(float x) {
-    float r = __builtin_rintf(x);   // round half to even
-    r = r < 0.0f ? 0.0f : r;
-    r = r > 255.0f ? 255.0f : r;
-    return (uint8_t)(int)r;
+    const int r = (int)__builtin_rintf(x);
+    return (uint8_t)min(max(r, 0), 255);
 }
 
 __device__ __forceinline__ int8_t sat_cast_s8(float x) {
-    float r = __builtin_rintf(x);   // round half to even
-    r = r < -128.0f ? -128.0f : r;
-    r = r > 127.0f ? 127.0f : r;
-    return (int8_t)(int)r;
+    const int r = (int)__builtin_rintf(x);
+    return (int8_t)min(max(r, -128), 127);
 }
 
 }  // namespace bk

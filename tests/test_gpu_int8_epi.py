@@ -283,3 +283,20 @@ def test_u8_workspace_path_bit_identical(gpu, epi):
     kw = dict(c=c, bias=bias, alpha=1.0 / (64.0 * k), beta=0.5)
     assert np.array_equal(_run_u8(epi, P.ElementKind.F32, a, b, ws=True, **kw),
                           _run_u8(epi, P.ElementKind.F32, a, b, ws=False, **kw))
+
+
+@pytest.mark.parametrize("layout", [P.LayoutSku.Rcr, P.LayoutSku.Rrr])
+def test_s8_saturation_of_non_finite_and_huge_bias(gpu, layout):
+    # z = alpha*acc + bias with bias in {+inf, -inf, NaN, +1e10, -1e10, 0.4}:
+    # the int8 store saturates to 127 / -128, NaN stores 0 (the hardware
+    # conversion; the reference's sat_cast has no NaN case), finite values
+    # round half to even.  Staged (whole tile) and per-quad (edge) paths.
+    for m, n, k in [(256, 256, 128), (70, 36, 64)]:
+        g = rng(m + n)
+        a = int8_uniform(g, (m, k))
+        b = int8_uniform(g, (k, n)) if layout == P.LayoutSku.Rrr else int8_uniform(g, (n, k))
+        special = np.array([np.inf, -np.inf, np.nan, 1e10, -1e10, 0.4], np.float32)
+        bias = special[np.arange(n) % 6]
+        got = _run(layout, P.EpilogueKind.Bias, P.ElementKind.F32, a, b, bias=bias, alpha=1e-9)
+        want_col = np.array([127, -128, 0, 127, -128, 0], np.int8)[np.arange(n) % 6]
+        assert np.array_equal(got, np.broadcast_to(want_col, (m, n))), (m, n, k)
