@@ -44,14 +44,20 @@ template <int FMT, int EPI, bool VecOut, int ACT>
 struct F8Epilogue {
     const F8Args &p;
     // F8_OUT, whole group of 4 columns (N % 4 == 0): the 4 result bytes.
-    // HasC: beta != 0 and C given (decided once per tile by the caller).
-    template <bool HasC>
+    // HasC: beta != 0 and C given; CVec: the 4 C bytes read as one dword
+    // (ldc and C 4-byte aligned) -- both decided once per tile by the caller.
+    template <bool HasC, bool CVec = false>
     __device__ __forceinline__ uint32_t pack_fp8(int m, int n0, const v4f &v) const {
         float z[4];
+        uint32_t c4 = 0;
+        if constexpr (HasC && CVec) c4 = *reinterpret_cast<const uint32_t *>(p.c + (int64_t)m * p.ldc + n0);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             z[r] = p.alpha * v[r];
-            if constexpr (HasC) z[r] += p.beta * fp8_to_f32<FMT>(p.c[(int64_t)m * p.ldc + n0 + r]);
+            if constexpr (HasC) {
+                const uint8_t cb = CVec ? (uint8_t)(c4 >> (8 * r)) : p.c[(int64_t)m * p.ldc + n0 + r];
+                z[r] += p.beta * fp8_to_f32<FMT>(cb);
+            }
             if constexpr (ACT != ACT_NONE) {
                 z[r] += p.bias[n0 + r];
                 z[r] = activation<ACT>(z[r]);
@@ -187,11 +193,13 @@ __global__ __launch_bounds__(F8DmaCfg::NT, 1) void gemm_fp8_dma_kernel(F8Args p)
                 M2::store_u8x4_staged<P>(
                     acc, scratch,
                     [&](int r, int c, const v4f &v) {
-                        if constexpr (decltype(whole)::value)
-                            return epi.template pack_fp8<decltype(has_c)::value>(wrow + r, wcol + c, v);
+                        // whole tiles with C: C rows read as dwords when aligned
+                        constexpr bool kC = decltype(has_c)::value, kW = decltype(whole)::value;
+                        if constexpr (kW)
+                            return epi.template pack_fp8<kC, kC>(wrow + r, wcol + c, v);
                         else
                             return (wrow + r < p.M && wcol + c < p.N)
-                                       ? epi.template pack_fp8<decltype(has_c)::value>(wrow + r, wcol + c, v)
+                                       ? epi.template pack_fp8<kC>(wrow + r, wcol + c, v)
                                        : 0u;
                     },
                     [&](int r) {
@@ -203,8 +211,9 @@ __global__ __launch_bounds__(F8DmaCfg::NT, 1) void gemm_fp8_dma_kernel(F8Args p)
             using T_ = std::true_type;
             using F_ = std::false_type;
             const bool has_c = p.beta != 0.0f && p.c != nullptr;
+            const bool c_vec = p.ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(p.c) & 3u) == 0;
             if (has_c) {
-                if (full) staged(T_{}, T_{});
+                if (full && c_vec) staged(T_{}, T_{});
                 else staged(T_{}, F_{});
             } else {
                 if (full) staged(F_{}, T_{});

@@ -421,18 +421,22 @@ struct U8Epilogue {
     const int *cs;        // [256] tile column sums of B
     uint32_t kcorr;       // 16384 * K_pad (mod 2^32), subtracted
     // Whole group of 4 columns (N % 4 == 0): the 4 result bytes.
-    // HasC: beta != 0 and C given (decided once per tile by the caller).
-    template <bool HasC>
+    // HasC: beta != 0 and C given; CVec: the 4 C bytes read as one dword
+    // (ldc and C 4-byte aligned) -- both decided once per tile by the caller.
+    template <bool HasC, bool CVec = false>
     __device__ __forceinline__ uint32_t pack_u8(int ml, int nl, const v4i &v, int m_base, int n_base) const {
         const int m = m_base + ml, n0 = n_base + nl;
         const uint32_t rsum = (uint32_t)rs[ml];
         const uint8_t *c = reinterpret_cast<const uint8_t *>(p.c);
+        uint32_t c4 = 0;
+        if constexpr (HasC && CVec) c4 = *reinterpret_cast<const uint32_t *>(c + (int64_t)m * p.ldc + n0);
         uint32_t w = 0;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const uint32_t au = (uint32_t)v[r] + 128u * (rsum + (uint32_t)cs[nl + r]) - kcorr;
             float z = p.alpha * (float)(int32_t)au;
-            if constexpr (HasC) z += p.beta * (float)c[(int64_t)m * p.ldc + n0 + r];
+            if constexpr (HasC)
+                z += p.beta * (float)(CVec ? (uint8_t)(c4 >> (8 * r)) : c[(int64_t)m * p.ldc + n0 + r]);
             if constexpr (ACT != ACT_NONE) {
                 z += (float)static_cast<const BiasT *>(p.bias)[n0 + r];
                 z = activation<ACT>(z);
@@ -489,19 +493,26 @@ __device__ __forceinline__ void store_u8_tile(const mfma2::AccTile<P> &acc, int8
             const int wrow = (wave / DmaCfg::WAVES_N) * DmaCfg::WM;
             const int wcol = (wave % DmaCfg::WAVES_N) * DmaCfg::WN;
             int8_t *scratch = (wave < 4 ? stage0 : stage1) + (wave & 3) * (DmaCfg::WM * DmaCfg::WN);
-            auto staged = [&](auto has_c) {
+            auto staged = [&](auto has_c, auto c_vec) {
                 mfma2::store_u8x4_staged<P>(
                     acc, scratch,
                     [&](int r, int c, const v4i &v) {
-                        return epi.template pack_u8<decltype(has_c)::value>(wrow + r, wcol + c, v, m_base, n_base);
+                        return epi.template pack_u8<decltype(has_c)::value, decltype(c_vec)::value>(
+                            wrow + r, wcol + c, v, m_base, n_base);
                     },
                     [&](int r) {
                         return static_cast<int8_t *>(p.d) + (int64_t)(m_base + wrow + r) * p.ldd + n_base + wcol;
                     });
             };
             // the C term decided once per tile, not per element
-            if (p.beta != 0.0f && p.c != nullptr) staged(std::true_type{});
-            else staged(std::false_type{});
+            if (p.beta != 0.0f && p.c != nullptr) {
+                if (p.ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(p.c) & 3u) == 0)
+                    staged(std::true_type{}, std::true_type{});
+                else
+                    staged(std::true_type{}, std::false_type{});
+            } else {
+                staged(std::false_type{}, std::false_type{});
+            }
             return;
         }
     }

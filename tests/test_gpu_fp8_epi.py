@@ -135,3 +135,27 @@ def test_saturating_outputs(gpu, fmt, shape):
     assert np.array_equal(got, want)
     mx = 0x7E if fmt == "e4m3" else 0x7B
     assert ((got & 0x7F) == mx).mean() > 0.3
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("shape", [(256, 256, 128), (64, 64, 32)])
+def test_c_roundtrip_every_code(gpu, shape, fmt):
+    # alpha = 0, beta = 1: D = enc(0 * acc + dec(C)) = C for every code but
+    # 0x80 (+-0 by the sign of acc), the NaN codes (-> sign | 0x7f) and the e5m2
+    # infinities (-> the max finite, satfinite): the C decode on the LDS-DMA
+    # and general paths over all 256 codes, NaN signs included.
+    m, n, k = shape
+    print(f"case: fp8 C roundtrip {fmt} {shape}", flush=True)
+    g = rng(k)
+    a = O.f32_to_fp8(g.standard_normal((m, k)).astype(np.float32), fmt)
+    b = O.f32_to_fp8(g.standard_normal((n, k)).astype(np.float32), fmt)
+    c = (np.arange(m * n) % 256).astype(np.uint8).reshape(m, n)
+    got = _run(fmt, P.LayoutSku.Rcr, P.EpilogueKind.Identity, a, b, c=c, alpha=0.0, beta=1.0)
+    nan = (c & 0x7F) == 0x7F if fmt == "e4m3" else (c & 0x7F) > 0x7C
+    want = np.where(nan, (c & 0x80) | 0x7F, c).astype(np.uint8)
+    if fmt == "e5m2":
+        want = np.where((c & 0x7F) == 0x7C, (c & 0x80) | 0x7B, want).astype(np.uint8)
+    # -0 + (0 * acc): -0 where acc < 0, +0 otherwise
+    zero = c == 0x80
+    assert np.all((got[zero] == 0x80) | (got[zero] == 0x00))
+    assert np.array_equal(got[~zero], want[~zero])
