@@ -8,7 +8,9 @@ workspace where the plan reports one:
   * W8A8 bf16 out: bit-exact against the oracle's f32 epilogue;
   * u8 RCR u8 out: bit-exact against the oracle;
   * FP8 e4m3 RCR f32 out: within 1e-3 relative of the exact f64 sum, with the
-    1e-4 * sum|a*b| floor of the other FP8 tests.
+    1e-4 * sum|a*b| floor of the other FP8 tests;
+  * FP8 fp8-out (e4m3 RRR, e5m2 RCR / RRR) with C and BiasRelu: one grid step;
+  * RRR s8 BiasRelu with C and u8 RRR (with / without workspace): bit-exact.
 """
 import numpy as np
 import pytest
@@ -138,3 +140,29 @@ def test_u8_rrr_sweep(gpu, shape, use_ws):
     plan.run(dev(a), dev(b), d, alpha=alpha, workspace=_ws(plan, use_ws))
     sync()
     assert np.array_equal(d.cpu().numpy(), O.gemm_u8_epi(a, b, "rrr", alpha))
+
+
+@pytest.mark.parametrize("shape", SHAPES[2::3])
+@pytest.mark.parametrize("fmt,layout", [("e4m3", P.LayoutSku.Rrr), ("e5m2", P.LayoutSku.Rcr),
+                                        ("e5m2", P.LayoutSku.Rrr)])
+def test_fp8_out_with_c_sweep(gpu, shape, fmt, layout):
+    # fp8-out SKUs with C (beta = 0.5) and BiasRelu: within one grid step of
+    # the exactly rounded result plus the MFMA summation floor, differences
+    # on under 2% of the outputs (the bar of test_gpu_fp8_epi).
+    from tests.test_gpu_fp8_epi import _run as f8_run, _steps, _want as f8_want
+    m, n, k = shape
+    print(f"case: sweep fp8 out {fmt} {layout.value} {shape}", flush=True)
+    g = rng(7 * m + n + k)
+    a = O.f32_to_fp8(g.standard_normal((m, k)).astype(np.float32), fmt)
+    b = O.f32_to_fp8(g.standard_normal((k, n) if layout == P.LayoutSku.Rrr else (n, k)).astype(np.float32), fmt)
+    c = O.f32_to_fp8(g.standard_normal((m, n)).astype(np.float32), fmt)
+    bias = g.standard_normal(n).astype(np.float32)
+    alpha = 1.0 / 16
+    epi = P.EpilogueKind.BiasRelu
+    got = f8_run(fmt, layout, epi, a, b, c=c, bias=bias, alpha=alpha, beta=0.5)
+    want = f8_want(fmt, layout, epi, a, b, c, bias, alpha, 0.5)
+    fa = np.abs(O.fp8_to_f32(a, fmt).astype(np.float64))
+    fb = np.abs(O.fp8_to_f32(b, fmt).astype(np.float64))
+    floor = 1e-4 * alpha * (fa @ (fb if layout == P.LayoutSku.Rrr else fb.T))
+    st = _steps(got, want, fmt, floor)
+    assert st.max() <= 1.0 and (got != want).mean() < 0.02
