@@ -340,6 +340,23 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_s8_rcr_dma_kernel(S8Args p
             return;
         }
     }
+    if constexpr (EPI == EPI_I32 && VecOut) {
+        if (p.ldd % 4 == 0 && (reinterpret_cast<uintptr_t>(p.d) & 15u) == 0 && (full || p.N % 4 == 0)) {
+            // int32 rows staged in LDS (16 KiB per wave, two halves) and
+            // written as 256-byte row segments instead of 16-byte quads.
+            const int wave = threadIdx.x >> 6;
+            const int wrow = m_base + (wave / DmaCfg::WAVES_N) * DmaCfg::WM;
+            const int wcol = n_base + (wave % DmaCfg::WAVES_N) * DmaCfg::WN;
+            int8_t *scratch = (wave < 4 ? stage0 : stage1) + (wave & 3) * (DmaCfg::WM / 2 * 256);
+            M2::store_i32x4_staged<P>(
+                acc, scratch,
+                [&](int r) {
+                    return wrow + r < p.M ? static_cast<int32_t *>(p.d) + (int64_t)(wrow + r) * p.ldd + wcol : nullptr;
+                },
+                min(DmaCfg::WN, p.N - wcol));
+            return;
+        }
+    }
     {
         const S8Epilogue<EPI, VecOut, ACT, BiasT> epi{p};
         if constexpr (EPI == EPI_S8 && VecOut) {
