@@ -180,6 +180,28 @@ __global__ __launch_bounds__(F8DmaCfg::NT, 1) void gemm_fp8_dma_kernel(F8Args p)
             return;
         }
     }
+    if constexpr (EPI == F8_F32) {
+        // f32 rows staged in LDS (two halves) and written as 256-byte row
+        // segments: D = alpha * acc.
+        if (p.ldd % 4 == 0 && (reinterpret_cast<uintptr_t>(p.d) & 15u) == 0 && (full || p.N % 4 == 0)) {
+            const int wave = threadIdx.x >> 6;
+            const int wrow = m_base + (wave / F8DmaCfg::WAVES_N) * F8DmaCfg::WM;
+            const int wcol = n_base + (wave % F8DmaCfg::WAVES_N) * F8DmaCfg::WN;
+            int8_t *scratch = (wave < 4 ? stage0 : stage1) + (wave & 3) * (F8DmaCfg::WM / 2 * 256);
+            const float alpha = p.alpha;
+            M2::store_x32x4_staged<P>(
+                acc, scratch,
+                [&](int, int, const v4f &v) {
+                    return v4i{__float_as_int(alpha * v[0]), __float_as_int(alpha * v[1]),
+                               __float_as_int(alpha * v[2]), __float_as_int(alpha * v[3])};
+                },
+                [&](int r) {
+                    return wrow + r < p.M ? static_cast<float *>(p.d) + (int64_t)(wrow + r) * p.ldd + wcol : nullptr;
+                },
+                min(F8DmaCfg::WN, p.N - wcol));
+            return;
+        }
+    }
     const F8Epilogue<FMT, EPI, true, ACT> epi{p};
     if constexpr (EPI == F8_OUT) {
         // fp8 bytes staged per wave, written as 16-byte row segments.

@@ -718,15 +718,16 @@ __device__ __forceinline__ void store_u8x4_staged(const AccTile<P> &acc, int8_t 
     }
 }
 
-// 32-bit outputs of the int8 16x16 policy (WN = 64 columns, 256-byte
-// rows): the wave tile is staged in LDS in two halves of WM / 2 rows
-// (`scratch`: WM / 2 * 256 bytes private to this wave; unit u of row r at
-// unit u ^ (r & 15)), each half's rows written as 16-byte units, four rows
-// of 256 bytes per store instruction.  row_dst(r) gives row r's destination
-// (nullptr: skip); ncols: valid columns (a multiple of 4).
-template <class P, class RowDst>
-__device__ __forceinline__ void store_i32x4_staged(const AccTile<P> &acc, int8_t *scratch, RowDst &&row_dst,
-                                                   int ncols = P::Cfg::WN) {
+// 32-bit outputs of a policy whose wave tile is WN = 64 columns (256-byte
+// rows): each quad (4 columns of one row) is packed to 16 bytes by
+// pack(r, c, quad) and the wave tile staged in LDS in two halves of WM / 2
+// rows (`scratch`: WM / 2 * 256 bytes private to this wave; unit u of row r
+// at unit u ^ (r & 15)), each half's rows written as 16-byte units, four
+// rows of 256 bytes per store instruction.  row_dst(r) gives row r's
+// destination (nullptr: skip); ncols: valid columns (a multiple of 4).
+template <class P, class Pack, class RowDst>
+__device__ __forceinline__ void store_x32x4_staged(const AccTile<P> &acc, int8_t *scratch, Pack &&pack,
+                                                   RowDst &&row_dst, int ncols = P::Cfg::WN) {
     typedef typename P::Cfg C;
     static_assert(C::WN == 64 && P::TI % 2 == 0, "staged 32-bit store assumes 256-byte wave-tile rows");
     constexpr int HALF = C::WM / 2;
@@ -740,7 +741,7 @@ __device__ __forceinline__ void store_i32x4_staged(const AccTile<P> &acc, int8_t
                 P::visit(acc[i][j], i, j, lane, [&](int r, int c, const auto &v) {
                     const int rl = r - h * HALF;
                     const int unit = (c >> 2) ^ (rl & 15);
-                    *reinterpret_cast<v4i *>(scratch + rl * 256 + (unit << 4)) = v4i{v[0], v[1], v[2], v[3]};
+                    *reinterpret_cast<v4i *>(scratch + rl * 256 + (unit << 4)) = pack(r, c, v);
                 });
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -749,7 +750,7 @@ __device__ __forceinline__ void store_i32x4_staged(const AccTile<P> &acc, int8_t
         for (int q = 0; q < HALF / 4; ++q) {
             const int rl = q * 4 + (lane >> 4), u = lane & 15;
             const v4i v = *reinterpret_cast<const v4i *>(scratch + rl * 256 + ((u ^ (rl & 15)) << 4));
-            int32_t *dst = row_dst(h * HALF + rl);
+            auto *dst = row_dst(h * HALF + rl);   // 32-bit elements
             if (dst != nullptr && u * 4 < ncols) __builtin_nontemporal_store(v, reinterpret_cast<v4i *>(dst + u * 4));
         }
         // the second half reuses the scratch rows

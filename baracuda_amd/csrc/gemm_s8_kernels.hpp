@@ -340,20 +340,43 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_s8_rcr_dma_kernel(S8Args p
             return;
         }
     }
-    if constexpr (EPI == EPI_I32 && VecOut) {
+    if constexpr ((EPI == EPI_I32 || EPI == EPI_W8A8_F32) && VecOut) {
         if (p.ldd % 4 == 0 && (reinterpret_cast<uintptr_t>(p.d) & 15u) == 0 && (full || p.N % 4 == 0)) {
-            // int32 rows staged in LDS (16 KiB per wave, two halves) and
+            // 32-bit rows staged in LDS (16 KiB per wave, two halves) and
             // written as 256-byte row segments instead of 16-byte quads.
-            const int wave = threadIdx.x >> 6;
+            const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
             const int wrow = m_base + (wave / DmaCfg::WAVES_N) * DmaCfg::WM;
             const int wcol = n_base + (wave % DmaCfg::WAVES_N) * DmaCfg::WN;
             int8_t *scratch = (wave < 4 ? stage0 : stage1) + (wave & 3) * (DmaCfg::WM / 2 * 256);
-            M2::store_i32x4_staged<P>(
-                acc, scratch,
-                [&](int r) {
-                    return wrow + r < p.M ? static_cast<int32_t *>(p.d) + (int64_t)(wrow + r) * p.ldd + wcol : nullptr;
-                },
-                min(DmaCfg::WN, p.N - wcol));
+            auto row_dst = [&](int r) {
+                return wrow + r < p.M ? static_cast<int32_t *>(p.d) + (int64_t)(wrow + r) * p.ldd + wcol : nullptr;
+            };
+            if constexpr (EPI == EPI_I32) {
+                M2::store_x32x4_staged<P>(acc, scratch, [](int, int, const v4i &v) { return v; }, row_dst,
+                                          min(DmaCfg::WN, p.N - wcol));
+            } else {
+                // y = (sa[m] * sw[n]) * (float)acc, the scales fetched once per lane
+                float sam[P::TI];
+                v4f swv[P::TJ];
+#pragma unroll
+                for (int i = 0; i < P::TI; ++i) sam[i] = p.sa[min(wrow + i * 16 + (lane & 15), p.M - 1)];
+#pragma unroll
+                for (int j = 0; j < P::TJ; ++j) {
+                    const int col = wcol + j * 16 + (lane >> 4) * 4;
+                    swv[j] = col < p.N ? *reinterpret_cast<const v4f *>(p.sw + col) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+                }
+                M2::store_x32x4_staged<P>(
+                    acc, scratch,
+                    [&](int r, int c, const v4i &v) {
+                        const float sa_r = sam[r >> 4];
+                        const v4f sw_c = swv[c >> 4];
+                        return v4i{__float_as_int((sa_r * sw_c[0]) * (float)v[0]),
+                                   __float_as_int((sa_r * sw_c[1]) * (float)v[1]),
+                                   __float_as_int((sa_r * sw_c[2]) * (float)v[2]),
+                                   __float_as_int((sa_r * sw_c[3]) * (float)v[3])};
+                    },
+                    row_dst, min(DmaCfg::WN, p.N - wcol));
+            }
             return;
         }
     }
