@@ -760,6 +760,52 @@ __device__ __forceinline__ void store_x32x4_staged(const AccTile<P> &acc, int8_t
     }
 }
 
+// 64-bit outputs of the int8 16x16 policy (WN = 64 columns, 512-byte rows):
+// each quad is packed to 32 bytes by pack(r, c, quad) -> {lo, hi} (columns
+// c, c+1 and c+2, c+3) and the wave tile staged in LDS in four quarters of
+// WM / 4 rows (`scratch`: WM / 4 * 512 bytes private to this wave; 16-byte
+// unit u of row r at unit u ^ (r & 15)), two 512-byte rows per store
+// instruction.  row_dst(r): row r's destination (nullptr: skip); ncols:
+// valid columns (a multiple of 2).
+struct Quad64 { v4i lo, hi; };
+
+template <class P, class Pack, class RowDst>
+__device__ __forceinline__ void store_x64x4_staged(const AccTile<P> &acc, int8_t *scratch, Pack &&pack,
+                                                   RowDst &&row_dst, int ncols = P::Cfg::WN) {
+    typedef typename P::Cfg C;
+    static_assert(C::WN == 64 && P::TI % 4 == 0, "staged 64-bit store assumes 512-byte wave-tile rows");
+    constexpr int QR = C::WM / 4;
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+#pragma unroll
+        for (int i = h * (P::TI / 4); i < (h + 1) * (P::TI / 4); ++i)
+#pragma unroll
+            for (int j = 0; j < P::TJ; ++j)
+                P::visit(acc[i][j], i, j, lane, [&](int r, int c, const auto &v) {
+                    const int rl = r - h * QR;
+                    const Quad64 q = pack(r, c, v);
+                    const int u0 = (c >> 1) ^ (rl & 15), u1 = ((c >> 1) + 1) ^ (rl & 15);
+                    *reinterpret_cast<v4i *>(scratch + rl * 512 + (u0 << 4)) = q.lo;
+                    *reinterpret_cast<v4i *>(scratch + rl * 512 + (u1 << 4)) = q.hi;
+                });
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int q = 0; q < QR / 2; ++q) {
+            const int rl = q * 2 + (lane >> 5), u = lane & 31;
+            const v4i v = *reinterpret_cast<const v4i *>(scratch + rl * 512 + ((u ^ (rl & 15)) << 4));
+            auto *dst = row_dst(h * QR + rl);   // 64-bit elements
+            if (dst != nullptr && u * 2 < ncols) __builtin_nontemporal_store(v, reinterpret_cast<v4i *>(dst + u * 2));
+        }
+        // the next quarter reuses the scratch rows
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+}
+
 // 16-bit outputs of any policy whose wave tile is WN = 64 columns: each quad
 // (4 columns of one row) is packed to 4 halves by pack(r, c, quad) (8 bytes)
 // and staged in LDS; rows (128 bytes) are then written as 16-byte units,

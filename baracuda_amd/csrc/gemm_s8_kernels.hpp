@@ -380,6 +380,45 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_s8_rcr_dma_kernel(S8Args p
             return;
         }
     }
+    if constexpr (EPI == EPI_W8A8_F64 && VecOut) {
+        if (p.ldd % 2 == 0 && (reinterpret_cast<uintptr_t>(p.d) & 15u) == 0 && (full || p.N % 4 == 0)) {
+            // f64 rows staged in LDS (16 KiB per wave, four quarters) and
+            // written as 512-byte row segments:
+            // y = (double)(((float)sa[m] * (float)sw[n]) * (float)acc).
+            const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+            const int wrow = m_base + (wave / DmaCfg::WAVES_N) * DmaCfg::WM;
+            const int wcol = n_base + (wave % DmaCfg::WAVES_N) * DmaCfg::WN;
+            int8_t *scratch = (wave < 4 ? stage0 : stage1) + (wave & 3) * (DmaCfg::WM / 4 * 512);
+            const double *sa64 = reinterpret_cast<const double *>(p.sa);
+            const double *sw64 = reinterpret_cast<const double *>(p.sw);
+            float sam[P::TI], swf[P::TJ][4];
+#pragma unroll
+            for (int i = 0; i < P::TI; ++i) sam[i] = (float)sa64[min(wrow + i * 16 + (lane & 15), p.M - 1)];
+#pragma unroll
+            for (int j = 0; j < P::TJ; ++j)
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const int col = wcol + j * 16 + (lane >> 4) * 4 + t;
+                    swf[j][t] = col < p.N ? (float)sw64[col] : 0.0f;
+                }
+            auto bits = [](double x) { return (int64_t)__builtin_bit_cast(int64_t, x); };
+            M2::store_x64x4_staged<P>(
+                acc, scratch,
+                [&](int r, int c, const v4i &v) {
+                    const float sa_r = sam[r >> 4];
+                    int64_t y[4];
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) y[t] = bits((double)((sa_r * swf[c >> 4][t]) * (float)v[t]));
+                    return M2::Quad64{v4i{(int)y[0], (int)(y[0] >> 32), (int)y[1], (int)(y[1] >> 32)},
+                                      v4i{(int)y[2], (int)(y[2] >> 32), (int)y[3], (int)(y[3] >> 32)}};
+                },
+                [&](int r) {
+                    return wrow + r < p.M ? static_cast<double *>(p.d) + (int64_t)(wrow + r) * p.ldd + wcol : nullptr;
+                },
+                min(DmaCfg::WN, p.N - wcol));
+            return;
+        }
+    }
     {
         const S8Epilogue<EPI, VecOut, ACT, BiasT> epi{p};
         if constexpr (EPI == EPI_S8 && VecOut) {

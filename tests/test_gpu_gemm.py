@@ -304,12 +304,16 @@ def test_w8a8_config2_full_size_sampled_rows(gpu):
     assert np.array_equal(rowsum, a.astype(np.int64) @ w.astype(np.int64).sum(0))
 
 
-def test_quantized_linear_w8a8_f32(gpu):
-    a, w, sa, sw = w8a8(130, 70, 200, seed=8)
-    out = torch.empty((130, 70), dtype=torch.float32, device="cuda:0")
+@pytest.mark.parametrize("shape", [(130, 70, 200), (256, 256, 256), (300, 520, 384), (512, 768, 1024)])
+def test_quantized_linear_w8a8_f32(gpu, shape):
+    # general path (K = 200) and the LDS-DMA path with staged 256-byte row
+    # stores (whole and edge tiles)
+    m, n, k = shape
+    a, w, sa, sw = w8a8(m, n, k, seed=8)
+    out = torch.empty((m, n), dtype=torch.float32, device="cuda:0")
     from baracuda_amd.ffi import lib
     tw, ta, tsa, tsw = dev(w), dev(a), dev(sa), dev(sw)   # keep the buffers alive across the call
-    st = lib().quantized_linear_w8a8_f32_gfx950_run(130, 70, 200, tw.data_ptr(), ta.data_ptr(),
+    st = lib().quantized_linear_w8a8_f32_gfx950_run(m, n, k, tw.data_ptr(), ta.data_ptr(),
                                                     tsa.data_ptr(), tsw.data_ptr(), out.data_ptr(),
                                                     None, 0, torch.cuda.current_stream().cuda_stream)
     assert st == 0
@@ -319,18 +323,21 @@ def test_quantized_linear_w8a8_f32(gpu):
     assert np.array_equal(out.cpu().numpy(), want)
 
 
-def test_quantized_linear_w8a8_f64(gpu):
+@pytest.mark.parametrize("shape", [(130, 70, 200), (256, 256, 256), (300, 520, 384), (512, 768, 1024)])
+def test_quantized_linear_w8a8_f64(gpu, shape):
     # compose.cu:27-28 f64 SKU: f64 scales narrowed to f32, y = sa*sw*acc in
     # f32, widened to f64.  The f64 scales carry bits below f32 precision so
-    # a kernel that multiplied in f64 would differ.
-    a, w, _, _ = w8a8(130, 70, 200, seed=18)
+    # a kernel that multiplied in f64 would differ.  General path (K = 200),
+    # LDS-DMA path with the staged 512-byte row stores (whole and edge tiles).
+    m, n, k = shape
+    a, w, _, _ = w8a8(m, n, k, seed=18)
     g = rng(19)
-    sa = g.uniform(0.005, 0.02, 130)            # f64, not f32-representable
-    sw = g.uniform(0.001, 0.01, 70)
-    out = torch.empty((130, 70), dtype=torch.float64, device="cuda:0")
+    sa = g.uniform(0.005, 0.02, m)            # f64, not f32-representable
+    sw = g.uniform(0.001, 0.01, n)
+    out = torch.empty((m, n), dtype=torch.float64, device="cuda:0")
     from baracuda_amd.ffi import lib
     tw, ta, tsa, tsw = dev(w), dev(a), dev(sa), dev(sw)
-    st = lib().quantized_linear_w8a8_f64_gfx950_run(130, 70, 200, tw.data_ptr(), ta.data_ptr(),
+    st = lib().quantized_linear_w8a8_f64_gfx950_run(m, n, k, tw.data_ptr(), ta.data_ptr(),
                                                     tsa.data_ptr(), tsw.data_ptr(), out.data_ptr(),
                                                     None, 0, torch.cuda.current_stream().cuda_stream)
     assert st == 0
