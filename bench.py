@@ -32,6 +32,7 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E, GB/s
 OPS_PER_CLK = 256 * 8192
 HEAD_WARM_MS = 300.0        # wall time the headline kernel runs before its timed launches
 CLOCK_LOAD_S = 2.0          # the headline kernel in a loop while clock / power are sampled
+NO_CLOCK = [False]          # --no-clock
 # HBM bytes per launch measured with rocprofv3 PMC (FETCH_SIZE x2.00 and
 # WRITE_SIZE x1.00, scales calibrated on a plain device copy); the runs and
 # raw readings are in profiles/path_kernels_hbm_traffic.md.
@@ -200,8 +201,11 @@ class ClockSampler:
 
 
 def clock_under_load(fn, seconds=None):
-    """Clock / power summary (ClockSampler) while fn runs in a loop."""
+    """Clock / power summary (ClockSampler) while fn runs in a loop; skipped
+    (empty summary) with --no-clock, e.g. under a counter profiler."""
     import torch
+    if NO_CLOCK[0]:
+        return {"mhz_mean": None, "samples": 0, "source": "skipped (--no-clock)"}
     with ClockSampler() as clk:
         t_end = time.perf_counter() + (CLOCK_LOAD_S if seconds is None else seconds)
         while time.perf_counter() < t_end:
@@ -317,10 +321,13 @@ def main():
     ap.add_argument("--warmup", type=int, default=400)
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-clock", action="store_true",
+                    help="skip the 2 s clock / power loops (profiling runs)")
     ap.add_argument("--only", default="",
                     help="run only: w8a8|w8a8x|w8a8c|gemv|quant|fp8|moe|int8epi|te|embedding|gather|copy (profiling; copy = 256 MiB "
                          "device copy used to calibrate the HBM byte counters)")
     args = ap.parse_args()
+    NO_CLOCK[0] = args.no_clock
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path. "
               "Run with --gpus 1.", file=sys.stderr)
