@@ -213,16 +213,19 @@ __global__ __launch_bounds__(kDenseCols * kDenseSlices) void gemv_dense_m1_kerne
     }
 }
 
-// Vector path: a workgroup (16 waves) owns one 64-byte column segment (16
-// f32 or 32 f16/bf16 columns); a lane loads 16 bytes (one quad of the
-// segment) of a B row, four lanes cover the segment, so one wave instruction
-// reads 16 rows.  Wave w takes the K slice [w*per, (w+1)*per), its lanes the
-// rows k0 + r, k0 + r + 16, ... (r = lane / 4).  Partial sums are combined in
-// a fixed order -- a butterfly over the 16 row lanes, then the 16 waves in
-// LDS -- so results are bit-identical from launch to launch and independent
-// of the grid, as the reference's serial kernel's are; 4x / 8x the
-// workgroups of the scalar kernel at the same shape.  Workgroups sharing a
-// 128-byte line of B are placed on one XCD (consecutive segments per XCD).
+// Vector path: a workgroup (16 waves) owns one column segment of 16 columns
+// (64 bytes of f32, 32 bytes of f16/bf16); a lane loads 16 bytes of a B row,
+// LPR = 4 (f32) / 2 (16-bit) lanes cover the segment, so one wave
+// instruction reads 64 / LPR rows.  Wave w takes the K slice
+// [w*per, (w+1)*per), its lanes the rows k0 + r, k0 + r + 64/LPR, ...
+// (r = lane / LPR).  Partial sums are combined in a fixed order -- a
+// butterfly over the row lanes, then the 16 waves in LDS -- so results are
+// bit-identical from launch to launch and independent of the grid, as the
+// reference's serial kernel's are.  Workgroups sharing a 128-byte line of B
+// are placed on one XCD (consecutive segments per XCD).
+template <typename S>
+constexpr int vec_seg_bytes() { return sizeof(S) == 4 ? 64 : 32; }
+
 template <typename Tag>
 __global__ __launch_bounds__(1024) void gemv_dense_m1_vec_kernel(
     int n, int k, float alpha, float beta, const typename Codec<Tag>::S *__restrict__ a,
@@ -231,7 +234,9 @@ __global__ __launch_bounds__(1024) void gemv_dense_m1_vec_kernel(
     typedef Codec<Tag> C;
     typedef typename C::S S;
     constexpr int EPL = 16 / (int)sizeof(S);     // elements per 16-byte load
-    constexpr int COLS = 4 * EPL;                // columns per workgroup
+    constexpr int LPR = vec_seg_bytes<S>() / 16; // lanes per B row
+    constexpr int RPI = 64 / LPR;                // rows per wave instruction
+    constexpr int COLS = LPR * EPL;              // columns per workgroup
     constexpr int WAVES = 16;
     __shared__ float part[WAVES][COLS];
     const int slot = blockIdx.y;
@@ -239,7 +244,7 @@ __global__ __launch_bounds__(1024) void gemv_dense_m1_vec_kernel(
     const int bx = blockIdx.x;
     const int cb = nb % 8 == 0 ? (bx % 8) * (nb / 8) + bx / 8 : bx;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int q = lane & 3, r = lane >> 2;
+    const int q = lane % LPR, r = lane / LPR;
     const int col = cb * COLS + q * EPL;
     const S *arow = a + (int64_t)slot * stride_a;
     const S *bmat = b + (int64_t)slot * stride_b + col;
@@ -250,7 +255,7 @@ __global__ __launch_bounds__(1024) void gemv_dense_m1_vec_kernel(
 #pragma unroll
     for (int e = 0; e < EPL; ++e) acc[e] = 0.0f;
 #pragma unroll 4
-    for (int kk = k0 + r; kk < k1; kk += 16) {
+    for (int kk = k0 + r; kk < k1; kk += RPI) {
         const v4i w = *reinterpret_cast<const v4i *>(bmat + (int64_t)kk * ldb);
         const float av = C::ld(arow[kk]);
         if constexpr (EPL == 4) {
@@ -268,7 +273,7 @@ __global__ __launch_bounds__(1024) void gemv_dense_m1_vec_kernel(
 #pragma unroll
     for (int e = 0; e < EPL; ++e) {
 #pragma unroll
-        for (int off = 4; off < 64; off <<= 1) acc[e] += __shfl_xor(acc[e], off, 64);
+        for (int off = LPR; off < 64; off <<= 1) acc[e] += __shfl_xor(acc[e], off, 64);
     }
     if (r == 0) {
 #pragma unroll
@@ -288,7 +293,7 @@ __global__ __launch_bounds__(1024) void gemv_dense_m1_vec_kernel(
 }
 
 // Split-K path (optional caller workspace, large problems): B read in long
-// contiguous row spans instead of 64-byte column segments.  The column-
+// contiguous row spans instead of 32- / 64-byte column segments.  The column-
 // segment pattern of the kernel above is bound by its access pattern -- a
 // read-only probe of it moves the 32 MiB of a bf16 K = N = 4096 B in 16 us,
 // the same bytes read contiguously take 6 us.
@@ -442,9 +447,9 @@ int32_t launch_dense(int32_t m, int32_t n, int32_t k, int32_t batch, int32_t lay
     if (m == 0 || n == 0 || batch == 0) return kOk;
     if (!a || !b || !d) return kInvalid;
     typedef typename Codec<Tag>::S S;
-    // Vector path: whole 64-byte column segments and 16-byte aligned B rows
-    // (base, row pitch and batch stride).
-    constexpr int VCOLS = 64 / (int)sizeof(S);
+    // Vector path: whole column segments and 16-byte aligned B rows (base,
+    // row pitch and batch stride).
+    constexpr int VCOLS = vec_seg_bytes<S>() / (int)sizeof(S);
     const bool vec = n % VCOLS == 0 && ((int64_t)ldb * (int64_t)sizeof(S)) % 16 == 0 &&
                      ((int64_t)stride_b * (int64_t)sizeof(S)) % 16 == 0 &&
                      (reinterpret_cast<uintptr_t>(b) & 15u) == 0;
