@@ -125,7 +125,7 @@ class ClockSampler:
     def __init__(self, period_s=0.02):
         import threading
         self.period_s = period_s
-        self.samples = []   # (mhz mean over XCDs, socket power W)
+        self.samples = []   # (mhz mean over XCDs, socket power W, per-XCD mhz tuple)
         self.error = None
         self._stop = threading.Event()
         self._thr = threading.Thread(target=self._loop, daemon=True)
@@ -153,14 +153,14 @@ class ClockSampler:
             v = m.get("current_gfxclk")
             mhz = float(v) if isinstance(v, int) and 0 < v < 10000 else None
         pw = m.get("current_socket_power")
-        return mhz, (float(pw) if isinstance(pw, int) and 0 < pw < 100000 else None)
+        return mhz, (float(pw) if isinstance(pw, int) and 0 < pw < 100000 else None), tuple(xs)
 
     def _loop(self):
         while not self._stop.is_set():
             try:
-                mhz, pw = self._read()
+                mhz, pw, per = self._read()
                 if mhz is not None:
-                    self.samples.append((mhz, pw))
+                    self.samples.append((mhz, pw, per))
             except Exception as e:   # noqa: BLE001 -- telemetry only
                 self.error = repr(e)
                 return
@@ -193,9 +193,14 @@ class ClockSampler:
             return {"mhz_mean": None, "samples": len(self.samples), "source": src,
                     "error": self.error or "metrics table did not refresh during the sample"}
         live = self.samples[first:]
-        mh = [x for x, _ in live]
-        pw = [p for _, p in live if p is not None]
+        mh = [x for x, _, _ in live]
+        pw = [p for _, p, _ in live if p is not None]
+        per = [q for _, _, q in live if q and len(q) == len(live[0][2])]
+        # Each XCD runs at its own clock; a kernel whose tiles are spread
+        # evenly over the XCDs ends with the slowest one.
+        per_xcd = [round(sum(q[i] for q in per) / len(per), 1) for i in range(len(per[0]))] if per else None
         return {"mhz_mean": round(sum(mh) / len(mh), 1), "mhz_min": min(mh), "mhz_max": max(mh),
+                "mhz_per_xcd_mean": per_xcd,
                 "socket_power_w_mean": round(sum(pw) / len(pw), 1) if pw else None,
                 "samples": len(live), "source": src}
 
