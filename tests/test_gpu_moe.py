@@ -11,7 +11,8 @@ from tests.gpu_util import dev, host_bits16, sync
 pytestmark = pytest.mark.gpu
 
 
-def _run(tokens, E, topk, n, k, seed, topk_w=False, pairs_check=None, routing=None, ws_bytes=None):
+def _run(tokens, E, topk, n, k, seed, topk_w=False, pairs_check=None, routing=None, ws_bytes=None,
+         inputs=None):
     sorted_ids, expert_ids = routing if routing is not None else moe_routing(tokens, E, topk, seed=seed)
     size_m = tokens * topk
     g = rng(seed + 100)
@@ -47,6 +48,8 @@ def _run(tokens, E, topk, n, k, seed, topk_w=False, pairs_check=None, routing=No
         if tw is not None:
             y = (y * tw[p]).astype(np.float32)
         assert np.array_equal(got[p], O.f32_to_bf16_bits_fast(y)), p
+    if inputs is not None:
+        inputs.update(x=x, w=w, sa=sa, sw=sw, pair_e=pair_e)
     return got
 
 
@@ -87,6 +90,38 @@ def test_moe_config5_full_size_sampled(gpu):
     print("case: moe config5", flush=True)
     pairs = [0, 1, 2, 8191, 4095] + list(rng(51).integers(0, 8192, 27))
     _run(tokens=4096, E=8, topk=2, n=14336, k=4096, seed=5, pairs_check=pairs)
+
+
+def test_moe_config5_whole_output_sums(gpu):
+    # Config 5 over all 8192 x 14336 outputs, size-independent: each output is
+    # bf16((sa[t] * sw[e, n]) * acc), so v = out / (sa[t] * sw[e, n]) (f64)
+    # is acc within a relative 2^-8 (bf16 rounding) plus f32 slack.  Row sums
+    # of v against x[t] . sum_n W[e][n, :] and, per expert, column sums of v
+    # over its pairs against W[e] . sum_t x[t] (exact integers), each within
+    # 1.01 * 2^-8 * the sum of |v|.  Every pair and every column is checked;
+    # a missing, misplaced or mis-scaled row or tile moves a sum far beyond
+    # that bound.
+    print("case: moe config5 whole-output sums", flush=True)
+    tokens, E, topk, n, k = 4096, 8, 2, 14336, 4096
+    inp = {}
+    got = _run(tokens=tokens, E=E, topk=topk, n=n, k=k, seed=5, pairs_check=[0, 8191], inputs=inp)
+    x, w, sa, sw, pair_e = inp["x"], inp["w"], inp["sa"], inp["sw"], inp["pair_e"]
+    out = (got.astype(np.uint32) << 16).view(np.float32)
+    tok = np.arange(tokens * topk) // topk
+    sw2 = sw.reshape(E, n)
+    tol = 1.01 * 2.0 ** -8
+    x64 = x.astype(np.int64)
+    for e in range(E):
+        pe = np.nonzero(pair_e == e)[0]
+        if pe.size == 0:
+            continue
+        scale = (sa[tok[pe]].astype(np.float32)[:, None] * sw2[e][None, :]).astype(np.float64)
+        v = out[pe].astype(np.float64) / scale
+        we = w[e].astype(np.int64)
+        row_exact = x64[tok[pe]] @ we.sum(0)
+        assert np.all(np.abs(v.sum(1) - row_exact) <= tol * np.abs(v).sum(1)), e
+        col_exact = we @ x64[tok[pe]].sum(0)
+        assert np.all(np.abs(v.sum(0) - col_exact) <= tol * np.abs(v).sum(0)), e
 
 
 @pytest.mark.parametrize("E", [1, 8, 63, 64, 65, 300])
