@@ -230,8 +230,24 @@ typedef mfma2::Cfg<2, 4> DmaCfg;
 // measured 567 against 577 µs.
 constexpr int kMoeNBlock = 4;
 
+// Reordered tail of each XCD's range (see moe_dma_coords).  Config 5, two
+// boxes, six alternating passes each: windows of 16 / 32 / 48 / 64 / 128
+// positions 494 / 494 / 496 / 498 / 522 against 510 µs without (the
+// 128-position window reaches back into earlier n-blocks, whose weight
+// panels have left the caches).
+constexpr int kMoeTail = 32;
+
+// List position -> (slot, n-tile) in the n-block order.
+__device__ __forceinline__ void moe_list_tile(int r, int S, int n_tiles, int &slot, int &ntile) {
+    const int b = r / (S * kMoeNBlock);
+    const int bw = min(kMoeNBlock, n_tiles - b * kMoeNBlock);   // the last block may be narrower
+    const int i = r - b * S * kMoeNBlock;
+    slot = i / bw;
+    ntile = b * kMoeNBlock + i % bw;
+}
+
 __device__ __forceinline__ bool moe_dma_coords(const MoeArgs &p, const int32_t *s_off, int pid,
-                                               int n_tiles, int &slot, int &ntile) {
+                                               int n_tiles, int &slot, int &ntile, int *s_tail) {
     constexpr int XCDS = 8;
     int S = 0;
     for (int e = 0; e < p.E; ++e) {
@@ -239,15 +255,42 @@ __device__ __forceinline__ bool moe_dma_coords(const MoeArgs &p, const int32_t *
         S += (rows + 255) / 256;
     }
     const int T = S * n_tiles;
-    const int padded = (T + XCDS - 1) / XCDS * XCDS;
-    if (pid >= padded) return false;
-    const int r = (pid % XCDS) * (padded / XCDS) + pid / XCDS;
-    if (r >= T) return false;
-    const int b = r / (S * kMoeNBlock);
-    const int bw = min(kMoeNBlock, n_tiles - b * kMoeNBlock);   // the last block may be narrower
-    const int i = r - b * S * kMoeNBlock;
-    slot = i / bw;
-    ntile = b * kMoeNBlock + i % bw;
+    const int per = (T + XCDS - 1) / XCDS;
+    const int r0 = (pid % XCDS) * per;               // this XCD's range [r0, r0 + len)
+    const int len = min(per, T - r0);
+    int j = pid / XCDS;
+    if (pid >= per * XCDS || j >= len) return false;
+    // The last kMoeTail positions of the range run their tiles of more than
+    // 128 rows first and the smaller ones last (each group in list order), so
+    // that the tiles still running when the range runs dry are the short
+    // ones: a tile of at most 128 rows takes about 0.7 of a full one, and
+    // the ragged end of the last round is otherwise about one average tile
+    // long.  Workgroup-uniform branch; the permutation stays inside the
+    // window, so every tile still runs exactly once.
+    const int w0 = max(0, len - kMoeTail);
+    if (j >= w0) {
+        const int wn = len - w0;
+        for (int t = threadIdx.x; t < wn; t += blockDim.x) {
+            int sl, nt, e, seg0, rows;
+            moe_list_tile(r0 + w0 + t, S, n_tiles, sl, nt);
+            moe_find(p, s_off, sl, e, seg0, rows);
+            s_tail[t] = rows > 128;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            int nbig = 0;
+            for (int t = 0; t < wn; ++t) nbig += s_tail[t];
+            const int q = j - w0;
+            const int want = q < nbig ? 1 : 0;
+            int k = q < nbig ? q : q - nbig, pick = 0;
+            for (int t = 0; t < wn; ++t)
+                if (s_tail[t] == want && k-- == 0) { pick = t; break; }
+            s_tail[kMoeTail] = pick;
+        }
+        __syncthreads();
+        j = w0 + s_tail[kMoeTail];
+    }
+    moe_list_tile(r0 + j, S, n_tiles, slot, ntile);
     return true;
 }
 
@@ -266,7 +309,8 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void moe_grouped_dma_kernel(MoeArgs 
     __shared__ int32_t s_off[kMaxExperts + 1];
     moe_load_offsets(p, s_off);
     int slot, ntile, e, seg0, seg_rows;
-    if (!moe_dma_coords(p, s_off, blockIdx.x, p.N / M2::BN, slot, ntile)) return;   // whole workgroup exits
+    __shared__ int s_tail[kMoeTail + 1];
+    if (!moe_dma_coords(p, s_off, blockIdx.x, p.N / M2::BN, slot, ntile, s_tail)) return;   // whole workgroup exits
     if (!moe_find(p, s_off, slot, e, seg0, seg_rows)) return;
     const int n_base = ntile * M2::BN;
     for (int r = threadIdx.x; r < M2::BM; r += DmaCfg::NT)
