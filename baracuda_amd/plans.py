@@ -575,8 +575,8 @@ class MoeS8GroupedPlan:
         return cls(num_experts, topk, size_m, size_n, size_k)
 
     def workspace_size(self) -> int:
-        """Optional workspace: the K split of a partial last round of tiles
-        (bit-identical output with or without it)."""
+        """Always 0, as the reference's MoE plans (`moe/mod.rs:295`); a
+        workspace passed to `run` anyway is ignored."""
         return int(lib().moe_s8_grouped_bf16_gfx950_workspace_size(self.E, self.topk, self.size_m, self.n, self.k))
 
     def run(self, x, w, sorted_token_ids, expert_ids, out, expert_counts, expert_offsets,
