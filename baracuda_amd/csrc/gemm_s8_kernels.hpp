@@ -198,9 +198,18 @@ struct TailSplit {
     int split;        // K chunks per tail tile (1: no split)
 };
 
+// Last rows of M run by gemm_s8_rcr_rows_kernel instead of a row of
+// 256-row tiles: M % 256 in [1, kRowsPathMax], M > 256, N % 16 == 0.
+constexpr int kRowsPathMax = 64;
+inline int rows_path_rows(int M, int N) {
+    const int rem = M % 256;
+    return (M > 256 && rem > 0 && rem <= kRowsPathMax && N % 16 == 0) ? rem : 0;
+}
+
 inline TailSplit tail_split_plan(int M, int N, int K) {
     TailSplit t{0, 0, 1};
     if (M <= 0 || N <= 0 || K <= 0 || K % 128 != 0) return t;
+    if (rows_path_rows(M, N) != 0) return t;   // the rows path takes those shapes
     const int tiles_m = (M + 255) / 256, tiles_n = (N + 255) / 256;
     const int64_t T = (int64_t)tiles_m * tiles_n;
     const int64_t full = T / 256 * 256;
@@ -452,6 +461,76 @@ __global__ __launch_bounds__(256) void gemm_s8_tail_reduce_kernel(S8Args p, Tail
     }
     const S8Epilogue<EPI, VecOut, ACT, BiasT> epi{p};
     epi(m, n0, acc);
+}
+
+// The last M - m0 (<= kRowsPathMax) rows of an RCR GEMM whose other rows
+// run as whole 256-row tiles (K % 128 == 0, 16-byte aligned rows, N % 16 ==
+// 0).  A 256-row tile for them would stream its whole B panel at the pace of
+// a full tile; here one workgroup of 8 waves owns 16 output columns, the
+// waves split K into 8 contiguous runs of 64-byte chunks and stream their
+// 16 B rows and the (at most 16 RF) A rows straight from global memory, U
+// chunks in flight per batch, one v_mfma_i32_16x16x64_i8 per chunk and
+// 16-row fragment of A (B first, A second, both taking k = 64 c + 16
+// (lane / 16) + byte, so lane l ends with row m0 + 16 f + l % 16 and columns
+// 4 (l / 16) .. + 3 of its 16).  The eight partial sums are added in LDS
+// (int32 wrap-around, so the order does not matter) and go through the
+// tiles' epilogue.
+template <int EPI, bool VecOut, int ACT, typename BiasT, int RF>
+__global__ __launch_bounds__(512) void gemm_s8_rcr_rows_kernel(S8Args p, int m0) {
+    constexpr int U = RF == 1 ? 8 : 4, WAVES = 8;
+    __shared__ v4i part[WAVES][RF][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int n0 = blockIdx.x * 16;
+    const int8_t *arow[RF];
+#pragma unroll
+    for (int f = 0; f < RF; ++f) arow[f] = p.a + (int64_t)min(m0 + 16 * f + r16, p.M - 1) * p.lda + g * 16;
+    const int8_t *brow = p.b + (int64_t)(n0 + r16) * p.ldb + g * 16;
+    const int chunks = p.K >> 6;
+    v4i acc[RF];
+#pragma unroll
+    for (int f = 0; f < RF; ++f) acc[f] = v4i{0, 0, 0, 0};
+    // Wave w takes the contiguous chunks [c0, c1): 64 * (c1 - c0) bytes of
+    // each of its 16 B rows in one span.
+    const int c1 = (wave + 1) * chunks / WAVES;
+    int c = wave * chunks / WAVES;
+    for (; c + U <= c1; c += U) {
+        v4i bv[U], av[U][RF];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            bv[u] = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(brow + (int64_t)(c + u) * 64));
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int f = 0; f < RF; ++f) av[u][f] = *reinterpret_cast<const v4i *>(arow[f] + (int64_t)(c + u) * 64);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int f = 0; f < RF; ++f) acc[f] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bv[u], av[u][f], acc[f], 0, 0, 0);
+    }
+    for (; c < c1; ++c) {
+        const v4i bv = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(brow + (int64_t)c * 64));
+#pragma unroll
+        for (int f = 0; f < RF; ++f) {
+            const v4i av = *reinterpret_cast<const v4i *>(arow[f] + (int64_t)c * 64);
+            acc[f] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bv, av, acc[f], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int f = 0; f < RF; ++f) part[wave][f][lane] = acc[f];
+    __syncthreads();
+    // wave w < RF adds up fragment w over the 8 waves
+    if (wave >= RF) return;
+    v4i sum = part[0][wave][lane];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) {
+        const v4i v = part[w][wave][lane];
+        sum = v4i{(int)((uint32_t)sum[0] + (uint32_t)v[0]), (int)((uint32_t)sum[1] + (uint32_t)v[1]),
+                  (int)((uint32_t)sum[2] + (uint32_t)v[2]), (int)((uint32_t)sum[3] + (uint32_t)v[3])};
+    }
+    const S8Epilogue<EPI, VecOut, ACT, BiasT> epi{p};
+    epi(m0 + 16 * wave + r16, n0 + 4 * g, sum);   // rows past M are not stored
 }
 
 // RRR fast path: A through the interior DMA, row-major B through the
@@ -921,6 +1000,25 @@ int32_t launch_u8_rcr(const S8Args &p, hipStream_t stream) {
 template <int EPI, bool VecOut, int ACT, typename BiasT>
 void launch_kernel(const S8Args &p, bool fast_k, hipStream_t stream, void *workspace, size_t workspace_bytes) {
     if (fast_k) {
+        const int rem = rows_path_rows(p.M, p.N);
+        if (rem != 0) {
+            // whole 256-row tiles, then the last rows (gemm_s8_rcr_rows_kernel)
+            S8Args pm = p;
+            pm.M = p.M - rem;
+            const int tiles = (pm.M / mfma2::BM) * ((p.N + mfma2::BN - 1) / mfma2::BN);
+            hipLaunchKernelGGL((gemm_s8_rcr_dma_kernel<EPI, VecOut, ACT, BiasT>), dim3(tiles), dim3(DmaCfg::NT), 0,
+                               stream, pm, TailSplit{0, 0, 1}, (int32_t *)nullptr);
+            if (rem <= 16)
+                hipLaunchKernelGGL((gemm_s8_rcr_rows_kernel<EPI, VecOut, ACT, BiasT, 1>), dim3(p.N / 16), dim3(512),
+                                   0, stream, p, pm.M);
+            else if (rem <= 32)
+                hipLaunchKernelGGL((gemm_s8_rcr_rows_kernel<EPI, VecOut, ACT, BiasT, 2>), dim3(p.N / 16), dim3(512),
+                                   0, stream, p, pm.M);
+            else
+                hipLaunchKernelGGL((gemm_s8_rcr_rows_kernel<EPI, VecOut, ACT, BiasT, 4>), dim3(p.N / 16), dim3(512),
+                                   0, stream, p, pm.M);
+            return;
+        }
         const int tiles = ((p.M + mfma2::BM - 1) / mfma2::BM) * ((p.N + mfma2::BN - 1) / mfma2::BN);
         TailSplit ts = tail_split_plan(p.M, p.N, p.K);
         const size_t need = tail_split_workspace(p.M, p.N, p.K);

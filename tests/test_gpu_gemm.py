@@ -117,12 +117,12 @@ def _ws(plan):
     return torch.full((max(n, 1),), 0x5A, dtype=torch.uint8, device="cuda:0") if n else None
 
 
-def test_tail_split_w8a8_m4097_bit_identical(gpu):
-    # M = 4097 at the config-2 width: 272 tiles, the 17th tile row (one valid
-    # row) runs split along K through the optional workspace; the output
+def test_tail_split_w8a8_m4192_bit_identical(gpu):
+    # M = 4192 at the config-2 width: 272 tiles, the 17th tile row (96 valid
+    # rows) runs split along K through the optional workspace; the output
     # equals the unsplit launch's and the oracle's.
-    m, n, k = 4097, 4096, 4096
-    print("case: tail split w8a8 M=4097", flush=True)
+    m, n, k = 4192, 4096, 4096
+    print("case: tail split w8a8 M=4192", flush=True)
     a, w, sa, sw = w8a8(m, n, k, seed=41)
     plan = P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, output=P.ElementKind.Bf16))
     ws = _ws(plan)
@@ -134,7 +134,7 @@ def test_tail_split_w8a8_m4097_bit_identical(gpu):
         sync()
         outs.append(host_bits16(d))
     assert np.array_equal(outs[0], outs[1])
-    for r in (0, 4095, 4096):
+    for r in (0, 4095, 4096, 4191):
         assert np.array_equal(outs[1][r], O.gemm_w8a8_bf16(a, w, sa, sw, rows=(r, r + 1), nthreads=8)[0]), r
 
 
