@@ -199,17 +199,26 @@ struct TailSplit {
 };
 
 // Last rows of M run by gemm_s8_rcr_rows_kernel instead of a row of
-// 256-row tiles: M % 256 in [1, kRowsPathMax], M > 256, N % 16 == 0.
-constexpr int kRowsPathMax = 64;
-inline int rows_path_rows(int M, int N) {
+// 256-row tiles (N % 16 == 0): M % 256 in [1, kRowsPathMax] (all of M when
+// M <= kRowsPathMax: no tiles at all), when that row of tiles would start
+// another round of tiles on the 256 CUs (it costs nothing extra when it
+// fits the idle CUs of the last round).  Up to kRowsPathAlways rows always;
+// more only when no tail-split workspace is given.
+constexpr int kRowsPathMax = 128;
+constexpr int kRowsPathAlways = 64;
+inline int rows_path_rows(int M, int N, int limit = kRowsPathMax) {
+    if (N <= 0 || N % 16 != 0 || M <= 0) return 0;
     const int rem = M % 256;
-    return (M > 256 && rem > 0 && rem <= kRowsPathMax && N % 16 == 0) ? rem : 0;
+    if (rem == 0 || rem > limit) return 0;
+    const int64_t tn = (N + 255) / 256, main_tiles = (int64_t)(M - rem) / 256 * tn;
+    if (main_tiles > 0 && (main_tiles + tn + 255) / 256 == (main_tiles + 255) / 256) return 0;
+    return rem;
 }
 
 inline TailSplit tail_split_plan(int M, int N, int K) {
     TailSplit t{0, 0, 1};
     if (M <= 0 || N <= 0 || K <= 0 || K % 128 != 0) return t;
-    if (rows_path_rows(M, N) != 0) return t;   // the rows path takes those shapes
+    if (rows_path_rows(M, N, kRowsPathAlways) != 0) return t;   // the rows path takes those shapes
     const int tiles_m = (M + 255) / 256, tiles_n = (N + 255) / 256;
     const int64_t T = (int64_t)tiles_m * tiles_n;
     const int64_t full = T / 256 * 256;
@@ -477,7 +486,7 @@ __global__ __launch_bounds__(256) void gemm_s8_tail_reduce_kernel(S8Args p, Tail
 // tiles' epilogue.
 template <int EPI, bool VecOut, int ACT, typename BiasT, int RF>
 __global__ __launch_bounds__(512) void gemm_s8_rcr_rows_kernel(S8Args p, int m0) {
-    constexpr int U = RF == 1 ? 8 : 4, WAVES = 8;
+    constexpr int U = RF == 1 ? 8 : RF <= 4 ? 4 : 2, WAVES = 8;
     __shared__ v4i part[WAVES][RF][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r16 = lane & 15, g = lane >> 4;
@@ -1000,30 +1009,32 @@ int32_t launch_u8_rcr(const S8Args &p, hipStream_t stream) {
 template <int EPI, bool VecOut, int ACT, typename BiasT>
 void launch_kernel(const S8Args &p, bool fast_k, hipStream_t stream, void *workspace, size_t workspace_bytes) {
     if (fast_k) {
-        const int rem = rows_path_rows(p.M, p.N);
+        TailSplit ts = tail_split_plan(p.M, p.N, p.K);
+        const size_t need = tail_split_workspace(p.M, p.N, p.K);
+        const bool split_ws = ts.split > 1 && workspace != nullptr && workspace_bytes >= need &&
+                              (reinterpret_cast<uintptr_t>(workspace) & 15u) == 0;
+        const int rem = split_ws ? 0 : rows_path_rows(p.M, p.N);
         if (rem != 0) {
             // whole 256-row tiles, then the last rows (gemm_s8_rcr_rows_kernel)
             S8Args pm = p;
             pm.M = p.M - rem;
             const int tiles = (pm.M / mfma2::BM) * ((p.N + mfma2::BN - 1) / mfma2::BN);
-            hipLaunchKernelGGL((gemm_s8_rcr_dma_kernel<EPI, VecOut, ACT, BiasT>), dim3(tiles), dim3(DmaCfg::NT), 0,
-                               stream, pm, TailSplit{0, 0, 1}, (int32_t *)nullptr);
+            if (tiles > 0)
+                hipLaunchKernelGGL((gemm_s8_rcr_dma_kernel<EPI, VecOut, ACT, BiasT>), dim3(tiles), dim3(DmaCfg::NT),
+                                   0, stream, pm, TailSplit{0, 0, 1}, (int32_t *)nullptr);
+            const dim3 grid(p.N / 16), block(512);
             if (rem <= 16)
-                hipLaunchKernelGGL((gemm_s8_rcr_rows_kernel<EPI, VecOut, ACT, BiasT, 1>), dim3(p.N / 16), dim3(512),
-                                   0, stream, p, pm.M);
+                hipLaunchKernelGGL((gemm_s8_rcr_rows_kernel<EPI, VecOut, ACT, BiasT, 1>), grid, block, 0, stream, p, pm.M);
             else if (rem <= 32)
-                hipLaunchKernelGGL((gemm_s8_rcr_rows_kernel<EPI, VecOut, ACT, BiasT, 2>), dim3(p.N / 16), dim3(512),
-                                   0, stream, p, pm.M);
+                hipLaunchKernelGGL((gemm_s8_rcr_rows_kernel<EPI, VecOut, ACT, BiasT, 2>), grid, block, 0, stream, p, pm.M);
+            else if (rem <= 64)
+                hipLaunchKernelGGL((gemm_s8_rcr_rows_kernel<EPI, VecOut, ACT, BiasT, 4>), grid, block, 0, stream, p, pm.M);
             else
-                hipLaunchKernelGGL((gemm_s8_rcr_rows_kernel<EPI, VecOut, ACT, BiasT, 4>), dim3(p.N / 16), dim3(512),
-                                   0, stream, p, pm.M);
+                hipLaunchKernelGGL((gemm_s8_rcr_rows_kernel<EPI, VecOut, ACT, BiasT, 8>), grid, block, 0, stream, p, pm.M);
             return;
         }
         const int tiles = ((p.M + mfma2::BM - 1) / mfma2::BM) * ((p.N + mfma2::BN - 1) / mfma2::BN);
-        TailSplit ts = tail_split_plan(p.M, p.N, p.K);
-        const size_t need = tail_split_workspace(p.M, p.N, p.K);
-        if (ts.split > 1 && workspace != nullptr && workspace_bytes >= need &&
-            (reinterpret_cast<uintptr_t>(workspace) & 15u) == 0) {
+        if (split_ws) {
             int32_t *slots = static_cast<int32_t *>(workspace);
             hipLaunchKernelGGL((gemm_s8_rcr_dma_kernel<EPI, VecOut, ACT, BiasT>),
                                dim3(ts.full_tiles + ts.tail_tiles * ts.split), dim3(DmaCfg::NT), 0, stream, p, ts,

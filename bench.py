@@ -685,9 +685,10 @@ def main():
         if only in ("", "w8a8x"):
             log("bench: w8a8 off-grid M and constant operands")
             # Token counts off the 256-row tile grid (edge tiles on the LDS-DMA
-            # path) at the config-2 width; 4 rotated operand sets.
+            # path, the streamed last-rows pass) and small token counts at the
+            # config-2 width; 4 rotated operand sets.
             og = {}
-            for mm in (4000, 4097, 4160):
+            for mm in (16, 64, 128, 4000, 4097, 4160):
                 sets = [(torch.randint(-127, 128, (mm, K), dtype=torch.int8, device=dev),
                          torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev),
                          torch.rand(mm, device=dev) * 0.015 + 0.005, torch.rand(N, device=dev) * 0.009 + 0.001,
@@ -700,11 +701,24 @@ def main():
                     op.run(xa, xw, xo, scale_a=xsa, scale_b=xsw, stream=stream)
                     oi[0] += 1
                 oms = time_launches(off_run, 100, 10, stream, warm_ms=50.0)
-                rows_pass = mm > 256 and 0 < mm % 256 <= 64 and N % 16 == 0   # last rows streamed, not tiled
+                # last rows streamed instead of a row of tiles that would start another round
+                rem = mm % 256
+                main_t = (mm - rem) // 256 * (N // 256)
+                rows_pass = (N % 16 == 0 and 0 < rem <= 128 and
+                             (main_t == 0 or -(-(main_t + N // 256) // 256) > -(-main_t // 256)))
                 og[f"m{mm}"] = {"us": round(oms * 1e3, 2),
                                 "useful_TOPS": round(2.0 * mm * N * K / (oms * 1e-3) / 1e12, 1),
                                 "tiles": (mm // 256 if rows_pass else -(-mm // 256)) * (N // 256),
                                 "last_rows_pass": mm % 256 if rows_pass else 0}
+                if mm <= 128:
+                    # small token counts are host-launch bound from Python: also
+                    # the device time per call, replayed from a HIP graph
+
+                    def off_cur():
+                        xa, xw, xsa, xsw, xo = sets[oi[0] % 4]
+                        op.run(xa, xw, xo, scale_a=xsa, scale_b=xsw)
+                        oi[0] += 1
+                    og[f"m{mm}"]["graph_replay_us"] = round(graph_us(off_cur, per_graph=96), 2)
                 if op.workspace_size() > 0:
                     # the optional workspace: the partial last round split along K
                     ows = torch.empty(op.workspace_size(), dtype=torch.uint8, device=dev)

@@ -15,9 +15,11 @@
  *   - workspace is never required: every _workspace_size returns 0 except
  *     the u8 RRR family's, gemv_dense_m1's (large shapes) and the int8 RCR
  *     SKUs' (s8 / i32 / W8A8 bf16 out and the bias family, when the last
- *     round of 256 x 256 tiles on the 256 CUs is at most half full and M %
- *     256 is not in [1, 64] -- those shapes run their last rows as a
- *     streamed second launch without any workspace), whose
+ *     round of 256 x 256 tiles on the 256 CUs is at most half full and the
+ *     last rows are not a streamed pass: M % 256 in [1, 64] whose row of
+ *     tiles would start another round, or M <= 64, runs its last rows as a
+ *     second launch without any workspace; 65..128 such rows do so when no
+ *     workspace is passed), whose
  *     optional workspace (when given at least that size, 256- / 16-byte
  *     aligned; contents on entry do not matter) selects a faster path: the
  *     u8 pre-pass, the dense GEMV's split-K, the int8 tail round split along

@@ -257,8 +257,9 @@ def test_tail_split_workspace_sizes():
     # last round more than half full, or K too short take none
     assert P.IntGemmPlan.select(P.IntGemmDescriptor(4192, 4096, 4096, output=P.ElementKind.Bf16)
                                 ).workspace_size() == 16 * 16 * 65536 * 4
-    # M % 256 in [1, 64] (M > 256, N % 16 == 0) runs the last-rows pass, no workspace
-    for m in (4097, 4112, 4128, 4160, 257):
+    # M % 256 in [1, 64] (N % 16 == 0) whose last row of tiles would start
+    # another round (or M <= 64) runs the last-rows pass, no workspace
+    for m in (4097, 4112, 4128, 4160, 1, 16, 64):
         assert P.IntGemmPlan.select(P.IntGemmDescriptor(m, 4096, 4096, output=P.ElementKind.Bf16)
                                     ).workspace_size() == 0
     assert P.IntGemmPlan.select(P.IntGemmDescriptor(512, 512, 8192, output=P.ElementKind.I32)

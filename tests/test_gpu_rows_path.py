@@ -1,7 +1,11 @@
-"""GPU parity of the int8 RCR last-rows path: M % 256 in [1, 64] (M > 256,
-N % 16 == 0, K % 128 == 0) runs whole 256-row tiles plus a streamed pass
-over the last rows.  Every SKU family of the RCR launch goes through it;
-all outputs bit-exact against the oracle (int64 matmul for int32 out)."""
+"""GPU parity of the int8 RCR last-rows path: when M % 256 is in [1, 128]
+(N % 16 == 0, K % 128 == 0; above 64 rows only without the tail-split
+workspace) and the last row of 256-row tiles would start another round of
+tiles on the 256 CUs -- or M itself is at most 128 -- the whole tiles run
+as usual and a streamed pass computes the last rows.  Every SKU family of
+the RCR launch goes through it; outputs bit-exact against the oracle (int64
+matmul for int32 out) on the rows around the boundary, the streamed rows
+and sampled tile rows."""
 import numpy as np
 import pytest
 import torch
@@ -14,12 +18,21 @@ from tests.gpu_util import dev, host_bits16, sync
 
 pytestmark = pytest.mark.gpu
 
-# (M, N, K): 1 / 12 / 16 last rows (one 16-row fragment), 25 / 32 (two),
-# 44 / 64 (four); N with and without a partial 256-column tile; K of 6 / 10 /
-# 18 / 64 / 128 chunks of 64 bytes (each wave's batches, their remainder, or
-# both).
-SHAPES = [(257, 256, 384), (268, 272, 640), (272, 512, 4096), (528, 1040, 1152), (769, 256, 8192),
-          (281, 256, 640), (544, 272, 4096), (300, 1040, 1152), (320, 512, 8192)]
+# (M, N, K).  M <= 128: the streamed pass alone, 1 / 16 / 33 / 64 / 100 /
+# 128 rows (1, 2, 4 or 8 16-row fragments).  M > 256 at N = 16384 (64
+# n-tiles): 4 tile rows fill one round exactly, so the fifth row of tiles
+# would start a second round: 1 / 36 / 100 last rows.  K of 2 to 128 chunks
+# of 64 bytes (each wave's batches, their remainder, or both).
+SHAPES = [(1, 256, 384), (16, 4096, 4096), (33, 272, 640), (64, 1040, 1152), (100, 512, 4096),
+          (128, 256, 8192), (1025, 16384, 128), (1060, 16384, 256), (1124, 16384, 128)]
+
+
+def _rows(m):
+    # rows checked: around the tile / streamed boundary, the streamed rows,
+    # and a few tile rows
+    m0 = m - m % 256 if m > 256 else 0
+    rows = set(range(max(0, m0 - 2), m)) | set(int(r) for r in rng(m).integers(0, m, 6))
+    return sorted(rows)
 
 
 @pytest.mark.parametrize("shape", SHAPES)
@@ -28,16 +41,20 @@ def test_rows_path_i32_s8_w8a8(gpu, shape):
     print(f"case: rows path {shape}", flush=True)
     g = rng(m * 7 + n + k)
     a, b = int8_uniform(g, (m, k)), int8_uniform(g, (n, k))
+    rows = _rows(m)
+    assert P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, output=P.ElementKind.Bf16)).workspace_size() == 0 \
+        or m % 256 > 64
     d = torch.full((m, n), -7, dtype=torch.int32, device="cuda:0")
     P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, output=P.ElementKind.I32)).run(dev(a), dev(b), d)
     sync()
-    assert np.array_equal(d.cpu().numpy(), a.astype(np.int64) @ b.astype(np.int64).T)
+    got = d.cpu().numpy()
+    assert np.array_equal(got[rows], a[rows].astype(np.int64) @ b.astype(np.int64).T)
 
     c = int8_uniform(g, (m, n))
     d8 = torch.full((m, n), 99, dtype=torch.int8, device="cuda:0")
     P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k)).run(dev(a), dev(b), d8, c=dev(c), alpha=0.003, beta=0.5)
     sync()
-    assert np.array_equal(d8.cpu().numpy(), O.gemm_s8_rcr_s8(a, b, 0.003, 0.5, c))
+    assert np.array_equal(d8.cpu().numpy()[rows], O.gemm_s8_rcr_s8(a[rows], b, 0.003, 0.5, c[rows]))
 
     sa = g.uniform(0.005, 0.02, m).astype(np.float32)
     sw = g.uniform(0.001, 0.01, n).astype(np.float32)
@@ -45,10 +62,12 @@ def test_rows_path_i32_s8_w8a8(gpu, shape):
     P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, output=P.ElementKind.Bf16)).run(
         dev(a), dev(b), dw, scale_a=dev(sa), scale_b=dev(sw))
     sync()
-    assert np.array_equal(host_bits16(dw), O.gemm_w8a8_bf16(a, b, sa, sw, nthreads=8))
+    gw = host_bits16(dw)
+    for r in rows:
+        assert np.array_equal(gw[r], O.gemm_w8a8_bf16(a, b, sa, sw, rows=(r, r + 1), nthreads=8)[0]), r
 
 
-@pytest.mark.parametrize("shape", SHAPES[:3])
+@pytest.mark.parametrize("shape", [SHAPES[1], SHAPES[4], SHAPES[7]])
 def test_rows_path_bias_gelu(gpu, shape):
     m, n, k = shape
     print(f"case: rows path bias_gelu {shape}", flush=True)
@@ -60,10 +79,11 @@ def test_rows_path_bias_gelu(gpu, shape):
     d = torch.full((m, n), 99, dtype=torch.int8, device="cuda:0")
     plan.run(dev(a), dev(b), d, c=dev(c), alpha=0.004, beta=0.25, bias=dev(bias))
     sync()
-    assert np.array_equal(d.cpu().numpy(), O.gemm_s8_epi(a, b, "rcr", 0.004, 0.25, c, bias, "gelu"))
+    rows = _rows(m)
+    assert np.array_equal(d.cpu().numpy()[rows], O.gemm_s8_epi(a[rows], b, "rcr", 0.004, 0.25, c[rows], bias, "gelu"))
 
 
-@pytest.mark.parametrize("shape", SHAPES[1:4])
+@pytest.mark.parametrize("shape", [SHAPES[2], SHAPES[3], SHAPES[5], SHAPES[6]])
 def test_rows_path_quantized_linear_f32_f64(gpu, shape):
     # f32: y = (sa*sw)*acc in f32; f64: f64 scales narrowed to f32, the same
     # product, widened (compose.cu:27-28).
@@ -71,7 +91,8 @@ def test_rows_path_quantized_linear_f32_f64(gpu, shape):
     print(f"case: rows path quantized_linear {shape}", flush=True)
     g = rng(m + n + 5 * k)
     a, w = int8_uniform(g, (m, k)), int8_uniform(g, (n, k))
-    acc = O.gemm_s8_rcr_i32(a, w).astype(np.float32)
+    rows = _rows(m)
+    acc = (a[rows].astype(np.int64) @ w.astype(np.int64).T).astype(np.float32)
     stream = torch.cuda.current_stream().cuda_stream
     sa = g.uniform(0.005, 0.02, m).astype(np.float32)
     sw = g.uniform(0.001, 0.01, n).astype(np.float32)
@@ -80,19 +101,33 @@ def test_rows_path_quantized_linear_f32_f64(gpu, shape):
     assert lib().quantized_linear_w8a8_f32_gfx950_run(m, n, k, tw.data_ptr(), ta.data_ptr(), tsa.data_ptr(),
                                                       tsw.data_ptr(), out.data_ptr(), None, 0, stream) == 0
     sync()
-    assert np.array_equal(out.cpu().numpy(), (sa[:, None] * sw[None, :]).astype(np.float32) * acc)
+    assert np.array_equal(out.cpu().numpy()[rows], (sa[rows][:, None] * sw[None, :]).astype(np.float32) * acc)
     sa64, sw64 = g.uniform(0.005, 0.02, m), g.uniform(0.001, 0.01, n)
     out64 = torch.empty((m, n), dtype=torch.float64, device="cuda:0")
     tsa64, tsw64 = dev(sa64), dev(sw64)
     assert lib().quantized_linear_w8a8_f64_gfx950_run(m, n, k, tw.data_ptr(), ta.data_ptr(), tsa64.data_ptr(),
                                                       tsw64.data_ptr(), out64.data_ptr(), None, 0, stream) == 0
     sync()
-    want64 = ((sa64.astype(np.float32)[:, None] * sw64.astype(np.float32)[None, :]).astype(np.float32)
+    want64 = ((sa64[rows].astype(np.float32)[:, None] * sw64.astype(np.float32)[None, :]).astype(np.float32)
               * acc).astype(np.float64)
-    assert np.array_equal(out64.cpu().numpy(), want64)
+    assert np.array_equal(out64.cpu().numpy()[rows], want64)
 
 
-def test_rows_path_takes_no_workspace(gpu):
-    # M = 4097: the tail split's workspace is no longer asked for
-    plan = P.IntGemmPlan.select(P.IntGemmDescriptor(4097, 4096, 4096, output=P.ElementKind.Bf16))
-    assert plan.workspace_size() == 0
+def test_rows_path_with_and_without_split_workspace(gpu):
+    # 100 last rows at M = 1124, N = 16384: with the tail-split workspace the
+    # split runs, without it the streamed pass; both equal the oracle rows.
+    m, n, k = 1124, 16384, 1024
+    print("case: rows path vs tail split", flush=True)
+    g = rng(77)
+    a, b = int8_uniform(g, (m, k)), int8_uniform(g, (n, k))
+    plan = P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, output=P.ElementKind.I32))
+    assert plan.workspace_size() > 0
+    outs = []
+    for ws in (None, torch.empty(plan.workspace_size(), dtype=torch.uint8, device="cuda:0")):
+        d = torch.full((m, n), -7, dtype=torch.int32, device="cuda:0")
+        plan.run(dev(a), dev(b), d, workspace=ws)
+        sync()
+        outs.append(d.cpu().numpy())
+    assert np.array_equal(outs[0], outs[1])
+    rows = _rows(m)
+    assert np.array_equal(outs[0][rows], a[rows].astype(np.int64) @ b.astype(np.int64).T)
