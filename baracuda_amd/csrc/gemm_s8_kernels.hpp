@@ -1057,7 +1057,6 @@ void launch_kernel(const S8Args &p, bool fast_k, hipStream_t stream, void *works
 template <int EPI, int ACT = ACT_NONE, typename BiasT = float>
 int32_t launch(const S8Args &p, hipStream_t stream, void *workspace = nullptr, size_t workspace_bytes = 0) {
     const int out_elem = (EPI == EPI_I32 || EPI == EPI_W8A8_F32) ? 4 : EPI == EPI_W8A8_F64 ? 8 : (EPI == EPI_S8 ? 1 : 2);
-    // The DMA path needs whole 256x256 tiles, whole K stages and 16-byte rows.
     // The DMA path needs whole K stages and 16-byte rows; edge tiles read
     // zeros past the operands, so the byte offsets of the padded extents
     // must stay below 2^31.
