@@ -34,6 +34,10 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{ROOT / 'include'}", f"-I{CSRC}",
 ]
+# Size of the allocation-free u8 RRR entry point's device array, which every
+# process that loads the library holds on each GPU it uses (default 64 MiB).
+if os.environ.get("BK_NOALLOC_SCRATCH_MIB"):
+    HIP_FLAGS.insert(-2, f"-DBARACUDA_U8_RRR_NOALLOC_SCRATCH_BYTES=((size_t){int(os.environ['BK_NOALLOC_SCRATCH_MIB'])}<<20)")
 
 
 def _compile(src: Path) -> Path:

@@ -206,17 +206,23 @@ __device__ __forceinline__ uint32_t u8_sum16(const v4i &f, uint32_t acc) {
 }
 
 
-// Round half to even to int32, then clamp (the reference's
-// __float2int_rn + max / min, baracuda_dtype.cuh:23-36): rint, v_cvt_i32_f32
-// (saturating; NaN converts to 0) and one v_med3_i32.
+// Round half to even, clamp, convert (the reference's __float2int_rn + max /
+// min, baracuda_dtype.cuh:23-36).  The clamp happens in float before the
+// conversion, so the conversion is always of an in-range integral value and
+// its result is defined by the language; NaN is mapped to 0 explicitly.
+// rint, a NaN select, one v_med3_f32 and the conversion.
+__device__ __forceinline__ float rne_clamp(float x, float lo, float hi) {
+    float r = __builtin_rintf(x);
+    r = (r == r) ? r : 0.0f;
+    return __builtin_amdgcn_fmed3f(r, lo, hi);
+}
+
 __device__ __forceinline__ uint8_t sat_cast_u8(float x) {
-    const int r = (int)__builtin_rintf(x);
-    return (uint8_t)min(max(r, 0), 255);
+    return (uint8_t)(int)rne_clamp(x, 0.0f, 255.0f);
 }
 
 __device__ __forceinline__ int8_t sat_cast_s8(float x) {
-    const int r = (int)__builtin_rintf(x);
-    return (int8_t)min(max(r, -128), 127);
+    return (int8_t)(int)rne_clamp(x, -128.0f, 127.0f);
 }
 
 }  // namespace bk

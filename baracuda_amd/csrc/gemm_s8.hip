@@ -68,6 +68,7 @@ int32_t baracuda_kernels_gemm_s8_rcr_gfx950_run(
     if (!a || !b || !d) return kInvalid;
     S8Args p{m, n, k, (const int8_t *)a, lda, (const int8_t *)b, ldb, (const int8_t *)c, ldc, d, ldd,
              alpha, beta, nullptr, nullptr, nullptr};
+    rcr_c_defaults_to_d(p);
     return launch<EPI_S8>(p, (hipStream_t)stream, workspace, workspace_bytes);
 }
 

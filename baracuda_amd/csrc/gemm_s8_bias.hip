@@ -46,6 +46,7 @@ extern "C" {
         if (!a || !b || !d || !bias) return kInvalid;                                                \
         S8Args p{m, n, k, (const int8_t *)a, lda, (const int8_t *)b, ldb, (const int8_t *)c, ldc, d, \
                  ldd, alpha, beta, nullptr, nullptr, bias};                                          \
+        rcr_c_defaults_to_d(p);                                                                      \
         return launch<EPI_S8, ACTV, BTY>(p, (hipStream_t)stream, workspace, workspace_bytes);        \
     }
 

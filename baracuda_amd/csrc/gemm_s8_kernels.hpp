@@ -38,6 +38,19 @@ struct S8Args {
     const void *bias;   // [N] f32 or i32, for ACT != ACT_NONE
 };
 
+// The RCR SKUs take the CUTLASS contract for a null C: the source operand is
+// D itself with D's pitch, so beta != 0 accumulates into D in place
+// (gemm_s8_rcr_sm80.cu:87-89, gemm_u8_rcr_sm80.cu:77-79,
+// gemm_s8_rcr_sm80_bias.cu:110-111).  Every output element's C read is made
+// by the thread that stores it and feeds that store, so in place is safe.
+// The RRR SKUs keep their own contract (null C: no beta term).
+inline void rcr_c_defaults_to_d(S8Args &p) {
+    if (p.c == nullptr) {
+        p.c = static_cast<const int8_t *>(p.d);
+        p.ldc = p.ldd;
+    }
+}
+
 // Epilogue on one group of 4 consecutive output columns of row m.
 template <int EPI, bool VecOut, int ACT = ACT_NONE, typename BiasT = float>
 struct S8Epilogue {

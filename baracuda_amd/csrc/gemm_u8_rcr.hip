@@ -46,6 +46,7 @@ int32_t baracuda_kernels_gemm_u8_rcr_gfx950_run(
     if (!a || !b || !d) return kInvalid;
     S8Args p{m, n, k, (const int8_t *)a, lda, (const int8_t *)b, ldb, (const int8_t *)c, ldc, d, ldd,
              alpha, beta, nullptr, nullptr, nullptr};
+    rcr_c_defaults_to_d(p);
     return launch_u8_rcr<ACT_NONE, float>(p, (hipStream_t)stream);
 }
 
@@ -74,6 +75,7 @@ int32_t baracuda_kernels_gemm_u8_rcr_gfx950_run(
         if (!a || !b || !d || !bias) return kInvalid;                                                \
         S8Args p{m, n, k, (const int8_t *)a, lda, (const int8_t *)b, ldb, (const int8_t *)c, ldc, d, \
                  ldd, alpha, beta, nullptr, nullptr, bias};                                          \
+        rcr_c_defaults_to_d(p);                                                                      \
         return launch_u8_rcr<ACTV, BTY>(p, (hipStream_t)stream);                                     \
     }
 

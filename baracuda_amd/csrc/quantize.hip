@@ -51,12 +51,10 @@ __device__ __forceinline__ float block_max(float v, float *red) {
     return m;
 }
 
-// clamp(round_half_even(v * inv), qmin, qmax): the round-trip through int32
-// (v_cvt_i32_f32, saturating, NaN -> 0) and an integer clamp (v_med3_i32)
-// give the same result as clamping the rounded float for every input.
-__device__ __forceinline__ int8_t quant1(float v, float inv, int qmin, int qmax) {
-    const int r = (int)__builtin_rintf(v * inv);
-    return (int8_t)min(max(r, qmin), qmax);
+// clamp(round_half_even(v * inv), qmin, qmax), the clamp in float before the
+// conversion (rne_clamp: NaN -> 0, no out-of-range conversion).
+__device__ __forceinline__ int8_t quant1(float v, float inv, float qmin, float qmax) {
+    return (int8_t)(int)rne_clamp(v * inv, qmin, qmax);
 }
 
 // T: element type of x; S: type of the scale output.
@@ -66,6 +64,7 @@ __global__ __launch_bounds__(kQBlock) void quantize_per_token_kernel(
     int qmin, int qmax) {
     __shared__ float red[kQBlock / 64];
     const float fqmax = (float)qmax;
+    const float fqmin = (float)qmin;
     for (int n = blockIdx.x; n < N; n += gridDim.x) {
         const T *row = x + (int64_t)n * D;
         int8_t *qrow = q + (int64_t)n * D;
@@ -91,11 +90,11 @@ __global__ __launch_bounds__(kQBlock) void quantize_per_token_kernel(
 #pragma unroll
             for (int i = 0; i < kQMaxPerThread; ++i) {
                 const int e = threadIdx.x + kQBlock * i;
-                if (e < D) qrow[e] = quant1(vals[i], inv, qmin, qmax);
+                if (e < D) qrow[e] = quant1(vals[i], inv, fqmin, fqmax);
             }
         } else {
             for (int e = threadIdx.x; e < D; e += kQBlock)
-                qrow[e] = quant1(QIn<T>::ld(row + e), inv, qmin, qmax);
+                qrow[e] = quant1(QIn<T>::ld(row + e), inv, fqmin, fqmax);
         }
         __syncthreads();   // `red` is reused by the next row
     }
@@ -113,6 +112,7 @@ __global__ __launch_bounds__(kQBlock) void quantize_per_token_bf16v_kernel(
     int qmin, int qmax) {
     __shared__ float red[kQBlock / 64];
     const float fqmax = (float)qmax;
+    const float fqmin = (float)qmin;
     const int nch = D >> 3;
     for (int n = blockIdx.x; n < N; n += gridDim.x) {
         const v4i *row = reinterpret_cast<const v4i *>(x + (int64_t)n * D);
@@ -142,8 +142,8 @@ __global__ __launch_bounds__(kQBlock) void quantize_per_token_bf16v_kernel(
 #pragma unroll
             for (int h = 0; h < 4; ++h) {
                 const uint32_t u = (uint32_t)w[i][h];
-                const uint32_t q0 = (uint8_t)quant1(__uint_as_float(u << 16), inv, qmin, qmax);
-                const uint32_t q1 = (uint8_t)quant1(__uint_as_float(u & 0xffff0000u), inv, qmin, qmax);
+                const uint32_t q0 = (uint8_t)quant1(__uint_as_float(u << 16), inv, fqmin, fqmax);
+                const uint32_t q1 = (uint8_t)quant1(__uint_as_float(u & 0xffff0000u), inv, fqmin, fqmax);
                 const uint32_t pair = q0 | (q1 << 8);
                 if (h < 2) lo |= pair << (16 * h);
                 else hi |= pair << (16 * (h - 2));

@@ -287,8 +287,8 @@ class IntGemmPlan:
         self.can_implement(a, b, d, c, bias)
         desc, L, s = self.desc, lib(), _stream(stream)
         if desc.output in (ElementKind.S8, ElementKind.U8):
-            if c is None:
-                beta = 0.0
+            # beta is passed as given: with c None the RCR SKUs read D in place
+            # (CUTLASS, gemm_s8_rcr_sm80.cu:87-89), the RRR SKUs skip the term.
             args = [desc.m, desc.n, desc.k, _ptr(a), _ld(a), _ptr(b), _ld(b),
                     _ptr(c), _ld(c) if c is not None else 0, _ptr(d), _ld(d)]
             if desc.epilogue != EpilogueKind.Identity:

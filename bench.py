@@ -181,6 +181,15 @@ class ClockSampler:
         self._stop.set()
         if self._thr.is_alive():
             self._thr.join()
+        if self._h is not None:
+            # release the library's handles on the device, so nothing of the
+            # sampler outlives the measurement
+            try:
+                import amdsmi
+                amdsmi.amdsmi_shut_down()
+            except Exception:   # noqa: BLE001 -- telemetry only
+                pass
+            self._h = None
         return False
 
     def summary(self):
@@ -314,8 +323,29 @@ def cpu_baselines_extra(budget_s=4.0):
         dt = (time.perf_counter() - t0) / reps
         gr[f"n{nr}"] = {"us": round(dt * 1e6, 2), "threads": 1}
     out["gather_rows_bf16_128256x4096"] = gr
-    out["note"] = ("W8A8 is the headline cpu_baseline; the grouped MoE config is not sampled "
-                   "(its 470 MB expert slab dominates host set-up time)")
+    # config 5 (grouped int8 MoE, E=8, top-2, 4096 tokens, N=14336, K=4096):
+    # 64 of the 8192 routed pairs, evenly spaced over the expert-sorted order
+    # (so every expert with rows is sampled in proportion), through the
+    # oracle's grouped restatement (bo_moe_s8_grouped_i32, serial); each
+    # sampled pair's token row is gathered first so the sample's output has
+    # 64 rows instead of 8192.
+    from oracle.inputs import moe_routing
+    E, n, k, tokens, topk = 8, 14336, 4096, 4096, 2
+    sid, eid = moe_routing(tokens, E, topk, seed=5)
+    x = int8_uniform(g, (tokens, k))
+    wm = int8_uniform(g, (E, n, k))
+    pick = np.linspace(0, sid.size - 1, 64).astype(np.int64)
+    xs = np.ascontiguousarray(x[sid[pick] // topk])
+    _, offs = O.moe_expert_offsets(eid[pick], E)
+    t0 = time.perf_counter()
+    O.moe_s8_grouped_i32(xs, wm, np.arange(64, dtype=np.int32), offs, 1, 64)
+    dt = time.perf_counter() - t0
+    out["moe_s8_grouped_e8_top2_8192x14336x4096"] = {
+        "s": round(dt, 3), "sample_pairs": 64, "experts_sampled": int(np.count_nonzero(np.diff(offs))),
+        "TOPS": round(2.0 * 64 * n * k / dt / 1e12, 6), "threads": 1,
+        "extrapolated_full_s": round(dt * sid.size / 64, 1)}
+    del x, wm
+    out["note"] = "W8A8 is the headline cpu_baseline"
     return out
 
 

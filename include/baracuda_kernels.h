@@ -47,7 +47,10 @@ extern "C" {
 /* Replaces baracuda_kernels_gemm_s8_rcr_sm80_{run,workspace_size,can_implement}
  * (crates/baracuda-kernels-sys/src/cutlass_reexport.rs:661-666,
  *  crates/baracuda-cutlass-kernels-sys/kernels/gemm_s8_rcr_sm80.cu:169-198):
- * D = sat_s8(rne(alpha*acc + beta*C)); C may be NULL when beta == 0. */
+ * D = sat_s8(rne(alpha*acc + beta*C)).  A NULL C means C = D with ldc = ldd
+ * (the CUTLASS kernel's c_eff, gemm_s8_rcr_sm80.cu:87-89): beta != 0 then
+ * accumulates into D in place.  The same holds for the RCR bias family and
+ * the u8 RCR SKUs below; the RRR SKUs skip the beta term for a NULL C. */
 int32_t baracuda_kernels_gemm_s8_rcr_gfx950_run(
     int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,
     const void *c, int64_t ldc, void *d, int64_t ldd, float alpha, float beta,
@@ -139,7 +142,7 @@ BK_S8_RCR_BIAS_DECL(bias_silu, i32bias)
  *  crates/baracuda-kernels-sys/src/cutlass_reexport.rs:669-676) and
  * baracuda_kernels_gemm_{bias,bias_relu,bias_gelu,bias_silu}_{f32bias,i32bias}_u8_rcr_sm80_*
  * (gemm_u8_rcr_sm80_bias.cu; cutlass_reexport.rs:1062-1096, 1141-1176).
- * Workspace 0. */
+ * Workspace 0.  A NULL C reads D in place (gemm_u8_rcr_sm80.cu:77-79). */
 int32_t baracuda_kernels_gemm_u8_rcr_gfx950_run(
     int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,
     const void *c, int64_t ldc, void *d, int64_t ldd, float alpha, float beta,
@@ -280,7 +283,16 @@ int32_t baracuda_kernels_gemm_u8_rrr_gfx950_can_implement(
  * array, so calls that overlap on one GPU (different streams, or host
  * threads) race -- serialise them.  Results are identical to
  * baracuda_kernels_gemm_u8_rrr_gfx950_run. */
+/* The array is part of the library's code object: every process that loads
+ * the library holds this many bytes of device memory on each GPU it uses,
+ * whether or not it calls this entry point.  A build may set another size
+ * with -DBARACUDA_U8_RRR_NOALLOC_SCRATCH_BYTES=<bytes> (BK_NOALLOC_SCRATCH_MIB
+ * for baracuda_amd/build.py).  The array's device address is looked up once
+ * per device and kept: hipDeviceReset is not supported while the library is
+ * loaded. */
+#ifndef BARACUDA_U8_RRR_NOALLOC_SCRATCH_BYTES
 #define BARACUDA_U8_RRR_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+#endif
 int32_t baracuda_kernels_gemm_u8_rrr_gfx950_noalloc_run(
     int32_t m, int32_t n, int32_t k, const void *a, int64_t lda, const void *b, int64_t ldb,
     const void *c, int64_t ldc, void *d, int64_t ldd, float alpha, float beta, void *stream);

@@ -300,3 +300,41 @@ def test_s8_saturation_of_non_finite_and_huge_bias(gpu, layout):
         got = _run(layout, P.EpilogueKind.Bias, P.ElementKind.F32, a, b, bias=bias, alpha=1e-9)
         want_col = np.array([127, -128, 0, 127, -128, 0], np.int8)[np.arange(n) % 6]
         assert np.array_equal(got, np.broadcast_to(want_col, (m, n))), (m, n, k)
+
+
+@pytest.mark.parametrize("elem", [P.ElementKind.S8, P.ElementKind.U8])
+@pytest.mark.parametrize("epi", [P.EpilogueKind.Identity, P.EpilogueKind.BiasRelu])
+@pytest.mark.parametrize("layout", [RCR, RRR])
+@pytest.mark.parametrize("shape", [(512, 512, 256), (300, 520, 200), (1, 256, 4096), (4097, 256, 256)])
+def test_null_c_with_beta(gpu, shape, layout, epi, elem):
+    # C = NULL with beta != 0.  RCR follows the CUTLASS contract of the
+    # reference (gemm_s8_rcr_sm80.cu:87-89, gemm_u8_rcr_sm80.cu:77-79): the
+    # source operand is D itself, so the GEMM accumulates into D in place.
+    # RRR follows its bespoke kernel (baracuda_int8_rrr_sm80.cuh:274): no
+    # beta term.  Shapes reach the whole-tile DMA kernel, the general kernel
+    # (K tail), the last-rows pass (M = 1) and tiles plus last rows (4097).
+    m, n, k = shape
+    u8 = elem == P.ElementKind.U8
+    print(f"case: null C {layout.value} {epi.value} {elem.value} {shape}", flush=True)
+    g = rng(m + 3 * n + 5 * k + (7 if u8 else 0))
+    if u8:
+        a = g.integers(0, 256, (m, k), dtype=np.uint8)
+        b = _u8_b(g.integers(0, 256, k * n, dtype=np.uint8), k, n, layout)
+        d0 = g.integers(0, 256, (m, n), dtype=np.uint8)
+        alpha = 1.0 / (64.0 * k)
+    else:
+        a = int8_uniform(g, (m, k))
+        b = int8_uniform(g, (k, n)) if layout == RRR else int8_uniform(g, (n, k))
+        d0 = int8_uniform(g, (m, n))
+        alpha = 1.0 / (16.0 * np.sqrt(k))
+    bias = (g.standard_normal(n) * 8).astype(np.float32)
+    plan = P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, layout=layout, epilogue=epi,
+                                                    bias_element=P.ElementKind.F32, element=elem, output=elem))
+    d = dev(d0)
+    plan.run(dev(a), dev(b), d, c=None, alpha=alpha, beta=0.5,
+             bias=None if epi == P.EpilogueKind.Identity else dev(bias))
+    sync()
+    f = O.gemm_u8_epi if u8 else O.gemm_s8_epi
+    want = f(a, b, _LNAME[layout], alpha, 0.5, d0 if layout == RCR else None,
+             None if epi == P.EpilogueKind.Identity else bias, ACT[epi])
+    _check(d.cpu().numpy(), want, epi)
