@@ -14,6 +14,8 @@
 //   output row of pair p      = sorted_token_ids[p]
 //   int8:      out[row, n] = bf16( ((sa[in_row] * sw[e*N + n]) * acc) [* topk_weights[row]] )
 //   bf16/f16:  out[row, n] = T( acc [* topk_weights[row]] )   (baracuda_moe.cuh:929-941)
+//   int8, i32: out[row, n] = acc (int32), the accumulator the W8A8 SKU
+//              dequantizes: same kernel, same mainloop, no epilogue arithmetic
 //
 // Differences by design: expert offsets are computed by one workgroup with
 // LDS counters (no global atomics, no memset: graph-capturable), and the GEMM
@@ -79,13 +81,15 @@ __global__ __launch_bounds__(1024) void moe_offsets_kernel(const int32_t *__rest
     }
 }
 
-// Operand kinds: int8 (W8A8 epilogue), bf16, f16 (16-bit float elements).
-enum MoeKind : int { MOE_S8 = 0, MOE_BF16 = 1, MOE_F16 = 2 };
+// Operand kinds: int8 (W8A8 epilogue), bf16, f16 (16-bit float elements),
+// int8 with the int32 accumulator as output.
+enum MoeKind : int { MOE_S8 = 0, MOE_BF16 = 1, MOE_F16 = 2, MOE_S8_I32 = 3 };
 
 template <int KIND> struct MoeElem;
 template <> struct MoeElem<MOE_S8> { static constexpr Elem E = Elem::S8; static constexpr int SIZE = 1; };
 template <> struct MoeElem<MOE_BF16> { static constexpr Elem E = Elem::BF16; static constexpr int SIZE = 2; };
 template <> struct MoeElem<MOE_F16> { static constexpr Elem E = Elem::F16; static constexpr int SIZE = 2; };
+template <> struct MoeElem<MOE_S8_I32> { static constexpr Elem E = Elem::S8; static constexpr int SIZE = 1; };
 
 struct MoeArgs {
     const int8_t *x;            // [tokens, K] elements (bytes addressed)
@@ -95,7 +99,7 @@ struct MoeArgs {
     const float *topk_w;        // [size_m] or nullptr
     const float *sa;            // [tokens]   (int8 only)
     const float *sw;            // [E, N]     (int8 only)
-    uint16_t *out;              // [size_m, N] bf16 / f16
+    void *out;                  // [size_m, N] bf16 / f16 (int32 for MOE_S8_I32)
     int E, topk, size_m, N, K;  // K in elements
 };
 
@@ -146,7 +150,21 @@ __device__ __forceinline__ void moe_store(const MoeArgs &p, const int32_t *rows_
 #pragma unroll
         for (int r = 0; r < 4; ++r) y[r] = y[r] * tw;
     }
-    store4_bf16(p.out + (int64_t)tok * p.N + n0, y, count == 4 && (p.N % 4 == 0), count);
+    store4_bf16(static_cast<uint16_t *>(p.out) + (int64_t)tok * p.N + n0, y, count == 4 && (p.N % 4 == 0),
+                count);
+}
+
+// int32 accumulator out, one group of 4 columns of tile row ml.
+__device__ __forceinline__ void moe_store_i32(const MoeArgs &p, const int32_t *rows_tok, int seg_rows, int ml,
+                                              int n0, const v4i &v) {
+    if (ml >= seg_rows || n0 >= p.N) return;
+    int32_t *d = static_cast<int32_t *>(p.out) + (int64_t)rows_tok[ml] * p.N + n0;
+    const int count = p.N - n0 < 4 ? p.N - n0 : 4;
+    if (count == 4 && (reinterpret_cast<uintptr_t>(d) & 15u) == 0) {
+        *reinterpret_cast<v4i *>(d) = v;
+    } else {
+        for (int r = 0; r < count; ++r) d[r] = v[r];
+    }
 }
 
 // bf16 / f16 epilogue of one group of 4 columns: out = T(acc [* topk_w]).
@@ -163,7 +181,7 @@ __device__ __forceinline__ void moe_store_h(const MoeArgs &p, const int32_t *row
         const float y = p.topk_w ? v[r] * tw : v[r];
         h[r] = KIND == MOE_BF16 ? f32_to_bf16_rne(y) : f32_to_f16_rne(y);
     }
-    uint16_t *d = p.out + (int64_t)tok * p.N + n0;
+    uint16_t *d = static_cast<uint16_t *>(p.out) + (int64_t)tok * p.N + n0;
     if (count == 4 && (reinterpret_cast<uintptr_t>(d) & 7u) == 0) {
         *reinterpret_cast<v2i *>(d) = v2i{(int)((uint32_t)h[0] | ((uint32_t)h[1] << 16)),
                                           (int)((uint32_t)h[2] | ((uint32_t)h[3] << 16))};
@@ -201,6 +219,10 @@ __global__ __launch_bounds__(NT, 1) void moe_grouped_kernel(MoeArgs p) {
         const float *swe = p.sw + (int64_t)e * p.N;
         for_each_fragment(acc, [&](int ml, int nl, const v4i &v) {
             moe_store(p, s_rows_tok, seg_rows, in_div, swe, ml, n_base + nl, v);
+        });
+    } else if constexpr (KIND == MOE_S8_I32) {
+        for_each_fragment(acc, [&](int ml, int nl, const v4i &v) {
+            moe_store_i32(p, s_rows_tok, seg_rows, ml, n_base + nl, v);
         });
     } else {
         for_each_fragment(acc, [&](int ml, int nl, const v4f &v) {
@@ -294,7 +316,7 @@ __device__ __forceinline__ bool moe_dma_coords(const MoeArgs &p, const int32_t *
     return true;
 }
 
-template <int KIND> struct MoePolicy { typedef mfma2::PolicyI8<DmaCfg> type; };
+template <int KIND> struct MoePolicy { typedef mfma2::PolicyI8<DmaCfg> type; };   // MOE_S8, MOE_S8_I32
 template <> struct MoePolicy<MOE_BF16> { typedef mfma2::PolicyH16<DmaCfg, true> type; };
 template <> struct MoePolicy<MOE_F16> { typedef mfma2::PolicyH16<DmaCfg, false> type; };
 
@@ -332,7 +354,21 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void moe_grouped_dma_kernel(MoeArgs 
     }
     M2::AccTile<P> acc;
     M2::mainloop<P>(stage0, stage1, d, kb, acc);
-    if constexpr (KIND != MOE_S8) {
+    if constexpr (KIND == MOE_S8_I32) {
+        // int32 rows staged per wave in two halves of 64 rows and written as
+        // 16-byte units of the pair's output row; padding rows are skipped.
+        const int wave = threadIdx.x >> 6;
+        const int wr = (wave / DmaCfg::WAVES_N) * DmaCfg::WM;
+        const int wc = n_base + (wave % DmaCfg::WAVES_N) * DmaCfg::WN;
+        int8_t *scratch = (wave < 4 ? stage0 : stage1) + (wave & 3) * (DmaCfg::WM / 2 * 256);
+        M2::store_x32x4_staged<P>(
+            acc, scratch, [&](int, int, const v4i &v) { return v; },
+            [&](int r) -> int32_t * {
+                return wr + r < seg_rows ? static_cast<int32_t *>(p.out) + (int64_t)s_rows_tok[wr + r] * p.N + wc
+                                         : nullptr;
+            });
+        return;
+    } else if constexpr (KIND != MOE_S8) {
         if ((reinterpret_cast<uintptr_t>(p.out) & 15u) == 0) {
             // Rows staged per wave in LDS and written as 16-byte units of the
             // token's output row; padding rows of a partial tile are skipped.
@@ -354,7 +390,8 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void moe_grouped_dma_kernel(MoeArgs 
                                (int)((uint32_t)h[2] | ((uint32_t)h[3] << 16))};
                 },
                 [&](int r) -> uint16_t * {
-                    return wr + r < seg_rows ? p.out + (int64_t)s_rows_tok[wr + r] * p.N + wc : nullptr;
+                    return wr + r < seg_rows ? static_cast<uint16_t *>(p.out) + (int64_t)s_rows_tok[wr + r] * p.N + wc
+                                             : nullptr;
                 });
             return;
         }
@@ -382,7 +419,8 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void moe_grouped_dma_kernel(MoeArgs 
         for (int j = 0; j < P::TJ; ++j) swv[j] = *reinterpret_cast<const v4f *>(swe + wc + j * 16 + (lane >> 4) * 4);
         int8_t *scratch = (wave < 4 ? stage0 : stage1) + (wave & 3) * (DmaCfg::WM * DmaCfg::WN * 2);
         auto dst = [&](int r) -> uint16_t * {
-            return wr + r < seg_rows ? p.out + (int64_t)s_rows_tok[wr + r] * p.N + wc : nullptr;
+            return wr + r < seg_rows ? static_cast<uint16_t *>(p.out) + (int64_t)s_rows_tok[wr + r] * p.N + wc
+                                     : nullptr;
         };
         if (p.topk_w) M2::store_w8a8_bf16_staged<P, true>(acc, scratch, sam, post, swv, dst);
         else M2::store_w8a8_bf16_staged<P, false>(acc, scratch, sam, post, swv, dst);
@@ -456,13 +494,38 @@ int32_t baracuda_kernels_moe_s8_grouped_bf16_gfx950_run(
                                                                            size_n, size_k);
     if (st != kOk) return st;
     MoeArgs p{(const int8_t *)input, (const int8_t *)weights, sorted_token_ids, expert_offsets,
-              topk_weights, scale_a, scale_w, (uint16_t *)output, num_experts, topk, size_m,
+              topk_weights, scale_a, scale_w, output, num_experts, topk, size_m,
               size_n, size_k};
     // The staged W8A8 epilogue writes 16-byte units of output rows and reads
     // 16-byte groups of column scales.
     return launch_moe<MOE_S8>(p, expert_ids, expert_counts,
                               mfma::aligned16(output) && mfma::aligned16(scale_w),
                               (hipStream_t)stream_ptr);
+}
+
+// int32-accumulator SKU of the grouped int8 MoE (no counterpart in the
+// reference, which has no int8 MoE): the W8A8 SKU's arguments without the
+// scales and topk_weights; input row of pair p = sorted_token_ids[p] / topk,
+// out[sorted_token_ids[p], n] = acc (int32).  It exposes, for a whole-output
+// exact check, the accumulator that the bf16 SKU's epilogue dequantizes.
+int32_t baracuda_kernels_moe_s8_grouped_i32_gfx950_can_implement(
+    int32_t num_experts, int32_t topk, int32_t size_m, int32_t size_n, int32_t size_k) {
+    return baracuda_kernels_moe_s8_grouped_bf16_gfx950_can_implement(num_experts, topk, size_m, size_n, size_k);
+}
+
+int32_t baracuda_kernels_moe_s8_grouped_i32_gfx950_run(
+    const void *input, const void *weights, const int32_t *sorted_token_ids, const int32_t *expert_ids,
+    void *output, int32_t *expert_counts, int32_t *expert_offsets, int32_t num_experts, int32_t topk,
+    int32_t size_m, int32_t size_n, int32_t size_k, void *stream_ptr) {
+    if (!input || !weights || !sorted_token_ids || !expert_ids || !output || !expert_counts || !expert_offsets)
+        return kInvalid;
+    int32_t st = baracuda_kernels_moe_s8_grouped_bf16_gfx950_can_implement(num_experts, topk, size_m,
+                                                                           size_n, size_k);
+    if (st != kOk) return st;
+    MoeArgs p{(const int8_t *)input, (const int8_t *)weights, sorted_token_ids, expert_offsets,
+              nullptr, nullptr, nullptr, output, num_experts, topk, size_m, size_n, size_k};
+    return launch_moe<MOE_S8_I32>(p, expert_ids, expert_counts, mfma::aligned16(output),
+                                  (hipStream_t)stream_ptr);
 }
 
 // Same ABI as baracuda_kernels_moe_wmma_{f16,bf16}_{run,can_implement}
@@ -491,7 +554,7 @@ int32_t baracuda_kernels_moe_s8_grouped_bf16_gfx950_run(
             num_experts, topk, size_m, size_n, size_k);                                            \
         if (st != kOk) return st;                                                                  \
         MoeArgs p{(const int8_t *)input, (const int8_t *)weights, sorted_token_ids, expert_offsets, \
-                  topk_weights, nullptr, nullptr, (uint16_t *)output, num_experts, topk, size_m,   \
+                  topk_weights, nullptr, nullptr, output, num_experts, topk, size_m,               \
                   size_n, size_k};                                                                 \
         return launch_moe<KIND>(p, expert_ids, expert_counts, true, (hipStream_t)stream_ptr);      \
     }

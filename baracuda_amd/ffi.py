@@ -59,6 +59,9 @@ _sig("baracuda_kernels_moe_s8_grouped_bf16_gfx950_run", i32, vp, vp, vp, vp, vp,
      i32, i32, i32, i32, i32, vp, vp, vp, sz, vp)
 _sig("baracuda_kernels_moe_s8_grouped_bf16_gfx950_can_implement", i32, i32, i32, i32, i32, i32)
 _sig("baracuda_kernels_moe_s8_grouped_bf16_gfx950_workspace_size", sz, i32, i32, i32, i32, i32)
+_sig("baracuda_kernels_moe_s8_grouped_i32_gfx950_run", i32, vp, vp, vp, vp, vp, vp, vp,
+     i32, i32, i32, i32, i32, vp)
+_sig("baracuda_kernels_moe_s8_grouped_i32_gfx950_can_implement", i32, i32, i32, i32, i32, i32)
 
 for _t in ("f32", "f64"):
     _sig(f"baracuda_kernels_dynamic_range_quantize_per_token_sym_{_t}_s8_run", i32, i32, i32, i32, i32,

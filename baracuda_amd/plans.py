@@ -599,6 +599,24 @@ class MoeS8GroupedPlan:
             _ptr(scale_a), _ptr(scale_w), _ptr(workspace), _nbytes(workspace), _stream(stream))
         check(st, "MoeS8GroupedPlan::run")
 
+    def run_i32(self, x, w, sorted_token_ids, expert_ids, out, expert_counts, expert_offsets,
+                stream=None) -> None:
+        """The int32-accumulator SKU: out[id, n] = acc (int32 [size_m, N]),
+        input row = id / topk; the same kernel as `run` without its epilogue."""
+        _need(x.dtype == torch.int8 and w.dtype == torch.int8 and out.dtype == torch.int32, "dtypes")
+        _need(w.numel() == self.E * self.n * self.k and x.shape[-1] == self.k, "shapes")
+        _need(x.is_contiguous() and w.is_contiguous() and out.is_contiguous(), "x, w, out contiguous")
+        _need(out.numel() >= self.size_m * self.n, "out too small")
+        _vec(sorted_token_ids, self.size_m, torch.int32, "sorted_token_ids")
+        _vec(expert_ids, self.size_m, torch.int32, "expert_ids")
+        _vec(expert_counts, self.E, torch.int32, "expert_counts")
+        _vec(expert_offsets, self.E + 1, torch.int32, "expert_offsets")
+        st = lib().moe_s8_grouped_i32_gfx950_run(
+            _ptr(x), _ptr(w), _ptr(sorted_token_ids), _ptr(expert_ids), _ptr(out),
+            _ptr(expert_counts), _ptr(expert_offsets), self.E, self.topk, self.size_m, self.n, self.k,
+            _stream(stream))
+        check(st, "MoeS8GroupedPlan::run_i32")
+
 
 # ---- per-token dynamic quantization + quantized_linear ----------------------
 def dynamic_range_quantize_per_token_sym(x, scale, q, qmin=-127, qmax=127, stream=None) -> None:

@@ -523,6 +523,18 @@ int32_t baracuda_kernels_moe_s8_grouped_bf16_gfx950_can_implement(
 size_t baracuda_kernels_moe_s8_grouped_bf16_gfx950_workspace_size(
     int32_t num_experts, int32_t topk, int32_t size_m, int32_t size_n, int32_t size_k);
 
+/* int32-accumulator form of the grouped int8 MoE (no counterpart in the
+ * reference, which has no int8 MoE; for callers that dequantize themselves
+ * and for whole-output exact checks): the bf16 SKU's routing and kernel with
+ * out[id, n] = acc as int32 [size_m, N]; input row = id / topk (no
+ * topk_weights, no scales).  Workspace 0. */
+int32_t baracuda_kernels_moe_s8_grouped_i32_gfx950_run(
+    const void *input, const void *weights, const int32_t *sorted_token_ids,
+    const int32_t *expert_ids, void *output, int32_t *expert_counts, int32_t *expert_offsets,
+    int32_t num_experts, int32_t topk, int32_t size_m, int32_t size_n, int32_t size_k, void *stream);
+int32_t baracuda_kernels_moe_s8_grouped_i32_gfx950_can_implement(
+    int32_t num_experts, int32_t topk, int32_t size_m, int32_t size_n, int32_t size_k);
+
 #ifdef __cplusplus
 }
 #endif

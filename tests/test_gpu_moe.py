@@ -216,3 +216,108 @@ def test_moe_dma_no_valid_rows(gpu):
     sync()
     assert torch.all(counts == 0) and torch.all(offs == 0)
     assert torch.all(out == 3.0)
+
+
+def _moe_i32(x, w, sorted_ids, expert_ids, E, topk, size_m, n, k):
+    out = torch.full((size_m, n), -7, dtype=torch.int32, device="cuda:0")
+    counts = torch.zeros(E, dtype=torch.int32, device="cuda:0")
+    offs = torch.zeros(E + 1, dtype=torch.int32, device="cuda:0")
+    P.MoeS8GroupedPlan.select(E, topk, size_m, n, k).run_i32(
+        x, w, dev(sorted_ids), dev(expert_ids), out, counts, offs)
+    sync()
+    return out
+
+
+@pytest.mark.parametrize("case", ["dma", "general", "boundaries"])
+def test_moe_i32_all_pairs_vs_oracle(gpu, case):
+    # The int32-accumulator SKU against the oracle's grouped restatement
+    # (bo_moe_s8_grouped_i32, baracuda_moe.cuh:1121-1162) on every pair: the
+    # LDS-DMA kernel, the general kernel (N off the 256 grid, K tail) and
+    # last tiles of 1 / 128 / 129 rows with an empty expert.
+    print(f"case: moe i32 {case}", flush=True)
+    if case == "dma":
+        tokens, E, topk, n, k = 700, 8, 2, 512, 384
+        sorted_ids, expert_ids = moe_routing(tokens, E, topk, seed=9)
+    elif case == "general":
+        tokens, E, topk, n, k = 300, 8, 3, 272, 200
+        sorted_ids, expert_ids = moe_routing(tokens, E, topk, seed=6)
+    else:
+        tokens, (sorted_ids, expert_ids) = _block_routing([257, 128, 0, 129, 256], seed=12)
+        E, topk, n, k = 5, 1, 512, 256
+    size_m = tokens * topk
+    g = rng(size_m + n)
+    x, w = int8_uniform(g, (tokens, k)), int8_uniform(g, (E, n, k))
+    got = _moe_i32(dev(x), dev(w), sorted_ids, expert_ids, E, topk, size_m, n, k).cpu().numpy()
+    _, offs = O.moe_expert_offsets(expert_ids, E)
+    want = O.moe_s8_grouped_i32(x, w, sorted_ids, offs, topk, size_m)
+    assert np.array_equal(got, want)
+
+
+def test_moe_config5_i32_whole_output_exact_and_bf16_epilogue(gpu):
+    # BASELINE.json config 5 (8 experts, 4096 tokens top-2 Zipf(1.1), N 14336,
+    # K 4096) through the int32 SKU, over all 8192 x 14336 accumulators:
+    #  - every pair's row sum equals x[t] . sum_n W[e][n, :] exactly and, per
+    #    expert, every column sum over its pairs equals W[e] . sum_t x[t]
+    #    exactly (int64 on the left; f64 on the right, exact since every
+    #    partial sum is an integer below 2^53);
+    #  - one pair in every (expert, 256-row tile), and the last pair of every
+    #    expert's last (partial) tile, equal int64 dot products in full;
+    #  - the bf16 SKU's whole output equals bf16_rne((sa[t] * sw[e, n]) *
+    #    f32(acc)) bit for bit (its epilogue over the same accumulators).
+    print("case: moe config5 i32 whole output", flush=True)
+    tokens, E, topk, n, k = 4096, 8, 2, 14336, 4096
+    size_m = tokens * topk
+    sorted_ids, expert_ids = moe_routing(tokens, E, topk, seed=5)
+    g = rng(105)
+    x, w = int8_uniform(g, (tokens, k)), int8_uniform(g, (E, n, k))
+    sa = g.uniform(0.005, 0.02, tokens).astype(np.float32)
+    sw = g.uniform(0.001, 0.01, E * n).astype(np.float32)
+    xd, wd = dev(x), dev(w)
+    acc = _moe_i32(xd, wd, sorted_ids, expert_ids, E, topk, size_m, n, k)
+    pair_e = np.empty(size_m, np.int32)
+    pair_e[sorted_ids] = expert_ids
+    pe_d = torch.from_numpy(pair_e.astype(np.int64)).cuda()
+    tok_d = torch.arange(size_m, device="cuda:0") // topk
+    x64 = xd.to(torch.float64)
+    # rows: acc[p, :].sum() == x[t] . wsum[e]
+    row_got = acc.to(torch.int64).sum(1)
+    wsum = torch.stack([wd[e].to(torch.float64).sum(0) for e in range(E)])     # [E, K]
+    row_exact = (x64[tok_d] * wsum[pe_d]).sum(1)
+    assert torch.equal(row_got, row_exact.to(torch.int64))
+    # columns, per expert: sum over its pairs of acc[p, n] == W[e][n] . sum x[t_p]
+    for e in range(E):
+        sel = torch.nonzero(pe_d == e).flatten()
+        if sel.numel() == 0:
+            continue
+        col_got = acc[sel].to(torch.int64).sum(0)
+        xs = x64[tok_d[sel]].sum(0)
+        col_exact = wd[e].to(torch.float64) @ xs
+        assert torch.equal(col_got, col_exact.to(torch.int64)), e
+    # sampled pairs in full: one per (expert, tile) + each expert's last pair
+    _, offs = O.moe_expert_offsets(expert_ids, E)
+    acc_h = acc.cpu().numpy()
+    pick = []
+    gp = rng(55)
+    for e in range(E):
+        o0, o1 = int(offs[e]), int(offs[e + 1])
+        for t0 in range(o0, o1, 256):
+            pick.append(int(gp.integers(t0, min(t0 + 256, o1))))
+        if o1 > o0:
+            pick.append(o1 - 1)
+    assert len(pick) >= 37 + E
+    for s in pick:
+        p = int(sorted_ids[s])
+        e, t = pair_e[p], p // topk
+        want = w[e].astype(np.int64) @ x[t].astype(np.int64)
+        assert np.array_equal(acc_h[p].astype(np.int64), want), (s, p, e)
+    # the bf16 SKU over the same inputs: its epilogue applied to these accumulators
+    out = torch.zeros((size_m, n), dtype=torch.bfloat16, device="cuda:0")
+    counts = torch.zeros(E, dtype=torch.int32, device="cuda:0")
+    offs_d = torch.zeros(E + 1, dtype=torch.int32, device="cuda:0")
+    sa_d, sw_d = dev(sa), dev(sw).view(E, n)
+    P.MoeS8GroupedPlan.select(E, topk, size_m, n, k).run(xd, wd, dev(sorted_ids), dev(expert_ids), out,
+                                                         counts, offs_d, sa_d, dev(sw))
+    sync()
+    scale = sa_d[tok_d][:, None] * sw_d[pe_d]                 # f32, rounded once
+    want_bf16 = (scale * acc.to(torch.float32)).to(torch.bfloat16)
+    assert torch.equal(out.view(torch.int16), want_bf16.view(torch.int16))
