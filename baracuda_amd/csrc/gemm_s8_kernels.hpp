@@ -555,6 +555,96 @@ __global__ __launch_bounds__(512) void gemm_s8_rcr_rows_kernel(S8Args p, int m0)
     epi(m0 + 16 * wave + r16, n0 + 4 * g, sum);   // rows past M are not stored
 }
 
+// The last rows (at most 16 * RF), B streamed through LDS: K % 1024 == 0,
+// K <= kRowsDmaMaxK, B 16-byte aligned with N * ldb < 2^31, dynamic LDS of
+// max(16 * K, 16 KiB * RF) bytes.  A workgroup of 16 waves owns 16 output
+// columns: wave w LDS-DMAs B row n0 + w whole, 1 KiB per instruction (every
+// load a contiguous kilobyte of W, the GEMV's pattern, which streams HBM
+// about 1.4x faster than 64-byte pieces of 16 rows), all of it issued before
+// anything waits.  16-byte unit u of row r sits at slot u ^ r of the row,
+// so the 16 rows of a fragment read fall in distinct banks; the swizzle
+// stays inside each kilobyte, so every DMA instruction still fetches one
+// contiguous kilobyte.  After one barrier wave w multiplies its contiguous
+// K/16 bytes: B fragments from LDS, the RF 16-row A fragments of those
+// bytes from global memory (issued before the barrier), one
+// v_mfma_i32_16x16x64_i8 per 64 bytes and fragment with the operand roles
+// of gemm_s8_rcr_rows_kernel, so lane l ends with row 16 f + l % 16 and
+// columns 4 (l / 16) .. + 3.  The 16 partial sums go through LDS (int32
+// wrap-around, order-free) and the tiles' epilogue.
+constexpr int kRowsDmaMaxK = 8192;
+// Up to this many last rows take gemm_s8_rcr_rows_dma_kernel (N = K = 4096,
+// rotated weights: M = 1 / 16 / 32 in 5.45 / 6.8 / 8.6 us against 6.7 / 7.9
+// / ... for gemm_s8_rcr_rows_kernel); past it the A rows, which every one of
+// the N / 16 workgroups reads in full, dominate both kernels equally.
+constexpr int kRowsDmaMaxRows = 32;
+constexpr int kRowsDmaWaves = 16;
+
+template <int EPI, bool VecOut, int ACT, typename BiasT, int RF>
+__global__ __launch_bounds__(1024) void gemm_s8_rcr_rows_dma_kernel(S8Args p, int m0) {
+    constexpr int WAVES = kRowsDmaWaves;
+    constexpr int U = 4;                          // 64-byte chunks per batch of A loads
+    extern __shared__ __attribute__((aligned(1024))) int8_t lds[];   // max(16 * K, 16 KiB * RF) bytes
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r16 = lane & 15, g = lane >> 4;
+    const int n0 = blockIdx.x * 16;
+    const int mb = m0;                            // first of the last rows
+    // B row n0 + wave, K bytes, into LDS row `wave` (K bytes per row).
+    {
+        const v4i rsrc = mfma2::make_rsrc(p.b, (uint32_t)((int64_t)p.N * p.ldb));
+        const int voff = (n0 + wave) * (int)p.ldb + 16 * (lane ^ wave);
+        int8_t *dst = lds + wave * p.K;
+        for (int i = 0; i < p.K / 1024; ++i)
+            mfma2::dma16(rsrc, voff, __builtin_amdgcn_readfirstlane(i * 1024), dst + i * 1024);
+    }
+    const int8_t *arow[RF];
+#pragma unroll
+    for (int f = 0; f < RF; ++f) arow[f] = p.a + (int64_t)min(mb + 16 * f + r16, p.M - 1) * p.lda + g * 16;
+    const int span = p.K / WAVES;                 // bytes of K per wave, a multiple of 64
+    const int kw = wave * span;
+    v4i acc[RF];
+#pragma unroll
+    for (int f = 0; f < RF; ++f) acc[f] = v4i{0, 0, 0, 0};
+    for (int c0 = 0; c0 < span; c0 += 64 * U) {
+        v4i av[U][RF];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int f = 0; f < RF; ++f)
+                av[u][f] = c0 + 64 * u < span ? *reinterpret_cast<const v4i *>(arow[f] + kw + c0 + 64 * u)
+                                              : v4i{0, 0, 0, 0};
+        if (c0 == 0) {
+            // every DMA of the workgroup has landed (the A loads above were
+            // issued after this wave's DMAs; vmcnt counts in order)
+            mfma2::wait_dma();
+            __syncthreads();
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (c0 + 64 * u >= span) break;
+            const int unit = (kw + c0 + 64 * u) / 16 + g;   // 16-byte unit of row r16
+            const v4i bv = *reinterpret_cast<const v4i *>(lds + r16 * p.K + 16 * (unit ^ r16));
+#pragma unroll
+            for (int f = 0; f < RF; ++f) acc[f] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bv, av[u][f], acc[f], 0, 0, 0);
+        }
+    }
+    __syncthreads();   // B no longer read: the partial sums reuse its LDS
+    v4i *part = reinterpret_cast<v4i *>(lds);      // [WAVES][RF][64]
+#pragma unroll
+    for (int f = 0; f < RF; ++f) part[(wave * RF + f) * 64 + lane] = acc[f];
+    __syncthreads();
+    if (wave >= RF) return;
+    v4i sum = part[wave * 64 + lane];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) {
+        const v4i v = part[(w * RF + wave) * 64 + lane];
+        sum = v4i{(int)((uint32_t)sum[0] + (uint32_t)v[0]), (int)((uint32_t)sum[1] + (uint32_t)v[1]),
+                  (int)((uint32_t)sum[2] + (uint32_t)v[2]), (int)((uint32_t)sum[3] + (uint32_t)v[3])};
+    }
+    const S8Epilogue<EPI, VecOut, ACT, BiasT> epi{p};
+    epi(mb + 16 * wave + r16, n0 + 4 * g, sum);   // rows past M are not stored
+}
+
 // RRR fast path: A through the interior DMA, row-major B through the
 // transposing fragment reads (PolicyI8RowB); same tiles and epilogue as RCR.
 template <bool VecOut, int ACT, typename BiasT>
@@ -1035,6 +1125,19 @@ void launch_kernel(const S8Args &p, bool fast_k, hipStream_t stream, void *works
             if (tiles > 0)
                 hipLaunchKernelGGL((gemm_s8_rcr_dma_kernel<EPI, VecOut, ACT, BiasT>), dim3(tiles), dim3(DmaCfg::NT),
                                    0, stream, pm, TailSplit{0, 0, 1}, (int32_t *)nullptr);
+            const bool dma_b = rem <= kRowsDmaMaxRows && p.K % 1024 == 0 && p.K <= kRowsDmaMaxK &&
+                               p.ldb % 16 == 0 && aligned16(p.b) && (int64_t)p.N * p.ldb < (1ll << 31);
+            if (dma_b) {
+                // B rows; the 16 waves' partial sums reuse the same LDS
+                const size_t lds = std::max((size_t)16 * p.K, (size_t)kRowsDmaWaves * 2 * 1024);
+                if (rem <= 16)
+                    hipLaunchKernelGGL((gemm_s8_rcr_rows_dma_kernel<EPI, VecOut, ACT, BiasT, 1>), dim3(p.N / 16),
+                                       dim3(1024), lds, stream, p, pm.M);
+                else
+                    hipLaunchKernelGGL((gemm_s8_rcr_rows_dma_kernel<EPI, VecOut, ACT, BiasT, 2>), dim3(p.N / 16),
+                                       dim3(1024), lds, stream, p, pm.M);
+                return;
+            }
             const dim3 grid(p.N / 16), block(512);
             if (rem <= 16)
                 hipLaunchKernelGGL((gemm_s8_rcr_rows_kernel<EPI, VecOut, ACT, BiasT, 1>), grid, block, 0, stream, p, pm.M);

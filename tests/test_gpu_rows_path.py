@@ -25,6 +25,11 @@ pytestmark = pytest.mark.gpu
 # of 64 bytes (each wave's batches, their remainder, or both).
 SHAPES = [(1, 256, 384), (16, 4096, 4096), (33, 272, 640), (64, 1040, 1152), (100, 512, 4096),
           (128, 256, 8192), (1025, 16384, 128), (1060, 16384, 256), (1124, 16384, 128)]
+# At most 32 last rows with K % 1024 == 0, K <= 8192: B streamed through LDS
+# (gemm_s8_rcr_rows_dma_kernel; 1 or 2 fragments, 1 to 8 chunks of 64 bytes
+# per wave, 16 last rows under 4 tile rows).
+DMA_SHAPES = [(1, 4096, 1024), (17, 512, 2048), (20, 1040, 3072), (32, 272, 8192), (1040, 16384, 1024)]
+SHAPES += DMA_SHAPES
 
 
 def _rows(m):
@@ -67,7 +72,7 @@ def test_rows_path_i32_s8_w8a8(gpu, shape):
         assert np.array_equal(gw[r], O.gemm_w8a8_bf16(a, b, sa, sw, rows=(r, r + 1), nthreads=8)[0]), r
 
 
-@pytest.mark.parametrize("shape", [SHAPES[1], SHAPES[4], SHAPES[7]])
+@pytest.mark.parametrize("shape", [SHAPES[1], SHAPES[4], SHAPES[7], DMA_SHAPES[1], DMA_SHAPES[4]])
 def test_rows_path_bias_gelu(gpu, shape):
     m, n, k = shape
     print(f"case: rows path bias_gelu {shape}", flush=True)
@@ -83,7 +88,7 @@ def test_rows_path_bias_gelu(gpu, shape):
     assert np.array_equal(d.cpu().numpy()[rows], O.gemm_s8_epi(a[rows], b, "rcr", 0.004, 0.25, c[rows], bias, "gelu"))
 
 
-@pytest.mark.parametrize("shape", [SHAPES[2], SHAPES[3], SHAPES[5], SHAPES[6]])
+@pytest.mark.parametrize("shape", [SHAPES[2], SHAPES[3], SHAPES[5], SHAPES[6], DMA_SHAPES[2], DMA_SHAPES[3]])
 def test_rows_path_quantized_linear_f32_f64(gpu, shape):
     # f32: y = (sa*sw)*acc in f32; f64: f64 scales narrowed to f32, the same
     # product, widened (compose.cu:27-28).
