@@ -20,6 +20,9 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libbaracuda_kernels.so"
+# Measurement kernels of bench.py (not product), built beside the library.
+PROBES = PKG / "probes"
+PROBE_LIB = PKG / "libbaracuda_probes.so"
 # Digest of the sources and flags the library was built from, written beside it.
 STAMP = PKG / "libbaracuda_kernels.so.srchash"
 
@@ -53,7 +56,8 @@ def source_digest() -> str:
     """SHA-256 over every kernel source, public header and the build flags."""
     h = hashlib.sha256()
     h.update(" ".join(HIP_FLAGS[:-2]).encode())
-    files = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.hpp")) + sorted((ROOT / "include").glob("*.h"))
+    files = (sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.hpp")) + sorted((ROOT / "include").glob("*.h"))
+             + sorted(PROBES.glob("*.hip")))
     for f in files:
         h.update(f.name.encode())
         h.update(f.read_bytes())
@@ -62,7 +66,7 @@ def source_digest() -> str:
 
 def is_stale() -> bool:
     """True when the library is missing or was built from other sources."""
-    if not LIB.exists() or not STAMP.exists():
+    if not LIB.exists() or not STAMP.exists() or (any(PROBES.glob("*.hip")) and not PROBE_LIB.exists()):
         return True
     return STAMP.read_text().strip() != source_digest()
 
@@ -72,6 +76,20 @@ def ensure_built(verbose: bool = False) -> Path:
     if is_stale():
         build(verbose=verbose)
     return LIB
+
+
+def _build_probes() -> None:
+    """Measurement kernels (probes/*.hip) into their own library, so the
+    product library exports exactly what include/baracuda_kernels.h declares."""
+    srcs = sorted(PROBES.glob("*.hip"))
+    if not srcs:
+        return
+    tmp = PROBE_LIB.with_suffix(".so.tmp")
+    cmd = [HIPCC, *HIP_FLAGS, "-shared", *map(str, srcs), "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed for the probes:\n{res.stderr}")
+    os.replace(tmp, PROBE_LIB)
 
 
 def build(verbose: bool = False) -> Path:
@@ -87,6 +105,7 @@ def build(verbose: bool = False) -> Path:
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
     os.replace(tmp, LIB)
+    _build_probes()
     STAMP.write_text(digest + "\n")
     if verbose:
         # stderr: callers such as bench.py keep stdout for their own output

@@ -69,23 +69,29 @@ __device__ __forceinline__ float dot16_s8_bf16(const v4i w, const v4i xlo, const
 // Fast path: K % 1024 == 0, 16-byte aligned rows; one wave per workgroup
 // (finer dispatch than 4-wave groups: 11.9 vs 12.4 us at 14336 x 4096).
 // Each wave writes its two outputs with one 4-byte store.
-template <int ROWS, int B>
+// CHUNKS: the K / 1024 chunk count when fixed at compile time (K = 4096),
+// 0 for any.  EVEN: N % ROWS == 0 and d 4-byte aligned, so no wave clamps a
+// row and each stores its two outputs with one unconditional 4-byte store
+// (0.1 us less at 14336 x 4096 than the per-wave test).
+template <int ROWS, int B, int CHUNKS = 0, bool EVEN = false>
 __global__ __launch_bounds__(64) void gemv_s8w_m1_kernel(
     int N, int K, const uint16_t *__restrict__ x, const int8_t *__restrict__ w, int64_t ldw,
     const float *__restrict__ scale, uint16_t *__restrict__ d) {
     const int lane = threadIdx.x & 63;
     const int row0 = blockIdx.x * ROWS;
-    if (row0 >= N) return;
-    const int chunks = K >> 10;
-    const int8_t *wr[ROWS];
-#pragma unroll
-    for (int r = 0; r < ROWS; ++r) wr[r] = w + (int64_t)min(row0 + r, N - 1) * ldw + lane * 16;
-    const v4i *xv = reinterpret_cast<const v4i *>(x) + lane * 2;
-    // The row scales are fetched up front: loaded after the reduction, their
-    // latency would add to every wave's tail.
+    if (!EVEN && row0 >= N) return;
+    // Rows past N (the last wave of an odd N) re-read row N - 1; wave-uniform.
+    const bool whole = EVEN || row0 + ROWS <= N;
+    // The row scales are requested up front: loaded after the reduction,
+    // their latency would add to every wave's tail.
     float sc[ROWS];
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r) sc[r] = scale[min(row0 + r, N - 1)];
+    for (int r = 0; r < ROWS; ++r) sc[r] = scale[whole ? row0 + r : min(row0 + r, N - 1)];
+    const int chunks = CHUNKS ? CHUNKS : K >> 10;
+    const int8_t *wr[ROWS];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) wr[r] = w + (int64_t)(whole ? row0 + r : min(row0 + r, N - 1)) * ldw + lane * 16;
+    const v4i *xv = reinterpret_cast<const v4i *>(x) + lane * 2;
     float acc[ROWS];
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) acc[r] = 0.0f;
@@ -121,7 +127,7 @@ __global__ __launch_bounds__(64) void gemv_s8w_m1_kernel(
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) o[r] = f32_to_bf16_rne(wave_sum_lane63(acc[r]) * sc[r]);
     if (lane == 63) {
-        if (ROWS == 2 && row0 + 1 < N && (reinterpret_cast<uintptr_t>(d + row0) & 3u) == 0) {
+        if (ROWS == 2 && (EVEN || (row0 + 1 < N && (reinterpret_cast<uintptr_t>(d + row0) & 3u) == 0))) {
             *reinterpret_cast<uint32_t *>(d + row0) = (uint32_t)o[0] | ((uint32_t)o[ROWS - 1] << 16);
         } else {
 #pragma unroll
@@ -513,7 +519,14 @@ int32_t baracuda_kernels_gemv_s8w_m1_bf16_gfx950_run(int32_t n, int32_t k, const
     if (fast) {
         const int waves = (n + kGemvRows - 1) / kGemvRows;
         const int chunks = k / 1024;
-        if (chunks % 4 == 0)
+        const bool even = n % kGemvRows == 0 && (reinterpret_cast<uintptr_t>(d) & 3u) == 0;
+        if (chunks == 4 && even)
+            hipLaunchKernelGGL((gemv_s8w_m1_kernel<kGemvRows, 4, 4, true>), dim3(waves), dim3(64), 0, stream, n, k,
+                               (const uint16_t *)x, (const int8_t *)w, ldw, (const float *)scale, (uint16_t *)d);
+        else if (chunks == 4)
+            hipLaunchKernelGGL((gemv_s8w_m1_kernel<kGemvRows, 4, 4>), dim3(waves), dim3(64), 0, stream, n, k,
+                               (const uint16_t *)x, (const int8_t *)w, ldw, (const float *)scale, (uint16_t *)d);
+        else if (chunks % 4 == 0)
             hipLaunchKernelGGL((gemv_s8w_m1_kernel<kGemvRows, 4>), dim3(waves), dim3(64), 0, stream, n, k,
                                (const uint16_t *)x, (const int8_t *)w, ldw, (const float *)scale, (uint16_t *)d);
         else if (chunks % 2 == 0)

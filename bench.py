@@ -97,6 +97,36 @@ def graph_us(fn, per_graph=100, replays=20):
     return st.elapsed_time(en) * 1e3 / (replays * per_graph)
 
 
+def gemv_ceiling_probes(ws, n):
+    """Device µs per launch (graph replay, no host launch gaps) of each
+    streaming probe of libbaracuda_probes.so over the rotated weight copies
+    `ws` ([n, 4096] int8); {} without the library."""
+    import ctypes
+    import torch
+    from baracuda_amd.build import PROBE_LIB
+    if not PROBE_LIB.exists():
+        return {}
+    lib = ctypes.CDLL(str(PROBE_LIB))
+    lib.baracuda_probe_name.restype = ctypes.c_char_p
+    lib.baracuda_probe_name.argtypes = [ctypes.c_int]
+    lib.baracuda_probe_run.restype = ctypes.c_int
+    lib.baracuda_probe_run.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
+                                       ctypes.c_void_p]
+    out = torch.empty(n, dtype=torch.int32, device=ws[0].device)
+    res, kind = {}, 0
+    while lib.baracuda_probe_name(kind):
+        it = [0]
+
+        def probe():
+            st = lib.baracuda_probe_run(kind, ws[it[0] % len(ws)].data_ptr(), n, out.data_ptr(),
+                                        torch.cuda.current_stream().cuda_stream)
+            assert st == 0
+            it[0] += 1
+        res[lib.baracuda_probe_name(kind).decode()] = round(graph_us(probe, per_graph=100), 3)
+        kind += 1
+    return res
+
+
 def cpu_cores():
     """Host threads for the CPU baseline: every core this process may run on,
     bounded by OMP_NUM_THREADS when the host sets it (the GPU box allots 16
@@ -444,6 +474,14 @@ def main():
                                                    nbytes / (ggs * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
                                                "bytes_per_call": nbytes, "weight_copies_rotated": copies,
                                                "hbm_traffic_pmc": int(TRAFFIC_GEMV_14336x4096)}
+            # What a kernel streaming the same weights can reach: read-only
+            # probes in several launch shapes (baracuda_amd/probes), same
+            # rotation and timing, on the weight bytes only.
+            probes = gemv_ceiling_probes(ws, n)
+            if probes:
+                best = min(v for kp, v in probes.items() if "store" not in kp)
+                extra["gemv_s8w_m1_14336x4096"]["stream_probes_graph_replay_us"] = probes
+                extra["gemv_s8w_m1_14336x4096"]["graph_replay_vs_best_read_probe"] = round(ggs / best, 3)
             del ws
         if only in ("", "fp8"):
             log("bench: fp8 2048x14336x4096")
