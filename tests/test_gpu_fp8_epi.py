@@ -7,7 +7,7 @@ quantized to the encoding, alpha = 0.25, bias ((j%5)-2)/2.  Every product and
 partial sum of these is exact in f32, so Identity / Bias / BiasRelu are
 bit-exact; BiasGelu / BiasSilu are within one grid step (the reference allows
 two).  Random N(0,1) operands with C, on the LDS-DMA shapes too: within one
-grid step plus the f8f6f4 MFMA's own summation error (1e-4 * alpha * sum|a*b|,
+grid step plus the f8f6f4 MFMA's own summation error (FP8_FLOOR * alpha * sum|a*b|,
 the floor the e4m3 accumulator tests establish against hipBLASLt) of the
 exactly rounded result, with differences on under 2% of the outputs.
 """
@@ -18,7 +18,7 @@ import torch
 from baracuda_amd import plans as P
 from oracle import oracle as O
 from oracle.inputs import rng
-from tests.gpu_util import dev, sync
+from tests.gpu_util import FP8_FLOOR, dev, sync
 
 pytestmark = pytest.mark.gpu
 
@@ -103,7 +103,7 @@ def test_random_with_c(gpu, shape, fmt, layout, epi):
     fa = np.abs(O.fp8_to_f32(a, fmt).astype(np.float64))
     fb = np.abs(O.fp8_to_f32(b, fmt).astype(np.float64))
     absum = fa @ (fb if layout == P.LayoutSku.Rrr else fb.T)
-    floor = 1e-4 * alpha * absum
+    floor = FP8_FLOOR * alpha * absum
     st = _steps(got, want, fmt, floor)
     assert st.max() <= 1.0 and (got != want).mean() < 0.02
 

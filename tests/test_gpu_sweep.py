@@ -8,7 +8,7 @@ workspace where the plan reports one:
   * W8A8 bf16 out: bit-exact against the oracle's f32 epilogue;
   * u8 RCR u8 out: bit-exact against the oracle;
   * FP8 e4m3 RCR f32 out: within 1e-3 relative of the exact f64 sum, with the
-    1e-4 * sum|a*b| floor of the other FP8 tests;
+    FP8_FLOOR * sum|a*b| floor of the other FP8 tests;
   * FP8 fp8-out (e4m3 RRR, e5m2 RCR / RRR) with C and BiasRelu: one grid step;
   * RRR s8 BiasRelu with C and u8 RRR (with / without workspace): bit-exact.
 """
@@ -19,7 +19,7 @@ import torch
 from baracuda_amd import plans as P
 from oracle import oracle as O
 from oracle.inputs import int8_uniform, rng
-from tests.gpu_util import dev, host_bits16, sync
+from tests.gpu_util import FP8_FLOOR, dev, host_bits16, sync
 
 pytestmark = pytest.mark.gpu
 
@@ -104,7 +104,7 @@ def test_fp8_sweep(gpu, shape):
     exact = O.gemm_fp8_e4m3_f64(a, b, nthreads=8)
     ta, tb = np.abs(O.e4m3_to_f32(a).astype(np.float64)), np.abs(O.e4m3_to_f32(b).astype(np.float64))
     err = np.abs(d.cpu().numpy().astype(np.float64) - exact)
-    assert np.all(err <= 1e-3 * np.abs(exact) + 1e-4 * (ta @ tb.T)), err.max()
+    assert np.all(err <= 1e-3 * np.abs(exact) + FP8_FLOOR * (ta @ tb.T)), err.max()
 
 
 @pytest.mark.parametrize("shape", SHAPES)
@@ -163,6 +163,6 @@ def test_fp8_out_with_c_sweep(gpu, shape, fmt, layout):
     want = f8_want(fmt, layout, epi, a, b, c, bias, alpha, 0.5)
     fa = np.abs(O.fp8_to_f32(a, fmt).astype(np.float64))
     fb = np.abs(O.fp8_to_f32(b, fmt).astype(np.float64))
-    floor = 1e-4 * alpha * (fa @ (fb if layout == P.LayoutSku.Rrr else fb.T))
+    floor = FP8_FLOOR * alpha * (fa @ (fb if layout == P.LayoutSku.Rrr else fb.T))
     st = _steps(got, want, fmt, floor)
     assert st.max() <= 1.0 and (got != want).mean() < 0.02
