@@ -244,6 +244,16 @@ class ClockSampler:
                 "samples": len(live), "source": src}
 
 
+def energy(power_w, us, ops):
+    """Socket energy per launch (mJ) and ops per joule (T/J = TOPS/W) from
+    the socket power read while the kernel ran in a loop and its mean launch
+    time: under the package power limit, energy per op ranks schedules."""
+    if not power_w or not us:
+        return {}
+    j = power_w * us * 1e-6
+    return {"energy_per_launch_mJ": round(j * 1e3, 2), "tera_ops_per_joule": round(ops / j / 1e12, 3)}
+
+
 def clock_under_load(fn, seconds=None):
     """Clock / power summary (ClockSampler) while fn runs in a loop; skipped
     (empty summary) with --no-clock, e.g. under a counter profiler."""
@@ -389,7 +399,7 @@ def main():
     ap.add_argument("--no-clock", action="store_true",
                     help="skip the 2 s clock / power loops (profiling runs)")
     ap.add_argument("--only", default="",
-                    help="run only: w8a8|w8a8x|w8a8c|gemv|quant|fp8|moe|int8epi|te|embedding|gather|copy (profiling; copy = 256 MiB "
+                    help="run only: w8a8|w8a8x|w8a8c|energy|gemv|quant|fp8|moe|int8epi|te|embedding|gather|copy (profiling; copy = 256 MiB "
                          "device copy used to calibrate the HBM byte counters)")
     args = ap.parse_args()
     NO_CLOCK[0] = args.no_clock
@@ -523,7 +533,9 @@ def main():
                                                       "data": "N(0,1), absmax -> 448, e4m3 RNE; scales absmax/448",
                                                       "resident_operands_us": round(frs * 1e3, 2),
                                                       "sclk_mhz": fclk.get("mhz_mean"),
-                                                      "socket_power_w": fclk.get("socket_power_w_mean")}
+                                                      "socket_power_w": fclk.get("socket_power_w_mean"),
+                                                      **energy(fclk.get("socket_power_w_mean"), fms * 1e3,
+                                                               2.0 * m * n * k)}
             del fsets, fa, fb, ra, rb, rd
         if only in ("", "moe"):
             log("bench: moe grouped int8")
@@ -552,7 +564,8 @@ def main():
                 "tiles": tiles_m * (n // 256), "tile_rounds_on_256_cus": round(tiles_m * (n // 256) / 256, 2),
                 "padded_rows": tiles_m * 256, "routed_rows": int(rows_e.sum()),
                 "padding_frac": round(1 - rows_e.sum() / (tiles_m * 256), 4),
-                "sclk_mhz": mclk.get("mhz_mean"), "socket_power_w": mclk.get("socket_power_w_mean")}
+                "sclk_mhz": mclk.get("mhz_mean"), "socket_power_w": mclk.get("socket_power_w_mean"),
+                **energy(mclk.get("socket_power_w_mean"), mms * 1e3, 2.0 * tokens * topk * n * k)}
             del mx, mw, mo
             log("bench: moe grouped bf16 (moe_wmma ABI)")
             bx = torch.randn((tokens, k), device=dev).to(torch.bfloat16)
@@ -809,6 +822,30 @@ def main():
                     del ows
                 del sets
             extra["w8a8_off_grid_n4096_k4096"] = og
+        if only in ("", "energy"):
+            log("bench: energy per launch, ours vs hipBLASLt (int8 4096^3, one resident random set)")
+            # Under the package power limit the clock follows the power draw,
+            # so time and energy per op rank schedules together; hipBLASLt's
+            # int8 GEMM (torch._int_mm, int32 out) on the same operands is the
+            # reference point, beside this library's int32-out and bf16-out SKUs.
+            pi = P.IntGemmPlan.select(P.IntGemmDescriptor(M, N, K, output=P.ElementKind.I32))
+            oi32 = torch.empty((M, N), dtype=torch.int32, device=dev)
+            wt = dw.t()
+            cands = {
+                "ours_w8a8_bf16": run_resident,
+                "ours_i32": lambda: pi.run(da, dw, oi32, stream=stream),
+                "hipblaslt_int_mm_i32": lambda: torch._int_mm(da, wt),
+            }
+            et = {}
+            for name, fn in cands.items():
+                with torch.cuda.stream(stream):
+                    ems = time_launches(fn, 100, 10, stream, warm_ms=50.0)
+                    eclk = clock_under_load(fn)
+                et[name] = {"us": round(ems * 1e3, 2), "TOPS": round(ops / (ems * 1e-3) / 1e12, 1),
+                            "sclk_mhz": eclk.get("mhz_mean"), "socket_power_w": eclk.get("socket_power_w_mean"),
+                            **energy(eclk.get("socket_power_w_mean"), ems * 1e3, ops)}
+            extra["energy_int8_4096_cubed_resident"] = et
+            del oi32
         if only in ("", "w8a8c"):
             log("bench: w8a8 random vs constant operands (resident)")
             if only == "w8a8c":   # the random-operand phase this mode profiles against
@@ -826,6 +863,7 @@ def main():
             extra["w8a8_4096_cubed_constant_operands"] = {
                 "us": round(cms * 1e3, 2), "TOPS": round(ops / (cms * 1e-3) / 1e12, 1),
                 "sclk_mhz": csclk.get("mhz_mean"), "socket_power_w": csclk.get("socket_power_w_mean"),
+                **energy(csclk.get("socket_power_w_mean"), cms * 1e3, ops),
                 "note": "A = W = all ones, one resident set: compare with w8a8_4096_cubed_resident_operands "
                         "and with roofline.sclk (random operands)"}
             del ca, cw, co
@@ -889,7 +927,7 @@ def main():
                                       if sclk.get("mhz_mean") else None),
             "frac_at_measured_sclk": (round(tops / (OPS_PER_CLK * sclk["mhz_mean"] * 1e6 / 1e12), 4)
                                       if sclk.get("mhz_mean") else None),
-            "warmup_ms": HEAD_WARM_MS},
+            "warmup_ms": HEAD_WARM_MS, **energy(sclk.get("socket_power_w_mean"), ms * 1e3, ops)},
         "cpu_baseline": cpu,
         "cpu_baseline_extra": cpu_extra,
         "extra": extra,
