@@ -166,3 +166,36 @@ def test_fp8_out_with_c_sweep(gpu, shape, fmt, layout):
     floor = FP8_FLOOR * alpha * (fa @ (fb if layout == P.LayoutSku.Rrr else fb.T))
     st = _steps(got, want, fmt, floor)
     assert st.max() <= 1.0 and (got != want).mean() < 0.02
+
+
+def _small_m_shapes(count, seed):
+    # the W8A8 last-rows kernels: M <= 128 (no tiles) with N % 16 == 0 and
+    # K % 128 == 0; K % 1024 == 0 and M <= 32 take the LDS-streamed B kernel
+    g = rng(seed)
+    out = []
+    for i in range(count):
+        m = int(g.integers(1, 33)) if i % 2 == 0 else int(g.integers(1, 129))
+        n = 16 * int(g.integers(1, 160))
+        k = 1024 * int(g.integers(1, 9)) if i % 4 != 3 else 128 * int(g.integers(1, 40))
+        out.append((m, n, k))
+    return out
+
+
+@pytest.mark.parametrize("shape", _small_m_shapes(16, 77))
+def test_int8_small_m_sweep(gpu, shape):
+    m, n, k = shape
+    print(f"case: sweep small-M int8 {shape}", flush=True)
+    g = rng(m * 7 + n * 13 + k)
+    a, b = int8_uniform(g, (m, k)), int8_uniform(g, (n, k))
+    pi = P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, output=P.ElementKind.I32))
+    d = torch.full((m, n), -7, dtype=torch.int32, device="cuda:0")
+    pi.run(dev(a), dev(b), d)
+    sync()
+    assert np.array_equal(d.cpu().numpy(), a.astype(np.int64) @ b.astype(np.int64).T)
+    sa = g.uniform(0.005, 0.02, m).astype(np.float32)
+    sw = g.uniform(0.001, 0.01, n).astype(np.float32)
+    dw = torch.empty((m, n), dtype=torch.bfloat16, device="cuda:0")
+    P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, output=P.ElementKind.Bf16)).run(
+        dev(a), dev(b), dw, scale_a=dev(sa), scale_b=dev(sw))
+    sync()
+    assert np.array_equal(host_bits16(dw), O.gemm_w8a8_bf16(a, b, sa, sw, nthreads=8))
