@@ -136,3 +136,19 @@ def test_rows_path_with_and_without_split_workspace(gpu):
     assert np.array_equal(outs[0], outs[1])
     rows = _rows(m)
     assert np.array_equal(outs[0][rows], a[rows].astype(np.int64) @ b.astype(np.int64).T)
+
+
+@pytest.mark.parametrize("shape", [(7, 512, 2048), (30, 4096, 1024)])
+def test_rows_dma_padded_leading_dimensions(gpu, shape):
+    # A and B views with row pitches past K (16-byte multiples): the
+    # LDS-streamed B kernel addresses rows by ldb and A rows by lda.
+    m, n, k = shape
+    print(f"case: rows dma padded ld {shape}", flush=True)
+    g = rng(m + n + k + 3)
+    a_full, b_full = int8_uniform(g, (m, k + 64)), int8_uniform(g, (n, k + 128))
+    ta, tb = dev(a_full)[:, :k], dev(b_full)[:, :k]
+    d = torch.full((m, n), -7, dtype=torch.int32, device="cuda:0")
+    P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, output=P.ElementKind.I32)).run(ta, tb, d)
+    sync()
+    want = a_full[:, :k].astype(np.int64) @ b_full[:, :k].astype(np.int64).T
+    assert np.array_equal(d.cpu().numpy(), want)
