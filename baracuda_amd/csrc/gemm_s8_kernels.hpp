@@ -216,9 +216,13 @@ struct TailSplit {
 // M <= kRowsPathMax: no tiles at all), when that row of tiles would start
 // another round of tiles on the 256 CUs (it costs nothing extra when it
 // fits the idle CUs of the last round).  Up to kRowsPathAlways rows always;
-// more only when no tail-split workspace is given.
+// up to kRowsPathMax when K % kRowsStagedSB == 0 (the staged last-rows
+// kernel), otherwise only when no tail-split workspace is given.  At
+// N = K = 4096 the staged pass beats the split tail round and its reduction:
+// M = 100 / 128 / 4196 in 11.9 / 12.8 / 66.1 us against 22.3 / 23.0 / 71.0.
 constexpr int kRowsPathMax = 128;
 constexpr int kRowsPathAlways = 64;
+constexpr int kRowsStagedSB = 512, kRowsStagedDepth = 2;
 inline int rows_path_rows(int M, int N, int limit = kRowsPathMax) {
     if (N <= 0 || N % 16 != 0 || M <= 0) return 0;
     const int rem = M % 256;
@@ -231,7 +235,8 @@ inline int rows_path_rows(int M, int N, int limit = kRowsPathMax) {
 inline TailSplit tail_split_plan(int M, int N, int K) {
     TailSplit t{0, 0, 1};
     if (M <= 0 || N <= 0 || K <= 0 || K % 128 != 0) return t;
-    if (rows_path_rows(M, N, kRowsPathAlways) != 0) return t;   // the rows path takes those shapes
+    // the rows path takes those shapes
+    if (rows_path_rows(M, N, K % kRowsStagedSB == 0 ? kRowsPathMax : kRowsPathAlways) != 0) return t;
     const int tiles_m = (M + 255) / 256, tiles_n = (N + 255) / 256;
     const int64_t T = (int64_t)tiles_m * tiles_n;
     const int64_t full = T / 256 * 256;
@@ -643,6 +648,106 @@ __global__ __launch_bounds__(1024) void gemm_s8_rcr_rows_dma_kernel(S8Args p, in
     }
     const S8Epilogue<EPI, VecOut, ACT, BiasT> epi{p};
     epi(mb + 16 * wave + r16, n0 + 4 * g, sum);   // rows past M are not stored
+}
+
+// The last rows, 33 to 16 RF of them, with A and B streamed through LDS in
+// K stages of SB bytes, DEPTH stages in flight (K % SB == 0; A and B 16-byte
+// aligned, (m0 + 16 RF) * lda and N * ldb below 2^31; dynamic LDS of
+// DEPTH * (16 RF + 16) * SB bytes).  gemm_s8_rcr_rows_kernel reads its A
+// fragments from global memory as 64-byte pieces of 16 rows, and every one
+// of the N / 16 workgroups reads all of A: that pattern moves L2-resident
+// bytes 2.5x slower than whole kilobytes (64 MB of A at M = 64: 8.1
+// against 3.2 us) and dominated the pass.  Here a workgroup of 16 waves
+// LDS-DMAs each K stage of its 16 RF A rows (rows past M land as zeros) and
+// of its 16 B rows, 1024 / SB whole row pieces per instruction, all before
+// anything waits.  16-byte unit u of row r of a stage sits at slot
+// u ^ (r & 15), so fragment reads are conflict-free.  Wave w owns 64-byte
+// chunk w % CH of every stage (CH = SB / 64) and row fragments
+// w / CH + (16 / CH) i; its sums over the stages go through LDS (int32
+// wrap-around: order-free) and waves 0 .. RF - 1 run the tiles' epilogue
+// for fragment w.
+// 512-byte stages, two in flight: at N = K = 4096 (M = 33 / 64 / 100 / 128)
+// 8.0 / 8.8 / 11.3 / 11.6 us, against 9.8-10.3 / 10.0-10.5 / 12.0-13.2 /
+// 12.3-13.5 us for 256-byte stages two to four deep; three 512-byte stages
+// measure the same as two (kRowsStagedSB, kRowsStagedDepth).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
+
+template <int EPI, bool VecOut, int ACT, typename BiasT, int RF, int SB, int DEPTH>
+__global__ __launch_bounds__(1024) void gemm_s8_rcr_rows_staged_kernel(S8Args p, int m0) {
+    constexpr int WAVES = 16, CH = SB / 64;                  // 64-byte chunks per stage
+    constexpr int FPW = RF * CH / WAVES;                      // row fragments per wave
+    constexpr int FSTEP = WAVES / CH;
+    constexpr int ROWS = 16 * RF + 16;                        // A then B rows of a stage
+    constexpr int STAGE = ROWS * SB;                          // bytes
+    constexpr int RPI = 1024 / SB, UPR = SB / 16;             // rows per DMA instruction, units per row
+    constexpr int NI = ROWS / RPI;                            // DMA instructions per stage
+    constexpr int HI = (NI + WAVES - 1) / WAVES, LO = NI / WAVES;
+    static_assert(FPW >= 1 && RF * CH % WAVES == 0 && ROWS % RPI == 0 && DEPTH >= 2 && DEPTH <= 4,
+                  "stage split");
+    extern __shared__ __attribute__((aligned(1024))) int8_t lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r16 = lane & 15, g = lane >> 4;
+    const int n0 = blockIdx.x * 16;
+    const v4i ra = mfma2::make_rsrc(p.a, (uint32_t)((int64_t)p.M * p.lda));
+    const v4i rb = mfma2::make_rsrc(p.b, (uint32_t)((int64_t)p.N * p.ldb));
+    // this wave's DMA instructions j = wave, wave + 16, ...: rows RPI j ..
+    // of the stage (A rows first), lane L fetching row RPI j + L / UPR at
+    // slot L % UPR
+    auto dma_stage = [&](int st, int8_t *buf) {
+        const int k0 = st * SB;
+        for (int j = wave; j < NI; j += WAVES) {
+            const int r = RPI * j + lane / UPR, slot = lane % UPR;
+            const int unit = slot ^ (r & 15);
+            if (r < 16 * RF)
+                mfma2::dma16(ra, (int)((int64_t)(m0 + r) * p.lda) + 16 * unit, k0, buf + j * 1024);
+            else
+                mfma2::dma16(rb, (int)((int64_t)(n0 + r - 16 * RF) * p.ldb) + 16 * unit, k0, buf + j * 1024);
+        }
+    };
+    // waves below NI % 16 issue HI instructions per stage, the others LO
+    const bool hi = NI % WAVES == 0 || wave < NI % WAVES;
+    const int ns = p.K / SB;
+    for (int st = 0; st < DEPTH && st < ns; ++st) dma_stage(st, lds + st * STAGE);
+    const int c = wave % CH, f0 = wave / CH;
+    v4i acc[FPW];
+#pragma unroll
+    for (int i = 0; i < FPW; ++i) acc[i] = v4i{0, 0, 0, 0};
+    for (int st = 0; st < ns; ++st) {
+        // stage st has landed once at most the later stages' DMAs are outstanding
+        const int later = min(DEPTH - 1, ns - 1 - st);
+        if (later == 0) wait_vmcnt<0>();
+        else if (later == 1) { if (hi) wait_vmcnt<HI>(); else wait_vmcnt<LO>(); }
+        else if (later == 2) { if (hi) wait_vmcnt<2 * HI>(); else wait_vmcnt<2 * LO>(); }
+        else { if (hi) wait_vmcnt<3 * HI>(); else wait_vmcnt<3 * LO>(); }
+        __syncthreads();
+        int8_t *buf = lds + (st % DEPTH) * STAGE;
+        const int sl = 16 * ((4 * c + g) ^ r16);                 // row & 15 == r16 for every fragment row
+        const v4i bv = *reinterpret_cast<const v4i *>(buf + (16 * RF + r16) * SB + sl);
+#pragma unroll
+        for (int i = 0; i < FPW; ++i) {
+            const v4i av = *reinterpret_cast<const v4i *>(buf + (16 * (f0 + FSTEP * i) + r16) * SB + sl);
+            acc[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bv, av, acc[i], 0, 0, 0);
+        }
+        __syncthreads();   // every wave is done with this buffer
+        if (st + DEPTH < ns) dma_stage(st + DEPTH, buf);
+    }
+    // partial sums of fragment f, chunk c: part[f][c][lane]
+    v4i *part = reinterpret_cast<v4i *>(lds);
+#pragma unroll
+    for (int i = 0; i < FPW; ++i) part[((f0 + FSTEP * i) * CH + c) * 64 + lane] = acc[i];
+    __syncthreads();
+    if (wave >= RF) return;
+    v4i sum = part[(wave * CH) * 64 + lane];
+#pragma unroll
+    for (int cc = 1; cc < CH; ++cc) {
+        const v4i v = part[(wave * CH + cc) * 64 + lane];
+        sum = v4i{(int)((uint32_t)sum[0] + (uint32_t)v[0]), (int)((uint32_t)sum[1] + (uint32_t)v[1]),
+                  (int)((uint32_t)sum[2] + (uint32_t)v[2]), (int)((uint32_t)sum[3] + (uint32_t)v[3])};
+    }
+    const S8Epilogue<EPI, VecOut, ACT, BiasT> epi{p};
+    epi(m0 + 16 * wave + r16, n0 + 4 * g, sum);   // rows past M are not stored
 }
 
 // RRR fast path: A through the interior DMA, row-major B through the
@@ -1136,6 +1241,22 @@ void launch_kernel(const S8Args &p, bool fast_k, hipStream_t stream, void *works
                 else
                     hipLaunchKernelGGL((gemm_s8_rcr_rows_dma_kernel<EPI, VecOut, ACT, BiasT, 2>), dim3(p.N / 16),
                                        dim3(1024), lds, stream, p, pm.M);
+                return;
+            }
+            const int rf_staged = rem <= 64 ? 4 : 8;
+            const bool staged = rem > kRowsDmaMaxRows && p.K % kRowsStagedSB == 0 && aligned16(p.a) &&
+                                aligned16(p.b) && p.lda % 16 == 0 && p.ldb % 16 == 0 &&
+                                (int64_t)(pm.M + 16 * rf_staged) * p.lda < (1ll << 31) &&
+                                (int64_t)p.M * p.lda < (1ll << 31) && (int64_t)p.N * p.ldb < (1ll << 31);
+            if (staged) {
+                constexpr int SB = kRowsStagedSB, DEPTH = kRowsStagedDepth;
+                const size_t lds = (size_t)DEPTH * (16 * rf_staged + 16) * SB;
+                if (rf_staged == 4)
+                    hipLaunchKernelGGL((gemm_s8_rcr_rows_staged_kernel<EPI, VecOut, ACT, BiasT, 4, SB, DEPTH>),
+                                       dim3(p.N / 16), dim3(1024), lds, stream, p, pm.M);
+                else
+                    hipLaunchKernelGGL((gemm_s8_rcr_rows_staged_kernel<EPI, VecOut, ACT, BiasT, 8, SB, DEPTH>),
+                                       dim3(p.N / 16), dim3(1024), lds, stream, p, pm.M);
                 return;
             }
             const dim3 grid(p.N / 16), block(512);

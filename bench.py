@@ -771,7 +771,7 @@ def main():
             # operand sets (20 x 16.8 MB of weights, past the 256 MB Infinity
             # Cache), so every call reads its weights from HBM; the others 4.
             og = {}
-            for mm in (1, 16, 32, 64, 128, 4000, 4097, 4160):
+            for mm in (1, 16, 32, 33, 64, 100, 128, 4000, 4097, 4160, 4196):
                 nsets = 20 if mm <= 128 else 4
                 sets = [(torch.randint(-127, 128, (mm, K), dtype=torch.int8, device=dev),
                          torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev),

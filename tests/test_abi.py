@@ -255,13 +255,17 @@ def test_plan_select_and_sku():
 def test_tail_split_workspace_sizes():
     # the optional split-K workspace of a partial last round: whole rounds, a
     # last round more than half full, or K too short take none
-    assert P.IntGemmPlan.select(P.IntGemmDescriptor(4192, 4096, 4096, output=P.ElementKind.Bf16)
+    assert P.IntGemmPlan.select(P.IntGemmDescriptor(4296, 4096, 4096, output=P.ElementKind.Bf16)
                                 ).workspace_size() == 16 * 16 * 65536 * 4
     # M % 256 in [1, 64] (N % 16 == 0) whose last row of tiles would start
-    # another round (or M <= 64) runs the last-rows pass, no workspace
-    for m in (4097, 4112, 4128, 4160, 1, 16, 64):
+    # another round (or M <= 64) runs the last-rows pass, no workspace; so
+    # does M % 256 in [65, 128] when K % 512 == 0 (the staged last rows)
+    for m in (4097, 4112, 4128, 4160, 1, 16, 64, 65, 100, 128, 4192, 4224):
         assert P.IntGemmPlan.select(P.IntGemmDescriptor(m, 4096, 4096, output=P.ElementKind.Bf16)
                                     ).workspace_size() == 0
+    # ... and K % 512 != 0 leaves those to the split when a workspace is given
+    assert P.IntGemmPlan.select(P.IntGemmDescriptor(4192, 4096, 3968, output=P.ElementKind.Bf16)
+                                ).workspace_size() == 16 * 15 * 65536 * 4
     assert P.IntGemmPlan.select(P.IntGemmDescriptor(512, 512, 8192, output=P.ElementKind.I32)
                                 ).workspace_size() == 4 * 32 * 65536 * 4
     # whole rounds, or a last round more than half full, or K too short: no workspace

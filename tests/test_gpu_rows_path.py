@@ -30,6 +30,11 @@ SHAPES = [(1, 256, 384), (16, 4096, 4096), (33, 272, 640), (64, 1040, 1152), (10
 # per wave, 16 last rows under 4 tile rows).
 DMA_SHAPES = [(1, 4096, 1024), (17, 512, 2048), (20, 1040, 3072), (32, 272, 8192), (1040, 16384, 1024)]
 SHAPES += DMA_SHAPES
+# 33 to 128 last rows with K % 512 == 0: A and B streamed through LDS in
+# 512-byte K stages (gemm_s8_rcr_rows_staged_kernel; 4 or 8 fragments, 1 to
+# 16 stages, the last-rows pass under 4 tile rows).
+STAGED_SHAPES = [(33, 512, 512), (65, 272, 1024), (97, 1040, 2560), (1060, 16384, 1536), (1124, 16384, 512)]
+SHAPES += STAGED_SHAPES
 
 
 def _rows(m):
@@ -72,7 +77,7 @@ def test_rows_path_i32_s8_w8a8(gpu, shape):
         assert np.array_equal(gw[r], O.gemm_w8a8_bf16(a, b, sa, sw, rows=(r, r + 1), nthreads=8)[0]), r
 
 
-@pytest.mark.parametrize("shape", [SHAPES[1], SHAPES[4], SHAPES[7], DMA_SHAPES[1], DMA_SHAPES[4]])
+@pytest.mark.parametrize("shape", [SHAPES[1], SHAPES[4], SHAPES[7], DMA_SHAPES[1], DMA_SHAPES[4], STAGED_SHAPES[2], STAGED_SHAPES[4]])
 def test_rows_path_bias_gelu(gpu, shape):
     m, n, k = shape
     print(f"case: rows path bias_gelu {shape}", flush=True)
@@ -88,7 +93,7 @@ def test_rows_path_bias_gelu(gpu, shape):
     assert np.array_equal(d.cpu().numpy()[rows], O.gemm_s8_epi(a[rows], b, "rcr", 0.004, 0.25, c[rows], bias, "gelu"))
 
 
-@pytest.mark.parametrize("shape", [SHAPES[2], SHAPES[3], SHAPES[5], SHAPES[6], DMA_SHAPES[2], DMA_SHAPES[3]])
+@pytest.mark.parametrize("shape", [SHAPES[2], SHAPES[3], SHAPES[5], SHAPES[6], DMA_SHAPES[2], DMA_SHAPES[3], STAGED_SHAPES[1], STAGED_SHAPES[3]])
 def test_rows_path_quantized_linear_f32_f64(gpu, shape):
     # f32: y = (sa*sw)*acc in f32; f64: f64 scales narrowed to f32, the same
     # product, widened (compose.cu:27-28).
@@ -119,9 +124,10 @@ def test_rows_path_quantized_linear_f32_f64(gpu, shape):
 
 
 def test_rows_path_with_and_without_split_workspace(gpu):
-    # 100 last rows at M = 1124, N = 16384: with the tail-split workspace the
-    # split runs, without it the streamed pass; both equal the oracle rows.
-    m, n, k = 1124, 16384, 1024
+    # 100 last rows at M = 1124, N = 16384, K = 1152 (not a multiple of the
+    # staged kernel's 512-byte stages): with the tail-split workspace the
+    # split runs, without it the last-rows pass; both equal the oracle rows.
+    m, n, k = 1124, 16384, 1152
     print("case: rows path vs tail split", flush=True)
     g = rng(77)
     a, b = int8_uniform(g, (m, k)), int8_uniform(g, (n, k))
@@ -138,10 +144,10 @@ def test_rows_path_with_and_without_split_workspace(gpu):
     assert np.array_equal(outs[0][rows], a[rows].astype(np.int64) @ b.astype(np.int64).T)
 
 
-@pytest.mark.parametrize("shape", [(7, 512, 2048), (30, 4096, 1024)])
+@pytest.mark.parametrize("shape", [(7, 512, 2048), (30, 4096, 1024), (100, 1024, 2048), (60, 512, 1536)])
 def test_rows_dma_padded_leading_dimensions(gpu, shape):
     # A and B views with row pitches past K (16-byte multiples): the
-    # LDS-streamed B kernel addresses rows by ldb and A rows by lda.
+    # LDS-streamed kernels address rows by ldb and A rows by lda.
     m, n, k = shape
     print(f"case: rows dma padded ld {shape}", flush=True)
     g = rng(m + n + k + 3)
