@@ -578,10 +578,12 @@ __global__ __launch_bounds__(512) void gemm_s8_rcr_rows_kernel(S8Args p, int m0)
 // wrap-around, order-free) and the tiles' epilogue.
 constexpr int kRowsDmaMaxK = 8192;
 // Up to this many last rows take gemm_s8_rcr_rows_dma_kernel (N = K = 4096,
-// rotated weights: M = 1 / 16 / 32 in 5.45 / 6.8 / 8.6 us against 6.7 / 7.9
-// / ... for gemm_s8_rcr_rows_kernel); past it the A rows, which every one of
-// the N / 16 workgroups reads in full, dominate both kernels equally.
-constexpr int kRowsDmaMaxRows = 32;
+// rotated weights: M = 1 / 16 in 5.45 / 6.8 us against 6.7 / 7.9 for
+// gemm_s8_rcr_rows_kernel, and against 6.2 / 6.6 us for the staged kernel
+// below with 1 KiB stages three deep).  From 17 rows on the staged kernel
+// is faster: M = 17 / 24 / 32 in 6.96 / 7.05 / 7.18 us against 7.4 / 7.9 /
+// 8.6 for this kernel with two fragments.
+constexpr int kRowsDmaMaxRows = 16;
 constexpr int kRowsDmaWaves = 16;
 
 template <int EPI, bool VecOut, int ACT, typename BiasT, int RF>
@@ -650,7 +652,7 @@ __global__ __launch_bounds__(1024) void gemm_s8_rcr_rows_dma_kernel(S8Args p, in
     epi(mb + 16 * wave + r16, n0 + 4 * g, sum);   // rows past M are not stored
 }
 
-// The last rows, 33 to 16 RF of them, with A and B streamed through LDS in
+// The last rows, 17 to 16 RF of them, with A and B streamed through LDS in
 // K stages of SB bytes, DEPTH stages in flight (K % SB == 0; A and B 16-byte
 // aligned, (m0 + 16 RF) * lda and N * ldb below 2^31; dynamic LDS of
 // DEPTH * (16 RF + 16) * SB bytes).  gemm_s8_rcr_rows_kernel reads its A
@@ -1230,33 +1232,31 @@ void launch_kernel(const S8Args &p, bool fast_k, hipStream_t stream, void *works
             if (tiles > 0)
                 hipLaunchKernelGGL((gemm_s8_rcr_dma_kernel<EPI, VecOut, ACT, BiasT>), dim3(tiles), dim3(DmaCfg::NT),
                                    0, stream, pm, TailSplit{0, 0, 1}, (int32_t *)nullptr);
-            const bool dma_b = rem <= kRowsDmaMaxRows && p.K % 1024 == 0 && p.K <= kRowsDmaMaxK &&
-                               p.ldb % 16 == 0 && aligned16(p.b) && (int64_t)p.N * p.ldb < (1ll << 31);
-            if (dma_b) {
-                // B rows; the 16 waves' partial sums reuse the same LDS
-                const size_t lds = std::max((size_t)16 * p.K, (size_t)kRowsDmaWaves * 2 * 1024);
-                if (rem <= 16)
-                    hipLaunchKernelGGL((gemm_s8_rcr_rows_dma_kernel<EPI, VecOut, ACT, BiasT, 1>), dim3(p.N / 16),
-                                       dim3(1024), lds, stream, p, pm.M);
+            const int rf_staged = rem <= 32 ? 2 : rem <= 64 ? 4 : 8;
+            // fast_k already holds A and B 16-byte aligned, lda and ldb multiples
+            // of 16 and both extents (rows rounded up to 256) below 2^31
+            if (rem > kRowsDmaMaxRows && p.K % kRowsStagedSB == 0) {
+                constexpr int SB = kRowsStagedSB;
+                // two fragments: three stages in flight (6.96 / 7.18 us at M = 17 / 32
+                // against 7.44 / 7.64 with two, 7.22 / 7.44 with four)
+                const int depth = rf_staged == 2 ? 3 : kRowsStagedDepth;
+                const size_t lds = (size_t)depth * (16 * rf_staged + 16) * SB;
+                if (rf_staged == 2)
+                    hipLaunchKernelGGL((gemm_s8_rcr_rows_staged_kernel<EPI, VecOut, ACT, BiasT, 2, SB, 3>),
+                                       dim3(p.N / 16), dim3(1024), lds, stream, p, pm.M);
+                else if (rf_staged == 4)
+                    hipLaunchKernelGGL((gemm_s8_rcr_rows_staged_kernel<EPI, VecOut, ACT, BiasT, 4, SB, kRowsStagedDepth>),
+                                       dim3(p.N / 16), dim3(1024), lds, stream, p, pm.M);
                 else
-                    hipLaunchKernelGGL((gemm_s8_rcr_rows_dma_kernel<EPI, VecOut, ACT, BiasT, 2>), dim3(p.N / 16),
-                                       dim3(1024), lds, stream, p, pm.M);
+                    hipLaunchKernelGGL((gemm_s8_rcr_rows_staged_kernel<EPI, VecOut, ACT, BiasT, 8, SB, kRowsStagedDepth>),
+                                       dim3(p.N / 16), dim3(1024), lds, stream, p, pm.M);
                 return;
             }
-            const int rf_staged = rem <= 64 ? 4 : 8;
-            const bool staged = rem > kRowsDmaMaxRows && p.K % kRowsStagedSB == 0 && aligned16(p.a) &&
-                                aligned16(p.b) && p.lda % 16 == 0 && p.ldb % 16 == 0 &&
-                                (int64_t)(pm.M + 16 * rf_staged) * p.lda < (1ll << 31) &&
-                                (int64_t)p.M * p.lda < (1ll << 31) && (int64_t)p.N * p.ldb < (1ll << 31);
-            if (staged) {
-                constexpr int SB = kRowsStagedSB, DEPTH = kRowsStagedDepth;
-                const size_t lds = (size_t)DEPTH * (16 * rf_staged + 16) * SB;
-                if (rf_staged == 4)
-                    hipLaunchKernelGGL((gemm_s8_rcr_rows_staged_kernel<EPI, VecOut, ACT, BiasT, 4, SB, DEPTH>),
-                                       dim3(p.N / 16), dim3(1024), lds, stream, p, pm.M);
-                else
-                    hipLaunchKernelGGL((gemm_s8_rcr_rows_staged_kernel<EPI, VecOut, ACT, BiasT, 8, SB, DEPTH>),
-                                       dim3(p.N / 16), dim3(1024), lds, stream, p, pm.M);
+            if (rem <= kRowsDmaMaxRows && p.K % 1024 == 0 && p.K <= kRowsDmaMaxK) {
+                // B rows; the 16 waves' partial sums reuse the same LDS
+                const size_t lds = std::max((size_t)16 * p.K, (size_t)kRowsDmaWaves * 1024);
+                hipLaunchKernelGGL((gemm_s8_rcr_rows_dma_kernel<EPI, VecOut, ACT, BiasT, 1>), dim3(p.N / 16),
+                                   dim3(1024), lds, stream, p, pm.M);
                 return;
             }
             const dim3 grid(p.N / 16), block(512);

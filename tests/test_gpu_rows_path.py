@@ -25,15 +25,16 @@ pytestmark = pytest.mark.gpu
 # of 64 bytes (each wave's batches, their remainder, or both).
 SHAPES = [(1, 256, 384), (16, 4096, 4096), (33, 272, 640), (64, 1040, 1152), (100, 512, 4096),
           (128, 256, 8192), (1025, 16384, 128), (1060, 16384, 256), (1124, 16384, 128)]
-# At most 32 last rows with K % 1024 == 0, K <= 8192: B streamed through LDS
-# (gemm_s8_rcr_rows_dma_kernel; 1 or 2 fragments, 1 to 8 chunks of 64 bytes
-# per wave, 16 last rows under 4 tile rows).
+# At most 16 last rows with K % 1024 == 0, K <= 8192: B streamed through LDS
+# (gemm_s8_rcr_rows_dma_kernel; 1 to 8 chunks of 64 bytes per wave, 16 last
+# rows under 4 tile rows); 17 to 32 rows (K % 512 == 0) take the staged
+# kernel with two fragments.
 DMA_SHAPES = [(1, 4096, 1024), (17, 512, 2048), (20, 1040, 3072), (32, 272, 8192), (1040, 16384, 1024)]
 SHAPES += DMA_SHAPES
-# 33 to 128 last rows with K % 512 == 0: A and B streamed through LDS in
-# 512-byte K stages (gemm_s8_rcr_rows_staged_kernel; 4 or 8 fragments, 1 to
-# 16 stages, the last-rows pass under 4 tile rows).
-STAGED_SHAPES = [(33, 512, 512), (65, 272, 1024), (97, 1040, 2560), (1060, 16384, 1536), (1124, 16384, 512)]
+# 17 to 128 last rows with K % 512 == 0: A and B streamed through LDS in
+# 512-byte K stages (gemm_s8_rcr_rows_staged_kernel; 2, 4 or 8 fragments, 1
+# to 16 stages, the last-rows pass under 4 tile rows).
+STAGED_SHAPES = [(17, 256, 512), (31, 1040, 1536), (33, 512, 512), (65, 272, 1024), (97, 1040, 2560), (1060, 16384, 1536), (1124, 16384, 512)]
 SHAPES += STAGED_SHAPES
 
 
@@ -77,7 +78,7 @@ def test_rows_path_i32_s8_w8a8(gpu, shape):
         assert np.array_equal(gw[r], O.gemm_w8a8_bf16(a, b, sa, sw, rows=(r, r + 1), nthreads=8)[0]), r
 
 
-@pytest.mark.parametrize("shape", [SHAPES[1], SHAPES[4], SHAPES[7], DMA_SHAPES[1], DMA_SHAPES[4], STAGED_SHAPES[2], STAGED_SHAPES[4]])
+@pytest.mark.parametrize("shape", [SHAPES[1], SHAPES[4], SHAPES[7], DMA_SHAPES[1], DMA_SHAPES[4], STAGED_SHAPES[0], STAGED_SHAPES[4], STAGED_SHAPES[6]])
 def test_rows_path_bias_gelu(gpu, shape):
     m, n, k = shape
     print(f"case: rows path bias_gelu {shape}", flush=True)
@@ -93,7 +94,7 @@ def test_rows_path_bias_gelu(gpu, shape):
     assert np.array_equal(d.cpu().numpy()[rows], O.gemm_s8_epi(a[rows], b, "rcr", 0.004, 0.25, c[rows], bias, "gelu"))
 
 
-@pytest.mark.parametrize("shape", [SHAPES[2], SHAPES[3], SHAPES[5], SHAPES[6], DMA_SHAPES[2], DMA_SHAPES[3], STAGED_SHAPES[1], STAGED_SHAPES[3]])
+@pytest.mark.parametrize("shape", [SHAPES[2], SHAPES[3], SHAPES[5], SHAPES[6], DMA_SHAPES[2], DMA_SHAPES[3], STAGED_SHAPES[1], STAGED_SHAPES[3], STAGED_SHAPES[5]])
 def test_rows_path_quantized_linear_f32_f64(gpu, shape):
     # f32: y = (sa*sw)*acc in f32; f64: f64 scales narrowed to f32, the same
     # product, widened (compose.cu:27-28).
