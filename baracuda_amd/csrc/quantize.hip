@@ -154,6 +154,64 @@ __global__ __launch_bounds__(kQBlock) void quantize_per_token_bf16v_kernel(
     }
 }
 
+// Rows of D <= 4096 bf16 values (D % 8 == 0, 16-byte aligned rows): one
+// wave per row, four rows per workgroup, chunk c = lane + 64 i of the row
+// in registers (kChunks <= 8), the max over a wave butterfly (no LDS, no
+// barrier), 8-byte non-temporal int8 stores.  kEven: D == 512 kChunks, no
+// per-chunk guards (they cost 0.7 us at 4096 x 4096).  4096 x 4096 over 24
+// rotated input / output pairs: 10.05 us against 10.7-10.9 for
+// quantize_per_token_bf16v_kernel and 9.45 us for a copy with the same
+// loads and stores and no arithmetic (bit-identical).
+constexpr int kQRowsPerBlock = 4;
+template <typename S, int kChunks, bool kEven>
+__global__ __launch_bounds__(64 * kQRowsPerBlock) void quantize_per_token_bf16w_kernel(
+    const uint16_t *__restrict__ x, S *__restrict__ scale, int8_t *__restrict__ q, int N, int D,
+    int qmin, int qmax) {
+    const float fqmax = (float)qmax;
+    const float fqmin = (float)qmin;
+    const int nch = D >> 3, lane = threadIdx.x & 63;
+    for (int n = blockIdx.x * kQRowsPerBlock + (threadIdx.x >> 6); n < N; n += gridDim.x * kQRowsPerBlock) {
+        const v4i *row = reinterpret_cast<const v4i *>(x + (int64_t)n * D);
+        v4i w[kChunks];
+        float m = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kChunks; ++i) {
+            const int c = lane + 64 * i;
+            w[i] = (kEven || c < nch) ? __builtin_nontemporal_load(row + c) : v4i{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int i = 0; i < kChunks; ++i)
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                const uint32_t u = (uint32_t)w[i][h];
+                m = fmaxf(m, fabsf(__uint_as_float(u << 16)));
+                m = fmaxf(m, fabsf(__uint_as_float(u & 0xffff0000u)));
+            }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+        const float s = m > 0.0f ? m / fqmax : 1.0f;
+        const float inv = s != 0.0f ? 1.0f / s : 0.0f;
+        if (lane == 0) scale[n] = (S)s;
+        int8_t *qrow = q + (int64_t)n * D;
+#pragma unroll
+        for (int i = 0; i < kChunks; ++i) {
+            const int c = lane + 64 * i;
+            if (!kEven && c >= nch) break;
+            uint32_t lo = 0, hi = 0;
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                const uint32_t u = (uint32_t)w[i][h];
+                const uint32_t q0 = (uint8_t)quant1(__uint_as_float(u << 16), inv, fqmin, fqmax);
+                const uint32_t q1 = (uint8_t)quant1(__uint_as_float(u & 0xffff0000u), inv, fqmin, fqmax);
+                const uint32_t pair = q0 | (q1 << 8);
+                if (h < 2) lo |= pair << (16 * h);
+                else hi |= pair << (16 * (h - 2));
+            }
+            __builtin_nontemporal_store(v2i{(int)lo, (int)hi}, reinterpret_cast<v2i *>(qrow + 8 * c));
+        }
+    }
+}
+
 int32_t quant_check(int32_t N, int32_t D, int32_t qmin, int32_t qmax) {
     if (N < 0 || D < 0) return kInvalid;
     if (qmin > qmax) return kInvalid;
@@ -178,6 +236,24 @@ int32_t launch_quant(int32_t N, int32_t D, int32_t qmin, int32_t qmax, const voi
             S *sc = (S *)scale;
             int8_t *qo = (int8_t *)output;
             const int nch = D / 8;
+            if (nch <= 64 * 8) {
+                const int wgrid = (N + kQRowsPerBlock - 1) / kQRowsPerBlock < 65535
+                                      ? (N + kQRowsPerBlock - 1) / kQRowsPerBlock : 65535;
+                const dim3 wb(64 * kQRowsPerBlock);
+#define BK_QW(CH)                                                                                          \
+    if (nch == 64 * (CH))                                                                                  \
+        hipLaunchKernelGGL((quantize_per_token_bf16w_kernel<S, CH, true>), dim3(wgrid), wb, 0, stream, xi, \
+                           sc, qo, N, D, qmin, qmax);                                                      \
+    else                                                                                                   \
+        hipLaunchKernelGGL((quantize_per_token_bf16w_kernel<S, CH, false>), dim3(wgrid), wb, 0, stream, xi, \
+                           sc, qo, N, D, qmin, qmax);
+                if (nch <= 64) { BK_QW(1) }
+                else if (nch <= 128) { BK_QW(2) }
+                else if (nch <= 256) { BK_QW(4) }
+                else { BK_QW(8) }
+#undef BK_QW
+                return launch_status();
+            }
             if (nch <= kQBlock)
                 hipLaunchKernelGGL((quantize_per_token_bf16v_kernel<S, 1>), dim3(grid), dim3(kQBlock), 0, stream,
                                    xi, sc, qo, N, D, qmin, qmax);

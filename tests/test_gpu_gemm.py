@@ -513,7 +513,8 @@ def _quant_gpu(x, dtype, qmin=-127, qmax=127):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.bfloat16])
 @pytest.mark.parametrize("shape", [(64, 4096), (7, 333), (3, 20000), (1, 1), (5, 16384), (9, 24), (6, 8192),
-                                   (5, 8200), (13, 8), (4, 2048), (4, 2056), (4, 4104)])
+                                   (5, 8200), (13, 8), (4, 2048), (4, 2056), (4, 4104), (5, 4096), (3, 4088),
+                                   (10, 520), (6, 1032), (7, 512), (9, 1024)])
 def test_quantize_per_token_bit_exact(gpu, dtype, shape):
     print(f"case: quantize {dtype} {shape}", flush=True)
     g = rng(shape[0] * 31 + shape[1])
@@ -614,13 +615,14 @@ def test_i32_operand_beyond_2gib(gpu):
     del a
 
 
-def test_quantize_bf16_input_beyond_2gib(gpu):
-    # 131080 x 16384 bf16: 2^31 + 131072 elements (4 GiB of input, 2 GiB of
-    # int8 output), so element indices and byte offsets pass 2^31: 64-bit row
-    # offsets in the 16-byte-chunk path; sampled rows (the last lie wholly
-    # past element 2^31) bit-exact.
-    n, dd = 131080, 16384
-    assert n * dd > 2 ** 31 and 131072 * dd == 2 ** 31
+@pytest.mark.parametrize("n, dd", [(131080, 16384), (524290, 4096)])
+def test_quantize_bf16_input_beyond_2gib(gpu, n, dd):
+    # 2^31 + 131072 / 8192 elements (4 GiB of input, 2 GiB of int8 output),
+    # so element indices and byte offsets pass 2^31: 64-bit row offsets in
+    # the 16-byte-chunk paths (a workgroup per row for D = 16384, a wave per
+    # row for D = 4096); sampled rows (the last lie wholly past element
+    # 2^31) bit-exact.
+    assert n * dd > 2 ** 31
     print(f"case: quantize beyond 2^31 elements {n}x{dd}", flush=True)
     gen = torch.Generator(device="cuda:0").manual_seed(93)
     x = torch.empty((n, dd), device="cuda:0", dtype=torch.bfloat16)
@@ -629,9 +631,13 @@ def test_quantize_bf16_input_beyond_2gib(gpu):
     scale = torch.empty(n, dtype=torch.float32, device="cuda:0")
     P.dynamic_range_quantize_per_token_sym(x, scale, q)
     sync()
-    rows = [0, 1, 65535, 131071, 131072, 131075, n - 1] + list(rng(94).integers(0, n, 4))
-    seen = x[rows].float().cpu().numpy()
+    first_past = 2 ** 31 // dd
+    rows = [0, 1, 65535, first_past - 1, first_past, min(first_past + 3, n - 1), n - 1]
+    rows += list(rng(94).integers(0, n, 4))
+    # rows read through basic-index views (x[r]), which raise on an index
+    # past N on the host instead of handing it to a device gather
+    seen = np.stack([x[int(r)].float().cpu().numpy() for r in rows])
     wq, ws = O.quantize_per_token_sym(seen)
-    assert np.array_equal(q[rows].cpu().numpy(), wq)
-    assert np.array_equal(scale[rows].cpu().numpy(), ws)
+    assert np.array_equal(np.stack([q[int(r)].cpu().numpy() for r in rows]), wq)
+    assert np.array_equal(np.array([scale[int(r)].item() for r in rows], dtype=np.float32), ws)
     del x, q
