@@ -560,6 +560,50 @@ __global__ __launch_bounds__(512) void gemm_s8_rcr_rows_kernel(S8Args p, int m0)
     epi(m0 + 16 * wave + r16, n0 + 4 * g, sum);   // rows past M are not stored
 }
 
+// One last row (M = 1 decode steps; K % (1024 BT) == 0): a workgroup of 4
+// waves owns 4 output columns and wave w streams B row n0 + w over all of K,
+// 16 bytes per lane of every kilobyte straight into registers (BT kilobytes
+// requested before their dot products), beside the same 16 bytes of the A
+// row (an L2 hit); v_dot4_i32_i8 sums the products exactly in int32 (wrapping
+// like the MFMA), a wave butterfly and LDS gather the 4 column sums and
+// lane 0 of wave 0 runs the tiles' epilogue.  No LDS staging and 4096 waves
+// at N = 4096: M = 1, N = K = 4096 over 20 rotated weight sets 4.84-4.96 us
+// against 5.47-5.49 for gemm_s8_rcr_rows_dma_kernel (bit-identical), and
+// 4.73 us for the same loads without the arithmetic.  From 2 rows on the A
+// loads and dot products cost more than the layout saves (M = 2 / 4 / 8:
+// 5.48 / 6.59 / 10.9 us against 5.52 / 5.66 / 5.98).
+template <int EPI, bool VecOut, int ACT, typename BiasT, int BT>
+__global__ __launch_bounds__(256) void gemm_s8_rcr_row1_kernel(S8Args p, int m0) {
+    __shared__ int colsum[4];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n0 = blockIdx.x * 4;
+    const int nch = p.K >> 10;
+    const int8_t *brow = p.b + (int64_t)(n0 + wave) * p.ldb + lane * 16;
+    const int8_t *arow = p.a + (int64_t)m0 * p.lda + lane * 16;
+    int acc = 0;
+    for (int c0 = 0; c0 < nch; c0 += BT) {
+        v4i av[BT], bv[BT];
+#pragma unroll
+        for (int u = 0; u < BT; ++u) av[u] = *reinterpret_cast<const v4i *>(arow + (int64_t)(c0 + u) * 1024);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < BT; ++u)
+            bv[u] = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(brow + (int64_t)(c0 + u) * 1024));
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < BT; ++u)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) acc = __builtin_amdgcn_sdot4(av[u][q], bv[u][q], acc, false);
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) acc = (int)((uint32_t)acc + (uint32_t)__shfl_xor(acc, off, 64));
+    if (lane == 0) colsum[wave] = acc;
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    const S8Epilogue<EPI, VecOut, ACT, BiasT> epi{p};
+    epi(m0, n0, v4i{colsum[0], colsum[1], colsum[2], colsum[3]});
+}
+
 // The last rows (at most 16 * RF), B streamed through LDS: K % 1024 == 0,
 // K <= kRowsDmaMaxK, B 16-byte aligned with N * ldb < 2^31, dynamic LDS of
 // max(16 * K, 16 KiB * RF) bytes.  A workgroup of 16 waves owns 16 output
@@ -1250,6 +1294,15 @@ void launch_kernel(const S8Args &p, bool fast_k, hipStream_t stream, void *works
                 else
                     hipLaunchKernelGGL((gemm_s8_rcr_rows_staged_kernel<EPI, VecOut, ACT, BiasT, 8, SB, kRowsStagedDepth>),
                                        dim3(p.N / 16), dim3(1024), lds, stream, p, pm.M);
+                return;
+            }
+            if (rem == 1 && p.K % 1024 == 0) {
+                if (p.K % 2048 == 0)
+                    hipLaunchKernelGGL((gemm_s8_rcr_row1_kernel<EPI, VecOut, ACT, BiasT, 2>), dim3(p.N / 4), dim3(256),
+                                       0, stream, p, pm.M);
+                else
+                    hipLaunchKernelGGL((gemm_s8_rcr_row1_kernel<EPI, VecOut, ACT, BiasT, 1>), dim3(p.N / 4), dim3(256),
+                                       0, stream, p, pm.M);
                 return;
             }
             if (rem <= kRowsDmaMaxRows && p.K % 1024 == 0 && p.K <= kRowsDmaMaxK) {

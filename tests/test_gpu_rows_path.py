@@ -25,12 +25,17 @@ pytestmark = pytest.mark.gpu
 # of 64 bytes (each wave's batches, their remainder, or both).
 SHAPES = [(1, 256, 384), (16, 4096, 4096), (33, 272, 640), (64, 1040, 1152), (100, 512, 4096),
           (128, 256, 8192), (1025, 16384, 128), (1060, 16384, 256), (1124, 16384, 128)]
-# At most 16 last rows with K % 1024 == 0, K <= 8192: B streamed through LDS
+# 2 to 16 last rows with K % 1024 == 0, K <= 8192: B streamed through LDS
 # (gemm_s8_rcr_rows_dma_kernel; 1 to 8 chunks of 64 bytes per wave, 16 last
 # rows under 4 tile rows); 17 to 32 rows (K % 512 == 0) take the staged
 # kernel with two fragments.
-DMA_SHAPES = [(1, 4096, 1024), (17, 512, 2048), (20, 1040, 3072), (32, 272, 8192), (1040, 16384, 1024)]
+DMA_SHAPES = [(1, 4096, 1024), (17, 512, 2048), (20, 1040, 3072), (32, 272, 8192), (1040, 16384, 1024),
+              (2, 272, 1024), (9, 512, 2048), (1039, 16384, 3072)]
 SHAPES += DMA_SHAPES
+# One last row with K % 1024 == 0: the dot4 row kernel (gemm_s8_rcr_row1_kernel;
+# 1 or 2 kilobytes per batch, the row under 4 tile rows).
+ROW1_SHAPES = [(1, 512, 2048), (1, 1040, 3072), (1, 4096, 4096), (1025, 16384, 2048)]
+SHAPES += ROW1_SHAPES
 # 17 to 128 last rows with K % 512 == 0: A and B streamed through LDS in
 # 512-byte K stages (gemm_s8_rcr_rows_staged_kernel; 2, 4 or 8 fragments, 1
 # to 16 stages, the last-rows pass under 4 tile rows).
@@ -78,7 +83,7 @@ def test_rows_path_i32_s8_w8a8(gpu, shape):
         assert np.array_equal(gw[r], O.gemm_w8a8_bf16(a, b, sa, sw, rows=(r, r + 1), nthreads=8)[0]), r
 
 
-@pytest.mark.parametrize("shape", [SHAPES[1], SHAPES[4], SHAPES[7], DMA_SHAPES[1], DMA_SHAPES[4], STAGED_SHAPES[0], STAGED_SHAPES[4], STAGED_SHAPES[6]])
+@pytest.mark.parametrize("shape", [SHAPES[1], SHAPES[4], SHAPES[7], DMA_SHAPES[1], DMA_SHAPES[4], STAGED_SHAPES[0], STAGED_SHAPES[4], STAGED_SHAPES[6], ROW1_SHAPES[0], ROW1_SHAPES[3], DMA_SHAPES[6]])
 def test_rows_path_bias_gelu(gpu, shape):
     m, n, k = shape
     print(f"case: rows path bias_gelu {shape}", flush=True)
@@ -94,7 +99,7 @@ def test_rows_path_bias_gelu(gpu, shape):
     assert np.array_equal(d.cpu().numpy()[rows], O.gemm_s8_epi(a[rows], b, "rcr", 0.004, 0.25, c[rows], bias, "gelu"))
 
 
-@pytest.mark.parametrize("shape", [SHAPES[2], SHAPES[3], SHAPES[5], SHAPES[6], DMA_SHAPES[2], DMA_SHAPES[3], STAGED_SHAPES[1], STAGED_SHAPES[3], STAGED_SHAPES[5]])
+@pytest.mark.parametrize("shape", [SHAPES[2], SHAPES[3], SHAPES[5], SHAPES[6], DMA_SHAPES[2], DMA_SHAPES[3], STAGED_SHAPES[1], STAGED_SHAPES[3], STAGED_SHAPES[5], ROW1_SHAPES[1]])
 def test_rows_path_quantized_linear_f32_f64(gpu, shape):
     # f32: y = (sa*sw)*acc in f32; f64: f64 scales narrowed to f32, the same
     # product, widened (compose.cu:27-28).
@@ -145,7 +150,7 @@ def test_rows_path_with_and_without_split_workspace(gpu):
     assert np.array_equal(outs[0][rows], a[rows].astype(np.int64) @ b.astype(np.int64).T)
 
 
-@pytest.mark.parametrize("shape", [(7, 512, 2048), (30, 4096, 1024), (100, 1024, 2048), (60, 512, 1536)])
+@pytest.mark.parametrize("shape", [(7, 512, 2048), (30, 4096, 1024), (100, 1024, 2048), (60, 512, 1536), (1, 1024, 2048)])
 def test_rows_dma_padded_leading_dimensions(gpu, shape):
     # A and B views with row pitches past K (16-byte multiples): the
     # LDS-streamed kernels address rows by ldb and A rows by lda.
