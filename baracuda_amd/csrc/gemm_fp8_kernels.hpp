@@ -247,6 +247,122 @@ __global__ __launch_bounds__(F8DmaCfg::NT, 1) void gemm_fp8_dma_kernel(F8Args p)
     M2::for_each_quad<P>(acc, [&](int ml, int nl, const v4f &v) { epi(m_base + ml, n_base + nl, v); });
 }
 
+// RCR last rows (1 to 16 RF of them, m0 = the first): A and B streamed
+// through LDS in K stages of SB bytes, DEPTH stages in flight.  A workgroup
+// of 16 waves owns 16 output columns; each stage holds its 16 RF A rows
+// (rows past M land as zeros) then its 16 B rows, row r at r * SB with
+// 16-byte unit u at slot u ^ (r & 15) (conflict-free fragment reads), each
+// DMA instruction filling 1 KiB of it (64 consecutive units of the
+// row-major stage), all issued before anything waits.  Wave w owns 128-byte
+// chunk w % CH of every stage (CH = SB / 128) and row fragments
+// w / CH + (16 / CH) i: one v_mfma_f32_16x16x128_f8f6f4 per fragment and
+// stage (B rows as the first operand, so lane l ends with A row l % 16 and
+// columns 4 (l / 16) .. + 3).  The CH chunk partials of a fragment are added
+// in chunk order through LDS and waves 0 .. RF - 1 run the tiles' epilogue.
+// Requirements (checked by the launcher): K % SB == 0, the fast path's
+// alignment and 2^31 extents, N % 16 == 0; dynamic LDS of
+// DEPTH * (16 RF + 16) * SB bytes.
+template <int FMT, int EPI, int ACT, int RF, int SB, int DEPTH>
+__global__ __launch_bounds__(1024) void gemm_fp8_rcr_rows_staged_kernel(F8Args p, int m0) {
+    constexpr int WAVES = 16, CH = SB / 128;
+    constexpr int FPW = RF * CH / WAVES;                 // row fragments per wave
+    constexpr int FSTEP = WAVES / CH;
+    constexpr int ROWS = 16 * RF + 16;                   // A then B rows of a stage
+    constexpr int STAGE = ROWS * SB;
+    constexpr int UPR = SB / 16;                         // 16-byte units per row
+    constexpr int NI = ROWS * UPR / 64;                  // 1 KiB DMA instructions per stage
+    constexpr int HI = (NI + WAVES - 1) / WAVES, LO = NI / WAVES;
+    static_assert(FPW >= 1 && RF * CH % WAVES == 0 && UPR >= 16 && (ROWS * UPR) % 64 == 0 && DEPTH >= 2 &&
+                      DEPTH <= 4 && RF * CH * 1024 <= DEPTH * STAGE,
+                  "stage split");
+    constexpr int F = FMT == FMT_E5M2 ? 1 : 0;
+    extern __shared__ __attribute__((aligned(1024))) int8_t lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r16 = lane & 15, g = lane >> 4;
+    const int n0 = blockIdx.x * 16;
+    const v4i ra = mfma2::make_rsrc(p.a, (uint32_t)((int64_t)p.M * p.lda));
+    const v4i rb = mfma2::make_rsrc(p.b, (uint32_t)((int64_t)p.N * p.ldb));
+    // DMA instruction j of a stage: units 64 j .. 64 j + 63 of the row-major
+    // stage, lane L fetching unit (64 j + L) % UPR of row (64 j + L) / UPR
+    auto dma_stage = [&](int st, int8_t *buf) {
+        const int k0 = st * SB;
+        for (int j = wave; j < NI; j += WAVES) {
+            const int idx = 64 * j + lane;
+            const int r = idx / UPR, slot = idx % UPR;
+            const int unit = slot ^ (r & 15);
+            if (r < 16 * RF)
+                mfma2::dma16(ra, (int)((int64_t)(m0 + r) * p.lda) + 16 * unit, k0, buf + j * 1024);
+            else
+                mfma2::dma16(rb, (int)((int64_t)(n0 + r - 16 * RF) * p.ldb) + 16 * unit, k0, buf + j * 1024);
+        }
+    };
+    const bool hi = NI % WAVES == 0 || wave < NI % WAVES;
+    const int ns = p.K / SB;
+    for (int st = 0; st < DEPTH && st < ns; ++st) dma_stage(st, lds + st * STAGE);
+    const int c = wave % CH, f0 = wave / CH;
+    v4f acc[FPW];
+#pragma unroll
+    for (int i = 0; i < FPW; ++i) acc[i] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    // 32 bytes of K per lane: logical units 8 c + 2 g and 8 c + 2 g + 1
+    const int u0 = 16 * ((8 * c + 2 * g) ^ r16), u1 = 16 * ((8 * c + 2 * g + 1) ^ r16);
+    for (int st = 0; st < ns; ++st) {
+        const int later = min(DEPTH - 1, ns - 1 - st);
+        if (later == 0) mfma2::wait_vmcnt<0>();
+        else if (later == 1) { if (hi) mfma2::wait_vmcnt<HI>(); else mfma2::wait_vmcnt<LO>(); }
+        else if (later == 2) { if (hi) mfma2::wait_vmcnt<2 * HI>(); else mfma2::wait_vmcnt<2 * LO>(); }
+        else { if (hi) mfma2::wait_vmcnt<3 * HI>(); else mfma2::wait_vmcnt<3 * LO>(); }
+        __syncthreads();
+        int8_t *buf = lds + (st % DEPTH) * STAGE;
+        const int8_t *brow = buf + (16 * RF + r16) * SB;
+        const v4i blo = *reinterpret_cast<const v4i *>(brow + u0), bhi = *reinterpret_cast<const v4i *>(brow + u1);
+        const v8i bv = (v8i){blo[0], blo[1], blo[2], blo[3], bhi[0], bhi[1], bhi[2], bhi[3]};
+#pragma unroll
+        for (int i = 0; i < FPW; ++i) {
+            const int8_t *arow = buf + (16 * (f0 + FSTEP * i) + r16) * SB;
+            const v4i alo = *reinterpret_cast<const v4i *>(arow + u0), ahi = *reinterpret_cast<const v4i *>(arow + u1);
+            const v8i av = (v8i){alo[0], alo[1], alo[2], alo[3], ahi[0], ahi[1], ahi[2], ahi[3]};
+            acc[i] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bv, av, acc[i], F, F, 0, 0, 0, 0);
+        }
+        __syncthreads();   // every wave is done with this buffer
+        if (st + DEPTH < ns) dma_stage(st + DEPTH, buf);
+    }
+    // partial sums of fragment f, chunk c: part[f][c][lane]
+    v4f *part = reinterpret_cast<v4f *>(lds);
+#pragma unroll
+    for (int i = 0; i < FPW; ++i) part[((f0 + FSTEP * i) * CH + c) * 64 + lane] = acc[i];
+    __syncthreads();
+    if (wave >= RF) return;
+    v4f sum = part[(wave * CH) * 64 + lane];
+#pragma unroll
+    for (int cc = 1; cc < CH; ++cc) {
+        const v4f v = part[(wave * CH + cc) * 64 + lane];
+        sum = v4f{sum[0] + v[0], sum[1] + v[1], sum[2] + v[2], sum[3] + v[3]};
+    }
+    const F8Epilogue<FMT, EPI, true, ACT> epi{p};
+    epi(m0 + 16 * wave + r16, n0 + 4 * g, sum);   // rows past M are not stored
+}
+
+// Stage shapes of the FP8 last-rows kernel per fragment count: 1 fragment
+// 2 KiB stages (a wave per 128-byte chunk), 2 fragments 1 KiB three deep,
+// 4 and 8 fragments 512 bytes two deep (128 / 144 / 80 / 144 KiB of LDS).
+template <int FMT, int EPI, int ACT>
+bool launch_fp8_rows(const F8Args &p, int m0, int rem, hipStream_t stream) {
+    const dim3 grid(p.N / 16), block(1024);
+#define BK_F8ROWS(RF, SB, DEPTH)                                                                         \
+    if (rem <= 16 * (RF) && p.K % (SB) == 0) {                                                           \
+        hipLaunchKernelGGL((gemm_fp8_rcr_rows_staged_kernel<FMT, EPI, ACT, RF, SB, DEPTH>), grid, block,  \
+                           (size_t)(DEPTH) * (16 * (RF) + 16) * (SB), stream, p, m0);                     \
+        return true;                                                                                     \
+    }
+    BK_F8ROWS(1, 2048, 2)
+    BK_F8ROWS(2, 1024, 3)
+    BK_F8ROWS(4, 512, 2)
+    BK_F8ROWS(8, 512, 2)
+#undef BK_F8ROWS
+    return false;
+}
+
 template <int FMT, int LAYOUT, int EPI, int ACT>
 int32_t launch_fp8(const F8Args &p, hipStream_t stream) {
     const int out_elem = EPI == F8_F32 ? 4 : (EPI == F8_BF16 ? 2 : 1);
@@ -260,6 +376,21 @@ int32_t launch_fp8(const F8Args &p, hipStream_t stream) {
     const bool fast = p.K % mfma2::BK == 0 && p.lda % 16 == 0 && p.ldb % 16 == 0 && aligned16(p.a) &&
                       aligned16(p.b) && p.N % 4 == 0 && pad_m * p.lda < (1ll << 31) && pad_b < (1ll << 31) &&
                       p.ldd % 4 == 0 && (reinterpret_cast<uintptr_t>(p.d) % (4 * out_elem)) == 0;
+    if (fast && LAYOUT == F8_RCR) {
+        // the last rows as their own pass when a row of tiles would start
+        // another round (decode-sized M: all of it)
+        const int rem = mfma2::last_rows_pass(p.M, p.N, 128);
+        if (rem != 0 && p.K % 512 == 0) {
+            F8Args pm = p;
+            pm.M = p.M - rem;
+            const int tiles = (pm.M / mfma2::BM) * ((p.N + mfma2::BN - 1) / mfma2::BN);
+            if (tiles > 0)
+                hipLaunchKernelGGL((gemm_fp8_dma_kernel<FMT, LAYOUT, EPI, ACT>), dim3(tiles), dim3(F8DmaCfg::NT),
+                                   0, stream, pm);
+            if (launch_fp8_rows<FMT, EPI, ACT>(p, pm.M, rem, stream)) return launch_status();
+            // K % 512 == 0 always finds a stage shape
+        }
+    }
     if (fast) {
         const int tiles = (int)(pad_m / mfma2::BM) * ((p.N + mfma2::BN - 1) / mfma2::BN);
         hipLaunchKernelGGL((gemm_fp8_dma_kernel<FMT, LAYOUT, EPI, ACT>), dim3(tiles), dim3(F8DmaCfg::NT),

@@ -472,6 +472,25 @@ __device__ __forceinline__ void dma16(const v4i &rsrc, int voff, int soff, const
 
 __device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// Wait until at most N of this wave's vector-memory operations (DMAs
+// included) are outstanding; they complete in issue order.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
+
+// Last rows of M run by a separate last-rows launch instead of a row of
+// 256-row tiles (N % 16 == 0): M % 256 in [1, limit] (all of M when
+// M <= limit: no tiles at all), when that row of tiles would start another
+// round of tiles on the 256 CUs (it costs nothing extra when it fits the
+// idle CUs of the last round).  Returns the number of last rows, or 0.
+inline int last_rows_pass(int M, int N, int limit) {
+    if (N <= 0 || N % 16 != 0 || M <= 0) return 0;
+    const int rem = M % 256;
+    if (rem == 0 || rem > limit) return 0;
+    const int64_t tn = (N + 255) / 256, main_tiles = (int64_t)(M - rem) / 256 * tn;
+    if (main_tiles > 0 && (main_tiles + tn + 255) / 256 == (main_tiles + 255) / 256) return 0;
+    return rem;
+}
+
 template <class C>
 __device__ __forceinline__ void dma_operand(int8_t *dst, const DmaOperand<false> &d, int kbyte) {
     constexpr int ROWS_PER_WAVE = C::ROWS_PER_WAVE;

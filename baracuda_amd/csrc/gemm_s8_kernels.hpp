@@ -223,14 +223,7 @@ struct TailSplit {
 constexpr int kRowsPathMax = 128;
 constexpr int kRowsPathAlways = 64;
 constexpr int kRowsStagedSB = 512, kRowsStagedDepth = 2;
-inline int rows_path_rows(int M, int N, int limit = kRowsPathMax) {
-    if (N <= 0 || N % 16 != 0 || M <= 0) return 0;
-    const int rem = M % 256;
-    if (rem == 0 || rem > limit) return 0;
-    const int64_t tn = (N + 255) / 256, main_tiles = (int64_t)(M - rem) / 256 * tn;
-    if (main_tiles > 0 && (main_tiles + tn + 255) / 256 == (main_tiles + 255) / 256) return 0;
-    return rem;
-}
+inline int rows_path_rows(int M, int N, int limit = kRowsPathMax) { return mfma2::last_rows_pass(M, N, limit); }
 
 inline TailSplit tail_split_plan(int M, int N, int K) {
     TailSplit t{0, 0, 1};
@@ -716,9 +709,6 @@ __global__ __launch_bounds__(1024) void gemm_s8_rcr_rows_dma_kernel(S8Args p, in
 // 8.0 / 8.8 / 11.3 / 11.6 us, against 9.8-10.3 / 10.0-10.5 / 12.0-13.2 /
 // 12.3-13.5 us for 256-byte stages two to four deep; three 512-byte stages
 // measure the same as two (kRowsStagedSB, kRowsStagedDepth).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
-
 template <int EPI, bool VecOut, int ACT, typename BiasT, int RF, int SB, int DEPTH>
 __global__ __launch_bounds__(1024) void gemm_s8_rcr_rows_staged_kernel(S8Args p, int m0) {
     constexpr int WAVES = 16, CH = SB / 64;                  // 64-byte chunks per stage
@@ -763,10 +753,10 @@ __global__ __launch_bounds__(1024) void gemm_s8_rcr_rows_staged_kernel(S8Args p,
     for (int st = 0; st < ns; ++st) {
         // stage st has landed once at most the later stages' DMAs are outstanding
         const int later = min(DEPTH - 1, ns - 1 - st);
-        if (later == 0) wait_vmcnt<0>();
-        else if (later == 1) { if (hi) wait_vmcnt<HI>(); else wait_vmcnt<LO>(); }
-        else if (later == 2) { if (hi) wait_vmcnt<2 * HI>(); else wait_vmcnt<2 * LO>(); }
-        else { if (hi) wait_vmcnt<3 * HI>(); else wait_vmcnt<3 * LO>(); }
+        if (later == 0) mfma2::wait_vmcnt<0>();
+        else if (later == 1) { if (hi) mfma2::wait_vmcnt<HI>(); else mfma2::wait_vmcnt<LO>(); }
+        else if (later == 2) { if (hi) mfma2::wait_vmcnt<2 * HI>(); else mfma2::wait_vmcnt<2 * LO>(); }
+        else { if (hi) mfma2::wait_vmcnt<3 * HI>(); else mfma2::wait_vmcnt<3 * LO>(); }
         __syncthreads();
         int8_t *buf = lds + (st % DEPTH) * STAGE;
         const int sl = 16 * ((4 * c + g) ^ r16);                 // row & 15 == r16 for every fragment row

@@ -1,0 +1,107 @@
+"""GPU parity of the FP8 RCR last-rows pass (gemm_fp8_rcr_rows_staged_kernel):
+decode-sized M (all of it) and the last M % 256 rows when a row of tiles would
+start another round, for every stage shape the launcher picks (1 fragment /
+2 KiB stages, 2 / 1 KiB, 4 and 8 / 512 B) and the fall-backs when K does not
+divide the preferred stage.
+
+The reference smoke pattern (fp8_bias_smoke.rs inputs: small dyadic values
+whose f32 partial sums are exact in any order) must come out bit-exact for
+Identity / Bias / BiasRelu and within one grid step for BiasGelu / BiasSilu,
+as on the tile path; random N(0,1) operands keep the tile path's tolerance
+(1e-3 relative + FP8_FLOOR * sum|a*b| for f32 accumulators, one bf16 ulp plus
+that floor for bf16 outputs).
+"""
+import numpy as np
+import pytest
+import torch
+
+from baracuda_amd import plans as P
+from oracle import oracle as O
+from tests.gpu_util import FP8_FLOOR, bf16_ulp, dev, sync
+from tests.test_gpu_fp8_epi import EPIS, ACT, _run, _steps, _want
+from tests.test_gpu_gemm import _fp8_check_acc, _fp8_inputs, _fp8_run
+
+pytestmark = pytest.mark.gpu
+
+# (M, N, K): last rows 1 / 16 (2 KiB stages), 5 with K % 2048 != 0 (1 KiB),
+# 17 / 32 (1 KiB), 9 and 20 with K % 1024 != 0 (512 B), 33 / 64 (512 B, 4
+# fragments), 65 / 100 / 128 (8 fragments); under 4 tile rows at N = 16384
+# (the tiles fill one round exactly): 1 / 40 / 128 last rows.
+SHAPES = [(1, 256, 4096), (16, 512, 2048), (5, 272, 1024), (17, 512, 1024), (32, 1040, 3072),
+          (9, 256, 1536), (20, 272, 512), (33, 512, 512), (64, 256, 2560), (65, 1040, 1024),
+          (100, 512, 4096), (128, 256, 512), (1025, 16384, 2048), (1064, 16384, 512), (1152, 16384, 1024)]
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_fp8_rows_f32_and_bf16(gpu, shape):
+    m, n, k = shape
+    print(f"case: fp8 rows f32/bf16 {shape}", flush=True)
+    a, b, sa, sb = _fp8_inputs(m, n, k, seed=m + n + k)
+    rows = (max(0, m - m % 256 - 2), m) if m > 256 else None
+    got = _fp8_run(a, b, P.ElementKind.F32, alpha=1.0).cpu().numpy()
+    exact = _fp8_check_acc(got[rows[0]:rows[1]] if rows else got, a, b, rows=rows)
+    gotb = _fp8_run(a, b, P.ElementKind.Bf16, scale_a=sa, scale_b=sb).float().cpu().numpy().astype(np.float64)
+    if rows:
+        gotb = gotb[rows[0]:rows[1]]
+    ta = np.abs(O.e4m3_to_f32(a).astype(np.float64))
+    tb = np.abs(O.e4m3_to_f32(b).astype(np.float64))
+    s = float(np.float32(sa) * np.float32(sb))
+    want = exact * s
+    tol = bf16_ulp(want) + FP8_FLOOR * ((ta[rows[0]:rows[1]] if rows else ta) @ tb.T) * s
+    assert np.all(np.abs(gotb - want) <= tol)
+
+
+@pytest.mark.parametrize("epi", EPIS)
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("shape", [SHAPES[0], SHAPES[3], SHAPES[7], SHAPES[10], SHAPES[13]])
+def test_fp8_rows_reference_pattern(gpu, shape, fmt, epi):
+    m, n, k = shape
+    print(f"case: fp8 rows pattern {fmt} {epi.value} {shape}", flush=True)
+    a = O.f32_to_fp8((((np.arange(m * k) * 5) % 13) - 6.0) * 0.125, fmt).reshape(m, k)
+    b = O.f32_to_fp8((((np.arange(k * n) * 7) % 11) - 5.0) * 0.125, fmt).reshape(n, k)
+    bias = (((np.arange(n) % 5) - 2) * 0.5).astype(np.float32)
+    got = _run(fmt, P.LayoutSku.Rcr, epi, a, b, bias=bias)
+    want = _want(fmt, P.LayoutSku.Rcr, epi, a, b, None, bias, 0.25, 0.0)
+    if ACT[epi] in (None, "relu"):
+        assert np.array_equal(got, want)
+    else:
+        assert _steps(got, want, fmt).max() <= 1.0
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("shape", [SHAPES[1], SHAPES[4], SHAPES[9], SHAPES[14]])
+def test_fp8_rows_random_with_c(gpu, shape, fmt):
+    # C (beta = 0.5) and a BiasGelu epilogue on random operands: one grid step
+    # plus the MFMA's summation floor, as the tile path's test.
+    m, n, k = shape
+    print(f"case: fp8 rows random with C {fmt} {shape}", flush=True)
+    g = np.random.default_rng(m * 7 + n + k)
+    a = O.f32_to_fp8(g.standard_normal((m, k)).astype(np.float32), fmt)
+    b = O.f32_to_fp8(g.standard_normal((n, k)).astype(np.float32), fmt)
+    c = O.f32_to_fp8(g.standard_normal((m, n)).astype(np.float32), fmt)
+    bias = g.standard_normal(n).astype(np.float32)
+    alpha = 1.0 / 16
+    epi = P.EpilogueKind.BiasGelu
+    got = _run(fmt, P.LayoutSku.Rcr, epi, a, b, c=c, bias=bias, alpha=alpha, beta=0.5)
+    want = _want(fmt, P.LayoutSku.Rcr, epi, a, b, c, bias, alpha, 0.5)
+    fa = np.abs(O.fp8_to_f32(a, fmt).astype(np.float64))
+    fb = np.abs(O.fp8_to_f32(b, fmt).astype(np.float64))
+    st = _steps(got, want, fmt, FP8_FLOOR * alpha * (fa @ fb.T))
+    assert st.max() <= 1.0 and (got != want).mean() < 0.02
+
+
+def test_fp8_rows_deterministic_and_untouched_columns(gpu):
+    # Repeated calls give identical bits (fixed chunk order); D columns and
+    # rows outside the problem (a wider, taller buffer) are not written.
+    m, n, k = 40, 512, 2048
+    a, b, sa, sb = _fp8_inputs(m, n, k, seed=11)
+    plan = P.Fp8GemmPlan.select(P.Fp8GemmDescriptor(m, n, k, output=P.ElementKind.Bf16))
+    outs = []
+    for _ in range(3):
+        big = torch.full((m + 3, n + 64), -7.0, dtype=torch.bfloat16, device="cuda:0")
+        plan.run(dev(a), dev(b), big[:m, :n], scale_a=sa, scale_b=sb)
+        sync()
+        h = big.float().cpu().numpy()
+        assert np.all(h[:, n:] == -7.0) and np.all(h[m:, :] == -7.0)
+        outs.append(h[:m, :n])
+    assert all(np.array_equal(outs[0], o) for o in outs[1:])
