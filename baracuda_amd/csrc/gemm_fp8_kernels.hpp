@@ -249,38 +249,39 @@ __global__ __launch_bounds__(F8DmaCfg::NT, 1) void gemm_fp8_dma_kernel(F8Args p)
 
 // RCR last rows (1 to 16 RF of them, m0 = the first): A and B streamed
 // through LDS in K stages of SB bytes, DEPTH stages in flight.  A workgroup
-// of 16 waves owns 16 output columns; each stage holds its 16 RF A rows
-// (rows past M land as zeros) then its 16 B rows, row r at r * SB with
+// of 16 waves owns 16 NB output columns; each stage holds its 16 RF A rows
+// (rows past M land as zeros) then its 16 NB B rows, row r at r * SB with
 // 16-byte unit u at slot u ^ (r & 15) (conflict-free fragment reads), each
 // DMA instruction filling 1 KiB of it (64 consecutive units of the
 // row-major stage), all issued before anything waits.  Wave w owns 128-byte
-// chunk w % CH of every stage (CH = SB / 128) and row fragments
-// w / CH + (16 / CH) i: one v_mfma_f32_16x16x128_f8f6f4 per fragment and
-// stage (B rows as the first operand, so lane l ends with A row l % 16 and
-// columns 4 (l / 16) .. + 3).  The CH chunk partials of a fragment are added
-// in chunk order through LDS and waves 0 .. RF - 1 run the tiles' epilogue.
-// Requirements (checked by the launcher): K % SB == 0, the fast path's
-// alignment and 2^31 extents, N % 16 == 0; dynamic LDS of
-// DEPTH * (16 RF + 16) * SB bytes.
-template <int FMT, int EPI, int ACT, int RF, int SB, int DEPTH>
+// chunk w % CH of every stage (CH = SB / 128), A row fragments
+// w / CH + (16 / CH) i and all NB B fragments: one
+// v_mfma_f32_16x16x128_f8f6f4 per fragment pair and stage (B rows as the
+// first operand, so lane l ends with A row l % 16 and columns 4 (l / 16) ..
+// + 3).  The CH chunk partials of a fragment pair are added in chunk order
+// through LDS and the waves run the tiles' epilogue, one fragment pair at a
+// time.  Requirements (checked by the launcher): K % SB == 0, the fast
+// path's alignment and 2^31 extents, N % (16 NB) == 0; dynamic LDS of
+// DEPTH * (16 RF + 16 NB) * SB bytes.
+template <int FMT, int EPI, int ACT, int RF, int NB, int SB, int DEPTH>
 __global__ __launch_bounds__(1024) void gemm_fp8_rcr_rows_staged_kernel(F8Args p, int m0) {
     constexpr int WAVES = 16, CH = SB / 128;
-    constexpr int FPW = RF * CH / WAVES;                 // row fragments per wave
+    constexpr int FPW = RF * CH / WAVES;                 // A row fragments per wave
     constexpr int FSTEP = WAVES / CH;
-    constexpr int ROWS = 16 * RF + 16;                   // A then B rows of a stage
+    constexpr int ROWS = 16 * RF + 16 * NB;              // A then B rows of a stage
     constexpr int STAGE = ROWS * SB;
     constexpr int UPR = SB / 16;                         // 16-byte units per row
     constexpr int NI = ROWS * UPR / 64;                  // 1 KiB DMA instructions per stage
     constexpr int HI = (NI + WAVES - 1) / WAVES, LO = NI / WAVES;
     static_assert(FPW >= 1 && RF * CH % WAVES == 0 && UPR >= 16 && (ROWS * UPR) % 64 == 0 && DEPTH >= 2 &&
-                      DEPTH <= 4 && RF * CH * 1024 <= DEPTH * STAGE,
+                      DEPTH <= 4 && RF * NB * CH * 1024 <= DEPTH * STAGE,
                   "stage split");
     constexpr int F = FMT == FMT_E5M2 ? 1 : 0;
     extern __shared__ __attribute__((aligned(1024))) int8_t lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r16 = lane & 15, g = lane >> 4;
-    const int n0 = blockIdx.x * 16;
+    const int n0 = blockIdx.x * 16 * NB;
     const v4i ra = mfma2::make_rsrc(p.a, (uint32_t)((int64_t)p.M * p.lda));
     const v4i rb = mfma2::make_rsrc(p.b, (uint32_t)((int64_t)p.N * p.ldb));
     // DMA instruction j of a stage: units 64 j .. 64 j + 63 of the row-major
@@ -301,9 +302,11 @@ __global__ __launch_bounds__(1024) void gemm_fp8_rcr_rows_staged_kernel(F8Args p
     const int ns = p.K / SB;
     for (int st = 0; st < DEPTH && st < ns; ++st) dma_stage(st, lds + st * STAGE);
     const int c = wave % CH, f0 = wave / CH;
-    v4f acc[FPW];
+    v4f acc[FPW][NB];
 #pragma unroll
-    for (int i = 0; i < FPW; ++i) acc[i] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = 0; i < FPW; ++i)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) acc[i][nb] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     // 32 bytes of K per lane: logical units 8 c + 2 g and 8 c + 2 g + 1
     const int u0 = 16 * ((8 * c + 2 * g) ^ r16), u1 = 16 * ((8 * c + 2 * g + 1) ^ r16);
     for (int st = 0; st < ns; ++st) {
@@ -314,51 +317,71 @@ __global__ __launch_bounds__(1024) void gemm_fp8_rcr_rows_staged_kernel(F8Args p
         else { if (hi) mfma2::wait_vmcnt<3 * HI>(); else mfma2::wait_vmcnt<3 * LO>(); }
         __syncthreads();
         int8_t *buf = lds + (st % DEPTH) * STAGE;
-        const int8_t *brow = buf + (16 * RF + r16) * SB;
-        const v4i blo = *reinterpret_cast<const v4i *>(brow + u0), bhi = *reinterpret_cast<const v4i *>(brow + u1);
-        const v8i bv = (v8i){blo[0], blo[1], blo[2], blo[3], bhi[0], bhi[1], bhi[2], bhi[3]};
+        v8i bv[NB];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            const int8_t *brow = buf + (16 * RF + 16 * nb + r16) * SB;
+            const v4i blo = *reinterpret_cast<const v4i *>(brow + u0), bhi = *reinterpret_cast<const v4i *>(brow + u1);
+            bv[nb] = (v8i){blo[0], blo[1], blo[2], blo[3], bhi[0], bhi[1], bhi[2], bhi[3]};
+        }
 #pragma unroll
         for (int i = 0; i < FPW; ++i) {
             const int8_t *arow = buf + (16 * (f0 + FSTEP * i) + r16) * SB;
             const v4i alo = *reinterpret_cast<const v4i *>(arow + u0), ahi = *reinterpret_cast<const v4i *>(arow + u1);
             const v8i av = (v8i){alo[0], alo[1], alo[2], alo[3], ahi[0], ahi[1], ahi[2], ahi[3]};
-            acc[i] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bv, av, acc[i], F, F, 0, 0, 0, 0);
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+                acc[i][nb] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bv[nb], av, acc[i][nb], F, F, 0, 0, 0, 0);
         }
         __syncthreads();   // every wave is done with this buffer
         if (st + DEPTH < ns) dma_stage(st + DEPTH, buf);
     }
-    // partial sums of fragment f, chunk c: part[f][c][lane]
+    // partial sums of (A fragment f, B fragment nb), chunk c: part[f][nb][c][lane]
     v4f *part = reinterpret_cast<v4f *>(lds);
 #pragma unroll
-    for (int i = 0; i < FPW; ++i) part[((f0 + FSTEP * i) * CH + c) * 64 + lane] = acc[i];
-    __syncthreads();
-    if (wave >= RF) return;
-    v4f sum = part[(wave * CH) * 64 + lane];
+    for (int i = 0; i < FPW; ++i)
 #pragma unroll
-    for (int cc = 1; cc < CH; ++cc) {
-        const v4f v = part[(wave * CH + cc) * 64 + lane];
-        sum = v4f{sum[0] + v[0], sum[1] + v[1], sum[2] + v[2], sum[3] + v[3]};
-    }
+        for (int nb = 0; nb < NB; ++nb) part[(((f0 + FSTEP * i) * NB + nb) * CH + c) * 64 + lane] = acc[i][nb];
+    __syncthreads();
     const F8Epilogue<FMT, EPI, true, ACT> epi{p};
-    epi(m0 + 16 * wave + r16, n0 + 4 * g, sum);   // rows past M are not stored
+    for (int e = wave; e < RF * NB; e += WAVES) {
+        const int f = e % RF, nb = e / RF;
+        v4f sum = part[((f * NB + nb) * CH) * 64 + lane];
+#pragma unroll
+        for (int cc = 1; cc < CH; ++cc) {
+            const v4f v = part[((f * NB + nb) * CH + cc) * 64 + lane];
+            sum = v4f{sum[0] + v[0], sum[1] + v[1], sum[2] + v[2], sum[3] + v[3]};
+        }
+        epi(m0 + 16 * f + r16, n0 + 16 * nb + 4 * g, sum);   // rows past M are not stored
+    }
 }
 
-// Stage shapes of the FP8 last-rows kernel per fragment count: 1 fragment
-// 2 KiB stages (a wave per 128-byte chunk), 2 fragments 1 KiB three deep,
-// 4 and 8 fragments 512 bytes two deep (128 / 144 / 80 / 144 KiB of LDS).
+// Stage shapes of the FP8 last-rows kernel (first match wins).  N = 14336,
+// K = 4096 over 8 rotated weight sets (HIP events): up to 64 rows, 4
+// fragments and 64 columns per workgroup, 512-byte stages: M = 1 / 16 / 32
+// / 64 in 14.2 / 14.3 / 14.6 / 15.6 us (48 us on 256-row tiles; 16 columns
+// per workgroup with 1 / 2 fragments: 16.1 / 17.5 / 20.7 / 23.4); up to 128
+// rows, 8 fragments and 64 columns, 256-byte stages: M = 65 / 100 / 128 in
+// 17.8 / 18.5 / 20.0 us (16 columns: 35.0 / 36.8 / 38.0; 32: 22.9 / 24.2 /
+// 26.1; 128 columns 24.2-25.9).  Wider groups read the A rows fewer times
+// (once per workgroup, from L2).  N not a multiple of 64 takes the narrower
+// shapes below them.
 template <int FMT, int EPI, int ACT>
 bool launch_fp8_rows(const F8Args &p, int m0, int rem, hipStream_t stream) {
-    const dim3 grid(p.N / 16), block(1024);
-#define BK_F8ROWS(RF, SB, DEPTH)                                                                         \
-    if (rem <= 16 * (RF) && p.K % (SB) == 0) {                                                           \
-        hipLaunchKernelGGL((gemm_fp8_rcr_rows_staged_kernel<FMT, EPI, ACT, RF, SB, DEPTH>), grid, block,  \
-                           (size_t)(DEPTH) * (16 * (RF) + 16) * (SB), stream, p, m0);                     \
+#define BK_F8ROWS(RF, NB, SB, DEPTH)                                                                     \
+    if (rem <= 16 * (RF) && p.K % (SB) == 0 && p.N % (16 * (NB)) == 0) {                                  \
+        hipLaunchKernelGGL((gemm_fp8_rcr_rows_staged_kernel<FMT, EPI, ACT, RF, NB, SB, DEPTH>),           \
+                           dim3(p.N / (16 * (NB))), dim3(1024), (size_t)(DEPTH) * (16 * (RF) + 16 * (NB)) * (SB), \
+                           stream, p, m0);                                                               \
         return true;                                                                                     \
     }
-    BK_F8ROWS(1, 2048, 2)
-    BK_F8ROWS(2, 1024, 3)
-    BK_F8ROWS(4, 512, 2)
-    BK_F8ROWS(8, 512, 2)
+    BK_F8ROWS(4, 4, 512, 2)
+    BK_F8ROWS(8, 4, 256, 2)
+    BK_F8ROWS(1, 1, 2048, 2)
+    BK_F8ROWS(2, 2, 1024, 2)
+    BK_F8ROWS(2, 1, 1024, 3)
+    BK_F8ROWS(4, 1, 512, 2)
+    BK_F8ROWS(8, 1, 512, 2)
 #undef BK_F8ROWS
     return false;
 }
