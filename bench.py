@@ -536,6 +536,24 @@ def main():
                                                       "socket_power_w": fclk.get("socket_power_w_mean"),
                                                       **energy(fclk.get("socket_power_w_mean"), fms * 1e3,
                                                                2.0 * m * n * k)}
+            # decode-sized M at the config-3 width (the FP8 last-rows pass): the
+            # same 5 weight sets rotated (293 MB > the 256 MB Infinity Cache),
+            # device time per call replayed from a HIP graph
+            fdec = {}
+            for mm in (1, 16, 64, 128):
+                douts = [torch.empty((mm, n), dtype=torch.bfloat16, device=dev) for _ in range(5)]
+                dp = P.Fp8GemmPlan.select(P.Fp8GemmDescriptor(mm, n, k, output=P.ElementKind.Bf16))
+                di = [0]
+
+                def fp8_dec():
+                    xa, xb, _, s_xa, s_xb = fsets[di[0] % 5]
+                    dp.run(xa[:mm], xb, douts[di[0] % 5], scale_a=s_xa, scale_b=s_xb)
+                    di[0] += 1
+                gus = graph_us(fp8_dec, per_graph=50)
+                fdec[f"m{mm}"] = {"graph_replay_us": round(gus, 2),
+                                  "graph_replay_weight_frac_hbm_peak": round(n * k / (gus * 1e-6) / 8e12, 3)}
+                del douts
+            extra["fp8_e4m3_decode_n14336_k4096"] = fdec
             del fsets, fa, fb, ra, rb, rd
         if only in ("", "moe"):
             log("bench: moe grouped int8")
