@@ -356,20 +356,21 @@ __global__ __launch_bounds__(1024) void gemm_fp8_rcr_rows_staged_kernel(F8Args p
     }
 }
 
-// Stage shapes of the FP8 last-rows kernel (first match wins).  N = 14336,
-// K = 4096 over 8 rotated weight sets (HIP events): up to 64 rows, 4
-// fragments and 64 columns per workgroup, 512-byte stages: M = 1 / 16 / 32
-// / 64 in 14.2 / 14.3 / 14.6 / 15.6 us (48 us on 256-row tiles; 16 columns
-// per workgroup with 1 / 2 fragments: 16.1 / 17.5 / 20.7 / 23.4); up to 128
-// rows, 8 fragments and 64 columns, 256-byte stages: M = 65 / 100 / 128 in
-// 17.8 / 18.5 / 20.0 us (16 columns: 35.0 / 36.8 / 38.0; 32: 22.9 / 24.2 /
-// 26.1; 128 columns 24.2-25.9).  Wider groups read the A rows fewer times
-// (once per workgroup, from L2).  N not a multiple of 64 takes the narrower
-// shapes below them.
+// Stage shapes of the FP8 last-rows kernel (first match wins), by the
+// column fragments per workgroup (mfma2::last_rows_col_frags).  N = 14336,
+// K = 4096 over 8 rotated weight sets (HIP events), 64 columns per
+// workgroup: up to 64 rows with 4 fragments and 512-byte stages, M = 1 / 16
+// / 32 / 64 in 14.2 / 14.3 / 14.6 / 15.6 us (48 us on 256-row tiles; 16
+// columns with 1 / 2 / 4 fragments: 16.1 / 17.5 / 20.7 / 23.4); 65-128 rows
+// with 8 fragments and 256-byte stages, M = 65 / 100 / 128 in 17.8 / 18.5 /
+// 20.0 us (16 columns: 35.0 / 36.8 / 38.0; 32: 22.9 / 24.2 / 26.1; 128
+// columns 24.2-25.9).  16 columns (N below 6144): 1 fragment with 2 KiB
+// stages, 2 with 1 KiB stages three deep, 4 and 8 with 512-byte stages.
 template <int FMT, int EPI, int ACT>
 bool launch_fp8_rows(const F8Args &p, int m0, int rem, hipStream_t stream) {
+    const int nb = mfma2::last_rows_col_frags(p.N);
 #define BK_F8ROWS(RF, NB, SB, DEPTH)                                                                     \
-    if (rem <= 16 * (RF) && p.K % (SB) == 0 && p.N % (16 * (NB)) == 0) {                                  \
+    if (rem <= 16 * (RF) && nb == (NB) && p.K % (SB) == 0) {                                              \
         hipLaunchKernelGGL((gemm_fp8_rcr_rows_staged_kernel<FMT, EPI, ACT, RF, NB, SB, DEPTH>),           \
                            dim3(p.N / (16 * (NB))), dim3(1024), (size_t)(DEPTH) * (16 * (RF) + 16 * (NB)) * (SB), \
                            stream, p, m0);                                                               \
@@ -377,8 +378,9 @@ bool launch_fp8_rows(const F8Args &p, int m0, int rem, hipStream_t stream) {
     }
     BK_F8ROWS(4, 4, 512, 2)
     BK_F8ROWS(8, 4, 256, 2)
+    BK_F8ROWS(4, 2, 512, 2)
+    BK_F8ROWS(8, 2, 512, 2)
     BK_F8ROWS(1, 1, 2048, 2)
-    BK_F8ROWS(2, 2, 1024, 2)
     BK_F8ROWS(2, 1, 1024, 3)
     BK_F8ROWS(4, 1, 512, 2)
     BK_F8ROWS(8, 1, 512, 2)

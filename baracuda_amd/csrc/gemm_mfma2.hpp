@@ -482,6 +482,19 @@ __device__ __forceinline__ void wait_vmcnt() { asm volatile("s_waitcnt vmcnt(%0)
 // M <= limit: no tiles at all), when that row of tiles would start another
 // round of tiles on the 256 CUs (it costs nothing extra when it fits the
 // idle CUs of the last round).  Returns the number of last rows, or 0.
+// Column fragments (16 columns each) per workgroup of a last-rows pass: the
+// widest of 4, 2, 1 that divides N / 16 and still leaves at least 192
+// workgroups (3/4 of the CUs).  Every workgroup reads the pass's A rows once,
+// so wider groups cut the A traffic, but fewer than ~a CU's worth of
+// workgroups leave CUs idle (int8, K = 4096, M = 32 / 128: N = 4096
+// 7.2 / 11.8 us with 16 columns against 7.8 / 13.2 with 32; N = 14336
+// 19.2 / 39.4 us with 16 columns against 14.5 / 20.0 with 64).
+inline int last_rows_col_frags(int N) {
+    for (int nb = 4; nb > 1; nb /= 2)
+        if (N % (16 * nb) == 0 && N / (16 * nb) >= 192) return nb;
+    return 1;
+}
+
 inline int last_rows_pass(int M, int N, int limit) {
     if (N <= 0 || N % 16 != 0 || M <= 0) return 0;
     const int rem = M % 256;

@@ -709,32 +709,34 @@ __global__ __launch_bounds__(1024) void gemm_s8_rcr_rows_dma_kernel(S8Args p, in
 // 8.0 / 8.8 / 11.3 / 11.6 us, against 9.8-10.3 / 10.0-10.5 / 12.0-13.2 /
 // 12.3-13.5 us for 256-byte stages two to four deep; three 512-byte stages
 // measure the same as two (kRowsStagedSB, kRowsStagedDepth).
-template <int EPI, bool VecOut, int ACT, typename BiasT, int RF, int SB, int DEPTH>
+template <int EPI, bool VecOut, int ACT, typename BiasT, int RF, int NB, int SB, int DEPTH>
 __global__ __launch_bounds__(1024) void gemm_s8_rcr_rows_staged_kernel(S8Args p, int m0) {
     constexpr int WAVES = 16, CH = SB / 64;                  // 64-byte chunks per stage
-    constexpr int FPW = RF * CH / WAVES;                      // row fragments per wave
+    constexpr int FPW = RF * CH / WAVES;                      // A row fragments per wave
     constexpr int FSTEP = WAVES / CH;
-    constexpr int ROWS = 16 * RF + 16;                        // A then B rows of a stage
+    constexpr int ROWS = 16 * RF + 16 * NB;                   // A then B rows of a stage
     constexpr int STAGE = ROWS * SB;                          // bytes
-    constexpr int RPI = 1024 / SB, UPR = SB / 16;             // rows per DMA instruction, units per row
-    constexpr int NI = ROWS / RPI;                            // DMA instructions per stage
+    constexpr int UPR = SB / 16;                              // 16-byte units per row
+    constexpr int NI = ROWS * UPR / 64;                       // 1 KiB DMA instructions per stage
     constexpr int HI = (NI + WAVES - 1) / WAVES, LO = NI / WAVES;
-    static_assert(FPW >= 1 && RF * CH % WAVES == 0 && ROWS % RPI == 0 && DEPTH >= 2 && DEPTH <= 4,
+    static_assert(FPW >= 1 && RF * CH % WAVES == 0 && UPR >= 16 && (ROWS * UPR) % 64 == 0 && DEPTH >= 2 &&
+                      DEPTH <= 4 && RF * NB * CH * 1024 <= 160 * 1024 && DEPTH * STAGE <= 160 * 1024,
                   "stage split");
     extern __shared__ __attribute__((aligned(1024))) int8_t lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r16 = lane & 15, g = lane >> 4;
-    const int n0 = blockIdx.x * 16;
+    const int n0 = blockIdx.x * 16 * NB;
     const v4i ra = mfma2::make_rsrc(p.a, (uint32_t)((int64_t)p.M * p.lda));
     const v4i rb = mfma2::make_rsrc(p.b, (uint32_t)((int64_t)p.N * p.ldb));
-    // this wave's DMA instructions j = wave, wave + 16, ...: rows RPI j ..
-    // of the stage (A rows first), lane L fetching row RPI j + L / UPR at
-    // slot L % UPR
+    // this wave's DMA instructions j = wave, wave + 16, ...: units 64 j ..
+    // 64 j + 63 of the row-major stage (A rows first), lane L fetching unit
+    // (64 j + L) % UPR of row (64 j + L) / UPR
     auto dma_stage = [&](int st, int8_t *buf) {
         const int k0 = st * SB;
         for (int j = wave; j < NI; j += WAVES) {
-            const int r = RPI * j + lane / UPR, slot = lane % UPR;
+            const int idx = 64 * j + lane;
+            const int r = idx / UPR, slot = idx % UPR;
             const int unit = slot ^ (r & 15);
             if (r < 16 * RF)
                 mfma2::dma16(ra, (int)((int64_t)(m0 + r) * p.lda) + 16 * unit, k0, buf + j * 1024);
@@ -747,9 +749,12 @@ __global__ __launch_bounds__(1024) void gemm_s8_rcr_rows_staged_kernel(S8Args p,
     const int ns = p.K / SB;
     for (int st = 0; st < DEPTH && st < ns; ++st) dma_stage(st, lds + st * STAGE);
     const int c = wave % CH, f0 = wave / CH;
-    v4i acc[FPW];
+    v4i acc[FPW][NB];
 #pragma unroll
-    for (int i = 0; i < FPW; ++i) acc[i] = v4i{0, 0, 0, 0};
+    for (int i = 0; i < FPW; ++i)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) acc[i][nb] = v4i{0, 0, 0, 0};
+    const int sl = 16 * ((4 * c + g) ^ r16);                     // row & 15 == r16 for every fragment row
     for (int st = 0; st < ns; ++st) {
         // stage st has landed once at most the later stages' DMAs are outstanding
         const int later = min(DEPTH - 1, ns - 1 - st);
@@ -759,31 +764,39 @@ __global__ __launch_bounds__(1024) void gemm_s8_rcr_rows_staged_kernel(S8Args p,
         else { if (hi) mfma2::wait_vmcnt<3 * HI>(); else mfma2::wait_vmcnt<3 * LO>(); }
         __syncthreads();
         int8_t *buf = lds + (st % DEPTH) * STAGE;
-        const int sl = 16 * ((4 * c + g) ^ r16);                 // row & 15 == r16 for every fragment row
-        const v4i bv = *reinterpret_cast<const v4i *>(buf + (16 * RF + r16) * SB + sl);
+        v4i bv[NB];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+            bv[nb] = *reinterpret_cast<const v4i *>(buf + (16 * RF + 16 * nb + r16) * SB + sl);
 #pragma unroll
         for (int i = 0; i < FPW; ++i) {
             const v4i av = *reinterpret_cast<const v4i *>(buf + (16 * (f0 + FSTEP * i) + r16) * SB + sl);
-            acc[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bv, av, acc[i], 0, 0, 0);
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+                acc[i][nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bv[nb], av, acc[i][nb], 0, 0, 0);
         }
         __syncthreads();   // every wave is done with this buffer
         if (st + DEPTH < ns) dma_stage(st + DEPTH, buf);
     }
-    // partial sums of fragment f, chunk c: part[f][c][lane]
+    // partial sums of (A fragment f, B fragment nb), chunk c: part[f][nb][c][lane]
     v4i *part = reinterpret_cast<v4i *>(lds);
 #pragma unroll
-    for (int i = 0; i < FPW; ++i) part[((f0 + FSTEP * i) * CH + c) * 64 + lane] = acc[i];
-    __syncthreads();
-    if (wave >= RF) return;
-    v4i sum = part[(wave * CH) * 64 + lane];
+    for (int i = 0; i < FPW; ++i)
 #pragma unroll
-    for (int cc = 1; cc < CH; ++cc) {
-        const v4i v = part[(wave * CH + cc) * 64 + lane];
-        sum = v4i{(int)((uint32_t)sum[0] + (uint32_t)v[0]), (int)((uint32_t)sum[1] + (uint32_t)v[1]),
-                  (int)((uint32_t)sum[2] + (uint32_t)v[2]), (int)((uint32_t)sum[3] + (uint32_t)v[3])};
-    }
+        for (int nb = 0; nb < NB; ++nb) part[(((f0 + FSTEP * i) * NB + nb) * CH + c) * 64 + lane] = acc[i][nb];
+    __syncthreads();
     const S8Epilogue<EPI, VecOut, ACT, BiasT> epi{p};
-    epi(m0 + 16 * wave + r16, n0 + 4 * g, sum);   // rows past M are not stored
+    for (int e = wave; e < RF * NB; e += WAVES) {
+        const int f = e % RF, nb = e / RF;
+        v4i sum = part[((f * NB + nb) * CH) * 64 + lane];
+#pragma unroll
+        for (int cc = 1; cc < CH; ++cc) {
+            const v4i v = part[((f * NB + nb) * CH + cc) * 64 + lane];
+            sum = v4i{(int)((uint32_t)sum[0] + (uint32_t)v[0]), (int)((uint32_t)sum[1] + (uint32_t)v[1]),
+                      (int)((uint32_t)sum[2] + (uint32_t)v[2]), (int)((uint32_t)sum[3] + (uint32_t)v[3])};
+        }
+        epi(m0 + 16 * f + r16, n0 + 16 * nb + 4 * g, sum);   // rows past M are not stored
+    }
 }
 
 // RRR fast path: A through the interior DMA, row-major B through the
@@ -1266,25 +1279,28 @@ void launch_kernel(const S8Args &p, bool fast_k, hipStream_t stream, void *works
             if (tiles > 0)
                 hipLaunchKernelGGL((gemm_s8_rcr_dma_kernel<EPI, VecOut, ACT, BiasT>), dim3(tiles), dim3(DmaCfg::NT),
                                    0, stream, pm, TailSplit{0, 0, 1}, (int32_t *)nullptr);
-            const int rf_staged = rem <= 32 ? 2 : rem <= 64 ? 4 : 8;
             // fast_k already holds A and B 16-byte aligned, lda and ldb multiples
             // of 16 and both extents (rows rounded up to 256) below 2^31
             if (rem > kRowsDmaMaxRows && p.K % kRowsStagedSB == 0) {
-                constexpr int SB = kRowsStagedSB;
-                // two fragments: three stages in flight (6.96 / 7.18 us at M = 17 / 32
-                // against 7.44 / 7.64 with two, 7.22 / 7.44 with four)
-                const int depth = rf_staged == 2 ? 3 : kRowsStagedDepth;
-                const size_t lds = (size_t)depth * (16 * rf_staged + 16) * SB;
-                if (rf_staged == 2)
-                    hipLaunchKernelGGL((gemm_s8_rcr_rows_staged_kernel<EPI, VecOut, ACT, BiasT, 2, SB, 3>),
-                                       dim3(p.N / 16), dim3(1024), lds, stream, p, pm.M);
-                else if (rf_staged == 4)
-                    hipLaunchKernelGGL((gemm_s8_rcr_rows_staged_kernel<EPI, VecOut, ACT, BiasT, 4, SB, kRowsStagedDepth>),
-                                       dim3(p.N / 16), dim3(1024), lds, stream, p, pm.M);
-                else
-                    hipLaunchKernelGGL((gemm_s8_rcr_rows_staged_kernel<EPI, VecOut, ACT, BiasT, 8, SB, kRowsStagedDepth>),
-                                       dim3(p.N / 16), dim3(1024), lds, stream, p, pm.M);
-                return;
+                const int nb = mfma2::last_rows_col_frags(p.N);
+#define BK_S8ROWS(RF, NB, SB, DEPTH)                                                                        \
+    if (rem <= 16 * (RF) && nb == (NB) && p.K % (SB) == 0) {                                                 \
+        hipLaunchKernelGGL((gemm_s8_rcr_rows_staged_kernel<EPI, VecOut, ACT, BiasT, RF, NB, SB, DEPTH>),     \
+                           dim3(p.N / (16 * (NB))), dim3(1024),                                             \
+                           std::max((size_t)(DEPTH) * (16 * (RF) + 16 * (NB)) * (SB), (size_t)(RF) * (NB) * ((SB) / 64) * 1024), \
+                           stream, p, pm.M);                                                                \
+        return;                                                                                             \
+    }
+                BK_S8ROWS(2, 1, 512, 3)
+                BK_S8ROWS(4, 1, 512, 2)
+                BK_S8ROWS(8, 1, 512, 2)
+                BK_S8ROWS(2, 2, 512, 3)
+                BK_S8ROWS(4, 2, 512, 2)
+                BK_S8ROWS(8, 2, 512, 2)
+                BK_S8ROWS(2, 4, 512, 3)
+                BK_S8ROWS(4, 4, 512, 2)
+                BK_S8ROWS(8, 4, 256, 2)
+#undef BK_S8ROWS
             }
             if (rem == 1 && p.K % 1024 == 0) {
                 if (p.K % 2048 == 0)

@@ -23,17 +23,18 @@ from tests.test_gpu_gemm import _fp8_check_acc, _fp8_inputs, _fp8_run
 
 pytestmark = pytest.mark.gpu
 
-# (M, N, K) and the stage shape they take.  N % 64 == 0: 4 fragments x 64
-# columns for up to 64 rows (1 / 16 / 9 with K % 1024 != 0 / 33 / 64), 8 x 64
-# with 256-byte stages for 65-128 (100 / 128).  Other N: 1 fragment, 2 KiB
-# stages (1 / 16, K % 2048 == 0), 2 x 32 columns (17), 2 x 16 (5 with
-# K % 2048 != 0, 32), 4 x 16 (20 with K % 1024 != 0), 8 x 16 (65).  Under 4
-# tile rows at N = 16384 (the tiles fill one round exactly): 1 / 40 / 128
-# last rows.
+# (M, N, K) and the stage shape they take: 16 columns per workgroup below
+# N = 6144 (1 fragment with 2 KiB stages: 1 / 16, K % 2048 == 0; 2 with
+# 1 KiB: 5 with K % 2048 != 0, 17, 32; 4 with 512 B: 9 and 20 with
+# K % 1024 != 0, 33, 64; 8: 65, 100, 128), 32 columns from N = 6144 (2 / 33
+# with 4 fragments, 128 with 8), 64 columns from N = 12288 (1 / 16 with 4
+# fragments, 100 with 8 and 256-byte stages).  Under 4 tile rows at
+# N = 16384 (the tiles fill one round exactly): 1 / 40 / 128 last rows.
 SHAPES = [(1, 256, 4096), (16, 512, 2048), (5, 272, 1024), (17, 288, 1024), (32, 1040, 3072),
           (9, 256, 1536), (20, 272, 512), (33, 512, 512), (64, 256, 2560), (65, 1040, 1024),
           (100, 512, 4096), (128, 256, 512), (1025, 16384, 2048), (1064, 16384, 512), (1152, 16384, 1024),
-          (1, 1040, 4096), (16, 272, 2048)]
+          (1, 1040, 4096), (16, 272, 2048), (2, 6144, 512), (33, 8192, 512), (128, 6144, 1024),
+          (1, 12288, 2048), (16, 14336, 1024), (100, 12288, 1024)]
 
 
 @pytest.mark.parametrize("shape", SHAPES)
@@ -57,7 +58,7 @@ def test_fp8_rows_f32_and_bf16(gpu, shape):
 
 @pytest.mark.parametrize("epi", EPIS)
 @pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
-@pytest.mark.parametrize("shape", [SHAPES[0], SHAPES[3], SHAPES[7], SHAPES[10], SHAPES[13], SHAPES[15]])
+@pytest.mark.parametrize("shape", [SHAPES[0], SHAPES[3], SHAPES[7], SHAPES[10], SHAPES[13], SHAPES[15], SHAPES[18], SHAPES[22]])
 def test_fp8_rows_reference_pattern(gpu, shape, fmt, epi):
     m, n, k = shape
     print(f"case: fp8 rows pattern {fmt} {epi.value} {shape}", flush=True)
@@ -73,7 +74,7 @@ def test_fp8_rows_reference_pattern(gpu, shape, fmt, epi):
 
 
 @pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
-@pytest.mark.parametrize("shape", [SHAPES[1], SHAPES[4], SHAPES[9], SHAPES[14], SHAPES[16]])
+@pytest.mark.parametrize("shape", [SHAPES[1], SHAPES[4], SHAPES[9], SHAPES[14], SHAPES[16], SHAPES[19], SHAPES[21]])
 def test_fp8_rows_random_with_c(gpu, shape, fmt):
     # C (beta = 0.5) and a BiasGelu epilogue on random operands: one grid step
     # plus the MFMA's summation floor, as the tile path's test.
