@@ -1281,8 +1281,11 @@ void launch_kernel(const S8Args &p, bool fast_k, hipStream_t stream, void *works
                                    0, stream, pm, TailSplit{0, 0, 1}, (int32_t *)nullptr);
             // fast_k already holds A and B 16-byte aligned, lda and ldb multiples
             // of 16 and both extents (rows rounded up to 256) below 2^31
-            if (rem > kRowsDmaMaxRows && p.K % kRowsStagedSB == 0) {
-                const int nb = mfma2::last_rows_col_frags(p.N);
+            // With 32- or 64-column workgroups the staged kernel also beats the
+            // B-only DMA kernel from 9 rows (N = 14336, K = 4096: M = 8 / 16
+            // 14.3 / 17.5 us on the DMA kernel, 14.5 us staged at 17 rows).
+            const int nb = mfma2::last_rows_col_frags(p.N);
+            if (rem > (nb > 1 ? 8 : kRowsDmaMaxRows) && p.K % kRowsStagedSB == 0) {
 #define BK_S8ROWS(RF, NB, SB, DEPTH)                                                                        \
     if (rem <= 16 * (RF) && nb == (NB) && p.K % (SB) == 0) {                                                 \
         hipLaunchKernelGGL((gemm_s8_rcr_rows_staged_kernel<EPI, VecOut, ACT, BiasT, RF, NB, SB, DEPTH>),     \

@@ -36,13 +36,14 @@ SHAPES += DMA_SHAPES
 # 1 or 2 kilobytes per batch, the row under 4 tile rows).
 ROW1_SHAPES = [(1, 512, 2048), (1, 1040, 3072), (1, 4096, 4096), (1025, 16384, 2048)]
 SHAPES += ROW1_SHAPES
-# 17 to 128 last rows with K % 512 == 0: A and B streamed through LDS in K
+# 17 (9 for N >= 6144) to 128 last rows with K % 512 == 0: A and B streamed through LDS in K
 # stages (gemm_s8_rcr_rows_staged_kernel; 2, 4 or 8 fragments, 1 to 16
 # stages, the last-rows pass under 4 tile rows), 16 columns per workgroup
-# below N = 6144, 32 from 6144 (20 / 64 / 128 rows), 64 from 12288 (17 rows;
+# below N = 6144, 32 from 6144 (16 / 20 / 64 / 128 rows), 64 from 12288 (9 / 17 rows;
 # 36 and 100 under the tile rows at N = 16384).
 STAGED_SHAPES = [(17, 256, 512), (31, 1040, 1536), (33, 512, 512), (65, 272, 1024), (97, 1040, 2560), (1060, 16384, 1536), (1124, 16384, 512),
-                 (20, 6144, 1024), (64, 8192, 512), (128, 6144, 1024), (17, 12288, 512)]
+                 (20, 6144, 1024), (64, 8192, 512), (128, 6144, 1024), (17, 12288, 512),
+                 (9, 14336, 1024), (16, 6144, 512)]
 SHAPES += STAGED_SHAPES
 
 
