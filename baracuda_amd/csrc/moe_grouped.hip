@@ -427,6 +427,130 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void moe_grouped_dma_kernel(MoeArgs 
     }
 }
 
+// Decode-sized MoE (size_m <= 16 RF, so no expert holds more rows): one
+// launch over (N / (16 NB) column groups) x E experts, after the offsets
+// kernel.  A workgroup of 16 waves reads its expert's offsets and exits when
+// the expert has no rows; otherwise, as the dense last-rows pass
+// (gemm_s8_rcr_rows_staged_kernel), it streams its 16 RF gathered A rows
+// (pair p's input row, through sorted_token_ids; rows past the expert's
+// count point past the input and land as zeros) and its 16 NB rows of the
+// expert's weight slab through LDS in K stages of SB bytes, DEPTH in
+// flight, 16-byte unit u of stage row r at slot u ^ (r & 15).  Wave w owns
+// 64-byte chunk w % CH of every stage (CH = SB / 64) and A fragments
+// w / CH + (16 / CH) i against all NB weight fragments (the int8 16x16x64 or
+// the 16-bit 16x16x32 MFMA, the same 16 bytes per lane); the chunk partials
+// are added in chunk order through LDS and the waves run the tile path's
+// per-quad epilogues (moe_store, moe_store_i32, moe_store_h).
+template <int KIND, int RF, int NB, int SB, int DEPTH>
+__global__ __launch_bounds__(1024) void moe_rows_staged_kernel(MoeArgs p) {
+    constexpr int WAVES = 16, CH = SB / 64;
+    constexpr int FPW = RF * CH / WAVES;
+    constexpr int FSTEP = WAVES / CH;
+    constexpr int ROWS = 16 * RF + 16 * NB;
+    constexpr int STAGE = ROWS * SB;
+    constexpr int UPR = SB / 16;
+    constexpr int NI = ROWS * UPR / 64;
+    constexpr int HI = (NI + WAVES - 1) / WAVES, LO = NI / WAVES;
+    constexpr bool INT = KIND == MOE_S8 || KIND == MOE_S8_I32;
+    constexpr int ES = MoeElem<KIND>::SIZE;
+    typedef typename std::conditional<INT, v4i, v4f>::type Acc;
+    static_assert(FPW >= 1 && RF * CH % WAVES == 0 && UPR >= 16 && (ROWS * UPR) % 64 == 0 && DEPTH >= 2 &&
+                      DEPTH <= 4 && DEPTH * STAGE + 64 * RF <= 160 * 1024 && RF * NB * CH * 1024 + 64 * RF <= 160 * 1024,
+                  "stage split");
+    // dynamic LDS: the stages (then the partial sums), then the A rows' pair ids
+    constexpr int MAIN = DEPTH * STAGE > RF * NB * CH * 1024 ? DEPTH * STAGE : RF * NB * CH * 1024;
+    extern __shared__ __attribute__((aligned(1024))) int8_t lds[];
+    int32_t *s_tok = reinterpret_cast<int32_t *>(lds + MAIN);
+    const int e = blockIdx.y;
+    const int o0 = min(p.offsets[e], p.size_m), o1 = min(p.offsets[e + 1], p.size_m);
+    const int rows = o1 - o0;
+    if (rows <= 0) return;   // whole workgroup: no rows routed to this expert
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r16 = lane & 15, g = lane >> 4;
+    const int n0 = blockIdx.x * 16 * NB;
+    const int kb = p.K * ES;
+    const int in_div = p.topk_w ? 1 : p.topk;
+    const int x_rows = p.topk_w ? p.size_m : (p.size_m + p.topk - 1) / p.topk;
+    for (int r = threadIdx.x; r < 16 * RF; r += blockDim.x) s_tok[r] = r < rows ? p.sorted_ids[o0 + r] : -1;
+    __syncthreads();
+    const v4i ra = mfma2::make_rsrc(p.x, (uint32_t)((int64_t)x_rows * kb));
+    const v4i rb = mfma2::make_rsrc(p.w + (int64_t)e * p.N * kb, (uint32_t)((int64_t)p.N * kb));
+    auto dma_stage = [&](int st, int8_t *buf) {
+        const int k0 = st * SB;
+        for (int j = wave; j < NI; j += WAVES) {
+            const int idx = 64 * j + lane;
+            const int r = idx / UPR, slot = idx % UPR;
+            const int unit = slot ^ (r & 15);
+            if (r < 16 * RF) {
+                const int tok = s_tok[r];
+                const int base = tok >= 0 ? (tok / in_div) * kb : x_rows * kb;   // past the input: zeros
+                mfma2::dma16(ra, base + 16 * unit, k0, buf + j * 1024);
+            } else {
+                mfma2::dma16(rb, (n0 + r - 16 * RF) * kb + 16 * unit, k0, buf + j * 1024);
+            }
+        }
+    };
+    const bool hi = NI % WAVES == 0 || wave < NI % WAVES;
+    const int ns = kb / SB;
+    for (int st = 0; st < DEPTH && st < ns; ++st) dma_stage(st, lds + st * STAGE);
+    const int c = wave % CH, f0 = wave / CH;
+    Acc acc[FPW][NB];
+#pragma unroll
+    for (int i = 0; i < FPW; ++i)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) acc[i][nb] = Acc{0, 0, 0, 0};
+    const int sl = 16 * ((4 * c + g) ^ r16);
+    for (int st = 0; st < ns; ++st) {
+        const int later = min(DEPTH - 1, ns - 1 - st);
+        if (later == 0) mfma2::wait_vmcnt<0>();
+        else if (later == 1) { if (hi) mfma2::wait_vmcnt<HI>(); else mfma2::wait_vmcnt<LO>(); }
+        else if (later == 2) { if (hi) mfma2::wait_vmcnt<2 * HI>(); else mfma2::wait_vmcnt<2 * LO>(); }
+        else { if (hi) mfma2::wait_vmcnt<3 * HI>(); else mfma2::wait_vmcnt<3 * LO>(); }
+        __syncthreads();
+        int8_t *buf = lds + (st % DEPTH) * STAGE;
+        v4i bv[NB];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+            bv[nb] = *reinterpret_cast<const v4i *>(buf + (16 * RF + 16 * nb + r16) * SB + sl);
+#pragma unroll
+        for (int i = 0; i < FPW; ++i) {
+            const v4i av = *reinterpret_cast<const v4i *>(buf + (16 * (f0 + FSTEP * i) + r16) * SB + sl);
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                if constexpr (INT) acc[i][nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bv[nb], av, acc[i][nb], 0, 0, 0);
+                else acc[i][nb] = mfma16x16x32_h<KIND == MOE_BF16>(bv[nb], av, acc[i][nb]);
+            }
+        }
+        __syncthreads();
+        if (st + DEPTH < ns) dma_stage(st + DEPTH, buf);
+    }
+    Acc *part = reinterpret_cast<Acc *>(lds);
+#pragma unroll
+    for (int i = 0; i < FPW; ++i)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) part[(((f0 + FSTEP * i) * NB + nb) * CH + c) * 64 + lane] = acc[i][nb];
+    __syncthreads();
+    const float *swe = INT && p.sw ? p.sw + (int64_t)e * p.N : nullptr;
+    for (int q = wave; q < RF * NB; q += WAVES) {
+        const int f = q % RF, nb = q / RF;
+        Acc sum = part[((f * NB + nb) * CH) * 64 + lane];
+#pragma unroll
+        for (int cc = 1; cc < CH; ++cc) {
+            const Acc v = part[((f * NB + nb) * CH + cc) * 64 + lane];
+            if constexpr (INT)
+                sum = v4i{(int)((uint32_t)sum[0] + (uint32_t)v[0]), (int)((uint32_t)sum[1] + (uint32_t)v[1]),
+                          (int)((uint32_t)sum[2] + (uint32_t)v[2]), (int)((uint32_t)sum[3] + (uint32_t)v[3])};
+            else
+                sum = v4f{sum[0] + v[0], sum[1] + v[1], sum[2] + v[2], sum[3] + v[3]};
+        }
+        const int ml = 16 * f + r16, nn = n0 + 16 * nb + 4 * g;
+        if constexpr (KIND == MOE_S8) moe_store(p, s_tok, rows, in_div, swe, ml, nn, sum);
+        else if constexpr (KIND == MOE_S8_I32) moe_store_i32(p, s_tok, rows, ml, nn, sum);
+        else moe_store_h<KIND>(p, s_tok, rows, ml, nn, sum);
+    }
+}
+
 // Offsets, then the grouped GEMM (DMA path when the problem fits it).
 template <int KIND>
 int32_t launch_moe(const MoeArgs &p, const int32_t *expert_ids, int32_t *expert_counts,
@@ -445,6 +569,30 @@ int32_t launch_moe(const MoeArgs &p, const int32_t *expert_ids, int32_t *expert_
     const bool fast = kb % mfma2::BK == 0 && p.N % mfma2::BN == 0 && mfma::aligned16(p.x) &&
                       mfma::aligned16(p.w) && x_rows * kb < (1ll << 31) &&
                       (int64_t)p.N * kb < (1ll << 31) && out_ok;
+    if (fast && p.size_m <= 64 && kb % 512 == 0) {
+        // decode-sized: no expert holds more than size_m rows.  N = 14336,
+        // K = 4096, E = 8, top-2: 1 / 4 / 16 tokens (2 / 5 / 7 experts) in
+        // 27.4 / 62.3 / 99.0 us against 43.5 / 100.5 / 117.8 on 256-row
+        // tiles; at size_m 96 / 128 8 row fragments ran level with the tiles
+        // (123 us), so larger size_m stays on them.
+        const int nb = mfma2::last_rows_col_frags(p.N);
+#define BK_MOEROWS(RF, NB, SB, DEPTH)                                                                        \
+        if (p.size_m <= 16 * (RF) && nb == (NB)) {                                                           \
+            hipLaunchKernelGGL((moe_rows_staged_kernel<KIND, RF, NB, SB, DEPTH>), dim3(p.N / (16 * (NB)), p.E), \
+                               dim3(1024),                                                                   \
+                               std::max((size_t)(DEPTH) * (16 * (RF) + 16 * (NB)) * (SB),                    \
+                                        (size_t)(RF) * (NB) * ((SB) / 64) * 1024) + 64 * (RF),               \
+                               stream, p);                                                                   \
+            return launch_status();                                                                          \
+        }
+        BK_MOEROWS(2, 1, 512, 3)
+        BK_MOEROWS(4, 1, 512, 2)
+        BK_MOEROWS(2, 2, 512, 3)
+        BK_MOEROWS(4, 2, 512, 2)
+        BK_MOEROWS(2, 4, 512, 3)
+        BK_MOEROWS(4, 4, 512, 2)
+#undef BK_MOEROWS
+    }
     if (fast) {
         const int work = slots * (p.N / mfma2::BN);
         const int padded = (work + 7) / 8 * 8;   // whole XCD groups

@@ -492,12 +492,15 @@ void bo_quantize_per_token_sym(const float *x, int64_t n, int64_t d, int32_t qmi
 }
 
 /* baracuda_moe.cuh:1121-1162: histogram of expert_ids, then exclusive
- * prefix sum into offsets[0..E], offsets[0] = 0. */
+ * prefix sum into offsets[0..E], offsets[0] = 0.  Ids outside [0, E) are
+ * not counted: the reference indexes its counters with them (out of
+ * bounds); the GPU offsets kernel skips them, and so does this restatement. */
 void bo_moe_expert_offsets(const int32_t *expert_ids, int64_t size_m,
                            int32_t num_experts, int32_t *counts,
                            int32_t *offsets) {
     for (int32_t e = 0; e < num_experts; ++e) counts[e] = 0;
-    for (int64_t i = 0; i < size_m; ++i) counts[expert_ids[i]] += 1;
+    for (int64_t i = 0; i < size_m; ++i)
+        if (expert_ids[i] >= 0 && expert_ids[i] < num_experts) counts[expert_ids[i]] += 1;
     offsets[0] = 0;
     for (int32_t e = 0; e < num_experts; ++e) offsets[e + 1] = offsets[e] + counts[e];
 }

@@ -321,3 +321,42 @@ def test_moe_config5_i32_whole_output_exact_and_bf16_epilogue(gpu):
     scale = sa_d[tok_d][:, None] * sw_d[pe_d]                 # f32, rounded once
     want_bf16 = (scale * acc.to(torch.float32)).to(torch.bfloat16)
     assert torch.equal(out.view(torch.int16), want_bf16.view(torch.int16))
+
+
+# ---- decode-sized MoE (size_m <= 64, K % 512 == 0: moe_rows_staged_kernel) --
+@pytest.mark.parametrize("case", [(1, 8, 2, 512, 1024, False), (3, 8, 2, 256, 512, True), (16, 8, 2, 512, 2048, False),
+                                  (32, 8, 2, 256, 512, True), (4, 8, 2, 6144, 512, False),
+                                  (2, 8, 2, 12288, 512, True), (21, 4, 3, 256, 1536, False)])
+def test_moe_decode_all_pairs(gpu, case):
+    # every pair bit-exact against the per-pair W8A8 formula; size_m 2 to 64
+    # (2 or 4 row fragments), 16 / 32 / 64 columns per workgroup
+    tokens, E, topk, n, k, tw = case
+    print(f"case: moe decode {case}", flush=True)
+    _run(tokens=tokens, E=E, topk=topk, n=n, k=k, seed=tokens * 7 + n, topk_w=tw)
+
+
+def test_moe_decode_i32_vs_oracle_empty_and_invalid_experts(gpu):
+    # int32 SKU on the decode pass against the oracle's grouped restatement:
+    # 16 experts, most empty, some pairs routed to out-of-range ids (not
+    # counted, their output rows untouched)
+    tokens, E, topk, n, k = 20, 16, 3, 512, 1024
+    size_m = tokens * topk
+    g = rng(41)
+    pair_e = g.integers(0, 4, size_m).astype(np.int32) * 5     # experts 0, 5, 10, 15
+    pair_e[[3, 17, 40]] = E + 2                                   # out of range
+    order = np.argsort(pair_e, kind="stable").astype(np.int32)
+    sorted_ids, expert_ids = order, pair_e[order]
+    x, w = int8_uniform(g, (tokens, k)), int8_uniform(g, (E, n, k))
+    got = _moe_i32(dev(x), dev(w), sorted_ids, expert_ids, E, topk, size_m, n, k).cpu().numpy()
+    _, offs = O.moe_expert_offsets(expert_ids, E)
+    want = O.moe_s8_grouped_i32(x, w, sorted_ids, offs, topk, size_m)
+    valid = pair_e < E
+    assert np.array_equal(got[valid], want[valid])
+    assert np.all(got[~valid] == -7)
+
+
+def test_moe_decode_one_expert_takes_all_rows(gpu):
+    # all 64 pairs on one expert: the largest segment the decode pass takes
+    tokens, routing = _block_routing([0, 64, 0], seed=3)
+    print("case: moe decode one expert", flush=True)
+    _run(tokens=tokens, E=3, topk=1, n=512, k=512, seed=4, routing=routing)

@@ -82,11 +82,13 @@ def test_reference_smoke_fixture(gpu, t):
 @pytest.mark.parametrize("topk_w", [False, True])
 @pytest.mark.parametrize("t", ["bf16", "f16"])
 @pytest.mark.parametrize("shape", [(64, 4, 2, 96, 100), (512, 8, 2, 512, 512), (300, 8, 2, 256, 1024),
-                                   (1024, 16, 4, 256, 256)])
+                                   (1024, 16, 4, 256, 256), (1, 8, 2, 512, 512), (16, 8, 2, 6144, 256),
+                                   (32, 16, 2, 512, 1024)])
 def test_random_routing(gpu, shape, t, topk_w):
     # Zipf routing; (512, ..., 512, 512) and (1024, ..., 256, 256) take the
     # LDS-DMA path (K a multiple of 64 elements, N of 256), the others the
-    # general path (K tail, N tail).
+    # general path (K tail, N tail); size_m = 2 / 32 / 64 with K a multiple
+    # of 256 elements the decode-sized pass (moe_rows_staged_kernel).
     tokens, E, topk, n, k = shape
     print(f"case: moe_wmma {t} topk_w={topk_w} {shape}", flush=True)
     sid, eid = moe_routing(tokens, E, topk, seed=tokens + n)

@@ -254,6 +254,17 @@ def test_moe_routing_offsets_and_grouped_gemm():
         assert np.array_equal(got[p], want)
 
 
+def test_moe_expert_offsets_skip_out_of_range_ids():
+    # ids outside [0, E) are not counted (and never index past the counters)
+    E = 4
+    ids = np.array([0, 0, 1, -1, 3, 7, 4, 3, 1 << 20], dtype=np.int32)
+    counts, offs = O.moe_expert_offsets(ids, E)
+    assert counts.tolist() == [2, 1, 0, 2]
+    assert offs.tolist() == [0, 2, 3, 3, 5]
+    counts, offs = O.moe_expert_offsets(np.full(9, E, dtype=np.int32), E)
+    assert counts.tolist() == [0] * E and offs.tolist() == [0] * (E + 1)
+
+
 def test_moe_routing_is_zipf_and_topk_distinct():
     sorted_ids, expert_ids = moe_routing(4096, 8, 2, seed=5)
     assert sorted(sorted_ids.tolist()) == list(range(8192))
