@@ -584,7 +584,31 @@ def main():
                 "padding_frac": round(1 - rows_e.sum() / (tiles_m * 256), 4),
                 "sclk_mhz": mclk.get("mhz_mean"), "socket_power_w": mclk.get("socket_power_w_mean"),
                 **energy(mclk.get("socket_power_w_mean"), mms * 1e3, 2.0 * tokens * topk * n * k)}
-            del mx, mw, mo
+            # decode-sized token counts (the per-expert staged pass): two
+            # weight sets rotated (940 MB), so the experts a call touches are
+            # read from HBM; device time per call replayed from a HIP graph
+            mw2 = torch.randint(-127, 128, (E, n, k), dtype=torch.int8, device=dev)
+            mdec = {}
+            for dt in (1, 4, 16):
+                dsid_d, deid_d = moe_routing(dt, E, topk, seed=5)
+                ne = int((np.bincount(deid_d, minlength=E) > 0).sum())
+                dx = mx[:dt].contiguous()
+                dsa = msa[:dt].contiguous()
+                dos = [torch.empty((dt * topk, n), dtype=torch.bfloat16, device=dev) for _ in range(2)]
+                ds_, de_ = torch.from_numpy(dsid_d).to(dev), torch.from_numpy(deid_d).to(dev)
+                dplan = P.MoeS8GroupedPlan.select(E, topk, dt * topk, n, k)
+                wsets = (mw, mw2)
+                di = [0]
+
+                def moe_dec():
+                    dplan.run(dx, wsets[di[0] % 2], ds_, de_, dos[di[0] % 2], cnt, off, dsa, msw)
+                    di[0] += 1
+                gus = graph_us(moe_dec, per_graph=20, replays=10)
+                mdec[f"tokens{dt}"] = {"graph_replay_us": round(gus, 2), "experts_touched": ne,
+                                       "touched_weight_frac_hbm_peak": round(ne * n * k / (gus * 1e-6) / 8e12, 3)}
+                del dos
+            extra["moe_s8_grouped_decode_e8_top2_14336x4096"] = mdec
+            del mx, mw, mw2, mo
             log("bench: moe grouped bf16 (moe_wmma ABI)")
             bx = torch.randn((tokens, k), device=dev).to(torch.bfloat16)
             bw = (torch.randn((E, n, k), device=dev) * 0.05).to(torch.bfloat16)
