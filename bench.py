@@ -540,19 +540,19 @@ def main():
             # same 5 weight sets rotated (293 MB > the 256 MB Infinity Cache),
             # device time per call replayed from a HIP graph
             fdec = {}
-            for mm in (1, 16, 64, 128):
-                douts = [torch.empty((mm, n), dtype=torch.bfloat16, device=dev) for _ in range(5)]
-                dp = P.Fp8GemmPlan.select(P.Fp8GemmDescriptor(mm, n, k, output=P.ElementKind.Bf16))
-                di = [0]
+            for fdec_m in (1, 16, 64, 128):
+                fdec_out = [torch.empty((fdec_m, n), dtype=torch.bfloat16, device=dev) for _ in range(5)]
+                fdec_plan = P.Fp8GemmPlan.select(P.Fp8GemmDescriptor(fdec_m, n, k, output=P.ElementKind.Bf16))
+                fdec_i = [0]
 
-                def fp8_dec():
-                    xa, xb, _, s_xa, s_xb = fsets[di[0] % 5]
-                    dp.run(xa[:mm], xb, douts[di[0] % 5], scale_a=s_xa, scale_b=s_xb)
-                    di[0] += 1
-                gus = graph_us(fp8_dec, per_graph=50)
-                fdec[f"m{mm}"] = {"graph_replay_us": round(gus, 2),
+                def fdec_call():
+                    xa, xb, _, s_xa, s_xb = fsets[fdec_i[0] % 5]
+                    fdec_plan.run(xa[:fdec_m], xb, fdec_out[fdec_i[0] % 5], scale_a=s_xa, scale_b=s_xb)
+                    fdec_i[0] += 1
+                gus = graph_us(fdec_call, per_graph=50)
+                fdec[f"m{fdec_m}"] = {"graph_replay_us": round(gus, 2),
                                   "graph_replay_weight_frac_hbm_peak": round(n * k / (gus * 1e-6) / 8e12, 3)}
-                del douts
+                del fdec_out
             extra["fp8_e4m3_decode_n14336_k4096"] = fdec
             del fsets, fa, fb, ra, rb, rd
         if only in ("", "moe"):
@@ -590,23 +590,23 @@ def main():
             mw2 = torch.randint(-127, 128, (E, n, k), dtype=torch.int8, device=dev)
             mdec = {}
             for dt in (1, 4, 16):
-                dsid_d, deid_d = moe_routing(dt, E, topk, seed=5)
-                ne = int((np.bincount(deid_d, minlength=E) > 0).sum())
-                dx = mx[:dt].contiguous()
-                dsa = msa[:dt].contiguous()
-                dos = [torch.empty((dt * topk, n), dtype=torch.bfloat16, device=dev) for _ in range(2)]
-                ds_, de_ = torch.from_numpy(dsid_d).to(dev), torch.from_numpy(deid_d).to(dev)
-                dplan = P.MoeS8GroupedPlan.select(E, topk, dt * topk, n, k)
-                wsets = (mw, mw2)
-                di = [0]
+                mdec_sid, mdec_eid = moe_routing(dt, E, topk, seed=5)
+                mdec_ne = int((np.bincount(mdec_eid, minlength=E) > 0).sum())
+                mdec_x = mx[:dt].contiguous()
+                mdec_sa = msa[:dt].contiguous()
+                mdec_out = [torch.empty((dt * topk, n), dtype=torch.bfloat16, device=dev) for _ in range(2)]
+                mdec_ds, mdec_de = torch.from_numpy(mdec_sid).to(dev), torch.from_numpy(mdec_eid).to(dev)
+                mdec_plan = P.MoeS8GroupedPlan.select(E, topk, dt * topk, n, k)
+                mdec_w = (mw, mw2)
+                mdec_i = [0]
 
-                def moe_dec():
-                    dplan.run(dx, wsets[di[0] % 2], ds_, de_, dos[di[0] % 2], cnt, off, dsa, msw)
-                    di[0] += 1
-                gus = graph_us(moe_dec, per_graph=20, replays=10)
-                mdec[f"tokens{dt}"] = {"graph_replay_us": round(gus, 2), "experts_touched": ne,
-                                       "touched_weight_frac_hbm_peak": round(ne * n * k / (gus * 1e-6) / 8e12, 3)}
-                del dos
+                def mdec_call():
+                    mdec_plan.run(mdec_x, mdec_w[mdec_i[0] % 2], mdec_ds, mdec_de, mdec_out[mdec_i[0] % 2], cnt, off, mdec_sa, msw)
+                    mdec_i[0] += 1
+                gus = graph_us(mdec_call, per_graph=20, replays=10)
+                mdec[f"tokens{dt}"] = {"graph_replay_us": round(gus, 2), "experts_touched": mdec_ne,
+                                       "touched_weight_frac_hbm_peak": round(mdec_ne * n * k / (gus * 1e-6) / 8e12, 3)}
+                del mdec_out
             extra["moe_s8_grouped_decode_e8_top2_14336x4096"] = mdec
             del mx, mw, mw2, mo
             log("bench: moe grouped bf16 (moe_wmma ABI)")
