@@ -225,9 +225,27 @@ constexpr int kRowsPathAlways = 64;
 constexpr int kRowsStagedSB = 512, kRowsStagedDepth = 2;
 inline int rows_path_rows(int M, int N, int limit = kRowsPathMax) { return mfma2::last_rows_pass(M, N, limit); }
 
+// Grids of at most kSmallTilesMax 256 x 256 tiles (under half a round on
+// the 256 CUs) run 128 x 128 tiles instead (Cfg<2, 2, 128>: 4 waves of
+// 64 x 64, two workgroups per CU), except that with a tail-split workspace
+// a deep K (>= 4096) on fewer than 64 small tiles splits K.  W8A8, N = K =
+// 4096, 8 rotated weight sets, no workspace: M = 256 / 512 / 1024 / 2048
+// 56 / 56 / 56 / 55 -> 24.2 / 24.9 / 26.7 / 36.0 us (the split workspace:
+// 29.9 / 32.2 / 38.2 / 52.0); 129-255 tiles stay on 256 x 256 (M = 2560 /
+// 3072: 46.5 / 49.6 us against 55.1 / 59.2 with small tiles).  512 x 512 x
+// 8192: small tiles 43.6 us, split 30.5.
+constexpr int kSmallTilesMax = 128;
+inline bool small_tiles_preferred(int M, int N, int K) {
+    const int64_t t256 = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
+    if (t256 > kSmallTilesMax) return false;
+    const int64_t t128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
+    return !(t128 < 64 && K >= 4096);
+}
+
 inline TailSplit tail_split_plan(int M, int N, int K) {
     TailSplit t{0, 0, 1};
     if (M <= 0 || N <= 0 || K <= 0 || K % 128 != 0) return t;
+    if (small_tiles_preferred(M, N, K)) return t;
     // the rows path takes those shapes
     if (rows_path_rows(M, N, K % kRowsStagedSB == 0 ? kRowsPathMax : kRowsPathAlways) != 0) return t;
     const int tiles_m = (M + 255) / 256, tiles_n = (N + 255) / 256;
@@ -265,11 +283,12 @@ typedef mfma2::Cfg<2, 4> DmaCfg;
 template <class P, bool HasC, bool Full, class Epi>
 __device__ __forceinline__ void store_s8_tile_staged_as(const mfma2::AccTile<P> &acc, int8_t *stage0, int8_t *stage1,
                                                         const S8Args &p, int m_base, int n_base, const Epi &epi) {
+    typedef typename P::Cfg C;
     const int wave = threadIdx.x >> 6;
-    const int wrow = (wave / DmaCfg::WAVES_N) * DmaCfg::WM;
-    const int wcol = (wave % DmaCfg::WAVES_N) * DmaCfg::WN;
-    int8_t *scratch = (wave < 4 ? stage0 : stage1) + (wave & 3) * (DmaCfg::WM * DmaCfg::WN);
-    const int ncols = min(DmaCfg::WN, p.N - (n_base + wcol));
+    const int wrow = (wave / C::WAVES_N) * C::WM;
+    const int wcol = (wave % C::WAVES_N) * C::WN;
+    int8_t *scratch = (wave < C::WAVES / 2 ? stage0 : stage1) + (wave % (C::WAVES / 2)) * (C::WM * C::WN);
+    const int ncols = min(C::WN, p.N - (n_base + wcol));
     mfma2::store_u8x4_staged<P>(
         acc, scratch,
         [&](int r, int c, const v4i &v) {
@@ -291,7 +310,7 @@ template <class P, class Epi>
 __device__ __forceinline__ void store_s8_tile_staged(const mfma2::AccTile<P> &acc, int8_t *stage0, int8_t *stage1,
                                                      const S8Args &p, int m_base, int n_base, const Epi &epi) {
     const bool has_c = p.beta != 0.0f && p.c != nullptr;
-    const bool full = m_base + mfma2::BM <= p.M && n_base + mfma2::BN <= p.N;
+    const bool full = m_base + P::Cfg::TB <= p.M && n_base + P::Cfg::TB <= p.N;
     if (has_c) {
         if (full) store_s8_tile_staged_as<P, true, true>(acc, stage0, stage1, p, m_base, n_base, epi);
         else store_s8_tile_staged_as<P, true, false>(acc, stage0, stage1, p, m_base, n_base, epi);
@@ -304,16 +323,16 @@ __device__ __forceinline__ void store_s8_tile_staged(const mfma2::AccTile<P> &ac
 // `ts`: workgroups below ts.full_tiles (all of them when ts.split == 1) run
 // whole tiles; the rest run K chunks of the tail tiles (tail_split_plan) and
 // store their accumulators in `slots`.
-template <int EPI, bool VecOut, int ACT = ACT_NONE, typename BiasT = float>
-__global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_s8_rcr_dma_kernel(S8Args p, TailSplit ts,
+template <int EPI, bool VecOut, int ACT = ACT_NONE, typename BiasT = float, class C = DmaCfg>
+__global__ __launch_bounds__(C::NT, C::NT == 256 ? 2 : 1) void gemm_s8_rcr_dma_kernel(S8Args p, TailSplit ts,
                                                                          int32_t *__restrict__ slots) {
     namespace M2 = mfma2;
-    typedef M2::PolicyI8<DmaCfg> P;
-    __shared__ __attribute__((aligned(1024))) int8_t stage0[2 * M2::OPER];
-    __shared__ __attribute__((aligned(1024))) int8_t stage1[2 * M2::OPER];
+    typedef M2::PolicyI8<C> P;
+    __shared__ __attribute__((aligned(1024))) int8_t stage0[2 * C::OPER];
+    __shared__ __attribute__((aligned(1024))) int8_t stage1[2 * C::OPER];
     // Edge tiles (M or N not a multiple of 256): operand rows past M / N
     // lie past the buffer resources' byte counts and load as zeros.
-    const int tiles_n = (p.N + M2::BN - 1) / M2::BN;
+    const int tiles_n = (p.N + C::TB - 1) / C::TB;
     int tm, tn, k0 = 0, klen = p.K, chunk = -1;
     if (ts.split > 1 && (int)blockIdx.x >= ts.full_tiles) {
         const int u = blockIdx.x - ts.full_tiles, ti = u / ts.split;
@@ -324,13 +343,13 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_s8_rcr_dma_kernel(S8Args p
         k0 = chunk * kt / ts.split * M2::BK;
         klen = (chunk + 1) * kt / ts.split * M2::BK - k0;
     } else {
-        const int tiles_m = ts.split > 1 ? ts.full_tiles / tiles_n : (p.M + M2::BM - 1) / M2::BM;
+        const int tiles_m = ts.split > 1 ? ts.full_tiles / tiles_n : (p.M + C::TB - 1) / C::TB;
         tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
     }
-    const int m_base = tm * M2::BM, n_base = tn * M2::BN;
+    const int m_base = tm * C::TB, n_base = tn * C::TB;
     M2::DmaRows<false, false> d;
-    d.a = M2::make_dma_interior<DmaCfg>(p.a, (uint32_t)(p.M * p.lda), (int)p.lda, m_base * (int)p.lda + k0);
-    d.b = M2::make_dma_interior<DmaCfg>(p.b, (uint32_t)(p.N * p.ldb), (int)p.ldb, n_base * (int)p.ldb + k0);
+    d.a = M2::make_dma_interior<C>(p.a, (uint32_t)(p.M * p.lda), (int)p.lda, m_base * (int)p.lda + k0);
+    d.b = M2::make_dma_interior<C>(p.b, (uint32_t)(p.N * p.ldb), (int)p.ldb, n_base * (int)p.ldb + k0);
     M2::AccTile<P> acc;
     M2::mainloop<P>(stage0, stage1, d, klen, acc);
     if (chunk >= 0) {
@@ -341,15 +360,15 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_s8_rcr_dma_kernel(S8Args p
         });
         return;
     }
-    const bool full = m_base + M2::BM <= p.M && n_base + M2::BN <= p.N;
+    const bool full = m_base + C::TB <= p.M && n_base + C::TB <= p.N;
     if constexpr (EPI == EPI_W8A8_BF16 && VecOut) {
         if (full || p.N % 8 == 0) {
             // Scales fetched once per lane, output staged in LDS (free after the
             // mainloop's last barrier) and written as full rows; in an edge tile
             // (N % 8 == 0 there) rows past M and 8-column units past N are skipped.
             const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-            const int wrow = m_base + (wave / DmaCfg::WAVES_N) * DmaCfg::WM;
-            const int wcol = n_base + (wave % DmaCfg::WAVES_N) * DmaCfg::WN;
+            const int wrow = m_base + (wave / C::WAVES_N) * C::WM;
+            const int wcol = n_base + (wave % C::WAVES_N) * C::WN;
             float sam[P::TI], none[P::TI];
             v4f swv[P::TJ];
 #pragma unroll
@@ -359,13 +378,13 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_s8_rcr_dma_kernel(S8Args p
                 const int col = wcol + j * 16 + (lane >> 4) * 4;
                 swv[j] = col < p.N ? *reinterpret_cast<const v4f *>(p.sw + col) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
             }
-            int8_t *scratch = (wave < 4 ? stage0 : stage1) + (wave & 3) * (DmaCfg::WM * DmaCfg::WN * 2);
+            int8_t *scratch = (wave < C::WAVES / 2 ? stage0 : stage1) + (wave % (C::WAVES / 2)) * (C::WM * C::WN * 2);
             M2::store_w8a8_bf16_staged<P, false>(
                 acc, scratch, sam, none, swv,
                 [&](int r) {
                     return wrow + r < p.M ? static_cast<uint16_t *>(p.d) + (int64_t)(wrow + r) * p.ldd + wcol : nullptr;
                 },
-                min(DmaCfg::WN, p.N - wcol));
+                min(C::WN, p.N - wcol));
             return;
         }
     }
@@ -374,15 +393,15 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_s8_rcr_dma_kernel(S8Args p
             // 32-bit rows staged in LDS (16 KiB per wave, two halves) and
             // written as 256-byte row segments instead of 16-byte quads.
             const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-            const int wrow = m_base + (wave / DmaCfg::WAVES_N) * DmaCfg::WM;
-            const int wcol = n_base + (wave % DmaCfg::WAVES_N) * DmaCfg::WN;
-            int8_t *scratch = (wave < 4 ? stage0 : stage1) + (wave & 3) * (DmaCfg::WM / 2 * 256);
+            const int wrow = m_base + (wave / C::WAVES_N) * C::WM;
+            const int wcol = n_base + (wave % C::WAVES_N) * C::WN;
+            int8_t *scratch = (wave < C::WAVES / 2 ? stage0 : stage1) + (wave % (C::WAVES / 2)) * (C::WM / 2 * 256);
             auto row_dst = [&](int r) {
                 return wrow + r < p.M ? static_cast<int32_t *>(p.d) + (int64_t)(wrow + r) * p.ldd + wcol : nullptr;
             };
             if constexpr (EPI == EPI_I32) {
                 M2::store_x32x4_staged<P>(acc, scratch, [](int, int, const v4i &v) { return v; }, row_dst,
-                                          min(DmaCfg::WN, p.N - wcol));
+                                          min(C::WN, p.N - wcol));
             } else {
                 // y = (sa[m] * sw[n]) * (float)acc, the scales fetched once per lane
                 float sam[P::TI];
@@ -404,7 +423,7 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_s8_rcr_dma_kernel(S8Args p
                                    __float_as_int((sa_r * sw_c[2]) * (float)v[2]),
                                    __float_as_int((sa_r * sw_c[3]) * (float)v[3])};
                     },
-                    row_dst, min(DmaCfg::WN, p.N - wcol));
+                    row_dst, min(C::WN, p.N - wcol));
             }
             return;
         }
@@ -415,9 +434,9 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_s8_rcr_dma_kernel(S8Args p
             // written as 512-byte row segments:
             // y = (double)(((float)sa[m] * (float)sw[n]) * (float)acc).
             const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-            const int wrow = m_base + (wave / DmaCfg::WAVES_N) * DmaCfg::WM;
-            const int wcol = n_base + (wave % DmaCfg::WAVES_N) * DmaCfg::WN;
-            int8_t *scratch = (wave < 4 ? stage0 : stage1) + (wave & 3) * (DmaCfg::WM / 4 * 512);
+            const int wrow = m_base + (wave / C::WAVES_N) * C::WM;
+            const int wcol = n_base + (wave % C::WAVES_N) * C::WN;
+            int8_t *scratch = (wave < C::WAVES / 2 ? stage0 : stage1) + (wave % (C::WAVES / 2)) * (C::WM / 4 * 512);
             const double *sa64 = reinterpret_cast<const double *>(p.sa);
             const double *sw64 = reinterpret_cast<const double *>(p.sw);
             float sam[P::TI], swf[P::TJ][4];
@@ -444,7 +463,7 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void gemm_s8_rcr_dma_kernel(S8Args p
                 [&](int r) {
                     return wrow + r < p.M ? static_cast<double *>(p.d) + (int64_t)(wrow + r) * p.ldd + wcol : nullptr;
                 },
-                min(DmaCfg::WN, p.N - wcol));
+                min(C::WN, p.N - wcol));
             return;
         }
     }
@@ -1340,6 +1359,13 @@ void launch_kernel(const S8Args &p, bool fast_k, hipStream_t stream, void *works
                                slots);
             hipLaunchKernelGGL((gemm_s8_tail_reduce_kernel<EPI, VecOut, ACT, BiasT>), dim3(ts.tail_tiles, 64),
                                dim3(256), 0, stream, p, ts, (const int32_t *)slots);
+            return;
+        }
+        if (tiles <= kSmallTilesMax) {
+            typedef mfma2::Cfg<2, 2, 128> SmallCfg;
+            const int tiles128 = ((p.M + 127) / 128) * ((p.N + 127) / 128);
+            hipLaunchKernelGGL((gemm_s8_rcr_dma_kernel<EPI, VecOut, ACT, BiasT, SmallCfg>), dim3(tiles128),
+                               dim3(SmallCfg::NT), 0, stream, p, TailSplit{0, 0, 1}, (int32_t *)nullptr);
             return;
         }
         hipLaunchKernelGGL((gemm_s8_rcr_dma_kernel<EPI, VecOut, ACT, BiasT>), dim3(tiles), dim3(DmaCfg::NT), 0, stream, p,

@@ -138,9 +138,42 @@ def test_tail_split_w8a8_m4296_bit_identical(gpu):
         assert np.array_equal(outs[1][r], O.gemm_w8a8_bf16(a, w, sa, sw, rows=(r, r + 1), nthreads=8)[0]), r
 
 
-@pytest.mark.parametrize("shape", [(512, 512, 8192), (300, 520, 1024), (200, 256, 4096), (1024, 768, 2048)])
+@pytest.mark.parametrize("shape", [(300, 1000, 512), (256, 4096, 4096), (129, 520, 1152), (1100, 3000, 256),
+                                   (2100, 4100, 256)])
+def test_small_tiles_all_epilogues(gpu, shape):
+    # Grids of at most 128 256x256 tiles run 128x128 tiles (no workspace),
+    # 2100 x 4100 (153 tiles) 256x256 edge tiles: int32 exact over the whole
+    # output (edge rows / columns included), s8 with C and beta through the
+    # staged byte store, W8A8 bf16 on rows at the tile-row boundaries.
+    m, n, k = shape
+    print(f"case: small tiles {shape}", flush=True)
+    g = rng(m + n + 7 * k)
+    a, b = int8_uniform(g, (m, k)), int8_uniform(g, (n, k))
+    pi = P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, output=P.ElementKind.I32))
+    d = torch.full((m, n), -7, dtype=torch.int32, device="cuda:0")
+    pi.run(dev(a), dev(b), d)
+    sync()
+    assert np.array_equal(d.cpu().numpy(), O.gemm_s8_rcr_i32(a, b, nthreads=8))
+    c = int8_uniform(g, (m, n))
+    d8 = torch.full((m, n), 99, dtype=torch.int8, device="cuda:0")
+    P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k)).run(dev(a), dev(b), d8, c=dev(c), alpha=0.002, beta=0.75)
+    sync()
+    assert np.array_equal(d8.cpu().numpy(), O.gemm_s8_rcr_s8(a, b, 0.002, 0.75, c))
+    sa = g.uniform(0.005, 0.02, m).astype(np.float32)
+    sw = g.uniform(0.001, 0.01, n).astype(np.float32)
+    db = torch.empty((m, n), dtype=torch.bfloat16, device="cuda:0")
+    P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, output=P.ElementKind.Bf16)).run(
+        dev(a), dev(b), db, scale_a=dev(sa), scale_b=dev(sw))
+    sync()
+    got = host_bits16(db)
+    for r in (0, 127, 128, m - 1):
+        assert np.array_equal(got[r], O.gemm_w8a8_bf16(a, b, sa, sw, rows=(r, r + 1), nthreads=8)[0]), r
+
+
+@pytest.mark.parametrize("shape", [(512, 512, 8192), (300, 520, 4096), (200, 256, 4096), (1024, 768, 4096)])
 def test_tail_split_small_grids(gpu, shape):
-    # Grids below one round (T < 256 tiles) split every tile along K: int32
+    # Grids of at most 128 tiles with K >= 4096 on fewer than 64 128x128
+    # tiles split every tile along K when given the workspace: int32
     # accumulators exact, s8 with C / beta and a bias epilogue equal the oracle.
     m, n, k = shape
     print(f"case: tail split {shape}", flush=True)
