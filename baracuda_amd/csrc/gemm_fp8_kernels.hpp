@@ -125,36 +125,36 @@ __global__ __launch_bounds__(NT, 1) void gemm_fp8_kernel(F8Args p) {
 
 typedef mfma2::Cfg<2, 4> F8DmaCfg;
 
-template <int FMT, int LAYOUT>
-struct F8DmaPolicy { typedef mfma2::PolicyF8<F8DmaCfg, FMT> type; };
-template <int FMT>
-struct F8DmaPolicy<FMT, F8_RRR> { typedef mfma2::PolicyF8RowB<F8DmaCfg, FMT> type; };
+template <int FMT, int LAYOUT, class C>
+struct F8DmaPolicy { typedef mfma2::PolicyF8<C, FMT> type; };
+template <int FMT, class C>
+struct F8DmaPolicy<FMT, F8_RRR, C> { typedef mfma2::PolicyF8RowB<C, FMT> type; };
 
 // Fast path: 256x256 tiles (edge tiles included), K % 128 == 0, 16-byte rows,
 // N % 4 == 0, vector stores.
-template <int FMT, int LAYOUT, int EPI, int ACT>
-__global__ __launch_bounds__(F8DmaCfg::NT, 1) void gemm_fp8_dma_kernel(F8Args p) {
+template <int FMT, int LAYOUT, int EPI, int ACT, class C = F8DmaCfg>
+__global__ __launch_bounds__(C::NT, C::NT == 256 ? 2 : 1) void gemm_fp8_dma_kernel(F8Args p) {
     namespace M2 = mfma2;
-    typedef typename F8DmaPolicy<FMT, LAYOUT>::type P;
-    __shared__ __attribute__((aligned(1024))) int8_t stage0[2 * M2::OPER];
-    __shared__ __attribute__((aligned(1024))) int8_t stage1[2 * M2::OPER];
+    typedef typename F8DmaPolicy<FMT, LAYOUT, C>::type P;
+    __shared__ __attribute__((aligned(1024))) int8_t stage0[2 * C::OPER];
+    __shared__ __attribute__((aligned(1024))) int8_t stage1[2 * C::OPER];
     // Edge tiles (M or N not a multiple of 256): rows past M / N load as
     // zeros (past the buffer resources' byte counts; RRR B columns past N
     // read the next k-row, reaching only output columns that are not stored).
     int tm, tn;
-    tile_coords(blockIdx.x, (p.M + M2::BM - 1) / M2::BM, (p.N + M2::BN - 1) / M2::BN, tm, tn);
-    const int m_base = tm * M2::BM, n_base = tn * M2::BN;
-    const bool full = m_base + M2::BM <= p.M && n_base + M2::BN <= p.N;
+    tile_coords(blockIdx.x, (p.M + C::TB - 1) / C::TB, (p.N + C::TB - 1) / C::TB, tm, tn);
+    const int m_base = tm * C::TB, n_base = tn * C::TB;
+    const bool full = m_base + C::TB <= p.M && n_base + C::TB <= p.N;
     M2::AccTile<P> acc;
     if constexpr (LAYOUT == F8_RCR) {
         M2::DmaRows<false, false> d;
-        d.a = M2::make_dma_interior<F8DmaCfg>(p.a, (uint32_t)(p.M * p.lda), (int)p.lda, m_base * (int)p.lda);
-        d.b = M2::make_dma_interior<F8DmaCfg>(p.b, (uint32_t)(p.N * p.ldb), (int)p.ldb, n_base * (int)p.ldb);
+        d.a = M2::make_dma_interior<C>(p.a, (uint32_t)(p.M * p.lda), (int)p.lda, m_base * (int)p.lda);
+        d.b = M2::make_dma_interior<C>(p.b, (uint32_t)(p.N * p.ldb), (int)p.ldb, n_base * (int)p.ldb);
         M2::mainloop<P>(stage0, stage1, d, p.K, acc);
     } else {
         M2::DmaRowsRrr d;
-        d.a = M2::make_dma_interior<F8DmaCfg>(p.a, (uint32_t)(p.M * p.lda), (int)p.lda, m_base * (int)p.lda);
-        d.b = M2::make_dma_row_b<F8DmaCfg>(p.b, (uint32_t)(p.K * p.ldb), (int)p.ldb, n_base);
+        d.a = M2::make_dma_interior<C>(p.a, (uint32_t)(p.M * p.lda), (int)p.lda, m_base * (int)p.lda);
+        d.b = M2::make_dma_row_b<C>(p.b, (uint32_t)(p.K * p.ldb), (int)p.ldb, n_base);
         M2::mainloop<P>(stage0, stage1, d, p.K, acc);
     }
     if constexpr (EPI == F8_BF16) {
@@ -162,9 +162,9 @@ __global__ __launch_bounds__(F8DmaCfg::NT, 1) void gemm_fp8_dma_kernel(F8Args p)
         // barrier), written as 16-byte units: D = bf16_rne(alpha * acc).
         if (p.ldd % 8 == 0 && (reinterpret_cast<uintptr_t>(p.d) & 15u) == 0 && (full || p.N % 8 == 0)) {
             const int wave = threadIdx.x >> 6;
-            const int wrow = m_base + (wave / F8DmaCfg::WAVES_N) * F8DmaCfg::WM;
-            const int wcol = n_base + (wave % F8DmaCfg::WAVES_N) * F8DmaCfg::WN;
-            int8_t *scratch = (wave < 4 ? stage0 : stage1) + (wave & 3) * (F8DmaCfg::WM * 128);
+            const int wrow = m_base + (wave / C::WAVES_N) * C::WM;
+            const int wcol = n_base + (wave % C::WAVES_N) * C::WN;
+            int8_t *scratch = (wave < C::WAVES / 2 ? stage0 : stage1) + (wave % (C::WAVES / 2)) * (C::WM * 128);
             const float alpha = p.alpha;
             M2::store_bf16x4_staged<P>(
                 acc, scratch,
@@ -176,7 +176,7 @@ __global__ __launch_bounds__(F8DmaCfg::NT, 1) void gemm_fp8_dma_kernel(F8Args p)
                     return wrow + r < p.M ? static_cast<uint16_t *>(p.d) + (int64_t)(wrow + r) * p.ldd + wcol
                                           : nullptr;
                 },
-                min(F8DmaCfg::WN, p.N - wcol));
+                min(C::WN, p.N - wcol));
             return;
         }
     }
@@ -185,9 +185,9 @@ __global__ __launch_bounds__(F8DmaCfg::NT, 1) void gemm_fp8_dma_kernel(F8Args p)
         // segments: D = alpha * acc.
         if (p.ldd % 4 == 0 && (reinterpret_cast<uintptr_t>(p.d) & 15u) == 0 && (full || p.N % 4 == 0)) {
             const int wave = threadIdx.x >> 6;
-            const int wrow = m_base + (wave / F8DmaCfg::WAVES_N) * F8DmaCfg::WM;
-            const int wcol = n_base + (wave % F8DmaCfg::WAVES_N) * F8DmaCfg::WN;
-            int8_t *scratch = (wave < 4 ? stage0 : stage1) + (wave & 3) * (F8DmaCfg::WM / 2 * 256);
+            const int wrow = m_base + (wave / C::WAVES_N) * C::WM;
+            const int wcol = n_base + (wave % C::WAVES_N) * C::WN;
+            int8_t *scratch = (wave < C::WAVES / 2 ? stage0 : stage1) + (wave % (C::WAVES / 2)) * (C::WM / 2 * 256);
             const float alpha = p.alpha;
             M2::store_x32x4_staged<P>(
                 acc, scratch,
@@ -198,7 +198,7 @@ __global__ __launch_bounds__(F8DmaCfg::NT, 1) void gemm_fp8_dma_kernel(F8Args p)
                 [&](int r) {
                     return wrow + r < p.M ? static_cast<float *>(p.d) + (int64_t)(wrow + r) * p.ldd + wcol : nullptr;
                 },
-                min(F8DmaCfg::WN, p.N - wcol));
+                min(C::WN, p.N - wcol));
             return;
         }
     }
@@ -207,9 +207,9 @@ __global__ __launch_bounds__(F8DmaCfg::NT, 1) void gemm_fp8_dma_kernel(F8Args p)
         // fp8 bytes staged per wave, written as 16-byte row segments.
         if (p.ldd % 16 == 0 && (reinterpret_cast<uintptr_t>(p.d) & 15u) == 0 && (full || p.N % 16 == 0)) {
             const int wave = threadIdx.x >> 6;
-            const int wrow = m_base + (wave / F8DmaCfg::WAVES_N) * F8DmaCfg::WM;
-            const int wcol = n_base + (wave % F8DmaCfg::WAVES_N) * F8DmaCfg::WN;
-            int8_t *scratch = (wave < 4 ? stage0 : stage1) + (wave & 3) * (F8DmaCfg::WM * F8DmaCfg::WN);
+            const int wrow = m_base + (wave / C::WAVES_N) * C::WM;
+            const int wcol = n_base + (wave % C::WAVES_N) * C::WN;
+            int8_t *scratch = (wave < C::WAVES / 2 ? stage0 : stage1) + (wave % (C::WAVES / 2)) * (C::WM * C::WN);
             // The C term and the M / N bounds decided once per tile, not per element.
             auto staged = [&](auto has_c, auto whole) {
                 M2::store_u8x4_staged<P>(
@@ -228,7 +228,7 @@ __global__ __launch_bounds__(F8DmaCfg::NT, 1) void gemm_fp8_dma_kernel(F8Args p)
                         return wrow + r < p.M ? static_cast<int8_t *>(p.d) + (int64_t)(wrow + r) * p.ldd + wcol
                                               : nullptr;
                     },
-                    min(F8DmaCfg::WN, p.N - wcol));
+                    min(C::WN, p.N - wcol));
             };
             using T_ = std::true_type;
             using F_ = std::false_type;
@@ -418,6 +418,15 @@ int32_t launch_fp8(const F8Args &p, hipStream_t stream) {
     }
     if (fast) {
         const int tiles = (int)(pad_m / mfma2::BM) * ((p.N + mfma2::BN - 1) / mfma2::BN);
+        if (LAYOUT == F8_RCR && tiles <= 128) {
+            // at most half a round of 256x256 tiles: 128x128 tiles of 4 waves
+            // (two workgroups per CU), as the int8 kernel
+            typedef mfma2::Cfg<2, 2, 128> SmallCfg;
+            const int tiles128 = ((p.M + 127) / 128) * ((p.N + 127) / 128);
+            hipLaunchKernelGGL((gemm_fp8_dma_kernel<FMT, F8_RCR, EPI, ACT, SmallCfg>), dim3(tiles128),
+                               dim3(SmallCfg::NT), 0, stream, p);
+            return launch_status();
+        }
         hipLaunchKernelGGL((gemm_fp8_dma_kernel<FMT, LAYOUT, EPI, ACT>), dim3(tiles), dim3(F8DmaCfg::NT),
                            0, stream, p);
     } else {
