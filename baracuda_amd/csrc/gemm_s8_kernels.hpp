@@ -728,7 +728,19 @@ __global__ __launch_bounds__(1024) void gemm_s8_rcr_rows_dma_kernel(S8Args p, in
 // 8.0 / 8.8 / 11.3 / 11.6 us, against 9.8-10.3 / 10.0-10.5 / 12.0-13.2 /
 // 12.3-13.5 us for 256-byte stages two to four deep; three 512-byte stages
 // measure the same as two (kRowsStagedSB, kRowsStagedDepth).
-template <int EPI, bool VecOut, int ACT, typename BiasT, int RF, int NB, int SB, int DEPTH>
+template <bool VecOut, int ACT, typename BiasT>
+struct U8Epilogue;
+// Zero row / column sums for U8Epilogue when the correction is already in
+// the accumulator.
+__device__ const int kZeroSums[16] = {0};
+
+// U8: u8 x u8 operands (RCR u8 SKUs; EPI unused) through the signed MFMA:
+// fragments flipped to u - 128 and the correction of
+// sum(u_a u_b) = acc_s + 128 (sum a' + sum b') + 16384 K folded into the same
+// accumulator: 64 * sum a' and 64 * sum b' are two MFMAs each against a
+// fragment of bytes 64 (int32 wrap-around, exact mod 2^32), 16384 K in the
+// epilogue.
+template <int EPI, bool VecOut, int ACT, typename BiasT, int RF, int NB, int SB, int DEPTH, bool U8 = false>
 __global__ __launch_bounds__(1024) void gemm_s8_rcr_rows_staged_kernel(S8Args p, int m0) {
     constexpr int WAVES = 16, CH = SB / 64;                  // 64-byte chunks per stage
     constexpr int FPW = RF * CH / WAVES;                      // A row fragments per wave
@@ -785,14 +797,25 @@ __global__ __launch_bounds__(1024) void gemm_s8_rcr_rows_staged_kernel(S8Args p,
         int8_t *buf = lds + (st % DEPTH) * STAGE;
         v4i bv[NB];
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
+        for (int nb = 0; nb < NB; ++nb) {
             bv[nb] = *reinterpret_cast<const v4i *>(buf + (16 * RF + 16 * nb + r16) * SB + sl);
+            if constexpr (U8) bv[nb] = u8_flip(bv[nb]);
+        }
+        constexpr v4i c64 = {0x40404040, 0x40404040, 0x40404040, 0x40404040};
 #pragma unroll
         for (int i = 0; i < FPW; ++i) {
-            const v4i av = *reinterpret_cast<const v4i *>(buf + (16 * (f0 + FSTEP * i) + r16) * SB + sl);
+            v4i av = *reinterpret_cast<const v4i *>(buf + (16 * (f0 + FSTEP * i) + r16) * SB + sl);
+            if constexpr (U8) av = u8_flip(av);
 #pragma unroll
-            for (int nb = 0; nb < NB; ++nb)
+            for (int nb = 0; nb < NB; ++nb) {
                 acc[i][nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bv[nb], av, acc[i][nb], 0, 0, 0);
+                if constexpr (U8) {
+                    acc[i][nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(c64, av, acc[i][nb], 0, 0, 0);
+                    acc[i][nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(c64, av, acc[i][nb], 0, 0, 0);
+                    acc[i][nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bv[nb], c64, acc[i][nb], 0, 0, 0);
+                    acc[i][nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bv[nb], c64, acc[i][nb], 0, 0, 0);
+                }
+            }
         }
         __syncthreads();   // every wave is done with this buffer
         if (st + DEPTH < ns) dma_stage(st + DEPTH, buf);
@@ -805,6 +828,8 @@ __global__ __launch_bounds__(1024) void gemm_s8_rcr_rows_staged_kernel(S8Args p,
         for (int nb = 0; nb < NB; ++nb) part[(((f0 + FSTEP * i) * NB + nb) * CH + c) * 64 + lane] = acc[i][nb];
     __syncthreads();
     const S8Epilogue<EPI, VecOut, ACT, BiasT> epi{p};
+    // u8: au = acc - kcorr with zero sums, kcorr = -16384 K (mod 2^32)
+    const U8Epilogue<VecOut, ACT, BiasT> epi_u8{p, kZeroSums, kZeroSums, 0u - 16384u * (uint32_t)p.K};
     for (int e = wave; e < RF * NB; e += WAVES) {
         const int f = e % RF, nb = e / RF;
         v4i sum = part[((f * NB + nb) * CH) * 64 + lane];
@@ -814,7 +839,8 @@ __global__ __launch_bounds__(1024) void gemm_s8_rcr_rows_staged_kernel(S8Args p,
             sum = v4i{(int)((uint32_t)sum[0] + (uint32_t)v[0]), (int)((uint32_t)sum[1] + (uint32_t)v[1]),
                       (int)((uint32_t)sum[2] + (uint32_t)v[2]), (int)((uint32_t)sum[3] + (uint32_t)v[3])};
         }
-        epi(m0 + 16 * f + r16, n0 + 16 * nb + 4 * g, sum);   // rows past M are not stored
+        if constexpr (U8) epi_u8(r16, 4 * g, sum, m0 + 16 * f, n0 + 16 * nb);   // rows past M are not stored
+        else epi(m0 + 16 * f + r16, n0 + 16 * nb + 4 * g, sum);
     }
 }
 
@@ -1256,8 +1282,55 @@ __global__ __launch_bounds__(NT, 1) void gemm_u8_rcr_kernel(S8Args p) {
     for_each_fragment(acc, [&](int ml, int nl, const v4i &v) { epi(ml, nl, v, m_base, n_base); });
 }
 
+// u8 RCR last rows (decode-sized M; M % 256 in [1, 128] when a row of tiles
+// would start another round) through the staged last-rows kernel; false
+// when the shape does not fit it.  N = K = 4096: M = 1 / 16 / 128 on the
+// register-staged general kernel took 68.9 / 68.1 / – us.
+template <int ACT, typename BiasT>
+bool launch_u8_rcr_rows(const S8Args &p, hipStream_t stream) {
+    const int rem = mfma2::last_rows_pass(p.M, p.N, 128);
+    if (rem == 0 || p.K % 512 != 0 || p.lda % 16 != 0 || p.ldb % 16 != 0 || !aligned16(p.a) || !aligned16(p.b) ||
+        !dma_extent_ok(p.M, p.lda) || !dma_extent_ok(p.N, p.ldb))
+        return false;
+    S8Args pm = p;
+    pm.M = p.M - rem;
+    if (pm.M > 0 && p.N % mfma2::BN != 0) return false;
+    const bool vec = p.ldd % 4 == 0 && (reinterpret_cast<uintptr_t>(p.d) % 4) == 0;
+    if (pm.M > 0) {
+        const int tiles = (pm.M / mfma2::BM) * (p.N / mfma2::BN);
+        if (vec)
+            hipLaunchKernelGGL((gemm_u8_rcr_dma_kernel<true, ACT, BiasT>), dim3(tiles), dim3(DmaCfg::NT), 0, stream, pm);
+        else
+            hipLaunchKernelGGL((gemm_u8_rcr_dma_kernel<false, ACT, BiasT>), dim3(tiles), dim3(DmaCfg::NT), 0, stream, pm);
+    }
+    const int nb = mfma2::last_rows_col_frags(p.N);
+#define BK_U8ROWS(RF, NB, SB, DEPTH)                                                                           \
+    if (rem <= 16 * (RF) && nb == (NB)) {                                                                       \
+        const size_t lds = std::max((size_t)(DEPTH) * (16 * (RF) + 16 * (NB)) * (SB), (size_t)(RF) * (NB) * ((SB) / 64) * 1024); \
+        if (vec)                                                                                                \
+            hipLaunchKernelGGL((gemm_s8_rcr_rows_staged_kernel<0, true, ACT, BiasT, RF, NB, SB, DEPTH, true>),    \
+                               dim3(p.N / (16 * (NB))), dim3(1024), lds, stream, p, pm.M);                      \
+        else                                                                                                    \
+            hipLaunchKernelGGL((gemm_s8_rcr_rows_staged_kernel<0, false, ACT, BiasT, RF, NB, SB, DEPTH, true>),   \
+                               dim3(p.N / (16 * (NB))), dim3(1024), lds, stream, p, pm.M);                      \
+        return true;                                                                                            \
+    }
+    BK_U8ROWS(2, 1, 512, 3)
+    BK_U8ROWS(4, 1, 512, 2)
+    BK_U8ROWS(8, 1, 512, 2)
+    BK_U8ROWS(2, 2, 512, 3)
+    BK_U8ROWS(4, 2, 512, 2)
+    BK_U8ROWS(8, 2, 512, 2)
+    BK_U8ROWS(2, 4, 512, 3)
+    BK_U8ROWS(4, 4, 512, 2)
+    BK_U8ROWS(8, 4, 256, 2)
+#undef BK_U8ROWS
+    return false;
+}
+
 template <int ACT, typename BiasT>
 int32_t launch_u8_rcr(const S8Args &p, hipStream_t stream) {
+    if (launch_u8_rcr_rows<ACT, BiasT>(p, stream)) return launch_status();
     const bool dma = p.K % mfma2::BK == 0 && p.M % mfma2::BM == 0 && p.N % mfma2::BN == 0 &&
                      p.lda % 16 == 0 && p.ldb % 16 == 0 && aligned16(p.a) && aligned16(p.b) &&
                      (int64_t)p.M * p.lda < (1ll << 31) && (int64_t)p.N * p.ldb < (1ll << 31);
