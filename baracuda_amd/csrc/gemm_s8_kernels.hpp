@@ -185,7 +185,11 @@ template <int ACT, typename BiasT>
 int32_t launch_rrr_dma(const S8Args &p, hipStream_t stream);
 
 template <int ACT, typename BiasT>
+bool launch_rrr_rows(const S8Args &p, hipStream_t stream);
+
+template <int ACT, typename BiasT>
 int32_t launch_rrr(const S8Args &p, hipStream_t stream) {
+    if (launch_rrr_rows<ACT, BiasT>(p, stream)) return launch_status();
     if (launch_rrr_dma<ACT, BiasT>(p, stream) == kOk) return launch_status();
     const int tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
     const bool aligned = p.K % BK == 0 && p.N % BN == 0 && p.lda % 16 == 0 && p.ldb % 4 == 0 &&
@@ -740,7 +744,15 @@ __device__ const int kZeroSums[16] = {0};
 // accumulator: 64 * sum a' and 64 * sum b' are two MFMAs each against a
 // fragment of bytes 64 (int32 wrap-around, exact mod 2^32), 16384 K in the
 // epilogue.
-template <int EPI, bool VecOut, int ACT, typename BiasT, int RF, int NB, int SB, int DEPTH, bool U8 = false>
+//
+// RowB: B row-major [K, N] (the RRR SKUs): a stage's B region holds its SB
+// k-rows of the 16 NB columns as they lie in memory (row pitch 16 NB bytes,
+// whole-row DMAs, the K position moving the row by k0 * ldb), and the B
+// fragments are rebuilt with ds_read_b64_tr_b8 as in PolicyI8RowB: the lane
+// pair (2j, 2j + 1) of a 16-lane group points at k-row j, lane i gets 8
+// consecutive k of column i.
+template <int EPI, bool VecOut, int ACT, typename BiasT, int RF, int NB, int SB, int DEPTH, bool U8 = false,
+          bool RowB = false>
 __global__ __launch_bounds__(1024) void gemm_s8_rcr_rows_staged_kernel(S8Args p, int m0) {
     constexpr int WAVES = 16, CH = SB / 64;                  // 64-byte chunks per stage
     constexpr int FPW = RF * CH / WAVES;                      // A row fragments per wave
@@ -759,7 +771,7 @@ __global__ __launch_bounds__(1024) void gemm_s8_rcr_rows_staged_kernel(S8Args p,
     const int r16 = lane & 15, g = lane >> 4;
     const int n0 = blockIdx.x * 16 * NB;
     const v4i ra = mfma2::make_rsrc(p.a, (uint32_t)((int64_t)p.M * p.lda));
-    const v4i rb = mfma2::make_rsrc(p.b, (uint32_t)((int64_t)p.N * p.ldb));
+    const v4i rb = mfma2::make_rsrc(p.b, (uint32_t)(RowB ? (int64_t)p.K * p.ldb : (int64_t)p.N * p.ldb));
     // this wave's DMA instructions j = wave, wave + 16, ...: units 64 j ..
     // 64 j + 63 of the row-major stage (A rows first), lane L fetching unit
     // (64 j + L) % UPR of row (64 j + L) / UPR
@@ -769,10 +781,16 @@ __global__ __launch_bounds__(1024) void gemm_s8_rcr_rows_staged_kernel(S8Args p,
             const int idx = 64 * j + lane;
             const int r = idx / UPR, slot = idx % UPR;
             const int unit = slot ^ (r & 15);
-            if (r < 16 * RF)
+            if (r < 16 * RF) {
                 mfma2::dma16(ra, (int)((int64_t)(m0 + r) * p.lda) + 16 * unit, k0, buf + j * 1024);
-            else
+            } else if constexpr (RowB) {
+                // unit ib of the B region: k-row ib / NB, 16 columns ib % NB
+                const int ib = idx - 16 * RF * UPR;
+                mfma2::dma16(rb, (ib / NB) * (int)p.ldb + n0 + 16 * (ib % NB),
+                             __builtin_amdgcn_readfirstlane(k0 * (int)p.ldb), buf + j * 1024);
+            } else {
                 mfma2::dma16(rb, (int)((int64_t)(n0 + r - 16 * RF) * p.ldb) + 16 * unit, k0, buf + j * 1024);
+            }
         }
     };
     // waves below NI % 16 issue HI instructions per stage, the others LO
@@ -798,7 +816,14 @@ __global__ __launch_bounds__(1024) void gemm_s8_rcr_rows_staged_kernel(S8Args p,
         v4i bv[NB];
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-            bv[nb] = *reinterpret_cast<const v4i *>(buf + (16 * RF + 16 * nb + r16) * SB + sl);
+            if constexpr (RowB) {
+                const int kb = 64 * c + 16 * g + (r16 >> 1);
+                const int8_t *q = buf + 16 * RF * SB + kb * (16 * NB) + 16 * nb + ((lane & 1) << 3);
+                const mfma2::v2i_t lo = mfma2::ds_read_tr8(q), hi = mfma2::ds_read_tr8(q + 8 * 16 * NB);
+                bv[nb] = v4i{lo[0], lo[1], hi[0], hi[1]};
+            } else {
+                bv[nb] = *reinterpret_cast<const v4i *>(buf + (16 * RF + 16 * nb + r16) * SB + sl);
+            }
             if constexpr (U8) bv[nb] = u8_flip(bv[nb]);
         }
         constexpr v4i c64 = {0x40404040, 0x40404040, 0x40404040, 0x40404040};
@@ -1488,6 +1513,48 @@ int32_t launch_rrr_dma(const S8Args &p, hipStream_t stream) {
     else
         hipLaunchKernelGGL((gemm_s8_rrr_dma_kernel<false, ACT, BiasT>), dim3(tiles), dim3(DmaCfg::NT), 0, stream, p);
     return kOk;
+}
+
+// s8 RRR last rows (decode-sized M; M % 256 in [1, 128] when a row of tiles
+// would start another round): the staged last-rows kernel reading row-major
+// B; false when the shape does not fit it (K % 512 == 0, 16-byte rows and
+// bases, N % (16 NB) == 0, K * ldb below 2^31).
+template <int ACT, typename BiasT>
+bool launch_rrr_rows(const S8Args &p, hipStream_t stream) {
+    const int rem = mfma2::last_rows_pass(p.M, p.N, 128);
+    if (rem == 0 || p.K % 512 != 0 || p.lda % 16 != 0 || p.ldb % 16 != 0 || !aligned16(p.a) || !aligned16(p.b) ||
+        !dma_extent_ok(p.M, p.lda) || (int64_t)p.K * p.ldb + mfma2::BN >= (1ll << 31))
+        return false;
+    // 64 columns per workgroup (64-byte row pieces of B): N = 4096 / 14336,
+    // K = 4096, M = 1: 13.4 / 21.6 us (32 columns 14.3 / 38.4, 16 columns
+    // 22.2 / 66.9, 128 columns 25.3 / 26.8; the 256x256 RRR tiles 40.5 / -)
+    const int nb = p.N % 64 == 0 ? 4 : p.N % 32 == 0 ? 2 : 1;
+    S8Args pm = p;
+    pm.M = p.M - rem;
+    if (pm.M > 0 && launch_rrr_dma<ACT, BiasT>(pm, stream) != kOk) return false;
+    const bool vec = p.N % 4 == 0 && p.ldd % 4 == 0 && (reinterpret_cast<uintptr_t>(p.d) % 4) == 0;
+#define BK_RRRROWS(RF, NB, SB, DEPTH)                                                                          \
+    if (rem <= 16 * (RF) && nb == (NB)) {                                                                       \
+        const size_t lds = std::max((size_t)(DEPTH) * (16 * (RF) + 16 * (NB)) * (SB), (size_t)(RF) * (NB) * ((SB) / 64) * 1024); \
+        if (vec)                                                                                                \
+            hipLaunchKernelGGL((gemm_s8_rcr_rows_staged_kernel<EPI_S8, true, ACT, BiasT, RF, NB, SB, DEPTH, false, true>), \
+                               dim3(p.N / (16 * (NB))), dim3(1024), lds, stream, p, pm.M);                      \
+        else                                                                                                    \
+            hipLaunchKernelGGL((gemm_s8_rcr_rows_staged_kernel<EPI_S8, false, ACT, BiasT, RF, NB, SB, DEPTH, false, true>), \
+                               dim3(p.N / (16 * (NB))), dim3(1024), lds, stream, p, pm.M);                      \
+        return true;                                                                                            \
+    }
+    BK_RRRROWS(2, 1, 512, 3)
+    BK_RRRROWS(4, 1, 512, 2)
+    BK_RRRROWS(8, 1, 512, 2)
+    BK_RRRROWS(2, 2, 512, 3)
+    BK_RRRROWS(4, 2, 512, 2)
+    BK_RRRROWS(8, 2, 512, 2)
+    BK_RRRROWS(2, 4, 512, 3)
+    BK_RRRROWS(4, 4, 512, 2)
+    BK_RRRROWS(8, 4, 256, 2)
+#undef BK_RRRROWS
+    return false;
 }
 
 int32_t check_rcr(int32_t m, int32_t n, int32_t k, int64_t lda, int64_t ldb, int64_t ldd) {

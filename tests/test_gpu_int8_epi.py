@@ -377,3 +377,28 @@ def test_u8_rcr_last_rows_large_k_exact(gpu):
     alpha = 255.0 / (255.0 * 255.0 * k)
     got = _run_u8(P.EpilogueKind.Identity, P.ElementKind.F32, a, b, alpha=alpha, layout=RCR)
     assert np.array_equal(got, O.gemm_u8_epi(a, b, "rcr", alpha))
+
+
+# s8 RRR last rows (decode-sized M, and M % 256 <= 128 under whole tile
+# rows): the staged last-rows kernel reading row-major B with transposing
+# LDS reads; 64 / 32 / 16 columns per workgroup (N % 64, % 32, % 16), 2 / 4 /
+# 8 row fragments, main RRR tiles above the rows.
+RRR_ROWS_SHAPES = [(1, 4096, 4096), (5, 256, 512), (33, 512, 1024), (20, 288, 512), (100, 272, 512),
+                   (128, 1024, 2048), (1025, 16384, 512), (1100, 16384, 1024)]
+
+
+@pytest.mark.parametrize("epi", [P.EpilogueKind.Identity, P.EpilogueKind.BiasGelu, P.EpilogueKind.BiasRelu])
+@pytest.mark.parametrize("shape", RRR_ROWS_SHAPES)
+def test_s8_rrr_last_rows(gpu, shape, epi):
+    m, n, k = shape
+    print(f"case: s8 rrr rows {epi.value} {shape}", flush=True)
+    g = rng(m + 5 * n + k)
+    a, b = int8_uniform(g, (m, k)), int8_uniform(g, (k, n))
+    c = int8_uniform(g, (m, n))
+    bias = (g.standard_normal(n) * 20).astype(np.float32)
+    has_bias = epi != P.EpilogueKind.Identity
+    alpha = 1.0 / (16.0 * k)
+    got = _run(RRR, epi, P.ElementKind.F32, a, b, c=c, bias=bias if has_bias else None, alpha=alpha, beta=0.5)
+    rows = slice(max(0, m - m % 256 - 2), m) if m > 256 else slice(0, m)
+    want = O.gemm_s8_epi(a[rows], b, "rrr", alpha, 0.5, c[rows], bias if has_bias else None, ACT[epi])
+    _check(got[rows], want, epi)
