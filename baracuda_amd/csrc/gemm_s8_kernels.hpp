@@ -1198,8 +1198,56 @@ inline bool u8_rrr_prepass_eligible(const S8Args &p) {
     return u8_rrr_dma_eligible(p) && (int64_t)p.K * p.N < (1ll << 31);
 }
 
+// u8 RRR last rows (decode-sized M; M % 256 in [1, 128] when a row of tiles
+// would start another round): the staged last-rows kernel with both its u8
+// and row-major-B flags, 64 columns per workgroup where N allows; main tiles
+// above the rows on the LDS-DMA u8 RRR kernel.  False when the shape does
+// not fit.  N = K = 4096, M = 1 / 16 on the general kernel: 87.4 / 86.6 us.
+template <int ACT, typename BiasT>
+bool launch_u8_rrr_rows(const S8Args &p, hipStream_t stream) {
+    const int rem = mfma2::last_rows_pass(p.M, p.N, 128);
+    if (rem == 0 || p.K % 512 != 0 || p.lda % 16 != 0 || p.ldb % 16 != 0 || !aligned16(p.a) || !aligned16(p.b) ||
+        !dma_extent_ok(p.M, p.lda) || (int64_t)p.K * p.ldb + mfma2::BN >= (1ll << 31))
+        return false;
+    S8Args pm = p;
+    pm.M = p.M - rem;
+    if (pm.M > 0 && !u8_rrr_dma_eligible(pm)) return false;
+    const bool vec = p.ldd % 4 == 0 && (reinterpret_cast<uintptr_t>(p.d) % 4) == 0;
+    if (pm.M > 0) {
+        const int tiles = (pm.M / mfma2::BM) * (p.N / mfma2::BN);
+        if (vec)
+            hipLaunchKernelGGL((gemm_u8_rrr_dma_kernel<true, ACT, BiasT>), dim3(tiles), dim3(DmaCfg::NT), 0, stream, pm);
+        else
+            hipLaunchKernelGGL((gemm_u8_rrr_dma_kernel<false, ACT, BiasT>), dim3(tiles), dim3(DmaCfg::NT), 0, stream, pm);
+    }
+    const int nb = p.N % 64 == 0 ? 4 : p.N % 32 == 0 ? 2 : 1;
+#define BK_U8RRRROWS(RF, NB, SB, DEPTH)                                                                        \
+    if (rem <= 16 * (RF) && nb == (NB)) {                                                                       \
+        const size_t lds = std::max((size_t)(DEPTH) * (16 * (RF) + 16 * (NB)) * (SB), (size_t)(RF) * (NB) * ((SB) / 64) * 1024); \
+        if (vec)                                                                                                \
+            hipLaunchKernelGGL((gemm_s8_rcr_rows_staged_kernel<0, true, ACT, BiasT, RF, NB, SB, DEPTH, true, true>), \
+                               dim3(p.N / (16 * (NB))), dim3(1024), lds, stream, p, pm.M);                      \
+        else                                                                                                    \
+            hipLaunchKernelGGL((gemm_s8_rcr_rows_staged_kernel<0, false, ACT, BiasT, RF, NB, SB, DEPTH, true, true>), \
+                               dim3(p.N / (16 * (NB))), dim3(1024), lds, stream, p, pm.M);                      \
+        return true;                                                                                            \
+    }
+    BK_U8RRRROWS(2, 1, 512, 3)
+    BK_U8RRRROWS(4, 1, 512, 2)
+    BK_U8RRRROWS(8, 1, 512, 2)
+    BK_U8RRRROWS(2, 2, 512, 3)
+    BK_U8RRRROWS(4, 2, 512, 2)
+    BK_U8RRRROWS(8, 2, 512, 2)
+    BK_U8RRRROWS(2, 4, 512, 3)
+    BK_U8RRRROWS(4, 4, 512, 2)
+    BK_U8RRRROWS(8, 4, 256, 2)
+#undef BK_U8RRRROWS
+    return false;
+}
+
 template <int ACT, typename BiasT>
 int32_t launch_u8_rrr(const S8Args &p, hipStream_t stream, void *workspace = nullptr, size_t workspace_bytes = 0) {
+    if (launch_u8_rrr_rows<ACT, BiasT>(p, stream)) return launch_status();
     const bool dma = u8_rrr_dma_eligible(p);
     if (u8_rrr_prepass_eligible(p) && workspace && workspace_bytes >= u8_rrr_workspace_bytes(p.M, p.N, p.K) &&
         (reinterpret_cast<uintptr_t>(workspace) & 255u) == 0) {

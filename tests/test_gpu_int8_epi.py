@@ -340,43 +340,47 @@ def test_null_c_with_beta(gpu, shape, layout, epi, elem):
     _check(d.cpu().numpy(), want, epi)
 
 
-# u8 RCR last rows (decode-sized M, and M % 256 <= 128 under whole tile
-# rows): the staged last-rows kernel with flipped operands and the
-# correction folded into its accumulator.  2 / 4 / 8 row fragments, 16 / 32
-# / 64 columns per workgroup, main 256x256 tiles above the rows.
+# u8 last rows (decode-sized M, and M % 256 <= 128 under whole tile rows):
+# the staged last-rows kernel with flipped operands and the correction
+# folded into its accumulator.  2 / 4 / 8 row fragments, 16 / 32 / 64
+# columns per workgroup, main 256x256 tiles above the rows.
 U8_ROWS_SHAPES = [(1, 4096, 4096), (5, 256, 512), (33, 512, 1024), (100, 6144, 512), (128, 12288, 512),
-                  (1025, 16384, 512), (1100, 16384, 1024)]
+                  (1025, 16384, 512), (1100, 16384, 1024), (20, 272, 512)]
 
 
+@pytest.mark.parametrize("layout", [RCR, RRR])
 @pytest.mark.parametrize("epi", [P.EpilogueKind.Identity, P.EpilogueKind.BiasGelu, P.EpilogueKind.BiasRelu])
 @pytest.mark.parametrize("shape", U8_ROWS_SHAPES)
-def test_u8_rcr_last_rows(gpu, shape, epi):
+def test_u8_last_rows(gpu, shape, epi, layout):
+    # RCR: 16 / 32 / 64 columns per workgroup by N; RRR (row-major B,
+    # transposing LDS reads): 64 columns where N % 64 == 0
     m, n, k = shape
-    print(f"case: u8 rcr rows {epi.value} {shape}", flush=True)
+    print(f"case: u8 {_LNAME[layout]} rows {epi.value} {shape}", flush=True)
     g = rng(m + 3 * n + k)
     a = g.integers(0, 256, (m, k), dtype=np.uint8)
-    b = g.integers(0, 256, (n, k), dtype=np.uint8)
+    b = _u8_b(g.integers(0, 256, n * k, dtype=np.uint8), k, n, layout)
     c = g.integers(0, 256, (m, n), dtype=np.uint8)
     bias = (g.standard_normal(n) * 30).astype(np.float32)
     alpha = 1.0 / (64.0 * k)
     has_bias = epi != P.EpilogueKind.Identity
     got = _run_u8(epi, P.ElementKind.F32, a, b, c=c, bias=bias if has_bias else None, alpha=alpha, beta=0.5,
-                  layout=RCR)
+                  layout=layout)
     rows = slice(max(0, m - m % 256 - 2), m) if m > 256 else slice(0, m)
-    want = O.gemm_u8_epi(a[rows], b, "rcr", alpha, 0.5, c[rows], bias if has_bias else None, ACT[epi])
+    want = O.gemm_u8_epi(a[rows], b, _LNAME[layout], alpha, 0.5, c[rows], bias if has_bias else None, ACT[epi])
     _check(got[rows], want, epi)
 
 
-def test_u8_rcr_last_rows_large_k_exact(gpu):
+@pytest.mark.parametrize("layout", [RCR, RRR])
+def test_u8_last_rows_large_k_exact(gpu, layout):
     # K = 8192 (255^2 K < 2^31): the folded 128 (sum a' + sum b') and the
     # 16384 K term, checked through an informative u8 output
     m, n, k = 16, 512, 8192
     g = rng(77)
     a = g.integers(0, 256, (m, k), dtype=np.uint8)
-    b = g.integers(0, 256, (n, k), dtype=np.uint8)
+    b = _u8_b(g.integers(0, 256, n * k, dtype=np.uint8), k, n, layout)
     alpha = 255.0 / (255.0 * 255.0 * k)
-    got = _run_u8(P.EpilogueKind.Identity, P.ElementKind.F32, a, b, alpha=alpha, layout=RCR)
-    assert np.array_equal(got, O.gemm_u8_epi(a, b, "rcr", alpha))
+    got = _run_u8(P.EpilogueKind.Identity, P.ElementKind.F32, a, b, alpha=alpha, layout=layout)
+    assert np.array_equal(got, O.gemm_u8_epi(a, b, _LNAME[layout], alpha))
 
 
 # s8 RRR last rows (decode-sized M, and M % 256 <= 128 under whole tile
