@@ -669,6 +669,30 @@ def main():
             extra["int8_s8out_4096_cubed"] = e
             del ua, ub, ud
             del ia, ib, ibr, idd
+            # decode-sized M (the last-rows passes) of the other int8 SKU
+            # families at N = K = 4096: 8 rotated B sets, device time per call
+            # replayed from a HIP graph
+            lr = {}
+            for lname, layout, el in (("s8_rrr", P.LayoutSku.Rrr, P.ElementKind.S8),
+                                      ("u8_rcr", P.LayoutSku.Rcr, P.ElementKind.U8),
+                                      ("u8_rrr", P.LayoutSku.Rrr, P.ElementKind.U8)):
+                ldt = torch.uint8 if el == P.ElementKind.U8 else torch.int8
+                lbs = [torch.randint(0, 127, (K, N) if layout == P.LayoutSku.Rrr else (N, K), dtype=torch.int8,
+                                     device=dev).to(ldt) for _ in range(8)]
+                for lm in (1, 16):
+                    la = torch.randint(0, 127, (lm, K), dtype=torch.int8, device=dev).to(ldt)
+                    ld_ = torch.empty((lm, N), dtype=ldt, device=dev)
+                    lp = P.IntGemmPlan.select(P.IntGemmDescriptor(lm, N, K, layout=layout, element=el, output=el))
+                    li = [0]
+
+                    def lcall():
+                        lp.run(la, lbs[li[0] % 8], ld_, alpha=1.0 / 65536)
+                        li[0] += 1
+                    lus = graph_us(lcall, per_graph=20, replays=10)
+                    lr[f"{lname}_m{lm}"] = {"graph_replay_us": round(lus, 2),
+                                            "graph_replay_weight_frac_hbm_peak": round(N * K / (lus * 1e-6) / 8e12, 3)}
+                del lbs
+            extra["int8_other_skus_decode_n4096_k4096"] = lr
         if only in ("", "gemv"):
             # gemv_dense_m1 (reference ABI, RRR B[K,N]) at the reference's own skinny
             # f32 contraction shape M=1, K=N=4096 (a figure adjacent to the BASELINE.json metric).
