@@ -576,6 +576,12 @@ __global__ __launch_bounds__(512) void gemm_s8_rcr_rows_kernel(S8Args p, int m0)
     epi(m0 + 16 * wave + r16, n0 + 4 * g, sum);   // rows past M are not stored
 }
 
+template <bool VecOut, int ACT, typename BiasT>
+struct U8Epilogue;
+// Zero row / column sums for U8Epilogue when the correction is already in
+// the accumulator.
+__device__ const int kZeroSums[16] = {0};
+
 // One last row (M = 1 decode steps; K % (1024 BT) == 0): a workgroup of 4
 // waves owns 4 output columns and wave w streams B row n0 + w over all of K,
 // 16 bytes per lane of every kilobyte straight into registers (BT kilobytes
@@ -588,7 +594,9 @@ __global__ __launch_bounds__(512) void gemm_s8_rcr_rows_kernel(S8Args p, int m0)
 // 4.73 us for the same loads without the arithmetic.  From 2 rows on the A
 // loads and dot products cost more than the layout saves (M = 2 / 4 / 8:
 // 5.48 / 6.59 / 10.9 us against 5.52 / 5.66 / 5.98).
-template <int EPI, bool VecOut, int ACT, typename BiasT, int BT>
+// U8: u8 operands (the u8 RCR SKUs): v_dot4_u32_u8 sums the products exactly
+// (mod 2^32, no flip), and U8Epilogue runs with zero sums and no correction.
+template <int EPI, bool VecOut, int ACT, typename BiasT, int BT, bool U8 = false>
 __global__ __launch_bounds__(256) void gemm_s8_rcr_row1_kernel(S8Args p, int m0) {
     __shared__ int colsum[4];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -609,15 +617,25 @@ __global__ __launch_bounds__(256) void gemm_s8_rcr_row1_kernel(S8Args p, int m0)
 #pragma unroll
         for (int u = 0; u < BT; ++u)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) acc = __builtin_amdgcn_sdot4(av[u][q], bv[u][q], acc, false);
+            for (int q = 0; q < 4; ++q) {
+                if constexpr (U8)
+                    acc = (int)__builtin_amdgcn_udot4((uint32_t)av[u][q], (uint32_t)bv[u][q], (uint32_t)acc, false);
+                else
+                    acc = __builtin_amdgcn_sdot4(av[u][q], bv[u][q], acc, false);
+            }
     }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) acc = (int)((uint32_t)acc + (uint32_t)__shfl_xor(acc, off, 64));
     if (lane == 0) colsum[wave] = acc;
     __syncthreads();
     if (threadIdx.x != 0) return;
-    const S8Epilogue<EPI, VecOut, ACT, BiasT> epi{p};
-    epi(m0, n0, v4i{colsum[0], colsum[1], colsum[2], colsum[3]});
+    if constexpr (U8) {
+        const U8Epilogue<VecOut, ACT, BiasT> epi{p, kZeroSums, kZeroSums, 0u};
+        epi(0, 0, v4i{colsum[0], colsum[1], colsum[2], colsum[3]}, m0, n0);
+    } else {
+        const S8Epilogue<EPI, VecOut, ACT, BiasT> epi{p};
+        epi(m0, n0, v4i{colsum[0], colsum[1], colsum[2], colsum[3]});
+    }
 }
 
 // The last rows (at most 16 * RF), B streamed through LDS: K % 1024 == 0,
@@ -732,11 +750,6 @@ __global__ __launch_bounds__(1024) void gemm_s8_rcr_rows_dma_kernel(S8Args p, in
 // 8.0 / 8.8 / 11.3 / 11.6 us, against 9.8-10.3 / 10.0-10.5 / 12.0-13.2 /
 // 12.3-13.5 us for 256-byte stages two to four deep; three 512-byte stages
 // measure the same as two (kRowsStagedSB, kRowsStagedDepth).
-template <bool VecOut, int ACT, typename BiasT>
-struct U8Epilogue;
-// Zero row / column sums for U8Epilogue when the correction is already in
-// the accumulator.
-__device__ const int kZeroSums[16] = {0};
 
 // U8: u8 x u8 operands (RCR u8 SKUs; EPI unused) through the signed MFMA:
 // fragments flipped to u - 128 and the correction of
@@ -1375,6 +1388,17 @@ bool launch_u8_rcr_rows(const S8Args &p, hipStream_t stream) {
             hipLaunchKernelGGL((gemm_u8_rcr_dma_kernel<true, ACT, BiasT>), dim3(tiles), dim3(DmaCfg::NT), 0, stream, pm);
         else
             hipLaunchKernelGGL((gemm_u8_rcr_dma_kernel<false, ACT, BiasT>), dim3(tiles), dim3(DmaCfg::NT), 0, stream, pm);
+    }
+    if (rem == 1 && p.K % 1024 == 0) {
+        // one row: the dot4 row kernel (N = K = 4096: 7.6 us on the staged kernel)
+        if (p.K % 2048 == 0) {
+            if (vec) hipLaunchKernelGGL((gemm_s8_rcr_row1_kernel<0, true, ACT, BiasT, 2, true>), dim3(p.N / 4), dim3(256), 0, stream, p, pm.M);
+            else hipLaunchKernelGGL((gemm_s8_rcr_row1_kernel<0, false, ACT, BiasT, 2, true>), dim3(p.N / 4), dim3(256), 0, stream, p, pm.M);
+        } else {
+            if (vec) hipLaunchKernelGGL((gemm_s8_rcr_row1_kernel<0, true, ACT, BiasT, 1, true>), dim3(p.N / 4), dim3(256), 0, stream, p, pm.M);
+            else hipLaunchKernelGGL((gemm_s8_rcr_row1_kernel<0, false, ACT, BiasT, 1, true>), dim3(p.N / 4), dim3(256), 0, stream, p, pm.M);
+        }
+        return true;
     }
     const int nb = mfma2::last_rows_col_frags(p.N);
 #define BK_U8ROWS(RF, NB, SB, DEPTH)                                                                           \

@@ -345,7 +345,7 @@ def test_null_c_with_beta(gpu, shape, layout, epi, elem):
 # folded into its accumulator.  2 / 4 / 8 row fragments, 16 / 32 / 64
 # columns per workgroup, main 256x256 tiles above the rows.
 U8_ROWS_SHAPES = [(1, 4096, 4096), (5, 256, 512), (33, 512, 1024), (100, 6144, 512), (128, 12288, 512),
-                  (1025, 16384, 512), (1100, 16384, 1024), (20, 272, 512)]
+                  (1025, 16384, 512), (1100, 16384, 1024), (20, 272, 512), (1, 256, 1024)]
 
 
 @pytest.mark.parametrize("layout", [RCR, RRR])
