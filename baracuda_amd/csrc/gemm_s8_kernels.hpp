@@ -766,7 +766,10 @@ __global__ __launch_bounds__(1024) void gemm_s8_rcr_rows_dma_kernel(S8Args p, in
 // consecutive k of column i.
 template <int EPI, bool VecOut, int ACT, typename BiasT, int RF, int NB, int SB, int DEPTH, bool U8 = false,
           bool RowB = false>
-__global__ __launch_bounds__(1024) void gemm_s8_rcr_rows_staged_kernel(S8Args p, int m0) {
+__global__ __launch_bounds__(1024) void gemm_s8_rcr_rows_staged_kernel(S8Args p, int m_first) {
+    // blockIdx.y: 16 RF-row block of the pass (several when the pass covers
+    // more rows than one workgroup holds)
+    const int m0 = m_first + blockIdx.y * 16 * RF;
     constexpr int WAVES = 16, CH = SB / 64;                  // 64-byte chunks per stage
     constexpr int FPW = RF * CH / WAVES;                      // A row fragments per wave
     constexpr int FSTEP = WAVES / CH;
@@ -1218,12 +1221,22 @@ inline bool u8_rrr_prepass_eligible(const S8Args &p) {
 // not fit.  N = K = 4096, M = 1 / 16 on the general kernel: 87.4 / 86.6 us.
 template <int ACT, typename BiasT>
 bool launch_u8_rrr_rows(const S8Args &p, hipStream_t stream) {
-    const int rem = mfma2::last_rows_pass(p.M, p.N, 128);
+    int rem = mfma2::last_rows_pass(p.M, p.N, 128), blocks = 1;
+    bool whole = false;
+    if (rem == 0 && (p.M <= 256 || (p.M <= 512 && p.M % 256 != 0)) && p.N % 16 == 0) {
+        // a small grid of 256-row tiles: all rows as 128-row blocks of the
+        // last-rows kernel.  N = K = 4096: M = 200 / 256 / 384 in 36.0 /
+        // 35.7 / 35.9 us against 87 / 60 (pre-pass workspace) / 114.7; whole-
+        // tile M = 512 stays on the tiles (60 us)
+        rem = 128;
+        blocks = (p.M + 127) / 128;
+        whole = true;
+    }
     if (rem == 0 || p.K % 512 != 0 || p.lda % 16 != 0 || p.ldb % 16 != 0 || !aligned16(p.a) || !aligned16(p.b) ||
         !dma_extent_ok(p.M, p.lda) || (int64_t)p.K * p.ldb + mfma2::BN >= (1ll << 31))
         return false;
     S8Args pm = p;
-    pm.M = p.M - rem;
+    pm.M = whole ? 0 : p.M - rem;
     if (pm.M > 0 && !u8_rrr_dma_eligible(pm)) return false;
     const bool vec = p.ldd % 4 == 0 && (reinterpret_cast<uintptr_t>(p.d) % 4) == 0;
     if (pm.M > 0) {
@@ -1239,10 +1252,10 @@ bool launch_u8_rrr_rows(const S8Args &p, hipStream_t stream) {
         const size_t lds = std::max((size_t)(DEPTH) * (16 * (RF) + 16 * (NB)) * (SB), (size_t)(RF) * (NB) * ((SB) / 64) * 1024); \
         if (vec)                                                                                                \
             hipLaunchKernelGGL((gemm_s8_rcr_rows_staged_kernel<0, true, ACT, BiasT, RF, NB, SB, DEPTH, true, true>), \
-                               dim3(p.N / (16 * (NB))), dim3(1024), lds, stream, p, pm.M);                      \
+                               dim3(p.N / (16 * (NB)), blocks), dim3(1024), lds, stream, p, pm.M);                      \
         else                                                                                                    \
             hipLaunchKernelGGL((gemm_s8_rcr_rows_staged_kernel<0, false, ACT, BiasT, RF, NB, SB, DEPTH, true, true>), \
-                               dim3(p.N / (16 * (NB))), dim3(1024), lds, stream, p, pm.M);                      \
+                               dim3(p.N / (16 * (NB)), blocks), dim3(1024), lds, stream, p, pm.M);                      \
         return true;                                                                                            \
     }
     BK_U8RRRROWS(2, 1, 512, 3)
@@ -1374,12 +1387,21 @@ __global__ __launch_bounds__(NT, 1) void gemm_u8_rcr_kernel(S8Args p) {
 // register-staged general kernel took 68.9 / 68.1 / – us.
 template <int ACT, typename BiasT>
 bool launch_u8_rcr_rows(const S8Args &p, hipStream_t stream) {
-    const int rem = mfma2::last_rows_pass(p.M, p.N, 128);
+    int rem = mfma2::last_rows_pass(p.M, p.N, 128), blocks = 1;
+    bool whole = false;
+    if (rem == 0 && p.M <= 512 && p.N % 16 == 0) {
+        // a small grid of 256-row tiles: all rows as 128-row blocks of the
+        // last-rows kernel.  N = K = 4096: M = 200 / 256 / 384 / 512 in
+        // 28.1 / 26.8 / 38.6 / 49.1 us against 65-69 on the tiles
+        rem = 128;
+        blocks = (p.M + 127) / 128;
+        whole = true;
+    }
     if (rem == 0 || p.K % 512 != 0 || p.lda % 16 != 0 || p.ldb % 16 != 0 || !aligned16(p.a) || !aligned16(p.b) ||
         !dma_extent_ok(p.M, p.lda) || !dma_extent_ok(p.N, p.ldb))
         return false;
     S8Args pm = p;
-    pm.M = p.M - rem;
+    pm.M = whole ? 0 : p.M - rem;
     if (pm.M > 0 && p.N % mfma2::BN != 0) return false;
     const bool vec = p.ldd % 4 == 0 && (reinterpret_cast<uintptr_t>(p.d) % 4) == 0;
     if (pm.M > 0) {
@@ -1389,7 +1411,7 @@ bool launch_u8_rcr_rows(const S8Args &p, hipStream_t stream) {
         else
             hipLaunchKernelGGL((gemm_u8_rcr_dma_kernel<false, ACT, BiasT>), dim3(tiles), dim3(DmaCfg::NT), 0, stream, pm);
     }
-    if (rem == 1 && p.K % 1024 == 0) {
+    if (rem == 1 && !whole && p.K % 1024 == 0) {
         // one row: the dot4 row kernel (N = K = 4096: 7.6 us on the staged kernel)
         if (p.K % 2048 == 0) {
             if (vec) hipLaunchKernelGGL((gemm_s8_rcr_row1_kernel<0, true, ACT, BiasT, 2, true>), dim3(p.N / 4), dim3(256), 0, stream, p, pm.M);
@@ -1406,10 +1428,10 @@ bool launch_u8_rcr_rows(const S8Args &p, hipStream_t stream) {
         const size_t lds = std::max((size_t)(DEPTH) * (16 * (RF) + 16 * (NB)) * (SB), (size_t)(RF) * (NB) * ((SB) / 64) * 1024); \
         if (vec)                                                                                                \
             hipLaunchKernelGGL((gemm_s8_rcr_rows_staged_kernel<0, true, ACT, BiasT, RF, NB, SB, DEPTH, true>),    \
-                               dim3(p.N / (16 * (NB))), dim3(1024), lds, stream, p, pm.M);                      \
+                               dim3(p.N / (16 * (NB)), blocks), dim3(1024), lds, stream, p, pm.M);                      \
         else                                                                                                    \
             hipLaunchKernelGGL((gemm_s8_rcr_rows_staged_kernel<0, false, ACT, BiasT, RF, NB, SB, DEPTH, true>),   \
-                               dim3(p.N / (16 * (NB))), dim3(1024), lds, stream, p, pm.M);                      \
+                               dim3(p.N / (16 * (NB)), blocks), dim3(1024), lds, stream, p, pm.M);                      \
         return true;                                                                                            \
     }
     BK_U8ROWS(2, 1, 512, 3)

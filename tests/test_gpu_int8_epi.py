@@ -406,3 +406,22 @@ def test_s8_rrr_last_rows(gpu, shape, epi):
     rows = slice(max(0, m - m % 256 - 2), m) if m > 256 else slice(0, m)
     want = O.gemm_s8_epi(a[rows], b, "rrr", alpha, 0.5, c[rows], bias if has_bias else None, ACT[epi])
     _check(got[rows], want, epi)
+
+
+@pytest.mark.parametrize("layout,shape", [(RCR, (200, 512, 1024)), (RCR, (384, 256, 512)), (RCR, (512, 512, 512)),
+                                          (RRR, (200, 512, 1024)), (RRR, (256, 512, 512)), (RRR, (384, 256, 512))])
+def test_u8_small_grid_row_blocks(gpu, layout, shape):
+    # u8 grids of at most 512 rows (RRR: 256, or 512 off the 256 grid): every row as 128-row
+    # blocks of the last-rows kernel; the whole output against the oracle
+    m, n, k = shape
+    print(f"case: u8 {_LNAME[layout]} row blocks {shape}", flush=True)
+    g = rng(m + 11 * n + k)
+    a = g.integers(0, 256, (m, k), dtype=np.uint8)
+    b = _u8_b(g.integers(0, 256, n * k, dtype=np.uint8), k, n, layout)
+    c = g.integers(0, 256, (m, n), dtype=np.uint8)
+    bias = (g.standard_normal(n) * 30).astype(np.float32)
+    alpha = 1.0 / (64.0 * k)
+    got = _run_u8(P.EpilogueKind.BiasRelu, P.ElementKind.F32, a, b, c=c, bias=bias, alpha=alpha, beta=0.5,
+                  layout=layout)
+    want = O.gemm_u8_epi(a, b, _LNAME[layout], alpha, 0.5, c, bias, "relu")
+    assert np.array_equal(got, want)
