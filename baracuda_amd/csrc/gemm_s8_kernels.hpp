@@ -1615,7 +1615,16 @@ int32_t launch_rrr_dma(const S8Args &p, hipStream_t stream) {
 // bases, N % (16 NB) == 0, K * ldb below 2^31).
 template <int ACT, typename BiasT>
 bool launch_rrr_rows(const S8Args &p, hipStream_t stream) {
-    const int rem = mfma2::last_rows_pass(p.M, p.N, 128);
+    int rem = mfma2::last_rows_pass(p.M, p.N, 128), blocks = 1;
+    bool whole = false;
+    if (rem == 0 && p.M <= 512 && p.N % 16 == 0) {
+        // a small grid of 256-row tiles: all rows as 128-row blocks.  N = K =
+        // 4096: M = 200 / 256 / 512 in 23.0 / 22.9 / 23.3 us against 44 on the
+        // tiles; from 768 rows the blocks need a second round (44.6 on tiles)
+        rem = 128;
+        blocks = (p.M + 127) / 128;
+        whole = true;
+    }
     if (rem == 0 || p.K % 512 != 0 || p.lda % 16 != 0 || p.ldb % 16 != 0 || !aligned16(p.a) || !aligned16(p.b) ||
         !dma_extent_ok(p.M, p.lda) || (int64_t)p.K * p.ldb + mfma2::BN >= (1ll << 31))
         return false;
@@ -1624,7 +1633,7 @@ bool launch_rrr_rows(const S8Args &p, hipStream_t stream) {
     // 22.2 / 66.9, 128 columns 25.3 / 26.8; the 256x256 RRR tiles 40.5 / -)
     const int nb = p.N % 64 == 0 ? 4 : p.N % 32 == 0 ? 2 : 1;
     S8Args pm = p;
-    pm.M = p.M - rem;
+    pm.M = whole ? 0 : p.M - rem;
     if (pm.M > 0 && launch_rrr_dma<ACT, BiasT>(pm, stream) != kOk) return false;
     const bool vec = p.N % 4 == 0 && p.ldd % 4 == 0 && (reinterpret_cast<uintptr_t>(p.d) % 4) == 0;
 #define BK_RRRROWS(RF, NB, SB, DEPTH)                                                                          \
@@ -1632,10 +1641,10 @@ bool launch_rrr_rows(const S8Args &p, hipStream_t stream) {
         const size_t lds = std::max((size_t)(DEPTH) * (16 * (RF) + 16 * (NB)) * (SB), (size_t)(RF) * (NB) * ((SB) / 64) * 1024); \
         if (vec)                                                                                                \
             hipLaunchKernelGGL((gemm_s8_rcr_rows_staged_kernel<EPI_S8, true, ACT, BiasT, RF, NB, SB, DEPTH, false, true>), \
-                               dim3(p.N / (16 * (NB))), dim3(1024), lds, stream, p, pm.M);                      \
+                               dim3(p.N / (16 * (NB)), blocks), dim3(1024), lds, stream, p, pm.M);                      \
         else                                                                                                    \
             hipLaunchKernelGGL((gemm_s8_rcr_rows_staged_kernel<EPI_S8, false, ACT, BiasT, RF, NB, SB, DEPTH, false, true>), \
-                               dim3(p.N / (16 * (NB))), dim3(1024), lds, stream, p, pm.M);                      \
+                               dim3(p.N / (16 * (NB)), blocks), dim3(1024), lds, stream, p, pm.M);                      \
         return true;                                                                                            \
     }
     BK_RRRROWS(2, 1, 512, 3)

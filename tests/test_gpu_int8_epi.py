@@ -425,3 +425,18 @@ def test_u8_small_grid_row_blocks(gpu, layout, shape):
                   layout=layout)
     want = O.gemm_u8_epi(a, b, _LNAME[layout], alpha, 0.5, c, bias, "relu")
     assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("shape", [(200, 512, 1024), (512, 256, 512), (300, 288, 512)])
+def test_s8_rrr_small_grid_row_blocks(gpu, shape):
+    # s8 RRR grids of at most 512 rows: every row as 128-row blocks of the
+    # last-rows kernel (row-major B); the whole output against the oracle
+    m, n, k = shape
+    print(f"case: s8 rrr row blocks {shape}", flush=True)
+    g = rng(m + 13 * n + k)
+    a, b = int8_uniform(g, (m, k)), int8_uniform(g, (k, n))
+    c = int8_uniform(g, (m, n))
+    bias = (g.standard_normal(n) * 20).astype(np.float32)
+    alpha = 1.0 / (16.0 * k)
+    got = _run(RRR, P.EpilogueKind.BiasRelu, P.ElementKind.F32, a, b, c=c, bias=bias, alpha=alpha, beta=0.5)
+    assert np.array_equal(got, O.gemm_s8_epi(a, b, "rrr", alpha, 0.5, c, bias, "relu"))
