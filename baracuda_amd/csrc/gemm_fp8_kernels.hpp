@@ -263,7 +263,14 @@ __global__ __launch_bounds__(C::NT, C::NT == 256 ? 2 : 1) void gemm_fp8_dma_kern
 // time.  Requirements (checked by the launcher): K % SB == 0, the fast
 // path's alignment and 2^31 extents, N % (16 NB) == 0; dynamic LDS of
 // DEPTH * (16 RF + 16 NB) * SB bytes.
-template <int FMT, int EPI, int ACT, int RF, int NB, int SB, int DEPTH>
+//
+// RowB: B row-major [K, N] (the RRR SKUs): the stage's B region holds its SB
+// k-rows of the 16 NB columns as they lie in memory (row pitch 16 NB bytes,
+// whole-row DMAs, the K position moving the row by k0 * ldb); the 32 k-bytes
+// of a lane's fragment come from four ds_read_b64_tr_b8 reads of 8 k-rows
+// each (lane pair (2j, 2j + 1) pointing at k-row j; lane i gets 8 k of
+// column i), as in PolicyF8RowB.
+template <int FMT, int EPI, int ACT, int RF, int NB, int SB, int DEPTH, bool RowB = false>
 __global__ __launch_bounds__(1024) void gemm_fp8_rcr_rows_staged_kernel(F8Args p, int m0) {
     constexpr int WAVES = 16, CH = SB / 128;
     constexpr int FPW = RF * CH / WAVES;                 // A row fragments per wave
@@ -283,7 +290,7 @@ __global__ __launch_bounds__(1024) void gemm_fp8_rcr_rows_staged_kernel(F8Args p
     const int r16 = lane & 15, g = lane >> 4;
     const int n0 = blockIdx.x * 16 * NB;
     const v4i ra = mfma2::make_rsrc(p.a, (uint32_t)((int64_t)p.M * p.lda));
-    const v4i rb = mfma2::make_rsrc(p.b, (uint32_t)((int64_t)p.N * p.ldb));
+    const v4i rb = mfma2::make_rsrc(p.b, (uint32_t)(RowB ? (int64_t)p.K * p.ldb : (int64_t)p.N * p.ldb));
     // DMA instruction j of a stage: units 64 j .. 64 j + 63 of the row-major
     // stage, lane L fetching unit (64 j + L) % UPR of row (64 j + L) / UPR
     auto dma_stage = [&](int st, int8_t *buf) {
@@ -292,10 +299,15 @@ __global__ __launch_bounds__(1024) void gemm_fp8_rcr_rows_staged_kernel(F8Args p
             const int idx = 64 * j + lane;
             const int r = idx / UPR, slot = idx % UPR;
             const int unit = slot ^ (r & 15);
-            if (r < 16 * RF)
+            if (r < 16 * RF) {
                 mfma2::dma16(ra, (int)((int64_t)(m0 + r) * p.lda) + 16 * unit, k0, buf + j * 1024);
-            else
+            } else if constexpr (RowB) {
+                const int ib = idx - 16 * RF * UPR;   // unit of the B region: k-row ib / NB
+                mfma2::dma16(rb, (ib / NB) * (int)p.ldb + n0 + 16 * (ib % NB),
+                             __builtin_amdgcn_readfirstlane(k0 * (int)p.ldb), buf + j * 1024);
+            } else {
                 mfma2::dma16(rb, (int)((int64_t)(n0 + r - 16 * RF) * p.ldb) + 16 * unit, k0, buf + j * 1024);
+            }
         }
     };
     const bool hi = NI % WAVES == 0 || wave < NI % WAVES;
@@ -320,9 +332,17 @@ __global__ __launch_bounds__(1024) void gemm_fp8_rcr_rows_staged_kernel(F8Args p
         v8i bv[NB];
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-            const int8_t *brow = buf + (16 * RF + 16 * nb + r16) * SB;
-            const v4i blo = *reinterpret_cast<const v4i *>(brow + u0), bhi = *reinterpret_cast<const v4i *>(brow + u1);
-            bv[nb] = (v8i){blo[0], blo[1], blo[2], blo[3], bhi[0], bhi[1], bhi[2], bhi[3]};
+            if constexpr (RowB) {
+                const int kb = 128 * c + 32 * g + (r16 >> 1);
+                const int8_t *q = buf + 16 * RF * SB + kb * (16 * NB) + 16 * nb + ((lane & 1) << 3);
+                const mfma2::v2i_t t0 = mfma2::ds_read_tr8(q), t1 = mfma2::ds_read_tr8(q + 8 * 16 * NB);
+                const mfma2::v2i_t t2 = mfma2::ds_read_tr8(q + 16 * 16 * NB), t3 = mfma2::ds_read_tr8(q + 24 * 16 * NB);
+                bv[nb] = (v8i){t0[0], t0[1], t1[0], t1[1], t2[0], t2[1], t3[0], t3[1]};
+            } else {
+                const int8_t *brow = buf + (16 * RF + 16 * nb + r16) * SB;
+                const v4i blo = *reinterpret_cast<const v4i *>(brow + u0), bhi = *reinterpret_cast<const v4i *>(brow + u1);
+                bv[nb] = (v8i){blo[0], blo[1], blo[2], blo[3], bhi[0], bhi[1], bhi[2], bhi[3]};
+            }
         }
 #pragma unroll
         for (int i = 0; i < FPW; ++i) {
@@ -401,6 +421,35 @@ int32_t launch_fp8(const F8Args &p, hipStream_t stream) {
     const bool fast = p.K % mfma2::BK == 0 && p.lda % 16 == 0 && p.ldb % 16 == 0 && aligned16(p.a) &&
                       aligned16(p.b) && p.N % 4 == 0 && pad_m * p.lda < (1ll << 31) && pad_b < (1ll << 31) &&
                       p.ldd % 4 == 0 && (reinterpret_cast<uintptr_t>(p.d) % (4 * out_elem)) == 0;
+    if (fast && LAYOUT == F8_RRR && p.K % 512 == 0 && (int64_t)p.K * p.ldb + mfma2::BN < (1ll << 31)) {
+        // RRR last rows: the staged kernel reading row-major B, 64 columns
+        // per workgroup where N allows (64-byte row pieces)
+        const int rem = mfma2::last_rows_pass(p.M, p.N, 128);
+        if (rem != 0) {
+            F8Args pm = p;
+            pm.M = p.M - rem;
+            const int tiles = (pm.M / mfma2::BM) * ((p.N + mfma2::BN - 1) / mfma2::BN);
+            if (tiles > 0)
+                hipLaunchKernelGGL((gemm_fp8_dma_kernel<FMT, LAYOUT, EPI, ACT>), dim3(tiles), dim3(F8DmaCfg::NT),
+                                   0, stream, pm);
+            const int nb = p.N % 64 == 0 ? 4 : p.N % 32 == 0 ? 2 : 1;
+#define BK_F8RRRROWS(RF, NB, SB, DEPTH)                                                                    \
+            if (rem <= 16 * (RF) && nb == (NB)) {                                                         \
+                hipLaunchKernelGGL((gemm_fp8_rcr_rows_staged_kernel<FMT, EPI, ACT, RF, NB, SB, DEPTH, true>), \
+                                   dim3(p.N / (16 * (NB))), dim3(1024),                                  \
+                                   (size_t)(DEPTH) * (16 * (RF) + 16 * (NB)) * (SB), stream, p, pm.M);    \
+                return launch_status();                                                                   \
+            }
+            BK_F8RRRROWS(4, 4, 512, 2)
+            BK_F8RRRROWS(8, 4, 256, 2)
+            BK_F8RRRROWS(4, 2, 512, 2)
+            BK_F8RRRROWS(8, 2, 512, 2)
+            BK_F8RRRROWS(2, 1, 1024, 3)
+            BK_F8RRRROWS(4, 1, 512, 2)
+            BK_F8RRRROWS(8, 1, 512, 2)
+#undef BK_F8RRRROWS
+        }
+    }
     if (fast && LAYOUT == F8_RCR) {
         // the last rows as their own pass when a row of tiles would start
         // another round (decode-sized M: all of it)

@@ -110,3 +110,48 @@ def test_fp8_rows_deterministic_and_untouched_columns(gpu):
         assert np.all(h[:, n:] == -7.0) and np.all(h[m:, :] == -7.0)
         outs.append(h[:m, :n])
     assert all(np.array_equal(outs[0], o) for o in outs[1:])
+
+
+# RRR (row-major B [K, N]) last rows: the staged kernel with transposing LDS
+# reads; 64 / 32 / 16 columns per workgroup by N, 2 / 4 / 8 fragments, main
+# RRR tiles above the rows at N = 16384.
+RRR_SHAPES = [(1, 256, 4096), (17, 288, 1024), (33, 272, 512), (5, 272, 2048), (100, 512, 1024),
+              (128, 1040, 512), (1025, 16384, 512)]
+
+
+@pytest.mark.parametrize("epi", EPIS)
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("shape", RRR_SHAPES)
+def test_fp8_rrr_rows_reference_pattern(gpu, shape, fmt, epi):
+    m, n, k = shape
+    print(f"case: fp8 rrr rows pattern {fmt} {epi.value} {shape}", flush=True)
+    a = O.f32_to_fp8((((np.arange(m * k) * 5) % 13) - 6.0) * 0.125, fmt).reshape(m, k)
+    b = O.f32_to_fp8((((np.arange(k * n) * 7) % 11) - 5.0) * 0.125, fmt).reshape(k, n)
+    bias = (((np.arange(n) % 5) - 2) * 0.5).astype(np.float32)
+    got = _run(fmt, P.LayoutSku.Rrr, epi, a, b, bias=bias)
+    rows = slice(max(0, m - m % 256 - 2), m) if m > 256 else slice(0, m)
+    want = _want(fmt, P.LayoutSku.Rrr, epi, a[rows], b, None, bias, 0.25, 0.0)
+    if ACT[epi] in (None, "relu"):
+        assert np.array_equal(got[rows], want)
+    else:
+        assert _steps(got[rows], want, fmt).max() <= 1.0
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("shape", [RRR_SHAPES[1], RRR_SHAPES[3], RRR_SHAPES[4]])
+def test_fp8_rrr_rows_random_with_c(gpu, shape, fmt):
+    m, n, k = shape
+    print(f"case: fp8 rrr rows random with C {fmt} {shape}", flush=True)
+    g = np.random.default_rng(m * 11 + n + k)
+    a = O.f32_to_fp8(g.standard_normal((m, k)).astype(np.float32), fmt)
+    b = O.f32_to_fp8(g.standard_normal((k, n)).astype(np.float32), fmt)
+    c = O.f32_to_fp8(g.standard_normal((m, n)).astype(np.float32), fmt)
+    bias = g.standard_normal(n).astype(np.float32)
+    alpha = 1.0 / 16
+    epi = P.EpilogueKind.BiasSilu
+    got = _run(fmt, P.LayoutSku.Rrr, epi, a, b, c=c, bias=bias, alpha=alpha, beta=0.5)
+    want = _want(fmt, P.LayoutSku.Rrr, epi, a, b, c, bias, alpha, 0.5)
+    fa = np.abs(O.fp8_to_f32(a, fmt).astype(np.float64))
+    fb = np.abs(O.fp8_to_f32(b, fmt).astype(np.float64))
+    st = _steps(got, want, fmt, FP8_FLOOR * alpha * (fa @ fb))
+    assert st.max() <= 1.0 and (got != want).mean() < 0.02
