@@ -53,3 +53,73 @@ def test_quantize_w8a8_graph_replays_match_eager(gpu, shape):
         assert torch.equal(q, q_e) and torch.equal(sa, sa_e)
         assert torch.equal(out.view(torch.int16), out_e.view(torch.int16))
         _ = (torch.randn(1024, device=dev) @ torch.randn(1024, device=dev))   # eager work in between
+
+
+def _decode_calls(kind):
+    """(inputs to refresh, call(out)) of one decode-sized path."""
+    dev = "cuda:0"
+    if kind == "w8a8_m1":          # one-row dot4 kernel
+        m, n, k = 1, 4096, 4096
+        a = torch.randint(-127, 128, (m, k), dtype=torch.int8, device=dev)
+        w = torch.randint(-127, 128, (n, k), dtype=torch.int8, device=dev)
+        sa, sw = torch.rand(m, device=dev) + 0.01, torch.rand(n, device=dev) * 0.01
+        plan = P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, output=P.ElementKind.Bf16))
+        return a, (m, n), torch.bfloat16, lambda o: plan.run(a, w, o, scale_a=sa, scale_b=sw)
+    if kind == "w8a8_m40_wide":    # staged last rows, 64 columns per workgroup
+        m, n, k = 40, 14336, 1024
+        a = torch.randint(-127, 128, (m, k), dtype=torch.int8, device=dev)
+        w = torch.randint(-127, 128, (n, k), dtype=torch.int8, device=dev)
+        sa, sw = torch.rand(m, device=dev) + 0.01, torch.rand(n, device=dev) * 0.01
+        plan = P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, output=P.ElementKind.Bf16))
+        return a, (m, n), torch.bfloat16, lambda o: plan.run(a, w, o, scale_a=sa, scale_b=sw)
+    if kind == "fp8_m16":          # FP8 last rows
+        m, n, k = 16, 14336, 1024
+        a = torch.randint(-100, 100, (m, k), dtype=torch.int8, device=dev).view(torch.uint8)
+        b = torch.randint(-100, 100, (n, k), dtype=torch.int8, device=dev).view(torch.uint8)
+        plan = P.Fp8GemmPlan.select(P.Fp8GemmDescriptor(m, n, k, output=P.ElementKind.Bf16))
+        return a, (m, n), torch.bfloat16, lambda o: plan.run(a, b, o, scale_a=0.01, scale_b=0.02)
+    if kind == "u8_rrr_m8":        # u8 RRR last rows (flip + transposing reads)
+        m, n, k = 8, 1024, 2048
+        a = torch.randint(0, 256, (m, k), dtype=torch.uint8, device=dev)
+        b = torch.randint(0, 256, (k, n), dtype=torch.uint8, device=dev)
+        plan = P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, layout=P.LayoutSku.Rrr, element=P.ElementKind.U8,
+                                                        output=P.ElementKind.U8))
+        return a, (m, n), torch.uint8, lambda o: plan.run(a, b, o, alpha=1.0 / (64 * k))
+    # int8 MoE decode: offsets kernel + per-expert staged pass
+    from oracle.inputs import moe_routing
+    tokens, E, topk, n, k = 4, 8, 2, 2048, 1024
+    sid, eid = moe_routing(tokens, E, topk, seed=3)
+    x = torch.randint(-127, 128, (tokens, k), dtype=torch.int8, device=dev)
+    w = torch.randint(-127, 128, (E, n, k), dtype=torch.int8, device=dev)
+    sa, sw = torch.rand(tokens, device=dev) + 0.01, torch.rand(E * n, device=dev) * 0.01
+    cnt = torch.empty(E, dtype=torch.int32, device=dev)
+    off = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    dsid, deid = torch.from_numpy(sid).to(dev), torch.from_numpy(eid).to(dev)
+    plan = P.MoeS8GroupedPlan.select(E, topk, tokens * topk, n, k)
+    return x, (tokens * topk, n), torch.bfloat16, lambda o: plan.run(x, w, dsid, deid, o, cnt, off, sa, sw)
+
+
+@pytest.mark.parametrize("kind", ["w8a8_m1", "w8a8_m40_wide", "fp8_m16", "u8_rrr_m8", "moe_decode"])
+def test_decode_paths_graph_replays_match_eager(gpu, kind):
+    # The decode-sized passes allocate nothing and set no memory: captured
+    # once, every replay (new inputs, eager work in between) equals the eager
+    # call bit for bit.
+    a, oshape, odt, call = _decode_calls(kind)
+    dev = "cuda:0"
+    out = torch.zeros(oshape, dtype=odt, device=dev)
+    call(out)
+    sync()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        call(out)
+    for rep in range(4):
+        fresh = torch.randint(0, 100, a.shape, dtype=torch.int8, device=dev).view(a.dtype)
+        a.copy_(fresh)
+        out_e = torch.zeros_like(out)
+        call(out_e)
+        sync()
+        g.replay()
+        sync()
+        print(f"case: decode graph replay {kind} {rep}", flush=True)
+        assert torch.equal(out.view(torch.uint8), out_e.view(torch.uint8))
+        _ = (torch.randn(1024, device=dev) @ torch.randn(1024, device=dev))
