@@ -288,7 +288,12 @@ __global__ __launch_bounds__(1024) void gemm_fp8_rcr_rows_staged_kernel(F8Args p
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r16 = lane & 15, g = lane >> 4;
-    const int n0 = blockIdx.x * 16 * NB;
+    // RowB: a workgroup reads 16 NB-byte pieces of every k-row, so adjacent
+    // column groups share 128-byte lines; workgroups go round-robin over the
+    // 8 XCDs, so column groups are numbered XCD-major (consecutive groups on
+    // one XCD's L2) and each line is fetched once (FETCH_SIZE 2.0x -> 1.0x of B)
+    const int cgroup = RowB && gridDim.x % 8 == 0 ? (blockIdx.x % 8) * (gridDim.x / 8) + blockIdx.x / 8 : blockIdx.x;
+    const int n0 = cgroup * 16 * NB;
     const v4i ra = mfma2::make_rsrc(p.a, (uint32_t)((int64_t)p.M * p.lda));
     const v4i rb = mfma2::make_rsrc(p.b, (uint32_t)(RowB ? (int64_t)p.K * p.ldb : (int64_t)p.N * p.ldb));
     // DMA instruction j of a stage: units 64 j .. 64 j + 63 of the row-major
