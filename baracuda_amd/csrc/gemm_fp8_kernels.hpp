@@ -427,8 +427,8 @@ int32_t launch_fp8(const F8Args &p, hipStream_t stream) {
                       aligned16(p.b) && p.N % 4 == 0 && pad_m * p.lda < (1ll << 31) && pad_b < (1ll << 31) &&
                       p.ldd % 4 == 0 && (reinterpret_cast<uintptr_t>(p.d) % (4 * out_elem)) == 0;
     if (fast && LAYOUT == F8_RRR && p.K % 512 == 0 && (int64_t)p.K * p.ldb + mfma2::BN < (1ll << 31)) {
-        // RRR last rows: the staged kernel reading row-major B, 64 columns
-        // per workgroup where N allows (64-byte row pieces)
+        // RRR last rows: the staged kernel reading row-major B, column groups
+        // by the last-rows rule (XCD-major in the kernel)
         const int rem = mfma2::last_rows_pass(p.M, p.N, 128);
         if (rem != 0) {
             F8Args pm = p;
@@ -437,7 +437,7 @@ int32_t launch_fp8(const F8Args &p, hipStream_t stream) {
             if (tiles > 0)
                 hipLaunchKernelGGL((gemm_fp8_dma_kernel<FMT, LAYOUT, EPI, ACT>), dim3(tiles), dim3(F8DmaCfg::NT),
                                    0, stream, pm);
-            const int nb = p.N % 64 == 0 ? 4 : p.N % 32 == 0 ? 2 : 1;
+            const int nb = mfma2::last_rows_col_frags(p.N);
 #define BK_F8RRRROWS(RF, NB, SB, DEPTH)                                                                    \
             if (rem <= 16 * (RF) && nb == (NB)) {                                                         \
                 hipLaunchKernelGGL((gemm_fp8_rcr_rows_staged_kernel<FMT, EPI, ACT, RF, NB, SB, DEPTH, true>), \

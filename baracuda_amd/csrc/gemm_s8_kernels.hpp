@@ -1251,7 +1251,7 @@ bool launch_u8_rrr_rows(const S8Args &p, hipStream_t stream) {
         else
             hipLaunchKernelGGL((gemm_u8_rrr_dma_kernel<false, ACT, BiasT>), dim3(tiles), dim3(DmaCfg::NT), 0, stream, pm);
     }
-    const int nb = p.N % 64 == 0 ? 4 : p.N % 32 == 0 ? 2 : 1;
+    const int nb = mfma2::last_rows_col_frags(p.N);   // as the s8 RRR pass
 #define BK_U8RRRROWS(RF, NB, SB, DEPTH)                                                                        \
     if (rem <= 16 * (RF) && nb == (NB)) {                                                                       \
         const size_t lds = std::max((size_t)(DEPTH) * (16 * (RF) + 16 * (NB)) * (SB), (size_t)(RF) * (NB) * ((SB) / 64) * 1024); \
@@ -1633,10 +1633,13 @@ bool launch_rrr_rows(const S8Args &p, hipStream_t stream) {
     if (rem == 0 || p.K % 512 != 0 || p.lda % 16 != 0 || p.ldb % 16 != 0 || !aligned16(p.a) || !aligned16(p.b) ||
         !dma_extent_ok(p.M, p.lda) || (int64_t)p.K * p.ldb + mfma2::BN >= (1ll << 31))
         return false;
-    // 64 columns per workgroup (64-byte row pieces of B): N = 4096 / 14336,
-    // K = 4096, M = 1: 13.4 / 21.6 us (32 columns 14.3 / 38.4, 16 columns
-    // 22.2 / 66.9, 128 columns 25.3 / 26.8; the 256x256 RRR tiles 40.5 / -)
-    const int nb = p.N % 64 == 0 ? 4 : p.N % 32 == 0 ? 2 : 1;
+    // column groups by the last-rows rule (16 / 32 / 64 columns, at least 192
+    // workgroups), numbered XCD-major in the kernel so the groups sharing a
+    // B line share an L2: N = 4096 / 14336, K = 4096, M = 1: 9.6 / 15.3 us
+    // (16 / 64 columns; 64 columns at N = 4096 13.1, 16 at N = 14336 23.1;
+    // before the XCD-major numbering 64 columns 13.4 / 21.6; the 256x256 RRR
+    // tiles 40.5 / 37.7)
+    const int nb = mfma2::last_rows_col_frags(p.N);
     S8Args pm = p;
     pm.M = whole ? 0 : p.M - rem;
     if (pm.M > 0 && launch_rrr_dma<ACT, BiasT>(pm, stream) != kOk) return false;

@@ -113,10 +113,10 @@ def test_fp8_rows_deterministic_and_untouched_columns(gpu):
 
 
 # RRR (row-major B [K, N]) last rows: the staged kernel with transposing LDS
-# reads; 64 / 32 / 16 columns per workgroup by N, 2 / 4 / 8 fragments, main
-# RRR tiles above the rows at N = 16384.
+# reads; 16 / 32 / 64 columns per workgroup by the last-rows rule, 1 / 2 / 4 /
+# 8 fragments, main RRR tiles above the rows at N = 16384.
 RRR_SHAPES = [(1, 256, 4096), (17, 288, 1024), (33, 272, 512), (5, 272, 2048), (100, 512, 1024),
-              (128, 1040, 512), (1025, 16384, 512)]
+              (128, 1040, 512), (1025, 16384, 512), (17, 6144, 1024), (64, 8192, 512)]
 
 
 @pytest.mark.parametrize("epi", EPIS)

@@ -385,10 +385,11 @@ def test_u8_last_rows_large_k_exact(gpu, layout):
 
 # s8 RRR last rows (decode-sized M, and M % 256 <= 128 under whole tile
 # rows): the staged last-rows kernel reading row-major B with transposing
-# LDS reads; 64 / 32 / 16 columns per workgroup (N % 64, % 32, % 16), 2 / 4 /
-# 8 row fragments, main RRR tiles above the rows.
+# LDS reads; 16 / 32 / 64 columns per workgroup by the last-rows rule (N
+# below 6144 / from 6144 / from 12288), 2 / 4 / 8 row fragments, main RRR
+# tiles above the rows.
 RRR_ROWS_SHAPES = [(1, 4096, 4096), (5, 256, 512), (33, 512, 1024), (20, 288, 512), (100, 272, 512),
-                   (128, 1024, 2048), (1025, 16384, 512), (1100, 16384, 1024)]
+                   (128, 1024, 2048), (1025, 16384, 512), (1100, 16384, 1024), (20, 6144, 512)]
 
 
 @pytest.mark.parametrize("epi", [P.EpilogueKind.Identity, P.EpilogueKind.BiasGelu, P.EpilogueKind.BiasRelu])
