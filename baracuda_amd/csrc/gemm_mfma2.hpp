@@ -489,9 +489,11 @@ __device__ __forceinline__ void wait_vmcnt() { asm volatile("s_waitcnt vmcnt(%0)
 // workgroups leave CUs idle (int8, K = 4096, M = 32 / 128: N = 4096
 // 7.2 / 11.8 us with 16 columns against 7.8 / 13.2 with 32; N = 14336
 // 19.2 / 39.4 us with 16 columns against 14.5 / 20.0 with 64).
-inline int last_rows_col_frags(int N) {
+// `blocks`: row blocks of the pass (gridDim.y), which multiply the
+// workgroup count.
+inline int last_rows_col_frags(int N, int blocks = 1) {
     for (int nb = 4; nb > 1; nb /= 2)
-        if (N % (16 * nb) == 0 && N / (16 * nb) >= 192) return nb;
+        if (N % (16 * nb) == 0 && N / (16 * nb) * blocks >= 192) return nb;
     return 1;
 }
 

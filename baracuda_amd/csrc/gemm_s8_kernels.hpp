@@ -1251,7 +1251,7 @@ bool launch_u8_rrr_rows(const S8Args &p, hipStream_t stream) {
         else
             hipLaunchKernelGGL((gemm_u8_rrr_dma_kernel<false, ACT, BiasT>), dim3(tiles), dim3(DmaCfg::NT), 0, stream, pm);
     }
-    const int nb = mfma2::last_rows_col_frags(p.N);   // as the s8 RRR pass
+    const int nb = mfma2::last_rows_col_frags(p.N, blocks);   // as the s8 RRR pass
 #define BK_U8RRRROWS(RF, NB, SB, DEPTH)                                                                        \
     if (rem <= 16 * (RF) && nb == (NB)) {                                                                       \
         const size_t lds = std::max((size_t)(DEPTH) * (16 * (RF) + 16 * (NB)) * (SB), (size_t)(RF) * (NB) * ((SB) / 64) * 1024); \
@@ -1427,7 +1427,7 @@ bool launch_u8_rcr_rows(const S8Args &p, hipStream_t stream) {
         }
         return true;
     }
-    const int nb = mfma2::last_rows_col_frags(p.N);
+    const int nb = mfma2::last_rows_col_frags(p.N, blocks);
 #define BK_U8ROWS(RF, NB, SB, DEPTH)                                                                           \
     if (rem <= 16 * (RF) && nb == (NB)) {                                                                       \
         const size_t lds = std::max((size_t)(DEPTH) * (16 * (RF) + 16 * (NB)) * (SB), (size_t)(RF) * (NB) * ((SB) / 64) * 1024); \
@@ -1639,7 +1639,7 @@ bool launch_rrr_rows(const S8Args &p, hipStream_t stream) {
     // (16 / 64 columns; 64 columns at N = 4096 13.1, 16 at N = 14336 23.1;
     // before the XCD-major numbering 64 columns 13.4 / 21.6; the 256x256 RRR
     // tiles 40.5 / 37.7)
-    const int nb = mfma2::last_rows_col_frags(p.N);
+    const int nb = mfma2::last_rows_col_frags(p.N, blocks);
     S8Args pm = p;
     pm.M = whole ? 0 : p.M - rem;
     if (pm.M > 0 && launch_rrr_dma<ACT, BiasT>(pm, stream) != kOk) return false;
