@@ -1487,6 +1487,28 @@ void launch_kernel(const S8Args &p, bool fast_k, hipStream_t stream, void *works
         const bool split_ws = ts.split > 1 && workspace != nullptr && workspace_bytes >= need &&
                               (reinterpret_cast<uintptr_t>(workspace) & 15u) == 0;
         const int rem = split_ws ? 0 : rows_path_rows(p.M, p.N);
+        // Small problems (129-512 rows) whose 128-row blocks of the staged
+        // last-rows kernel fit one round of workgroups run that way instead of
+        // tiles.  K = 4096, M = 129 / 256 / 512: N = 4096 12.8 / 13.4 / 17.9 us
+        // against 24.2 / 24.4 / 25.1 on 128x128 tiles; at N = 14336 the blocks
+        // need 2-4 rounds and lose from 384 rows (48.9 against 37.0).
+        const int blocks = (p.M + 127) / 128;
+        const int nbb = mfma2::last_rows_col_frags(p.N, blocks);
+        if (rem == 0 && !split_ws && p.M > 128 && p.M <= 512 && p.N % 16 == 0 && p.K % 512 == 0 &&
+            blocks * (p.N / (16 * nbb)) <= 256) {
+            const int nb = nbb;
+#define BK_S8BLOCKS(NB, SB)                                                                                  \
+            if (nb == (NB)) {                                                                                \
+                const size_t lds = std::max((size_t)2 * (128 + 16 * (NB)) * (SB), (size_t)8 * (NB) * ((SB) / 64) * 1024); \
+                hipLaunchKernelGGL((gemm_s8_rcr_rows_staged_kernel<EPI, VecOut, ACT, BiasT, 8, NB, SB, 2>),    \
+                                   dim3(p.N / (16 * (NB)), blocks), dim3(1024), lds, stream, p, 0);          \
+                return;                                                                                      \
+            }
+            BK_S8BLOCKS(1, 512)
+            BK_S8BLOCKS(2, 512)
+            BK_S8BLOCKS(4, 256)
+#undef BK_S8BLOCKS
+        }
         if (rem != 0) {
             // whole 256-row tiles, then the last rows (gemm_s8_rcr_rows_kernel)
             S8Args pm = p;
