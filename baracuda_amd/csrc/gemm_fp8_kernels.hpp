@@ -271,7 +271,9 @@ __global__ __launch_bounds__(C::NT, C::NT == 256 ? 2 : 1) void gemm_fp8_dma_kern
 // each (lane pair (2j, 2j + 1) pointing at k-row j; lane i gets 8 k of
 // column i), as in PolicyF8RowB.
 template <int FMT, int EPI, int ACT, int RF, int NB, int SB, int DEPTH, bool RowB = false>
-__global__ __launch_bounds__(1024) void gemm_fp8_rcr_rows_staged_kernel(F8Args p, int m0) {
+__global__ __launch_bounds__(1024) void gemm_fp8_rcr_rows_staged_kernel(F8Args p, int m_first) {
+    // blockIdx.y: 16 RF-row block of the pass
+    const int m0 = m_first + blockIdx.y * 16 * RF;
     constexpr int WAVES = 16, CH = SB / 128;
     constexpr int FPW = RF * CH / WAVES;                 // A row fragments per wave
     constexpr int FSTEP = WAVES / CH;
@@ -453,6 +455,29 @@ int32_t launch_fp8(const F8Args &p, hipStream_t stream) {
             BK_F8RRRROWS(4, 1, 512, 2)
             BK_F8RRRROWS(8, 1, 512, 2)
 #undef BK_F8RRRROWS
+        }
+    }
+    if (fast && LAYOUT == F8_RCR && p.M > 128 && p.M <= 512 && p.K % 512 == 0 && p.N % 16 == 0 &&
+        mfma2::last_rows_pass(p.M, p.N, 128) == 0) {
+        // small problems whose 128-row blocks of the last-rows kernel fit one
+        // round of workgroups: all rows that way instead of tiles.  K = 4096,
+        // M = 129 / 256 / 512: N = 4096 12.6 / 13.2 / 18.6 us against 23.9 /
+        // 24.2 / 24.3 on 128x128 tiles; N = 8192, M = 129 / 256: 17.5 / 18.6
+        // against 28.2 / 28.6
+        const int blocks = (p.M + 127) / 128;
+        const int nb = mfma2::last_rows_col_frags(p.N, blocks);
+        if (blocks * (p.N / (16 * nb)) <= 256) {
+#define BK_F8BLOCKS(NB, SB)                                                                              \
+            if (nb == (NB)) {                                                                            \
+                hipLaunchKernelGGL((gemm_fp8_rcr_rows_staged_kernel<FMT, EPI, ACT, 8, NB, SB, 2>),        \
+                                   dim3(p.N / (16 * (NB)), blocks), dim3(1024),                          \
+                                   (size_t)2 * (128 + 16 * (NB)) * (SB), stream, p, 0);                  \
+                return launch_status();                                                                  \
+            }
+            BK_F8BLOCKS(1, 512)
+            BK_F8BLOCKS(2, 512)
+            BK_F8BLOCKS(4, 256)
+#undef BK_F8BLOCKS
         }
     }
     if (fast && LAYOUT == F8_RCR) {

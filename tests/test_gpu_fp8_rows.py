@@ -30,11 +30,14 @@ pytestmark = pytest.mark.gpu
 # with 4 fragments, 128 with 8), 64 columns from N = 12288 (1 / 16 with 4
 # fragments, 100 with 8 and 256-byte stages).  Under 4 tile rows at
 # N = 16384 (the tiles fill one round exactly): 1 / 40 / 128 last rows.
+# 129-512 rows whose 128-row blocks fit one round of workgroups: every row
+# as blocks of the same kernel (200 / 384 / 512).
 SHAPES = [(1, 256, 4096), (16, 512, 2048), (5, 272, 1024), (17, 288, 1024), (32, 1040, 3072),
           (9, 256, 1536), (20, 272, 512), (33, 512, 512), (64, 256, 2560), (65, 1040, 1024),
           (100, 512, 4096), (128, 256, 512), (1025, 16384, 2048), (1064, 16384, 512), (1152, 16384, 1024),
           (1, 1040, 4096), (16, 272, 2048), (2, 6144, 512), (33, 8192, 512), (128, 6144, 1024),
-          (1, 12288, 2048), (16, 14336, 1024), (100, 12288, 1024)]
+          (1, 12288, 2048), (16, 14336, 1024), (100, 12288, 1024), (200, 512, 1024), (384, 1024, 512),
+          (512, 4096, 512)]
 
 
 @pytest.mark.parametrize("shape", SHAPES)
@@ -58,7 +61,7 @@ def test_fp8_rows_f32_and_bf16(gpu, shape):
 
 @pytest.mark.parametrize("epi", EPIS)
 @pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
-@pytest.mark.parametrize("shape", [SHAPES[0], SHAPES[3], SHAPES[7], SHAPES[10], SHAPES[13], SHAPES[15], SHAPES[18], SHAPES[22]])
+@pytest.mark.parametrize("shape", [SHAPES[0], SHAPES[3], SHAPES[7], SHAPES[10], SHAPES[13], SHAPES[15], SHAPES[18], SHAPES[22], SHAPES[23], SHAPES[25]])
 def test_fp8_rows_reference_pattern(gpu, shape, fmt, epi):
     m, n, k = shape
     print(f"case: fp8 rows pattern {fmt} {epi.value} {shape}", flush=True)
