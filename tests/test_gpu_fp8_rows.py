@@ -77,7 +77,7 @@ def test_fp8_rows_reference_pattern(gpu, shape, fmt, epi):
 
 
 @pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
-@pytest.mark.parametrize("shape", [SHAPES[1], SHAPES[4], SHAPES[9], SHAPES[14], SHAPES[16], SHAPES[19], SHAPES[21]])
+@pytest.mark.parametrize("shape", [SHAPES[1], SHAPES[4], SHAPES[9], SHAPES[14], SHAPES[16], SHAPES[19], SHAPES[21], SHAPES[24]])
 def test_fp8_rows_random_with_c(gpu, shape, fmt):
     # C (beta = 0.5) and a BiasGelu epilogue on random operands: one grid step
     # plus the MFMA's summation floor, as the tile path's test.
