@@ -383,6 +383,63 @@ __global__ __launch_bounds__(1024) void gemm_fp8_rcr_rows_staged_kernel(F8Args p
     }
 }
 
+// One last row (M = 1 decode steps; K % (1024 BT) == 0), no MFMA: a
+// workgroup of 4 waves owns 4 output columns and wave w streams B row
+// n0 + w over all of K, 16 bytes per lane of every kilobyte straight into
+// registers (BT kilobytes requested before their products), beside the same
+// 16 bytes of the A row (an L2 hit).  v_cvt_pk_f32_fp8 / _bf8 turn two codes
+// into two f32 per instruction and f32 FMAs add the products (exact in f32,
+// as in the MFMA) in a fixed per-lane order; a wave butterfly and LDS
+// gather the 4 column sums and lane 0 of wave 0 runs the tiles' epilogue.
+// NaN codes convert to NaN and stay NaN.
+// Codes 2 HI and 2 HI + 1 of a dword (HI: the upper half) as two f32.
+template <int FMT, bool HI>
+__device__ __forceinline__ v2f fp8x2_to_f32(int w) {
+    if constexpr (FMT == FMT_E5M2) return __builtin_amdgcn_cvt_pk_f32_bf8(w, HI);
+    else return __builtin_amdgcn_cvt_pk_f32_fp8(w, HI);
+}
+
+template <int FMT, int EPI, int ACT, int BT>
+__global__ __launch_bounds__(256) void gemm_fp8_rcr_row1_kernel(F8Args p, int m0) {
+    __shared__ float colsum[4];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n0 = blockIdx.x * 4;
+    const int nch = p.K >> 10;
+    const int8_t *brow = p.b + (int64_t)(n0 + wave) * p.ldb + lane * 16;
+    const int8_t *arow = p.a + (int64_t)m0 * p.lda + lane * 16;
+    float acc0 = 0.0f, acc1 = 0.0f;
+    for (int c0 = 0; c0 < nch; c0 += BT) {
+        v4i av[BT], bv[BT];
+#pragma unroll
+        for (int u = 0; u < BT; ++u) av[u] = *reinterpret_cast<const v4i *>(arow + (int64_t)(c0 + u) * 1024);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < BT; ++u)
+            bv[u] = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(brow + (int64_t)(c0 + u) * 1024));
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < BT; ++u)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+            {
+                const v2f a0 = fp8x2_to_f32<FMT, false>(av[u][q]), b0 = fp8x2_to_f32<FMT, false>(bv[u][q]);
+                const v2f a1 = fp8x2_to_f32<FMT, true>(av[u][q]), b1 = fp8x2_to_f32<FMT, true>(bv[u][q]);
+                acc0 = __builtin_fmaf(a0[0], b0[0], acc0);
+                acc1 = __builtin_fmaf(a0[1], b0[1], acc1);
+                acc0 = __builtin_fmaf(a1[0], b1[0], acc0);
+                acc1 = __builtin_fmaf(a1[1], b1[1], acc1);
+            }
+    }
+    float acc = acc0 + acc1;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if (lane == 0) colsum[wave] = acc;
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    const F8Epilogue<FMT, EPI, true, ACT> epi{p};
+    epi(m0, n0, v4f{colsum[0], colsum[1], colsum[2], colsum[3]});
+}
+
 // Stage shapes of the FP8 last-rows kernel (first match wins), by the
 // column fragments per workgroup (mfma2::last_rows_col_frags).  N = 14336,
 // K = 4096 over 8 rotated weight sets (HIP events), 64 columns per
@@ -395,6 +452,16 @@ __global__ __launch_bounds__(1024) void gemm_fp8_rcr_rows_staged_kernel(F8Args p
 // stages, 2 with 1 KiB stages three deep, 4 and 8 with 512-byte stages.
 template <int FMT, int EPI, int ACT>
 bool launch_fp8_rows(const F8Args &p, int m0, int rem, hipStream_t stream) {
+    // one row: the FMA row kernel (K = 4096 over rotated weights, graph
+    // replay: N = 14336 13.4 -> 10.4 us, N = 4096 5.2 -> 4.8 us against the
+    // staged kernel)
+    if (rem == 1 && p.K % 1024 == 0) {
+        if (p.K % 2048 == 0)
+            hipLaunchKernelGGL((gemm_fp8_rcr_row1_kernel<FMT, EPI, ACT, 2>), dim3(p.N / 4), dim3(256), 0, stream, p, m0);
+        else
+            hipLaunchKernelGGL((gemm_fp8_rcr_row1_kernel<FMT, EPI, ACT, 1>), dim3(p.N / 4), dim3(256), 0, stream, p, m0);
+        return true;
+    }
     const int nb = mfma2::last_rows_col_frags(p.N);
 #define BK_F8ROWS(RF, NB, SB, DEPTH)                                                                     \
     if (rem <= 16 * (RF) && nb == (NB) && p.K % (SB) == 0) {                                              \

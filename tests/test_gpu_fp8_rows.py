@@ -1,8 +1,9 @@
-"""GPU parity of the FP8 RCR last-rows pass (gemm_fp8_rcr_rows_staged_kernel):
-decode-sized M (all of it) and the last M % 256 rows when a row of tiles would
-start another round, for every stage shape the launcher picks (fragments x
-columns per workgroup and stage bytes) and the fall-backs when N or K does
-not divide the preferred one.
+"""GPU parity of the FP8 RCR last-rows pass (gemm_fp8_rcr_rows_staged_kernel,
+and gemm_fp8_rcr_row1_kernel for one row): decode-sized M (all of it) and
+the last M % 256 rows when a row of tiles would start another round, for
+every stage shape the launcher picks (fragments x columns per workgroup and
+stage bytes) and the fall-backs when N or K does not divide the preferred
+one.
 
 The reference smoke pattern (fp8_bias_smoke.rs inputs: small dyadic values
 whose f32 partial sums are exact in any order) must come out bit-exact for
@@ -31,13 +32,15 @@ pytestmark = pytest.mark.gpu
 # fragments, 100 with 8 and 256-byte stages).  Under 4 tile rows at
 # N = 16384 (the tiles fill one round exactly): 1 / 40 / 128 last rows.
 # 129-512 rows whose 128-row blocks fit one round of workgroups: every row
-# as blocks of the same kernel (200 / 384 / 512).
+# as blocks of the same kernel (200 / 384 / 512).  One row with K % 1024 == 0
+# (1 x 256 / 1040 / 12288 / 512, 1025 x 16384) takes the FMA row kernel
+# instead (2 KiB per batch, 1 KiB at K = 3072).
 SHAPES = [(1, 256, 4096), (16, 512, 2048), (5, 272, 1024), (17, 288, 1024), (32, 1040, 3072),
           (9, 256, 1536), (20, 272, 512), (33, 512, 512), (64, 256, 2560), (65, 1040, 1024),
           (100, 512, 4096), (128, 256, 512), (1025, 16384, 2048), (1064, 16384, 512), (1152, 16384, 1024),
           (1, 1040, 4096), (16, 272, 2048), (2, 6144, 512), (33, 8192, 512), (128, 6144, 1024),
           (1, 12288, 2048), (16, 14336, 1024), (100, 12288, 1024), (200, 512, 1024), (384, 1024, 512),
-          (512, 4096, 512)]
+          (512, 4096, 512), (1, 512, 3072)]
 
 
 @pytest.mark.parametrize("shape", SHAPES)
@@ -61,7 +64,7 @@ def test_fp8_rows_f32_and_bf16(gpu, shape):
 
 @pytest.mark.parametrize("epi", EPIS)
 @pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
-@pytest.mark.parametrize("shape", [SHAPES[0], SHAPES[3], SHAPES[7], SHAPES[10], SHAPES[13], SHAPES[15], SHAPES[18], SHAPES[22], SHAPES[23], SHAPES[25]])
+@pytest.mark.parametrize("shape", [SHAPES[0], SHAPES[3], SHAPES[7], SHAPES[10], SHAPES[13], SHAPES[15], SHAPES[18], SHAPES[22], SHAPES[23], SHAPES[25], SHAPES[26]])
 def test_fp8_rows_reference_pattern(gpu, shape, fmt, epi):
     m, n, k = shape
     print(f"case: fp8 rows pattern {fmt} {epi.value} {shape}", flush=True)
