@@ -497,6 +497,21 @@ inline int last_rows_col_frags(int N, int blocks = 1) {
     return 1;
 }
 
+// Row blocks of a last-rows pass of 33-128 rows when the rule above gives
+// 16-column workgroups (N below 6144), which would each stage all the rows:
+// blocks of 32 rows, or of 64 rows for more than 64 rows when N > 2048, the
+// column width by the rule over the blocks.  Measured at K = 4096 (graph
+// replay, rotated weights): N = 4096, M = 65 / 100 / 128 in 64-row blocks of
+// 32 columns 8.8 / 9.1 / 9.5 us, in 32-row blocks of 64 columns 9.6 / 9.9 /
+// 10.3; N = 2048 in 32-row blocks of 32 columns 6.4 / 6.4 / 6.5 us, in
+// 64-row blocks of 16 columns 6.9; 33-64 rows as two 32-row blocks: N =
+// 4096 / 2048, M = 48 7.8 / 5.8 us against 8.5 / 6.8 as one block.
+inline void last_rows_blocks(int rem, int N, int &rf, int &blocks, int &nb) {
+    rf = rem > 64 && N > 2048 ? 4 : 2;
+    blocks = (rem + 16 * rf - 1) / (16 * rf);
+    nb = last_rows_col_frags(N, blocks);
+}
+
 inline int last_rows_pass(int M, int N, int limit) {
     if (N <= 0 || N % 16 != 0 || M <= 0) return 0;
     const int rem = M % 256;

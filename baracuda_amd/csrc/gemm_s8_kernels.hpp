@@ -1523,6 +1523,25 @@ void launch_kernel(const S8Args &p, bool fast_k, hipStream_t stream, void *works
             // B-only DMA kernel from 9 rows (N = 14336, K = 4096: M = 8 / 16
             // 14.3 / 17.5 us on the DMA kernel, 14.5 us staged at 17 rows).
             const int nb = mfma2::last_rows_col_frags(p.N);
+            if (nb == 1 && rem > 32 && p.K % 512 == 0) {
+                // 33-128 rows where 16-column workgroups would each read all
+                // of them: 2-4 row blocks (last_rows_blocks).  K = 4096,
+                // rotated weights, graph replay: N = 4096, M = 48 / 100 / 128
+                // 8.5 / 11.6 / 11.9 -> 7.8 / 9.1 / 9.5 us; N = 2048, M = 48 /
+                // 128 6.8 / 9.9 -> 5.8 / 6.5 us
+                int rf, blk, nbb;
+                mfma2::last_rows_blocks(rem, p.N, rf, blk, nbb);
+#define BK_S8RBLK(RF, NB)                                                                                     \
+                if (rf == (RF) && nbb == (NB)) {                                                               \
+                    hipLaunchKernelGGL((gemm_s8_rcr_rows_staged_kernel<EPI, VecOut, ACT, BiasT, RF, NB, 512, 2>), \
+                                       dim3(p.N / (16 * (NB)), blk), dim3(1024),                               \
+                                       std::max((size_t)2 * (16 * (RF) + 16 * (NB)) * 512, (size_t)(RF) * (NB) * 8 * 1024), \
+                                       stream, p, pm.M);                                                       \
+                    return;                                                                                    \
+                }
+                BK_S8RBLK(2, 1) BK_S8RBLK(4, 1) BK_S8RBLK(2, 2) BK_S8RBLK(4, 2) BK_S8RBLK(2, 4) BK_S8RBLK(4, 4)
+#undef BK_S8RBLK
+            }
             if (rem > (nb > 1 ? 8 : kRowsDmaMaxRows) && p.K % kRowsStagedSB == 0) {
 #define BK_S8ROWS(RF, NB, SB, DEPTH)                                                                        \
     if (rem <= 16 * (RF) && nb == (NB) && p.K % (SB) == 0) {                                                 \

@@ -43,7 +43,10 @@ SHAPES += ROW1_SHAPES
 # 36 and 100 under the tile rows at N = 16384).
 STAGED_SHAPES = [(17, 256, 512), (31, 1040, 1536), (33, 512, 512), (65, 272, 1024), (97, 1040, 2560), (1060, 16384, 1536), (1124, 16384, 512),
                  (20, 6144, 1024), (64, 8192, 512), (128, 6144, 1024), (17, 12288, 512),
-                 (9, 14336, 1024), (16, 6144, 512)]
+                 (9, 14336, 1024), (16, 6144, 512),
+                 # 33-128 rows below N = 6144 in row blocks (mfma2::last_rows_blocks):
+                 # 64-row blocks of 32 columns, 32-row blocks of 32 columns, 3 blocks
+                 (100, 4096, 1024), (128, 2048, 512), (48, 4096, 512), (90, 3072, 512)]
 SHAPES += STAGED_SHAPES
 
 
