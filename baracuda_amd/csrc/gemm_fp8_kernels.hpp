@@ -531,6 +531,22 @@ int32_t launch_fp8(const F8Args &p, hipStream_t stream) {
         // M = 129 / 256 / 512: N = 4096 12.6 / 13.2 / 18.6 us against 23.9 /
         // 24.2 / 24.3 on 128x128 tiles; N = 8192, M = 129 / 256: 17.5 / 18.6
         // against 28.2 / 28.6
+        // 64-row blocks first while they fit one round (K = 4096, M = 129 /
+        // 256: N = 4096 12.3 / 12.8 -> 11.2 / 11.7 us, N = 2048 9.6 / 10.1
+        // -> 7.9 / 8.1 us; N = 8192 level), else 128-row blocks
+        const int b4 = (p.M + 63) / 64;
+        const int n4 = mfma2::last_rows_col_frags(p.N, b4);
+        if (b4 * (p.N / (16 * n4)) <= 256) {
+#define BK_F8BLK4(NB)                                                                                     \
+            if (n4 == (NB)) {                                                                             \
+                hipLaunchKernelGGL((gemm_fp8_rcr_rows_staged_kernel<FMT, EPI, ACT, 4, NB, 512, 2>),        \
+                                   dim3(p.N / (16 * (NB)), b4), dim3(1024), (size_t)2 * (64 + 16 * (NB)) * 512, \
+                                   stream, p, 0);                                                         \
+                return launch_status();                                                                   \
+            }
+            BK_F8BLK4(1) BK_F8BLK4(2) BK_F8BLK4(4)
+#undef BK_F8BLK4
+        }
         const int blocks = (p.M + 127) / 128;
         const int nb = mfma2::last_rows_col_frags(p.N, blocks);
         if (blocks * (p.N / (16 * nb)) <= 256) {

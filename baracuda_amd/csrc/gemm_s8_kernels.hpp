@@ -1492,6 +1492,28 @@ void launch_kernel(const S8Args &p, bool fast_k, hipStream_t stream, void *works
         // tiles.  K = 4096, M = 129 / 256 / 512: N = 4096 12.8 / 13.4 / 17.9 us
         // against 24.2 / 24.4 / 25.1 on 128x128 tiles; at N = 14336 the blocks
         // need 2-4 rounds and lose from 384 rows (48.9 against 37.0).
+        // 64-row blocks first, when they still fit one round of workgroups
+        // (K = 4096, M = 129 / 256: N = 4096 12.5 / 13.0 -> 11.0 / 11.4 us;
+        // N = 2048 9.8 / 10.3 -> 7.6 / 7.8 us, M = 512 12.1 -> 10.9 us; N =
+        // 8192 level).  Letting the 128-row blocks run two rounds was mixed
+        // (N = 14336, M = 129: 34.6 -> 32.7 us; N = 6144, M = 384: 25.2 ->
+        // 31.7 us), so they keep one.
+        if (rem == 0 && !split_ws && p.M > 128 && p.M <= 512 && p.N % 16 == 0 && p.K % 512 == 0) {
+            const int b4 = (p.M + 63) / 64;
+            const int n4 = mfma2::last_rows_col_frags(p.N, b4);
+            if (b4 * (p.N / (16 * n4)) <= 256) {
+#define BK_S8BLK4(NB)                                                                                        \
+                if (n4 == (NB)) {                                                                            \
+                    hipLaunchKernelGGL((gemm_s8_rcr_rows_staged_kernel<EPI, VecOut, ACT, BiasT, 4, NB, 512, 2>), \
+                                       dim3(p.N / (16 * (NB)), b4), dim3(1024),                              \
+                                       std::max((size_t)2 * (64 + 16 * (NB)) * 512, (size_t)4 * (NB) * 8 * 1024), \
+                                       stream, p, 0);                                                        \
+                    return;                                                                                  \
+                }
+                BK_S8BLK4(1) BK_S8BLK4(2) BK_S8BLK4(4)
+#undef BK_S8BLK4
+            }
+        }
         const int blocks = (p.M + 127) / 128;
         const int nbb = mfma2::last_rows_col_frags(p.N, blocks);
         if (rem == 0 && !split_ws && p.M > 128 && p.M <= 512 && p.N % 16 == 0 && p.K % 512 == 0 &&

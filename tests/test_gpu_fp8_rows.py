@@ -31,8 +31,9 @@ pytestmark = pytest.mark.gpu
 # with 4 fragments, 128 with 8), 64 columns from N = 12288 (1 / 16 with 4
 # fragments, 100 with 8 and 256-byte stages).  Under 4 tile rows at
 # N = 16384 (the tiles fill one round exactly): 1 / 40 / 128 last rows.
-# 129-512 rows whose 128-row blocks fit one round of workgroups: every row
-# as blocks of the same kernel (200 / 384 / 512).  One row with K % 1024 == 0
+# 129-512 rows whose row blocks fit one round of workgroups: every row as
+# blocks of the same kernel (64-row blocks at 200 / 384, 128-row blocks at
+# 512 x 4096).  One row with K % 1024 == 0
 # (1 x 256 / 1040 / 12288 / 512, 1025 x 16384) takes the FMA row kernel
 # instead (2 KiB per batch, 1 KiB at K = 3072).
 SHAPES = [(1, 256, 4096), (16, 512, 2048), (5, 272, 1024), (17, 288, 1024), (32, 1040, 3072),

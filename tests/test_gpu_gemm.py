@@ -139,12 +139,14 @@ def test_tail_split_w8a8_m4296_bit_identical(gpu):
 
 
 @pytest.mark.parametrize("shape", [(300, 1000, 512), (256, 4096, 4096), (129, 520, 1152), (1100, 3000, 256),
-                                   (2100, 4100, 256), (300, 512, 1024), (129, 4096, 1024), (512, 2048, 512)])
+                                   (2100, 4100, 256), (300, 512, 1024), (129, 4096, 1024), (512, 2048, 512),
+                                   (200, 8192, 512)])
 def test_small_tiles_all_epilogues(gpu, shape):
     # Grids of at most 128 256x256 tiles run 128x128 tiles (no workspace)
-    # unless 128-row blocks of the last-rows kernel fit one round (K % 512,
-    # N % 16: 256 x 4096, 300 x 512, 129 x 4096, 512 x 2048, partial last
-    # blocks included), 2100 x 4100 (153 tiles) 256x256 edge tiles: int32 exact over the whole
+    # unless row blocks of the last-rows kernel fit one round (K % 512,
+    # N % 16): 64-row blocks at 256 x 4096, 300 x 512, 129 x 4096, 512 x 2048,
+    # 128-row blocks at 200 x 8192, partial last blocks included; 2100 x 4100
+    # (153 tiles) 256x256 edge tiles: int32 exact over the whole
     # output (edge rows / columns included), s8 with C and beta through the
     # staged byte store, W8A8 bf16 on rows at the tile-row boundaries.
     m, n, k = shape
