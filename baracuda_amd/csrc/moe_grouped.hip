@@ -101,7 +101,39 @@ struct MoeArgs {
     const float *sw;            // [E, N]     (int8 only)
     void *out;                  // [size_m, N] bf16 / f16 (int32 for MOE_S8_I32)
     int E, topk, size_m, N, K;  // K in elements
+    // Decode launches only (size_m <= 64): the ids, and the counts / offsets
+    // they write in place of moe_offsets_kernel.
+    const int32_t *expert_ids = nullptr;   // [size_m], sorted
+    int32_t *counts = nullptr;             // [E]
 };
+
+// Decode launches (size_m <= 64, no offsets kernel): expert e's first
+// sorted position and row count from the ids, one ballot each in wave 0
+// (ids outside [0, E) are counted nowhere, as in moe_offsets_kernel); the
+// workgroups of column group 0 write the counts and offsets that kernel
+// would.  Workgroup-uniform results; contains a barrier.
+__device__ __forceinline__ void moe_decode_rows(const MoeArgs &p, int e, int &o0, int &rows) {
+    __shared__ int s_rows[2];
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        const int id = lane < p.size_m ? p.expert_ids[lane] : -1;
+        const int before = __popcll(__ballot(id >= 0 && id < e));
+        const int mine = __popcll(__ballot(id == e));
+        if (lane == 0) {
+            s_rows[0] = before;
+            s_rows[1] = mine;
+            if (blockIdx.x == 0) {
+                int32_t *off = const_cast<int32_t *>(p.offsets);
+                p.counts[e] = mine;
+                off[e + 1] = before + mine;
+                if (e == 0) off[0] = 0;
+            }
+        }
+    }
+    __syncthreads();
+    o0 = s_rows[0];
+    rows = s_rows[1];
+}
 
 // The E+1 offsets, clamped to size_m, loaded in one parallel step into LDS.
 __device__ __forceinline__ void moe_load_offsets(const MoeArgs &p, int32_t *s_off) {
@@ -462,8 +494,8 @@ __global__ __launch_bounds__(1024) void moe_rows_staged_kernel(MoeArgs p) {
     extern __shared__ __attribute__((aligned(1024))) int8_t lds[];
     int32_t *s_tok = reinterpret_cast<int32_t *>(lds + MAIN);
     const int e = blockIdx.y;
-    const int o0 = min(p.offsets[e], p.size_m), o1 = min(p.offsets[e + 1], p.size_m);
-    const int rows = o1 - o0;
+    int o0, rows;
+    moe_decode_rows(p, e, o0, rows);
     if (rows <= 0) return;   // whole workgroup: no rows routed to this expert
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -551,14 +583,86 @@ __global__ __launch_bounds__(1024) void moe_rows_staged_kernel(MoeArgs p) {
     }
 }
 
+// Decode-sized int8 MoE with a few rows per expert (K % 1024 == 0): one
+// launch over (N / 4 column groups) x E experts of 4 waves, no MFMA, the
+// layout of the dense one-row kernel (gemm_s8_rcr_row1_kernel).  Wave w
+// streams row n0 + w of the expert's weight slab, 16 bytes per lane of every
+// kilobyte, straight into registers and takes v_dot4_i32_i8 of it against
+// the same bytes of up to RMAX of the expert's gathered A rows (L2 hits);
+// an expert with more rows takes further passes over the slab rows (L2
+// hits).  Wave butterflies and LDS gather the 4 column sums of each row and
+// the tile path's per-quad epilogue (moe_store / moe_store_i32) writes them:
+// int32 sums are exact, so the output is bit-identical to the MFMA paths.
+template <int KIND, int RMAX, int BT>
+__global__ __launch_bounds__(256) void moe_row_kernel(MoeArgs p) {
+    static_assert(KIND == MOE_S8 || KIND == MOE_S8_I32, "int8 kinds");
+    __shared__ int32_t s_tok[RMAX];
+    __shared__ int colsum[RMAX][4];
+    const int e = blockIdx.y;
+    int o0, rows;
+    moe_decode_rows(p, e, o0, rows);
+    if (rows <= 0) return;   // whole workgroup: no rows routed to this expert
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n0 = blockIdx.x * 4;
+    const int kb = p.K;
+    const int nch = kb >> 10;
+    const int in_div = p.topk_w ? 1 : p.topk;
+    const int8_t *brow = p.w + ((int64_t)e * p.N + n0 + wave) * kb + lane * 16;
+    const float *swe = KIND == MOE_S8 ? p.sw + (int64_t)e * p.N : nullptr;
+    for (int r0 = 0; r0 < rows; r0 += RMAX) {
+        const int nr = min(RMAX, rows - r0);
+        if (threadIdx.x < RMAX) s_tok[threadIdx.x] = threadIdx.x < nr ? p.sorted_ids[o0 + r0 + threadIdx.x] : 0;
+        __syncthreads();
+        const int8_t *arow[RMAX];
+#pragma unroll
+        for (int r = 0; r < RMAX; ++r)
+            arow[r] = p.x + (int64_t)(s_tok[r < nr ? r : 0] / in_div) * kb + lane * 16;
+        int acc[RMAX];
+#pragma unroll
+        for (int r = 0; r < RMAX; ++r) acc[r] = 0;
+        for (int c0 = 0; c0 < nch; c0 += BT) {
+            v4i bv[BT], av[BT][RMAX];
+#pragma unroll
+            for (int u = 0; u < BT; ++u)
+#pragma unroll
+                for (int r = 0; r < RMAX; ++r)
+                    av[u][r] = r < nr ? *reinterpret_cast<const v4i *>(arow[r] + (int64_t)(c0 + u) * 1024)
+                                      : v4i{0, 0, 0, 0};
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int u = 0; u < BT; ++u)
+                bv[u] = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(brow + (int64_t)(c0 + u) * 1024));
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int u = 0; u < BT; ++u)
+#pragma unroll
+                for (int r = 0; r < RMAX; ++r)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) acc[r] = __builtin_amdgcn_sdot4(av[u][r][q], bv[u][q], acc[r], false);
+        }
+#pragma unroll
+        for (int r = 0; r < RMAX; ++r) {
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1)
+                acc[r] = (int)((uint32_t)acc[r] + (uint32_t)__shfl_xor(acc[r], off, 64));
+            if (lane == 0) colsum[r][wave] = acc[r];
+        }
+        __syncthreads();
+        if (threadIdx.x < nr) {
+            const int r = threadIdx.x;
+            const v4i v{colsum[r][0], colsum[r][1], colsum[r][2], colsum[r][3]};
+            if constexpr (KIND == MOE_S8) moe_store(p, s_tok, nr, in_div, swe, r, n0, v);
+            else moe_store_i32(p, s_tok, nr, r, n0, v);
+        }
+        __syncthreads();   // s_tok and colsum are rewritten by the next pass
+    }
+}
+
 // Offsets, then the grouped GEMM (DMA path when the problem fits it).
 template <int KIND>
 int32_t launch_moe(const MoeArgs &p, const int32_t *expert_ids, int32_t *expert_counts,
                    bool out_ok, hipStream_t stream) {
     constexpr int ES = MoeElem<KIND>::SIZE;
-    hipLaunchKernelGGL(moe_offsets_kernel, dim3(1), dim3(1024), 0, stream, expert_ids, p.size_m, p.E,
-                       expert_counts, const_cast<int32_t *>(p.offsets));
-    if (hipPeekAtLastError() != hipSuccess) return kLaunch;
     // Upper bound on ragged m-tiles: sum_e ceil(cnt_e / BM) <= ceil(size_m / BM) + E.
     const int slots = (p.size_m + BM - 1) / BM + p.E;
     // The DMA path needs whole 128-byte K stages, N a multiple of 256, 16-byte
@@ -569,6 +673,26 @@ int32_t launch_moe(const MoeArgs &p, const int32_t *expert_ids, int32_t *expert_
     const bool fast = kb % mfma2::BK == 0 && p.N % mfma2::BN == 0 && mfma::aligned16(p.x) &&
                       mfma::aligned16(p.w) && x_rows * kb < (1ll << 31) &&
                       (int64_t)p.N * kb < (1ll << 31) && out_ok;
+    // Decode launches (size_m <= 64) find their rows from the ids themselves
+    // and write the counts and offsets: no offsets kernel in front (N =
+    // 14336, K = 4096, E = 8, top-2, 2 rotated weight sets, graph replay: 1 /
+    // 2 / 4 / 8 / 16 tokens 27.3 / 60.4 / 72.6 / 86.2 / 98.2 -> 22.4 / 56.0 /
+    // 67.9 / 81.2 / 95.5 us, bit-identical).
+    MoeArgs q = p;
+    q.expert_ids = expert_ids;
+    q.counts = expert_counts;
+    if constexpr (KIND == MOE_S8 || KIND == MOE_S8_I32) {
+        // 3-8 pairs: the dot4 row kernel, 2 rows per pass over the weights
+        // (2 / 4 tokens: 56.0 / 67.9 -> 47.2 / 65.9 us; at 2 pairs 22.5
+        // against 22.4 us, from 16 pairs slower: 2 pairs stay staged)
+        if (fast && p.size_m > 2 && p.size_m <= 8 && kb % 1024 == 0 && p.N % 4 == 0) {
+            if (kb % 2048 == 0)
+                hipLaunchKernelGGL((moe_row_kernel<KIND, 2, 2>), dim3(p.N / 4, p.E), dim3(256), 0, stream, q);
+            else
+                hipLaunchKernelGGL((moe_row_kernel<KIND, 2, 1>), dim3(p.N / 4, p.E), dim3(256), 0, stream, q);
+            return launch_status();
+        }
+    }
     if (fast && p.size_m <= 64 && kb % 512 == 0) {
         // decode-sized: no expert holds more than size_m rows.  N = 14336,
         // K = 4096, E = 8, top-2: 1 / 4 / 16 tokens (2 / 5 / 7 experts) in
@@ -582,7 +706,7 @@ int32_t launch_moe(const MoeArgs &p, const int32_t *expert_ids, int32_t *expert_
                                dim3(1024),                                                                   \
                                std::max((size_t)(DEPTH) * (16 * (RF) + 16 * (NB)) * (SB),                    \
                                         (size_t)(RF) * (NB) * ((SB) / 64) * 1024) + 64 * (RF),               \
-                               stream, p);                                                                   \
+                               stream, q);                                                                   \
             return launch_status();                                                                          \
         }
         BK_MOEROWS(2, 1, 512, 3)
@@ -593,6 +717,9 @@ int32_t launch_moe(const MoeArgs &p, const int32_t *expert_ids, int32_t *expert_
         BK_MOEROWS(4, 4, 512, 2)
 #undef BK_MOEROWS
     }
+    hipLaunchKernelGGL(moe_offsets_kernel, dim3(1), dim3(1024), 0, stream, expert_ids, p.size_m, p.E,
+                       expert_counts, const_cast<int32_t *>(p.offsets));
+    if (hipPeekAtLastError() != hipSuccess) return kLaunch;
     if (fast) {
         const int work = slots * (p.N / mfma2::BN);
         const int padded = (work + 7) / 8 * 8;   // whole XCD groups

@@ -323,13 +323,19 @@ def test_moe_config5_i32_whole_output_exact_and_bf16_epilogue(gpu):
     assert torch.equal(out.view(torch.int16), want_bf16.view(torch.int16))
 
 
-# ---- decode-sized MoE (size_m <= 64, K % 512 == 0: moe_rows_staged_kernel) --
+# ---- decode-sized MoE (size_m <= 64, K % 512 == 0: moe_rows_staged_kernel;
+# 3-8 pairs with K % 1024 == 0: moe_row_kernel); no offsets kernel, the
+# counts and offsets written by the decode kernels (checked in _run) --
 @pytest.mark.parametrize("case", [(1, 8, 2, 512, 1024, False), (3, 8, 2, 256, 512, True), (16, 8, 2, 512, 2048, False),
                                   (32, 8, 2, 256, 512, True), (4, 8, 2, 6144, 512, False),
-                                  (2, 8, 2, 12288, 512, True), (21, 4, 3, 256, 1536, False)])
+                                  (2, 8, 2, 12288, 512, True), (21, 4, 3, 256, 1536, False),
+                                  (2, 8, 2, 512, 1024, False), (4, 8, 2, 1024, 4096, True), (3, 4, 2, 256, 3072, False),
+                                  (8, 1, 1, 256, 2048, False)])
 def test_moe_decode_all_pairs(gpu, case):
     # every pair bit-exact against the per-pair W8A8 formula; size_m 2 to 64
-    # (2 or 4 row fragments), 16 / 32 / 64 columns per workgroup
+    # (2 or 4 row fragments), 16 / 32 / 64 columns per workgroup; the row
+    # kernel at 4 / 8 / 6 pairs (1 or 2 KiB per batch) and with 8 rows on one
+    # expert (4 passes of 2 rows)
     tokens, E, topk, n, k, tw = case
     print(f"case: moe decode {case}", flush=True)
     _run(tokens=tokens, E=E, topk=topk, n=n, k=k, seed=tokens * 7 + n, topk_w=tw)
@@ -360,3 +366,44 @@ def test_moe_decode_one_expert_takes_all_rows(gpu):
     tokens, routing = _block_routing([0, 64, 0], seed=3)
     print("case: moe decode one expert", flush=True)
     _run(tokens=tokens, E=3, topk=1, n=512, k=512, seed=4, routing=routing)
+
+
+@pytest.mark.parametrize("size_m", [6, 60])
+@pytest.mark.parametrize("E", [1, 8, 65])
+def test_expert_counting_decode(gpu, E, size_m):
+    # Decode launches count in-kernel (one ballot per expert): unsorted ids
+    # with some outside [0, E), counts and offsets against the oracle's count
+    # and scan of the in-range ids (row kernel at 6 pairs, staged at 60).
+    n, k = 256, 1024
+    g = rng(E * 100 + size_m)
+    expert_ids = g.integers(-2, E + 2, size_m).astype(np.int32)
+    sorted_ids = np.arange(size_m, dtype=np.int32)
+    x, w = int8_uniform(g, (size_m, k)), int8_uniform(g, (E, n, k))
+    out = torch.zeros((size_m, n), dtype=torch.bfloat16, device="cuda:0")
+    counts = torch.full((E,), -7, dtype=torch.int32, device="cuda:0")
+    offs = torch.full((E + 1,), -7, dtype=torch.int32, device="cuda:0")
+    P.MoeS8GroupedPlan.select(E, 1, size_m, n, k).run(dev(x), dev(w), dev(sorted_ids), dev(expert_ids), out,
+                                                      counts, offs, dev(np.ones(size_m, np.float32)),
+                                                      dev(np.ones(E * n, np.float32)))
+    sync()
+    valid = expert_ids[(expert_ids >= 0) & (expert_ids < E)]
+    c_ref, o_ref = O.moe_expert_offsets(valid, E)
+    assert np.array_equal(counts.cpu().numpy(), c_ref)
+    assert np.array_equal(offs.cpu().numpy(), o_ref)
+
+
+def test_moe_decode_row_kernel_i32_vs_oracle(gpu):
+    # int32 SKU on the row kernel (7 pairs, one out of range: not counted,
+    # its output row untouched) against the oracle's grouped restatement
+    tokens, E, topk, n, k = 7, 8, 1, 512, 2048
+    g = rng(77)
+    pair_e = np.array([3, 3, 0, 7, E + 1, 3, 0], np.int32)
+    order = np.argsort(pair_e, kind="stable").astype(np.int32)
+    sorted_ids, expert_ids = order, pair_e[order]
+    x, w = int8_uniform(g, (tokens, k)), int8_uniform(g, (E, n, k))
+    got = _moe_i32(dev(x), dev(w), sorted_ids, expert_ids, E, topk, tokens, n, k).cpu().numpy()
+    _, offs = O.moe_expert_offsets(expert_ids, E)
+    want = O.moe_s8_grouped_i32(x, w, sorted_ids, offs, topk, tokens)
+    valid = pair_e < E
+    assert np.array_equal(got[valid], want[valid])
+    assert np.all(got[~valid] == -7)
