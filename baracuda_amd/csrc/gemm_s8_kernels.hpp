@@ -1224,6 +1224,41 @@ inline bool u8_rrr_prepass_eligible(const S8Args &p) {
 // and row-major-B flags, 64 columns per workgroup where N allows; main tiles
 // above the rows on the LDS-DMA u8 RRR kernel.  False when the shape does
 // not fit.  N = K = 4096, M = 1 / 16 on the general kernel: 87.4 / 86.6 us.
+// Row blocks of a last-rows launch of the u8 RCR and s8 / u8 RRR SKUs
+// (the int8 RCR launcher applies the same two rules inline): a small grid
+// (`whole`: all M rows) as 64-row blocks when they fit one round of
+// workgroups, else 128-row blocks; 33-128 last rows below N = 6144 as the
+// row blocks of mfma2::last_rows_blocks; otherwise one block of the fewest
+// fragments that hold the rows.  rf: 16-row fragments per block.  K = 4096,
+// graph replay, against one 128-row block (M = 100) or 128-row blocks
+// (M = 200 / 256): N = 4096, M = 100 u8 RCR 14.7 -> 12.4, s8 RRR 13.8 ->
+// 11.8, u8 RRR 18.3 -> 14.0 us; N = 2048, M = 100 / 256 u8 RCR 12.9 / 13.7
+// -> 8.8 / 11.5, s8 RRR 12.8 / 13.8 -> 9.8 / 11.7, u8 RRR 16.7 / 17.7 ->
+// 10.9 / 13.5 us; s8 RRR N = 4096, M = 200 / 256 14.3 / 15.0 -> 14.8 /
+// 15.1 us (the one loss).
+inline void rows_blocks_plan(int M, int N, int rem, bool whole, int &rf, int &blocks, int &nb) {
+    if (whole) {
+        const int b4 = (M + 63) / 64, n4 = mfma2::last_rows_col_frags(N, b4);
+        if (b4 * (N / (16 * n4)) <= 256) {
+            rf = 4;
+            blocks = b4;
+            nb = n4;
+            return;
+        }
+        rf = 8;
+        blocks = (M + 127) / 128;
+        nb = mfma2::last_rows_col_frags(N, blocks);
+        return;
+    }
+    nb = mfma2::last_rows_col_frags(N, 1);
+    if (nb == 1 && rem > 32) {
+        mfma2::last_rows_blocks(rem, N, rf, blocks, nb);
+        return;
+    }
+    rf = rem <= 32 ? 2 : (rem <= 64 ? 4 : 8);
+    blocks = 1;
+}
+
 template <int ACT, typename BiasT>
 bool launch_u8_rrr_rows(const S8Args &p, hipStream_t stream) {
     int rem = mfma2::last_rows_pass(p.M, p.N, 128), blocks = 1;
@@ -1251,9 +1286,10 @@ bool launch_u8_rrr_rows(const S8Args &p, hipStream_t stream) {
         else
             hipLaunchKernelGGL((gemm_u8_rrr_dma_kernel<false, ACT, BiasT>), dim3(tiles), dim3(DmaCfg::NT), 0, stream, pm);
     }
-    const int nb = mfma2::last_rows_col_frags(p.N, blocks);   // as the s8 RRR pass
+    int rf, nb;   // as the s8 RRR pass
+    rows_blocks_plan(p.M, p.N, rem, whole, rf, blocks, nb);
 #define BK_U8RRRROWS(RF, NB, SB, DEPTH)                                                                        \
-    if (rem <= 16 * (RF) && nb == (NB)) {                                                                       \
+    if (rf == (RF) && nb == (NB)) {                                                                              \
         const size_t lds = std::max((size_t)(DEPTH) * (16 * (RF) + 16 * (NB)) * (SB), (size_t)(RF) * (NB) * ((SB) / 64) * 1024); \
         if (vec)                                                                                                \
             hipLaunchKernelGGL((gemm_s8_rcr_rows_staged_kernel<0, true, ACT, BiasT, RF, NB, SB, DEPTH, true, true>), \
@@ -1427,9 +1463,10 @@ bool launch_u8_rcr_rows(const S8Args &p, hipStream_t stream) {
         }
         return true;
     }
-    const int nb = mfma2::last_rows_col_frags(p.N, blocks);
+    int rf, nb;
+    rows_blocks_plan(p.M, p.N, rem, whole, rf, blocks, nb);
 #define BK_U8ROWS(RF, NB, SB, DEPTH)                                                                           \
-    if (rem <= 16 * (RF) && nb == (NB)) {                                                                       \
+    if (rf == (RF) && nb == (NB)) {                                                                              \
         const size_t lds = std::max((size_t)(DEPTH) * (16 * (RF) + 16 * (NB)) * (SB), (size_t)(RF) * (NB) * ((SB) / 64) * 1024); \
         if (vec)                                                                                                \
             hipLaunchKernelGGL((gemm_s8_rcr_rows_staged_kernel<0, true, ACT, BiasT, RF, NB, SB, DEPTH, true>),    \
@@ -1702,13 +1739,14 @@ bool launch_rrr_rows(const S8Args &p, hipStream_t stream) {
     // (16 / 64 columns; 64 columns at N = 4096 13.1, 16 at N = 14336 23.1;
     // before the XCD-major numbering 64 columns 13.4 / 21.6; the 256x256 RRR
     // tiles 40.5 / 37.7)
-    const int nb = mfma2::last_rows_col_frags(p.N, blocks);
+    int rf, nb;
+    rows_blocks_plan(p.M, p.N, rem, whole, rf, blocks, nb);
     S8Args pm = p;
     pm.M = whole ? 0 : p.M - rem;
     if (pm.M > 0 && launch_rrr_dma<ACT, BiasT>(pm, stream) != kOk) return false;
     const bool vec = p.N % 4 == 0 && p.ldd % 4 == 0 && (reinterpret_cast<uintptr_t>(p.d) % 4) == 0;
 #define BK_RRRROWS(RF, NB, SB, DEPTH)                                                                          \
-    if (rem <= 16 * (RF) && nb == (NB)) {                                                                       \
+    if (rf == (RF) && nb == (NB)) {                                                                              \
         const size_t lds = std::max((size_t)(DEPTH) * (16 * (RF) + 16 * (NB)) * (SB), (size_t)(RF) * (NB) * ((SB) / 64) * 1024); \
         if (vec)                                                                                                \
             hipLaunchKernelGGL((gemm_s8_rcr_rows_staged_kernel<EPI_S8, true, ACT, BiasT, RF, NB, SB, DEPTH, false, true>), \

@@ -345,7 +345,9 @@ def test_null_c_with_beta(gpu, shape, layout, epi, elem):
 # folded into its accumulator.  2 / 4 / 8 row fragments, 16 / 32 / 64
 # columns per workgroup, main 256x256 tiles above the rows.
 U8_ROWS_SHAPES = [(1, 4096, 4096), (5, 256, 512), (33, 512, 1024), (100, 6144, 512), (128, 12288, 512),
-                  (1025, 16384, 512), (1100, 16384, 1024), (20, 272, 512), (1, 256, 1024)]
+                  (1025, 16384, 512), (1100, 16384, 1024), (20, 272, 512), (1, 256, 1024),
+                  # row blocks below N = 6144: two 64-row blocks, three 32-row blocks
+                  (100, 4096, 512), (90, 1024, 1024)]
 
 
 @pytest.mark.parametrize("layout", [RCR, RRR])
@@ -389,7 +391,7 @@ def test_u8_last_rows_large_k_exact(gpu, layout):
 # below 6144 / from 6144 / from 12288), 2 / 4 / 8 row fragments, main RRR
 # tiles above the rows.
 RRR_ROWS_SHAPES = [(1, 4096, 4096), (5, 256, 512), (33, 512, 1024), (20, 288, 512), (100, 272, 512),
-                   (128, 1024, 2048), (1025, 16384, 512), (1100, 16384, 1024), (20, 6144, 512)]
+                   (128, 1024, 2048), (1025, 16384, 512), (1100, 16384, 1024), (20, 6144, 512), (100, 4096, 512)]
 
 
 @pytest.mark.parametrize("epi", [P.EpilogueKind.Identity, P.EpilogueKind.BiasGelu, P.EpilogueKind.BiasRelu])
@@ -410,10 +412,12 @@ def test_s8_rrr_last_rows(gpu, shape, epi):
 
 
 @pytest.mark.parametrize("layout,shape", [(RCR, (200, 512, 1024)), (RCR, (384, 256, 512)), (RCR, (512, 512, 512)),
-                                          (RRR, (200, 512, 1024)), (RRR, (256, 512, 512)), (RRR, (384, 256, 512))])
+                                          (RRR, (200, 512, 1024)), (RRR, (256, 512, 512)), (RRR, (384, 256, 512)),
+                                          (RCR, (512, 4096, 512)), (RRR, (300, 4096, 512))])
 def test_u8_small_grid_row_blocks(gpu, layout, shape):
-    # u8 grids of at most 512 rows (RRR: 256, or 512 off the 256 grid): every row as 128-row
-    # blocks of the last-rows kernel; the whole output against the oracle
+    # u8 grids of at most 512 rows (RRR: 256, or 512 off the 256 grid): every row as 64-row
+    # blocks of the last-rows kernel (128-row blocks where the 64-row ones would
+    # need a second round: 512 x 4096, 300 x 4096); the whole output against the oracle
     m, n, k = shape
     print(f"case: u8 {_LNAME[layout]} row blocks {shape}", flush=True)
     g = rng(m + 11 * n + k)
@@ -428,7 +432,7 @@ def test_u8_small_grid_row_blocks(gpu, layout, shape):
     assert np.array_equal(got, want)
 
 
-@pytest.mark.parametrize("shape", [(200, 512, 1024), (512, 256, 512), (300, 288, 512)])
+@pytest.mark.parametrize("shape", [(200, 512, 1024), (512, 256, 512), (300, 288, 512), (300, 4096, 512)])
 def test_s8_rrr_small_grid_row_blocks(gpu, shape):
     # s8 RRR grids of at most 512 rows: every row as 128-row blocks of the
     # last-rows kernel (row-major B); the whole output against the oracle
