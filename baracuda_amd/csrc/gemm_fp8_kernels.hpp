@@ -462,6 +462,26 @@ bool launch_fp8_rows(const F8Args &p, int m0, int rem, hipStream_t stream) {
             hipLaunchKernelGGL((gemm_fp8_rcr_row1_kernel<FMT, EPI, ACT, 1>), dim3(p.N / 4), dim3(256), 0, stream, p, m0);
         return true;
     }
+    if (rem > 32 && mfma2::last_rows_col_frags(p.N) == 1) {
+        // 33-128 rows below N = 6144 as row blocks (mfma2::last_rows_blocks);
+        // 32-row blocks need 1 KiB stages here (a wave's 128-byte chunks
+        // must cover the 16 waves), which fit LDS up to 32 columns.  K =
+        // 4096, graph replay, rotated weights, M = 48 / 100 / 128: N = 4096
+        // 7.6 / 10.4 / 10.7 -> 6.8 / 8.1 / 8.1 us; N = 2048 7.0 / 9.5 / 9.6
+        // -> 5.3 / 6.0 / 6.2 us; N = 3072 7.1 / 9.7 / 9.9 -> 6.0 / 8.0 / 8.0
+        int rf, blk, nbb;
+        mfma2::last_rows_blocks(rem, p.N, rf, blk, nbb);
+#define BK_F8RB(RF, NB, SB, DEPTH)                                                                        \
+        if (rf == (RF) && nbb == (NB) && p.K % (SB) == 0) {                                                  \
+            hipLaunchKernelGGL((gemm_fp8_rcr_rows_staged_kernel<FMT, EPI, ACT, RF, NB, SB, DEPTH>),           \
+                               dim3(p.N / (16 * (NB)), blk), dim3(1024), (size_t)(DEPTH) * (16 * (RF) + 16 * (NB)) * (SB), \
+                               stream, p, m0);                                                               \
+            return true;                                                                                     \
+        }
+        BK_F8RB(4, 1, 512, 2) BK_F8RB(4, 2, 512, 2) BK_F8RB(4, 4, 512, 2)
+        BK_F8RB(2, 1, 1024, 3) BK_F8RB(2, 2, 1024, 2)
+#undef BK_F8RB
+    }
     const int nb = mfma2::last_rows_col_frags(p.N);
 #define BK_F8ROWS(RF, NB, SB, DEPTH)                                                                     \
     if (rem <= 16 * (RF) && nb == (NB) && p.K % (SB) == 0) {                                              \
