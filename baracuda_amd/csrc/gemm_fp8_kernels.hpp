@@ -526,6 +526,22 @@ int32_t launch_fp8(const F8Args &p, hipStream_t stream) {
             if (tiles > 0)
                 hipLaunchKernelGGL((gemm_fp8_dma_kernel<FMT, LAYOUT, EPI, ACT>), dim3(tiles), dim3(F8DmaCfg::NT),
                                    0, stream, pm);
+            if (rem > 32 && mfma2::last_rows_col_frags(p.N) == 1) {
+                // row blocks as the RCR pass (K = 4096, M = 100: N = 4096
+                // 13.8 -> 11.7 us, N = 2048 12.8 -> 9.8 us)
+                int rf, blk, nbb;
+                mfma2::last_rows_blocks(rem, p.N, rf, blk, nbb);
+#define BK_F8RRRB(RF, NB, SB, DEPTH)                                                                      \
+                if (rf == (RF) && nbb == (NB) && p.K % (SB) == 0) {                                          \
+                    hipLaunchKernelGGL((gemm_fp8_rcr_rows_staged_kernel<FMT, EPI, ACT, RF, NB, SB, DEPTH, true>), \
+                                       dim3(p.N / (16 * (NB)), blk), dim3(1024),                             \
+                                       (size_t)(DEPTH) * (16 * (RF) + 16 * (NB)) * (SB), stream, p, pm.M);   \
+                    return launch_status();                                                                  \
+                }
+                BK_F8RRRB(4, 1, 512, 2) BK_F8RRRB(4, 2, 512, 2) BK_F8RRRB(4, 4, 512, 2)
+                BK_F8RRRB(2, 1, 1024, 3) BK_F8RRRB(2, 2, 1024, 2)
+#undef BK_F8RRRB
+            }
             const int nb = mfma2::last_rows_col_frags(p.N);
 #define BK_F8RRRROWS(RF, NB, SB, DEPTH)                                                                    \
             if (rem <= 16 * (RF) && nb == (NB)) {                                                         \

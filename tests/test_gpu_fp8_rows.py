@@ -124,9 +124,11 @@ def test_fp8_rows_deterministic_and_untouched_columns(gpu):
 
 # RRR (row-major B [K, N]) last rows: the staged kernel with transposing LDS
 # reads; 16 / 32 / 64 columns per workgroup by the last-rows rule, 1 / 2 / 4 /
-# 8 fragments, main RRR tiles above the rows at N = 16384.
+# 8 fragments, main RRR tiles above the rows at N = 16384; row blocks below
+# N = 6144 with K % 1024 == 0 (100 x 512, 100 x 4096, 60 x 3072).
 RRR_SHAPES = [(1, 256, 4096), (17, 288, 1024), (33, 272, 512), (5, 272, 2048), (100, 512, 1024),
-              (128, 1040, 512), (1025, 16384, 512), (17, 6144, 1024), (64, 8192, 512)]
+              (128, 1040, 512), (1025, 16384, 512), (17, 6144, 1024), (64, 8192, 512),
+              (100, 4096, 1024), (60, 3072, 1024)]
 
 
 @pytest.mark.parametrize("epi", EPIS)
