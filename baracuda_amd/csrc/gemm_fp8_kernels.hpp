@@ -519,6 +519,29 @@ int32_t launch_fp8(const F8Args &p, hipStream_t stream) {
         // RRR last rows: the staged kernel reading row-major B, column groups
         // by the last-rows rule (XCD-major in the kernel)
         const int rem = mfma2::last_rows_pass(p.M, p.N, 128);
+        if (rem == 0 && p.M > 128 && p.M <= 512 && p.N % 16 == 0) {
+            // a small grid: every row as row blocks of the same kernel (64-row
+            // blocks, else 128-row) while they fit one round of workgroups.
+            // K = 4096, M = 129 / 256 / 512 against 256x256 RRR tiles: N =
+            // 4096 38.9 / 40.3 / 40.2 -> 17.4 / 17.4 / 27.1 us, N = 2048
+            // 38.7 / 40.8 / 40.7 -> 10.7 / 11.3 / 17.4 us
+            const int b4 = (p.M + 63) / 64, n4 = mfma2::last_rows_col_frags(p.N, b4);
+            const int b8 = (p.M + 127) / 128, n8 = mfma2::last_rows_col_frags(p.N, b8);
+            const bool use4 = b4 * (p.N / (16 * n4)) <= 256;
+            const int blk = use4 ? b4 : b8, nbb = use4 ? n4 : n8;
+            if (blk * (p.N / (16 * nbb)) <= 256) {
+#define BK_F8RRRW(RF, NB, SB)                                                                             \
+                if ((use4 ? 4 : 8) == (RF) && nbb == (NB)) {                                                 \
+                    hipLaunchKernelGGL((gemm_fp8_rcr_rows_staged_kernel<FMT, EPI, ACT, RF, NB, SB, 2, true>), \
+                                       dim3(p.N / (16 * (NB)), blk), dim3(1024),                             \
+                                       (size_t)2 * (16 * (RF) + 16 * (NB)) * (SB), stream, p, 0);            \
+                    return launch_status();                                                                  \
+                }
+                BK_F8RRRW(4, 1, 512) BK_F8RRRW(4, 2, 512) BK_F8RRRW(4, 4, 512)
+                BK_F8RRRW(8, 1, 512) BK_F8RRRW(8, 2, 512) BK_F8RRRW(8, 4, 256)
+#undef BK_F8RRRW
+            }
+        }
         if (rem != 0) {
             F8Args pm = p;
             pm.M = p.M - rem;

@@ -167,3 +167,23 @@ def test_fp8_rrr_rows_random_with_c(gpu, shape, fmt):
     fb = np.abs(O.fp8_to_f32(b, fmt).astype(np.float64))
     st = _steps(got, want, fmt, FP8_FLOOR * alpha * (fa @ fb))
     assert st.max() <= 1.0 and (got != want).mean() < 0.02
+
+
+# FP8 RRR small grids (129-512 rows): every row as row blocks of the staged
+# kernel with row-major B: 64-row blocks at 200 x 512, 128-row blocks at
+# 512 x 4096 and 300 x 1024, where 64-row blocks would need a second round.
+@pytest.mark.parametrize("epi", [P.EpilogueKind.Identity, P.EpilogueKind.BiasGelu])
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("shape", [(200, 512, 1024), (512, 4096, 512), (300, 1024, 512)])
+def test_fp8_rrr_small_grid_row_blocks(gpu, shape, fmt, epi):
+    m, n, k = shape
+    print(f"case: fp8 rrr small grid {fmt} {epi.value} {shape}", flush=True)
+    a = O.f32_to_fp8((((np.arange(m * k) * 5) % 13) - 6.0) * 0.125, fmt).reshape(m, k)
+    b = O.f32_to_fp8((((np.arange(k * n) * 7) % 11) - 5.0) * 0.125, fmt).reshape(k, n)
+    bias = (((np.arange(n) % 5) - 2) * 0.5).astype(np.float32)
+    got = _run(fmt, P.LayoutSku.Rrr, epi, a, b, bias=bias)
+    want = _want(fmt, P.LayoutSku.Rrr, epi, a, b, None, bias, 0.25, 0.0)
+    if ACT[epi] in (None, "relu"):
+        assert np.array_equal(got, want)
+    else:
+        assert _steps(got, want, fmt).max() <= 1.0
