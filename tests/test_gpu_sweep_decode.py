@@ -49,3 +49,32 @@ def test_moe_sweep(gpu, case):
     print(f"case: sweep moe E={len(counts)} rows={sum(counts)} n={n} k={k}", flush=True)
     tokens, routing = _block_routing(counts, seed=seed)
     _moe_run(tokens=tokens, E=len(counts), topk=1, n=n, k=k, seed=seed, routing=routing)
+
+
+def _moe_decode_cases(count, seed):
+    # at most 64 pairs: the decode kernels (staged, and the dot4 row kernel
+    # for 3-8 pairs with K % 1024 == 0); K on the 512 / 1024 grids and off
+    # them (the tile path)
+    g = rng(seed)
+    out = []
+    for i in range(count):
+        e = int(g.integers(1, 17))
+        cap = 8 if i % 3 == 0 else 64
+        counts = [0] * e
+        for _ in range(int(g.integers(1, cap + 1))):
+            counts[int(g.integers(0, e))] += 1
+        n = int(g.integers(1, 5)) * 256
+        k = (int(g.integers(1, 5)) * 1024 if i % 4 != 3 else int(g.integers(1, 9)) * 512) if i % 5 else \
+            int(g.integers(1, 20)) * 128
+        out.append((counts, n, k, seed + i))
+    return out
+
+
+@pytest.mark.parametrize("case", _moe_decode_cases(15, 401))
+def test_moe_decode_sweep(gpu, case):
+    # decode-sized routing (empty experts, one expert with many rows), every
+    # pair bit-exact, the counts and offsets the decode kernels write
+    counts, n, k, seed = case
+    print(f"case: sweep moe decode E={len(counts)} rows={sum(counts)} n={n} k={k}", flush=True)
+    tokens, routing = _block_routing(counts, seed=seed)
+    _moe_run(tokens=tokens, E=len(counts), topk=1, n=n, k=k, seed=seed, routing=routing)
