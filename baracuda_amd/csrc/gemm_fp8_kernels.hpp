@@ -275,14 +275,17 @@ __global__ __launch_bounds__(1024) void gemm_fp8_rcr_rows_staged_kernel(F8Args p
     // blockIdx.y: 16 RF-row block of the pass
     const int m0 = m_first + blockIdx.y * 16 * RF;
     constexpr int WAVES = 16, CH = SB / 128;
-    constexpr int FPW = RF * CH / WAVES;                 // A row fragments per wave
+    // With fewer (fragment, chunk) pairs than waves (RF * CH < 16) the first
+    // RF * CH waves hold one each and the others only DMA.
+    constexpr bool ALL = RF * CH >= WAVES;
+    constexpr int FPW = ALL ? RF * CH / WAVES : 1;       // A row fragments per wave
     constexpr int FSTEP = WAVES / CH;
     constexpr int ROWS = 16 * RF + 16 * NB;              // A then B rows of a stage
     constexpr int STAGE = ROWS * SB;
     constexpr int UPR = SB / 16;                         // 16-byte units per row
     constexpr int NI = ROWS * UPR / 64;                  // 1 KiB DMA instructions per stage
     constexpr int HI = (NI + WAVES - 1) / WAVES, LO = NI / WAVES;
-    static_assert(FPW >= 1 && RF * CH % WAVES == 0 && UPR >= 16 && (ROWS * UPR) % 64 == 0 && DEPTH >= 2 &&
+    static_assert((!ALL || RF * CH % WAVES == 0) && UPR >= 16 && (ROWS * UPR) % 64 == 0 && DEPTH >= 2 &&
                       DEPTH <= 4 && RF * NB * CH * 1024 <= DEPTH * STAGE,
                   "stage split");
     constexpr int F = FMT == FMT_E5M2 ? 1 : 0;
@@ -321,6 +324,7 @@ __global__ __launch_bounds__(1024) void gemm_fp8_rcr_rows_staged_kernel(F8Args p
     const int ns = p.K / SB;
     for (int st = 0; st < DEPTH && st < ns; ++st) dma_stage(st, lds + st * STAGE);
     const int c = wave % CH, f0 = wave / CH;
+    const bool active = ALL || wave < RF * CH;   // wave-uniform
     v4f acc[FPW][NB];
 #pragma unroll
     for (int i = 0; i < FPW; ++i)
@@ -336,6 +340,7 @@ __global__ __launch_bounds__(1024) void gemm_fp8_rcr_rows_staged_kernel(F8Args p
         else { if (hi) mfma2::wait_vmcnt<3 * HI>(); else mfma2::wait_vmcnt<3 * LO>(); }
         __syncthreads();
         int8_t *buf = lds + (st % DEPTH) * STAGE;
+        if (active) {
         v8i bv[NB];
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
@@ -360,15 +365,18 @@ __global__ __launch_bounds__(1024) void gemm_fp8_rcr_rows_staged_kernel(F8Args p
             for (int nb = 0; nb < NB; ++nb)
                 acc[i][nb] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bv[nb], av, acc[i][nb], F, F, 0, 0, 0, 0);
         }
+        }
         __syncthreads();   // every wave is done with this buffer
         if (st + DEPTH < ns) dma_stage(st + DEPTH, buf);
     }
     // partial sums of (A fragment f, B fragment nb), chunk c: part[f][nb][c][lane]
     v4f *part = reinterpret_cast<v4f *>(lds);
+    if (active) {
 #pragma unroll
-    for (int i = 0; i < FPW; ++i)
+        for (int i = 0; i < FPW; ++i)
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) part[(((f0 + FSTEP * i) * NB + nb) * CH + c) * 64 + lane] = acc[i][nb];
+            for (int nb = 0; nb < NB; ++nb) part[(((f0 + FSTEP * i) * NB + nb) * CH + c) * 64 + lane] = acc[i][nb];
+    }
     __syncthreads();
     const F8Epilogue<FMT, EPI, true, ACT> epi{p};
     for (int e = wave; e < RF * NB; e += WAVES) {
@@ -490,6 +498,14 @@ bool launch_fp8_rows(const F8Args &p, int m0, int rem, hipStream_t stream) {
                            stream, p, m0);                                                               \
         return true;                                                                                     \
     }
+    // up to 16 / 32 rows at 32 or 64 columns: 1 / 2 fragments, 4 / 8 waves
+    // with MFMA work (padding A rows cost DMA and LDS time: N = 14336, M = 2
+    // / 8 / 16 / 32 14.7 / 14.0 / 13.3 / 13.6 -> 13.4 / 12.8 / 12.3 / 12.9 us
+    // against 4 fragments; N = 8192, M = 2-16 8.9 -> 8.35 us)
+    BK_F8ROWS(1, 4, 512, 2)
+    BK_F8ROWS(2, 4, 512, 2)
+    BK_F8ROWS(1, 2, 512, 2)
+    BK_F8ROWS(2, 2, 512, 2)
     BK_F8ROWS(4, 4, 512, 2)
     BK_F8ROWS(8, 4, 256, 2)
     BK_F8ROWS(4, 2, 512, 2)

@@ -38,13 +38,16 @@ pytestmark = pytest.mark.gpu
 # instead (2 KiB per batch, 1 KiB at K = 3072).  33-128 rows below N = 6144
 # with K % 1024 == 0 run as row blocks: 64-row blocks of 32 / 16 columns
 # (100 x 4096, 90 x 2560), 32-row blocks with 1 KiB stages (60 x 3072,
-# 100 x 512).
+# 100 x 512).  From N = 6144 up to 16 / 32 rows take 1 / 2 fragments with
+# only 4 / 8 waves multiplying (9 x 8192, 16 x 14336, 20 x 8192, 30 x 14336;
+# 2 x 6144).
 SHAPES = [(1, 256, 4096), (16, 512, 2048), (5, 272, 1024), (17, 288, 1024), (32, 1040, 3072),
           (9, 256, 1536), (20, 272, 512), (33, 512, 512), (64, 256, 2560), (65, 1040, 1024),
           (100, 512, 4096), (128, 256, 512), (1025, 16384, 2048), (1064, 16384, 512), (1152, 16384, 1024),
           (1, 1040, 4096), (16, 272, 2048), (2, 6144, 512), (33, 8192, 512), (128, 6144, 1024),
           (1, 12288, 2048), (16, 14336, 1024), (100, 12288, 1024), (200, 512, 1024), (384, 1024, 512),
-          (512, 4096, 512), (1, 512, 3072), (100, 4096, 1024), (60, 3072, 1024), (90, 2560, 1024)]
+          (512, 4096, 512), (1, 512, 3072), (100, 4096, 1024), (60, 3072, 1024), (90, 2560, 1024),
+          (20, 8192, 1024), (30, 14336, 512), (9, 8192, 512)]
 
 
 @pytest.mark.parametrize("shape", SHAPES)
@@ -68,7 +71,7 @@ def test_fp8_rows_f32_and_bf16(gpu, shape):
 
 @pytest.mark.parametrize("epi", EPIS)
 @pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
-@pytest.mark.parametrize("shape", [SHAPES[0], SHAPES[3], SHAPES[7], SHAPES[10], SHAPES[13], SHAPES[15], SHAPES[18], SHAPES[22], SHAPES[23], SHAPES[25], SHAPES[26], SHAPES[27], SHAPES[28]])
+@pytest.mark.parametrize("shape", [SHAPES[0], SHAPES[3], SHAPES[7], SHAPES[10], SHAPES[13], SHAPES[15], SHAPES[18], SHAPES[22], SHAPES[23], SHAPES[25], SHAPES[26], SHAPES[27], SHAPES[28], SHAPES[30], SHAPES[31], SHAPES[32]])
 def test_fp8_rows_reference_pattern(gpu, shape, fmt, epi):
     m, n, k = shape
     print(f"case: fp8 rows pattern {fmt} {epi.value} {shape}", flush=True)
