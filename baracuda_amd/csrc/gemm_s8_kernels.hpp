@@ -771,14 +771,17 @@ __global__ __launch_bounds__(1024) void gemm_s8_rcr_rows_staged_kernel(S8Args p,
     // more rows than one workgroup holds)
     const int m0 = m_first + blockIdx.y * 16 * RF;
     constexpr int WAVES = 16, CH = SB / 64;                  // 64-byte chunks per stage
-    constexpr int FPW = RF * CH / WAVES;                      // A row fragments per wave
+    // With fewer (fragment, chunk) pairs than waves (RF * CH < 16) the first
+    // RF * CH waves hold one each and the others only DMA.
+    constexpr bool ALL = RF * CH >= WAVES;
+    constexpr int FPW = ALL ? RF * CH / WAVES : 1;            // A row fragments per wave
     constexpr int FSTEP = WAVES / CH;
     constexpr int ROWS = 16 * RF + 16 * NB;                   // A then B rows of a stage
     constexpr int STAGE = ROWS * SB;                          // bytes
     constexpr int UPR = SB / 16;                              // 16-byte units per row
     constexpr int NI = ROWS * UPR / 64;                       // 1 KiB DMA instructions per stage
     constexpr int HI = (NI + WAVES - 1) / WAVES, LO = NI / WAVES;
-    static_assert(FPW >= 1 && RF * CH % WAVES == 0 && UPR >= 16 && (ROWS * UPR) % 64 == 0 && DEPTH >= 2 &&
+    static_assert((!ALL || RF * CH % WAVES == 0) && UPR >= 16 && (ROWS * UPR) % 64 == 0 && DEPTH >= 2 &&
                       DEPTH <= 4 && RF * NB * CH * 1024 <= 160 * 1024 && DEPTH * STAGE <= 160 * 1024,
                   "stage split");
     extern __shared__ __attribute__((aligned(1024))) int8_t lds[];
@@ -819,6 +822,7 @@ __global__ __launch_bounds__(1024) void gemm_s8_rcr_rows_staged_kernel(S8Args p,
     const int ns = p.K / SB;
     for (int st = 0; st < DEPTH && st < ns; ++st) dma_stage(st, lds + st * STAGE);
     const int c = wave % CH, f0 = wave / CH;
+    const bool active = ALL || wave < RF * CH;   // wave-uniform
     v4i acc[FPW][NB];
 #pragma unroll
     for (int i = 0; i < FPW; ++i)
@@ -834,6 +838,7 @@ __global__ __launch_bounds__(1024) void gemm_s8_rcr_rows_staged_kernel(S8Args p,
         else { if (hi) mfma2::wait_vmcnt<3 * HI>(); else mfma2::wait_vmcnt<3 * LO>(); }
         __syncthreads();
         int8_t *buf = lds + (st % DEPTH) * STAGE;
+        if (active) {
         v4i bv[NB];
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
@@ -863,15 +868,18 @@ __global__ __launch_bounds__(1024) void gemm_s8_rcr_rows_staged_kernel(S8Args p,
                 }
             }
         }
+        }
         __syncthreads();   // every wave is done with this buffer
         if (st + DEPTH < ns) dma_stage(st + DEPTH, buf);
     }
     // partial sums of (A fragment f, B fragment nb), chunk c: part[f][nb][c][lane]
     v4i *part = reinterpret_cast<v4i *>(lds);
+    if (active) {
 #pragma unroll
-    for (int i = 0; i < FPW; ++i)
+        for (int i = 0; i < FPW; ++i)
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) part[(((f0 + FSTEP * i) * NB + nb) * CH + c) * 64 + lane] = acc[i][nb];
+            for (int nb = 0; nb < NB; ++nb) part[(((f0 + FSTEP * i) * NB + nb) * CH + c) * 64 + lane] = acc[i][nb];
+    }
     __syncthreads();
     const S8Epilogue<EPI, VecOut, ACT, BiasT> epi{p};
     // u8: au = acc - kcorr with zero sums, kcorr = -16384 K (mod 2^32)
@@ -1613,6 +1621,11 @@ void launch_kernel(const S8Args &p, bool fast_k, hipStream_t stream, void *works
                 BK_S8ROWS(2, 1, 512, 3)
                 BK_S8ROWS(4, 1, 512, 2)
                 BK_S8ROWS(8, 1, 512, 2)
+                // 9-16 rows from N = 6144: one fragment, 8 waves multiplying
+                // (N = 14336 / 8192, M = 12-16: 13.85 / 8.6-8.7 -> 13.3 /
+                // 8.5 us against two fragments)
+                BK_S8ROWS(1, 2, 512, 2)
+                BK_S8ROWS(1, 4, 512, 2)
                 BK_S8ROWS(2, 2, 512, 3)
                 BK_S8ROWS(4, 2, 512, 2)
                 BK_S8ROWS(8, 2, 512, 2)
