@@ -122,7 +122,7 @@ __device__ __forceinline__ void moe_decode_rows(const MoeArgs &p, int e, int &o0
         if (lane == 0) {
             s_rows[0] = before;
             s_rows[1] = mine;
-            if (blockIdx.x == 0) {
+            if (blockIdx.x == 0 && blockIdx.z == 0) {
                 int32_t *off = const_cast<int32_t *>(p.offsets);
                 p.counts[e] = mine;
                 off[e + 1] = before + mine;
@@ -459,11 +459,12 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void moe_grouped_dma_kernel(MoeArgs 
     }
 }
 
-// Decode-sized MoE (size_m <= 16 RF, so no expert holds more rows): one
-// launch over (N / (16 NB) column groups) x E experts, after the offsets
-// kernel.  A workgroup of 16 waves reads its expert's offsets and exits when
-// the expert has no rows; otherwise, as the dense last-rows pass
-// (gemm_s8_rcr_rows_staged_kernel), it streams its 16 RF gathered A rows
+// Decode-sized MoE (size_m <= 64): one launch over (N / (16 NB) column
+// groups) x E experts x (size_m / 16 RF row blocks), no offsets kernel in
+// front.  A workgroup of 16 waves finds its expert's rows from the ids
+// (moe_decode_rows) and exits when its block of them is empty; otherwise,
+// as the dense last-rows pass (gemm_s8_rcr_rows_staged_kernel; with RF * CH
+// < 16 only the first RF * CH waves multiply), it streams its 16 RF gathered A rows
 // (pair p's input row, through sorted_token_ids; rows past the expert's
 // count point past the input and land as zeros) and its 16 NB rows of the
 // expert's weight slab through LDS in K stages of SB bytes, DEPTH in
@@ -476,7 +477,9 @@ __global__ __launch_bounds__(DmaCfg::NT, 1) void moe_grouped_dma_kernel(MoeArgs 
 template <int KIND, int RF, int NB, int SB, int DEPTH>
 __global__ __launch_bounds__(1024) void moe_rows_staged_kernel(MoeArgs p) {
     constexpr int WAVES = 16, CH = SB / 64;
-    constexpr int FPW = RF * CH / WAVES;
+    // fewer (fragment, chunk) pairs than waves: the first RF * CH multiply
+    constexpr bool ALL = RF * CH >= WAVES;
+    constexpr int FPW = ALL ? RF * CH / WAVES : 1;
     constexpr int FSTEP = WAVES / CH;
     constexpr int ROWS = 16 * RF + 16 * NB;
     constexpr int STAGE = ROWS * SB;
@@ -486,7 +489,7 @@ __global__ __launch_bounds__(1024) void moe_rows_staged_kernel(MoeArgs p) {
     constexpr bool INT = KIND == MOE_S8 || KIND == MOE_S8_I32;
     constexpr int ES = MoeElem<KIND>::SIZE;
     typedef typename std::conditional<INT, v4i, v4f>::type Acc;
-    static_assert(FPW >= 1 && RF * CH % WAVES == 0 && UPR >= 16 && (ROWS * UPR) % 64 == 0 && DEPTH >= 2 &&
+    static_assert((!ALL || RF * CH % WAVES == 0) && UPR >= 16 && (ROWS * UPR) % 64 == 0 && DEPTH >= 2 &&
                       DEPTH <= 4 && DEPTH * STAGE + 64 * RF <= 160 * 1024 && RF * NB * CH * 1024 + 64 * RF <= 160 * 1024,
                   "stage split");
     // dynamic LDS: the stages (then the partial sums), then the A rows' pair ids
@@ -496,7 +499,10 @@ __global__ __launch_bounds__(1024) void moe_rows_staged_kernel(MoeArgs p) {
     const int e = blockIdx.y;
     int o0, rows;
     moe_decode_rows(p, e, o0, rows);
-    if (rows <= 0) return;   // whole workgroup: no rows routed to this expert
+    // blockIdx.z: 16 RF-row block of the expert's rows
+    o0 += blockIdx.z * 16 * RF;
+    rows = min(rows - (int)blockIdx.z * 16 * RF, 16 * RF);
+    if (rows <= 0) return;   // whole workgroup: no rows of this expert in this block
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r16 = lane & 15, g = lane >> 4;
@@ -527,6 +533,7 @@ __global__ __launch_bounds__(1024) void moe_rows_staged_kernel(MoeArgs p) {
     const int ns = kb / SB;
     for (int st = 0; st < DEPTH && st < ns; ++st) dma_stage(st, lds + st * STAGE);
     const int c = wave % CH, f0 = wave / CH;
+    const bool active = ALL || wave < RF * CH;   // wave-uniform
     Acc acc[FPW][NB];
 #pragma unroll
     for (int i = 0; i < FPW; ++i)
@@ -541,6 +548,7 @@ __global__ __launch_bounds__(1024) void moe_rows_staged_kernel(MoeArgs p) {
         else { if (hi) mfma2::wait_vmcnt<3 * HI>(); else mfma2::wait_vmcnt<3 * LO>(); }
         __syncthreads();
         int8_t *buf = lds + (st % DEPTH) * STAGE;
+        if (active) {
         v4i bv[NB];
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
@@ -554,14 +562,17 @@ __global__ __launch_bounds__(1024) void moe_rows_staged_kernel(MoeArgs p) {
                 else acc[i][nb] = mfma16x16x32_h<KIND == MOE_BF16>(bv[nb], av, acc[i][nb]);
             }
         }
+        }
         __syncthreads();
         if (st + DEPTH < ns) dma_stage(st + DEPTH, buf);
     }
     Acc *part = reinterpret_cast<Acc *>(lds);
+    if (active) {
 #pragma unroll
-    for (int i = 0; i < FPW; ++i)
+        for (int i = 0; i < FPW; ++i)
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) part[(((f0 + FSTEP * i) * NB + nb) * CH + c) * 64 + lane] = acc[i][nb];
+            for (int nb = 0; nb < NB; ++nb) part[(((f0 + FSTEP * i) * NB + nb) * CH + c) * 64 + lane] = acc[i][nb];
+    }
     __syncthreads();
     const float *swe = INT && p.sw ? p.sw + (int64_t)e * p.N : nullptr;
     for (int q = wave; q < RF * NB; q += WAVES) {
@@ -694,27 +705,33 @@ int32_t launch_moe(const MoeArgs &p, const int32_t *expert_ids, int32_t *expert_
         }
     }
     if (fast && p.size_m <= 64 && kb % 512 == 0) {
-        // decode-sized: no expert holds more than size_m rows.  N = 14336,
-        // K = 4096, E = 8, top-2: 1 / 4 / 16 tokens (2 / 5 / 7 experts) in
-        // 27.4 / 62.3 / 99.0 us against 43.5 / 100.5 / 117.8 on 256-row
-        // tiles; at size_m 96 / 128 8 row fragments ran level with the tiles
-        // (123 us), so larger size_m stays on them.
+        // decode-sized.  N = 14336, K = 4096, E = 8, top-2: 1 / 4 / 16 tokens
+        // (2 / 5 / 7 experts) in 27.4 / 62.3 / 99.0 us (with the offsets
+        // kernel) against 43.5 / 100.5 / 117.8 on 256-row tiles; at size_m
+        // 96 / 128 8 row fragments ran level with the tiles (123 us), so
+        // larger size_m stays on them.
         const int nb = mfma2::last_rows_col_frags(p.N);
+        // blocks of 16 rows up to 32 pairs, of 32 above (blockIdx.z): an
+        // expert's few rows stage fewer padding rows (N = 14336, K = 4096,
+        // 1 / 8 / 16 / 32 tokens top-2: 22.6 / 80.7 / 95.5 / 106.6 -> 21.6 /
+        // 77.8 / 92.7 / 100.1 us against one block of 32 or 64 rows)
+        const int rfz = p.size_m <= 32 ? 1 : 2;
 #define BK_MOEROWS(RF, NB, SB, DEPTH)                                                                        \
-        if (p.size_m <= 16 * (RF) && nb == (NB)) {                                                           \
-            hipLaunchKernelGGL((moe_rows_staged_kernel<KIND, RF, NB, SB, DEPTH>), dim3(p.N / (16 * (NB)), p.E), \
+        if (rfz == (RF) && nb == (NB)) {                                                                     \
+            hipLaunchKernelGGL((moe_rows_staged_kernel<KIND, RF, NB, SB, DEPTH>),                            \
+                               dim3(p.N / (16 * (NB)), p.E, (p.size_m + 16 * (RF) - 1) / (16 * (RF))),      \
                                dim3(1024),                                                                   \
                                std::max((size_t)(DEPTH) * (16 * (RF) + 16 * (NB)) * (SB),                    \
                                         (size_t)(RF) * (NB) * ((SB) / 64) * 1024) + 64 * (RF),               \
                                stream, q);                                                                   \
             return launch_status();                                                                          \
         }
+        BK_MOEROWS(1, 1, 512, 3)
+        BK_MOEROWS(1, 2, 512, 3)
+        BK_MOEROWS(1, 4, 512, 3)
         BK_MOEROWS(2, 1, 512, 3)
-        BK_MOEROWS(4, 1, 512, 2)
         BK_MOEROWS(2, 2, 512, 3)
-        BK_MOEROWS(4, 2, 512, 2)
         BK_MOEROWS(2, 4, 512, 3)
-        BK_MOEROWS(4, 4, 512, 2)
 #undef BK_MOEROWS
     }
     hipLaunchKernelGGL(moe_offsets_kernel, dim3(1), dim3(1024), 0, stream, expert_ids, p.size_m, p.E,

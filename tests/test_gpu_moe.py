@@ -407,3 +407,11 @@ def test_moe_decode_row_kernel_i32_vs_oracle(gpu):
     valid = pair_e < E
     assert np.array_equal(got[valid], want[valid])
     assert np.all(got[~valid] == -7)
+
+
+def test_moe_decode_row_blocks_of_one_expert(gpu):
+    # 30 of 32 pairs on one expert: 16-row blocks (blockIdx.z), the second
+    # holding 14 rows, the other experts' second blocks empty
+    tokens, routing = _block_routing([0, 30, 2], seed=8)
+    print("case: moe decode two row blocks", flush=True)
+    _run(tokens=tokens, E=3, topk=1, n=512, k=1024, seed=9, routing=routing)
