@@ -1609,6 +1609,15 @@ void launch_kernel(const S8Args &p, bool fast_k, hipStream_t stream, void *works
                 BK_S8RBLK(2, 1) BK_S8RBLK(4, 1) BK_S8RBLK(2, 2) BK_S8RBLK(4, 2) BK_S8RBLK(2, 4) BK_S8RBLK(4, 4)
 #undef BK_S8RBLK
             }
+            if (nb == 1 && rem > 10 && rem <= 16 && p.K % 512 == 0) {
+                // 11-16 rows below N = 6144: one fragment, 8 waves multiplying
+                // (K = 4096, M = 12 / 16: N = 4096 6.55 / 6.93 -> 6.37 /
+                // 6.42 us, N = 2048 4.95 / 5.27 -> 4.87 / 4.90 us against the
+                // B-through-LDS kernel, which stays ahead up to 8 rows)
+                hipLaunchKernelGGL((gemm_s8_rcr_rows_staged_kernel<EPI, VecOut, ACT, BiasT, 1, 1, 512, 3>),
+                                   dim3(p.N / 16), dim3(1024), (size_t)3 * 32 * 512, stream, p, pm.M);
+                return;
+            }
             if (rem > (nb > 1 ? 8 : kRowsDmaMaxRows) && p.K % kRowsStagedSB == 0) {
 #define BK_S8ROWS(RF, NB, SB, DEPTH)                                                                        \
     if (rem <= 16 * (RF) && nb == (NB) && p.K % (SB) == 0) {                                                 \

@@ -46,7 +46,9 @@ STAGED_SHAPES = [(17, 256, 512), (31, 1040, 1536), (33, 512, 512), (65, 272, 102
                  (9, 14336, 1024), (16, 6144, 512),
                  # 33-128 rows below N = 6144 in row blocks (mfma2::last_rows_blocks):
                  # 64-row blocks of 32 columns, 32-row blocks of 32 columns, 3 blocks
-                 (100, 4096, 1024), (128, 2048, 512), (48, 4096, 512), (90, 3072, 512)]
+                 (100, 4096, 1024), (128, 2048, 512), (48, 4096, 512), (90, 3072, 512),
+                 # 11-16 rows below N = 6144: one fragment, 8 of 16 waves multiplying
+                 (11, 1040, 1024), (16, 4096, 2048)]
 SHAPES += STAGED_SHAPES
 
 
