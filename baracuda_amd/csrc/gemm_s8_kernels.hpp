@@ -1237,7 +1237,7 @@ inline bool u8_rrr_prepass_eligible(const S8Args &p) {
 // (`whole`: all M rows) as 64-row blocks when they fit one round of
 // workgroups, else 128-row blocks; 33-128 last rows below N = 6144 as the
 // row blocks of mfma2::last_rows_blocks; otherwise one block of the fewest
-// fragments that hold the rows.  rf: 16-row fragments per block.  K = 4096,
+// fragments (1 / 2 / 4 / 8) that hold the rows.  rf: 16-row fragments per block.  K = 4096,
 // graph replay, against one 128-row block (M = 100) or 128-row blocks
 // (M = 200 / 256): N = 4096, M = 100 u8 RCR 14.7 -> 12.4, s8 RRR 13.8 ->
 // 11.8, u8 RRR 18.3 -> 14.0 us; N = 2048, M = 100 / 256 u8 RCR 12.9 / 13.7
@@ -1263,7 +1263,11 @@ inline void rows_blocks_plan(int M, int N, int rem, bool whole, int &rf, int &bl
         mfma2::last_rows_blocks(rem, N, rf, blocks, nb);
         return;
     }
-    rf = rem <= 32 ? 2 : (rem <= 64 ? 4 : 8);
+    // up to 16 rows: one fragment, 8 of the 16 waves multiplying (K = 4096,
+    // M = 1-16, against two fragments: N = 4096 u8 RCR 7.5 -> 6.6, s8 RRR
+    // 9.2 -> 8.5, u8 RRR 9.8 -> 8.7 us; N = 14336 14.0 -> 12.1, 14.8 ->
+    // 13.7, 17.5 -> 14.6 us)
+    rf = rem <= 16 ? 1 : rem <= 32 ? 2 : (rem <= 64 ? 4 : 8);
     blocks = 1;
 }
 
@@ -1307,6 +1311,9 @@ bool launch_u8_rrr_rows(const S8Args &p, hipStream_t stream) {
                                dim3(p.N / (16 * (NB)), blocks), dim3(1024), lds, stream, p, pm.M);                      \
         return true;                                                                                            \
     }
+    BK_U8RRRROWS(1, 1, 512, 3)
+    BK_U8RRRROWS(1, 2, 512, 3)
+    BK_U8RRRROWS(1, 4, 512, 3)
     BK_U8RRRROWS(2, 1, 512, 3)
     BK_U8RRRROWS(4, 1, 512, 2)
     BK_U8RRRROWS(8, 1, 512, 2)
@@ -1484,6 +1491,9 @@ bool launch_u8_rcr_rows(const S8Args &p, hipStream_t stream) {
                                dim3(p.N / (16 * (NB)), blocks), dim3(1024), lds, stream, p, pm.M);                      \
         return true;                                                                                            \
     }
+    BK_U8ROWS(1, 1, 512, 3)
+    BK_U8ROWS(1, 2, 512, 3)
+    BK_U8ROWS(1, 4, 512, 3)
     BK_U8ROWS(2, 1, 512, 3)
     BK_U8ROWS(4, 1, 512, 2)
     BK_U8ROWS(8, 1, 512, 2)
@@ -1778,6 +1788,9 @@ bool launch_rrr_rows(const S8Args &p, hipStream_t stream) {
                                dim3(p.N / (16 * (NB)), blocks), dim3(1024), lds, stream, p, pm.M);                      \
         return true;                                                                                            \
     }
+    BK_RRRROWS(1, 1, 512, 3)
+    BK_RRRROWS(1, 2, 512, 3)
+    BK_RRRROWS(1, 4, 512, 3)
     BK_RRRROWS(2, 1, 512, 3)
     BK_RRRROWS(4, 1, 512, 2)
     BK_RRRROWS(8, 1, 512, 2)

@@ -347,7 +347,9 @@ def test_null_c_with_beta(gpu, shape, layout, epi, elem):
 U8_ROWS_SHAPES = [(1, 4096, 4096), (5, 256, 512), (33, 512, 1024), (100, 6144, 512), (128, 12288, 512),
                   (1025, 16384, 512), (1100, 16384, 1024), (20, 272, 512), (1, 256, 1024),
                   # row blocks below N = 6144: two 64-row blocks, three 32-row blocks
-                  (100, 4096, 512), (90, 1024, 1024)]
+                  (100, 4096, 512), (90, 1024, 1024),
+                  # one fragment (up to 16 rows) at 32 / 64 columns
+                  (12, 14336, 1024), (9, 8192, 512)]
 
 
 @pytest.mark.parametrize("layout", [RCR, RRR])
@@ -391,7 +393,8 @@ def test_u8_last_rows_large_k_exact(gpu, layout):
 # below 6144 / from 6144 / from 12288), 2 / 4 / 8 row fragments, main RRR
 # tiles above the rows.
 RRR_ROWS_SHAPES = [(1, 4096, 4096), (5, 256, 512), (33, 512, 1024), (20, 288, 512), (100, 272, 512),
-                   (128, 1024, 2048), (1025, 16384, 512), (1100, 16384, 1024), (20, 6144, 512), (100, 4096, 512)]
+                   (128, 1024, 2048), (1025, 16384, 512), (1100, 16384, 1024), (20, 6144, 512), (100, 4096, 512),
+                   (9, 8192, 512), (16, 14336, 512)]
 
 
 @pytest.mark.parametrize("epi", [P.EpilogueKind.Identity, P.EpilogueKind.BiasGelu, P.EpilogueKind.BiasRelu])
