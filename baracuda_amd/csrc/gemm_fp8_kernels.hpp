@@ -589,6 +589,15 @@ int32_t launch_fp8(const F8Args &p, hipStream_t stream) {
                                    (size_t)(DEPTH) * (16 * (RF) + 16 * (NB)) * (SB), stream, p, pm.M);    \
                 return launch_status();                                                                   \
             }
+            // up to 16 / 32 rows: 1 / 2 fragments with 4 / 8 waves
+            // multiplying (K = 4096: M = 1-16 N = 4096 9.1 -> 8.8 us, N =
+            // 14336 18.4 -> 13.5 us; M = 17-32 N = 8192 12.6 -> 11.9 us, N =
+            // 14336 18.3 -> 14.5 us)
+            BK_F8RRRROWS(1, 1, 512, 3)
+            BK_F8RRRROWS(1, 2, 512, 3)
+            BK_F8RRRROWS(1, 4, 512, 3)
+            BK_F8RRRROWS(2, 2, 512, 2)
+            BK_F8RRRROWS(2, 4, 512, 2)
             BK_F8RRRROWS(4, 4, 512, 2)
             BK_F8RRRROWS(8, 4, 256, 2)
             BK_F8RRRROWS(4, 2, 512, 2)

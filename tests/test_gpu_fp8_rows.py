@@ -128,10 +128,12 @@ def test_fp8_rows_deterministic_and_untouched_columns(gpu):
 # RRR (row-major B [K, N]) last rows: the staged kernel with transposing LDS
 # reads; 16 / 32 / 64 columns per workgroup by the last-rows rule, 1 / 2 / 4 /
 # 8 fragments, main RRR tiles above the rows at N = 16384; row blocks below
-# N = 6144 with K % 1024 == 0 (100 x 512, 100 x 4096, 60 x 3072).
+# N = 6144 with K % 1024 == 0 (100 x 512, 100 x 4096, 60 x 3072); up to 16 /
+# 32 rows on 1 / 2 fragments with only some waves multiplying (1 x 256,
+# 5 x 272, 9 x 14336, 17 x 6144, 30 x 14336).
 RRR_SHAPES = [(1, 256, 4096), (17, 288, 1024), (33, 272, 512), (5, 272, 2048), (100, 512, 1024),
               (128, 1040, 512), (1025, 16384, 512), (17, 6144, 1024), (64, 8192, 512),
-              (100, 4096, 1024), (60, 3072, 1024)]
+              (100, 4096, 1024), (60, 3072, 1024), (9, 14336, 512), (30, 14336, 1024)]
 
 
 @pytest.mark.parametrize("epi", EPIS)
