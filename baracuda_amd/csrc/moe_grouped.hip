@@ -693,10 +693,11 @@ int32_t launch_moe(const MoeArgs &p, const int32_t *expert_ids, int32_t *expert_
     q.expert_ids = expert_ids;
     q.counts = expert_counts;
     if constexpr (KIND == MOE_S8 || KIND == MOE_S8_I32) {
-        // 3-8 pairs: the dot4 row kernel, 2 rows per pass over the weights
-        // (2 / 4 tokens: 56.0 / 67.9 -> 47.2 / 65.9 us; at 2 pairs 22.5
-        // against 22.4 us, from 16 pairs slower: 2 pairs stay staged)
-        if (fast && p.size_m > 2 && p.size_m <= 8 && kb % 1024 == 0 && p.N % 4 == 0) {
+        // 3-6 pairs: the dot4 row kernel, 2 rows per pass over the weights
+        // (2 / 3 tokens: 53.4 / 53.4 -> 48.0 / 48.0 us against the staged
+        // kernel's 16-row blocks; at 2 pairs 22.5 against 22.4 us, at 8
+        // 65.9 against 64.8 us: those stay staged)
+        if (fast && p.size_m > 2 && p.size_m <= 6 && kb % 1024 == 0 && p.N % 4 == 0) {
             if (kb % 2048 == 0)
                 hipLaunchKernelGGL((moe_row_kernel<KIND, 2, 2>), dim3(p.N / 4, p.E), dim3(256), 0, stream, q);
             else

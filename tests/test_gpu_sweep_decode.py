@@ -53,7 +53,7 @@ def test_moe_sweep(gpu, case):
 
 def _moe_decode_cases(count, seed):
     # at most 64 pairs: the decode kernels (staged, and the dot4 row kernel
-    # for 3-8 pairs with K % 1024 == 0); K on the 512 / 1024 grids and off
+    # for 3-6 pairs with K % 1024 == 0); K on the 512 / 1024 grids and off
     # them (the tile path)
     g = rng(seed)
     out = []
