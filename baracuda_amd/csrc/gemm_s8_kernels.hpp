@@ -1628,7 +1628,10 @@ void launch_kernel(const S8Args &p, bool fast_k, hipStream_t stream, void *works
                                    dim3(p.N / 16), dim3(1024), (size_t)3 * 32 * 512, stream, p, pm.M);
                 return;
             }
-            if (rem > (nb > 1 ? 8 : kRowsDmaMaxRows) && p.K % kRowsStagedSB == 0) {
+            // staged from 6 rows at 64 columns (one fragment: N = 14336 / 12288,
+            // M = 8 14.2 / 11.6 -> 13.2 / 10.8 us against the B-through-LDS
+            // kernel, level at 2-5 rows), from 9 at 32 columns, from 17 at 16
+            if (rem > (nb > 1 ? (nb == 4 ? 5 : 8) : kRowsDmaMaxRows) && p.K % kRowsStagedSB == 0) {
 #define BK_S8ROWS(RF, NB, SB, DEPTH)                                                                        \
     if (rem <= 16 * (RF) && nb == (NB) && p.K % (SB) == 0) {                                                 \
         hipLaunchKernelGGL((gemm_s8_rcr_rows_staged_kernel<EPI, VecOut, ACT, BiasT, RF, NB, SB, DEPTH>),     \
@@ -1640,9 +1643,9 @@ void launch_kernel(const S8Args &p, bool fast_k, hipStream_t stream, void *works
                 BK_S8ROWS(2, 1, 512, 3)
                 BK_S8ROWS(4, 1, 512, 2)
                 BK_S8ROWS(8, 1, 512, 2)
-                // 9-16 rows from N = 6144: one fragment, 8 waves multiplying
-                // (N = 14336 / 8192, M = 12-16: 13.85 / 8.6-8.7 -> 13.3 /
-                // 8.5 us against two fragments)
+                // up to 16 rows from N = 6144: one fragment, 8 waves
+                // multiplying (N = 14336 / 8192, M = 12-16: 13.85 / 8.6-8.7
+                // -> 13.3 / 8.5 us against two fragments)
                 BK_S8ROWS(1, 2, 512, 2)
                 BK_S8ROWS(1, 4, 512, 2)
                 BK_S8ROWS(2, 2, 512, 3)

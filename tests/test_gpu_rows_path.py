@@ -48,7 +48,9 @@ STAGED_SHAPES = [(17, 256, 512), (31, 1040, 1536), (33, 512, 512), (65, 272, 102
                  # 64-row blocks of 32 columns, 32-row blocks of 32 columns, 3 blocks
                  (100, 4096, 1024), (128, 2048, 512), (48, 4096, 512), (90, 3072, 512),
                  # 11-16 rows below N = 6144: one fragment, 8 of 16 waves multiplying
-                 (11, 1040, 1024), (16, 4096, 2048)]
+                 (11, 1040, 1024), (16, 4096, 2048),
+                 # 6-8 rows at 64 columns (N >= 12288): one fragment
+                 (6, 12288, 1024), (8, 14336, 512)]
 SHAPES += STAGED_SHAPES
 
 
