@@ -85,9 +85,23 @@ def _decode_calls(kind):
         plan = P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, layout=P.LayoutSku.Rrr, element=P.ElementKind.U8,
                                                         output=P.ElementKind.U8))
         return a, (m, n), torch.uint8, lambda o: plan.run(a, b, o, alpha=1.0 / (64 * k))
-    # int8 MoE decode: offsets kernel + per-expert staged pass
+    if kind == "fp8_m1":           # FP8 one-row FMA kernel
+        m, n, k = 1, 4096, 2048
+        a = torch.randint(-100, 100, (m, k), dtype=torch.int8, device=dev).view(torch.uint8)
+        b = torch.randint(-100, 100, (n, k), dtype=torch.int8, device=dev).view(torch.uint8)
+        plan = P.Fp8GemmPlan.select(P.Fp8GemmDescriptor(m, n, k, output=P.ElementKind.Bf16))
+        return a, (m, n), torch.bfloat16, lambda o: plan.run(a, b, o, scale_a=0.01, scale_b=0.02)
+    if kind == "w8a8_m100_blocks":  # 33-128 last rows as row blocks (blockIdx.y)
+        m, n, k = 100, 4096, 1024
+        a = torch.randint(-127, 128, (m, k), dtype=torch.int8, device=dev)
+        w = torch.randint(-127, 128, (n, k), dtype=torch.int8, device=dev)
+        sa, sw = torch.rand(m, device=dev) + 0.01, torch.rand(n, device=dev) * 0.01
+        plan = P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, output=P.ElementKind.Bf16))
+        return a, (m, n), torch.bfloat16, lambda o: plan.run(a, w, o, scale_a=sa, scale_b=sw)
+    # int8 MoE decode: counts and offsets in the decode kernels; 3 tokens top-2
+    # (6 pairs) take the dot4 row kernel, 4 tokens the staged 16-row blocks
     from oracle.inputs import moe_routing
-    tokens, E, topk, n, k = 4, 8, 2, 2048, 1024
+    tokens, E, topk, n, k = (3 if kind == "moe_decode_row" else 4), 8, 2, 2048, 1024
     sid, eid = moe_routing(tokens, E, topk, seed=3)
     x = torch.randint(-127, 128, (tokens, k), dtype=torch.int8, device=dev)
     w = torch.randint(-127, 128, (E, n, k), dtype=torch.int8, device=dev)
@@ -99,7 +113,8 @@ def _decode_calls(kind):
     return x, (tokens * topk, n), torch.bfloat16, lambda o: plan.run(x, w, dsid, deid, o, cnt, off, sa, sw)
 
 
-@pytest.mark.parametrize("kind", ["w8a8_m1", "w8a8_m40_wide", "fp8_m16", "u8_rrr_m8", "moe_decode"])
+@pytest.mark.parametrize("kind", ["w8a8_m1", "w8a8_m40_wide", "fp8_m16", "u8_rrr_m8", "moe_decode", "fp8_m1",
+                                  "w8a8_m100_blocks", "moe_decode_row"])
 def test_decode_paths_graph_replays_match_eager(gpu, kind):
     # The decode-sized passes allocate nothing and set no memory: captured
     # once, every replay (new inputs, eager work in between) equals the eager
