@@ -161,17 +161,22 @@ def test_rows_path_with_and_without_split_workspace(gpu):
     assert np.array_equal(outs[0][rows], a[rows].astype(np.int64) @ b.astype(np.int64).T)
 
 
-@pytest.mark.parametrize("shape", [(7, 512, 2048), (30, 4096, 1024), (100, 1024, 2048), (60, 512, 1536), (1, 1024, 2048)])
+@pytest.mark.parametrize("shape", [(7, 512, 2048), (30, 4096, 1024), (100, 1024, 2048), (60, 512, 1536), (1, 1024, 2048),
+                                   (12, 4096, 1024), (8, 12288, 1024), (200, 2048, 1024)])
 def test_rows_dma_padded_leading_dimensions(gpu, shape):
-    # A and B views with row pitches past K (16-byte multiples): the
-    # LDS-streamed kernels address rows by ldb and A rows by lda.
+    # A, B and D views with row pitches past K / N (16-byte multiples): the
+    # LDS-streamed kernels address rows by ldb and A rows by lda, the
+    # epilogue D rows by ldd (one-fragment blocks at 12 x 4096 and 8 x 12288,
+    # 64-row blocks of a small grid at 200 x 2048); columns past N untouched.
     m, n, k = shape
     print(f"case: rows dma padded ld {shape}", flush=True)
     g = rng(m + n + k + 3)
     a_full, b_full = int8_uniform(g, (m, k + 64)), int8_uniform(g, (n, k + 128))
     ta, tb = dev(a_full)[:, :k], dev(b_full)[:, :k]
-    d = torch.full((m, n), -7, dtype=torch.int32, device="cuda:0")
-    P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, output=P.ElementKind.I32)).run(ta, tb, d)
+    d_full = torch.full((m, n + 32), -7, dtype=torch.int32, device="cuda:0")
+    P.IntGemmPlan.select(P.IntGemmDescriptor(m, n, k, output=P.ElementKind.I32)).run(ta, tb, d_full[:, :n])
     sync()
     want = a_full[:, :k].astype(np.int64) @ b_full[:, :k].astype(np.int64).T
-    assert np.array_equal(d.cpu().numpy(), want)
+    got = d_full.cpu().numpy()
+    assert np.array_equal(got[:, :n], want)
+    assert np.all(got[:, n:] == -7)
