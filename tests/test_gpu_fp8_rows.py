@@ -192,3 +192,24 @@ def test_fp8_rrr_small_grid_row_blocks(gpu, shape, fmt, epi):
         assert np.array_equal(got, want)
     else:
         assert _steps(got, want, fmt).max() <= 1.0
+
+
+@pytest.mark.parametrize("shape", [(1, 4096, 2048), (16, 14336, 1024), (100, 4096, 1024), (256, 4096, 512)])
+def test_fp8_rows_padded_leading_dimensions(gpu, shape):
+    # A, B and D views with pitches past K / N: the one-row kernel, the
+    # partial-wave blocks, the row blocks and a small grid's blocks address
+    # rows by lda / ldb / ldd; f32 accumulators against the f64 sum, columns
+    # past N untouched.
+    m, n, k = shape
+    print(f"case: fp8 rows padded ld {shape}", flush=True)
+    a, b, _, _ = _fp8_inputs(m, n, k, seed=m + 2 * n + k)
+    a_full = np.zeros((m, k + 64), np.uint8)
+    b_full = np.zeros((n, k + 128), np.uint8)
+    a_full[:, :k], b_full[:, :k] = a, b
+    d_full = torch.full((m, n + 32), -7.0, dtype=torch.float32, device="cuda:0")
+    P.Fp8GemmPlan.select(P.Fp8GemmDescriptor(m, n, k, output=P.ElementKind.F32)).run(
+        dev(a_full)[:, :k], dev(b_full)[:, :k], d_full[:, :n], alpha=1.0)
+    sync()
+    got = d_full.cpu().numpy()
+    _fp8_check_acc(got[:, :n], a, b)
+    assert np.all(got[:, n:] == -7.0)
