@@ -330,12 +330,13 @@ def test_moe_config5_i32_whole_output_exact_and_bf16_epilogue(gpu):
                                   (32, 8, 2, 256, 512, True), (4, 8, 2, 6144, 512, False),
                                   (2, 8, 2, 12288, 512, True), (21, 4, 3, 256, 1536, False),
                                   (2, 8, 2, 512, 1024, False), (4, 8, 2, 1024, 4096, True), (3, 4, 2, 256, 3072, False),
-                                  (6, 1, 1, 256, 2048, False)])
+                                  (6, 1, 1, 256, 2048, False), (3, 8, 2, 512, 1024, True)])
 def test_moe_decode_all_pairs(gpu, case):
     # every pair bit-exact against the per-pair W8A8 formula; size_m 2 to 64
     # (16- or 32-row blocks), 16 / 32 / 64 columns per workgroup; the row
-    # kernel at 4 / 6 pairs (1 or 2 KiB per batch) and with 6 rows on one
-    # expert (3 passes of 2 rows); 8 pairs on the staged kernel
+    # kernel at 4 / 6 pairs (1 or 2 KiB per batch, with and without
+    # topk_weights) and with 6 rows on one expert (3 passes of 2 rows); 8
+    # pairs on the staged kernel
     tokens, E, topk, n, k, tw = case
     print(f"case: moe decode {case}", flush=True)
     _run(tokens=tokens, E=E, topk=topk, n=n, k=k, seed=tokens * 7 + n, topk_w=tw)
